@@ -1,0 +1,125 @@
+/*
+ * vsampler: token sampling for the vinfer engine on AMD Instinct MI355X (gfx950).
+ *
+ * A plain C ABI over hand-written HIP kernels. It replaces the body of the engine's per-token
+ * sampler, src/vinfer/runtime/sampler.py:50-77 (`filtered_probs` + `sample`), with one batched
+ * call over B rows, and adds what the engine names but does not implement: repetition,
+ * presence and frequency penalties (server/protocol.py:133-135), min-p (protocol.py:142), an
+ * inverse-CDF draw from caller-supplied uniforms, and the probability of a given draft id.
+ *
+ * Conventions (all entry points):
+ *  - Every buffer is caller-allocated device memory; the library never allocates or frees.
+ *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the null stream).
+ *    Nothing synchronises the host.
+ *  - Return 0 on success, a VSAMP_E_* code otherwise; vsamp_last_error() then describes the
+ *    failure (thread-local, valid until the next call on the same thread).
+ *  - No global mutable state: calls on different streams may run concurrently as long as they
+ *    use different workspaces.
+ */
+#ifndef VSAMPLER_H
+#define VSAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VSAMP_ABI_VERSION 1
+
+enum vsamp_dtype { VSAMP_BF16 = 0, VSAMP_F32 = 1 };
+
+enum vsamp_status {
+  VSAMP_OK = 0,
+  VSAMP_E_ARG = 1,       /* a null pointer, a bad size or a stride that does not fit */
+  VSAMP_E_DTYPE = 2,     /* logits dtype not in vsamp_dtype */
+  VSAMP_E_HIP = 3,       /* a HIP runtime call failed */
+  VSAMP_E_WORKSPACE = 4, /* workspace missing or smaller than vsamp_workspace_bytes() */
+  VSAMP_E_DEVICE = 5     /* the current device is not a gfx950 GPU */
+};
+
+/*
+ * One batch of B rows. Per-row parameter arrays have length B and live on the device; any of
+ * them may be NULL, which means the engine's default for every row (SamplingParams defaults,
+ * sampler.py:20-23): temperature 1, top_k 0 (off), top_p 1 (off), min_p 0 (off), repetition 1,
+ * presence 0, frequency 0 (penalties off).
+ */
+typedef struct vsamp_args {
+  /* Logits [B, V] in `dtype`; row r starts at element r * row_stride. */
+  const void* logits;
+  int32_t dtype; /* enum vsamp_dtype */
+  int32_t batch; /* B >= 0 */
+  int32_t vocab; /* V >= 1 */
+  int32_t reserved0;
+  int64_t row_stride; /* elements, >= V */
+
+  /* Per-row sampling parameters (sampler.py:18-41 plus the extensions). */
+  const float* temperature; /* 0 = greedy (argmax, sampler.py:70-71) */
+  const int32_t* top_k;     /* 0 or >= V = off */
+  const float* top_p;       /* in (0, 1]; 1 = off */
+  const float* min_p;       /* in [0, 1]; 0 = off */
+  const float* repetition_penalty;
+  const float* presence_penalty;
+  const float* frequency_penalty;
+
+  /* Token histories in CSR form: row r's ids are hist_ids[hist_offsets[r] .. hist_offsets[r+1]).
+   * Both NULL = empty histories. Ids outside [0, V) are ignored. */
+  const int32_t* hist_ids;
+  const int32_t* hist_offsets; /* B + 1 entries, non-decreasing, hist_offsets[0] = 0 */
+  int64_t hist_total;          /* hist_offsets[B], known to the caller (sizes the workspace) */
+
+  /* The draw: one uniform u in [0, 1) per row (required). */
+  const float* uniforms;
+  /* Optional draft ids (one per row, in [0, V)); with out_draft_prob, reports the final
+   * probability of that id after every filter. Both NULL or both set. */
+  const int32_t* draft_ids;
+
+  /* Outputs. */
+  int32_t* out_ids;      /* [B] sampled token ids */
+  float* out_draft_prob; /* [B] or NULL */
+
+  /* Scratch of at least vsamp_workspace_bytes(batch, vocab, hist_total) bytes, 256-byte
+   * aligned. May be NULL when that size is 0. */
+  void* workspace;
+  size_t workspace_bytes;
+
+  uint32_t flags; /* must be 0 */
+  uint32_t reserved1;
+} vsamp_args;
+
+/* The ABI version this library was built with (VSAMP_ABI_VERSION). */
+int vsamp_abi_version(void);
+
+/* 0 if `device` can run the kernels; otherwise a VSAMP_E_* code and, when why != NULL, a
+ * NUL-terminated reason in why[0..n). Backs the backend's `supports(ctx)` check, which the
+ * engine runs at startup (kernels/registry.py:38-43, :84-88). */
+int vsamp_query(int device, char* why, size_t n);
+
+/* Workspace bytes vsamp_sample / vsamp_probs / vsamp_penalized_logits need. */
+size_t vsamp_workspace_bytes(int32_t batch, int32_t vocab, int64_t hist_total);
+
+/* Sample one token per row: penalties, temperature, top-k, softmax, min-p, top-p, then the
+ * inverse-CDF draw over kept tokens in ascending id order. Replaces `sample(logits, params,
+ * seed, position)` (sampler.py:68-77) for B rows at once. */
+int vsamp_sample(const vsamp_args* args, void* stream);
+
+/* The final per-token probabilities [B, V] fp32 that vsamp_sample draws from (0 for dropped
+ * tokens); row r at out + r * out_stride. Replaces `filtered_probs` (sampler.py:50-65), with the
+ * extensions applied. `uniforms` and the outputs in `args` are not used. */
+int vsamp_probs(const vsamp_args* args, float* out, int64_t out_stride, void* stream);
+
+/* The penalised logits [B, V] fp32 (penalties only, no temperature); row r at
+ * out + r * out_stride. Optional `counts` [B, V] int32 receives the history count of every id
+ * (row r at counts + r * out_stride), or NULL. */
+int vsamp_penalized_logits(const vsamp_args* args, float* out, int32_t* counts,
+                           int64_t out_stride, void* stream);
+
+/* Description of the last failure on this thread ("" if none). */
+const char* vsamp_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VSAMPLER_H */

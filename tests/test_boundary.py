@@ -1,0 +1,146 @@
+"""The drop-in boundary: registry rules and messages (tests/unit/kernels/test_registry.py:22-72),
+KernelConfig parsing (tests/unit/test_config.py:22-33), SamplingParams validation
+(tests/unit/runtime/test_sampler.py:59-62) and the startup check of the ``hip`` backend."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from vinfer_amd.config import KernelConfig
+from vinfer_amd.kernels import resolve_kernels
+from vinfer_amd.registry import BackendContext, BackendRegistry
+from vinfer_amd.sampler import SAMPLER, HipSampler, ReferenceSampler
+from vinfer_amd.sampling import SamplingParams, pack_history, pack_params, uniform
+
+CPU, CUDA = torch.device("cpu"), torch.device("cuda")
+
+
+def _ctx(device, dtype=torch.float32):
+    return BackendContext(device, dtype)
+
+
+def _registry():
+    reg: BackendRegistry[object] = BackendRegistry("demo")
+
+    @reg.register("anywhere")
+    class Anywhere:
+        def __init__(self, ctx):
+            self.ctx = ctx
+
+    @reg.register("cuda-bf16", devices={"cuda"}, dtypes={torch.bfloat16})
+    class CudaOnly:
+        def __init__(self, ctx):
+            self.ctx = ctx
+
+    @reg.register("needs-gfx950", devices={"cuda"}, supports=lambda ctx: "needs gfx950")
+    class Picky:
+        def __init__(self, ctx):
+            self.ctx = ctx
+
+    return reg, Anywhere, CudaOnly
+
+
+def test_resolve_builds_the_backend_with_its_context():
+    reg, anywhere, cuda_only = _registry()
+    backend = reg.resolve("anywhere", _ctx(CPU))
+    assert isinstance(backend, anywhere) and backend.ctx == _ctx(CPU)
+    assert isinstance(reg.resolve("cuda-bf16", _ctx(CUDA, torch.bfloat16)), cuda_only)
+
+
+def test_unsupported_context_or_name_fails_instead_of_falling_back():
+    reg, _, _ = _registry()
+    with pytest.raises(ValueError, match="does not run on cpu"):
+        reg.resolve("cuda-bf16", _ctx(CPU, torch.bfloat16))
+    with pytest.raises(ValueError, match=r"does not support torch\.float32"):
+        reg.resolve("cuda-bf16", _ctx(CUDA))
+    with pytest.raises(ValueError, match=r"needs gfx950"):
+        reg.resolve("needs-gfx950", _ctx(CUDA))
+    with pytest.raises(ValueError, match=r"available: \['anywhere', 'cuda-bf16', 'needs-gfx950'\]"):
+        reg.resolve("missing", _ctx(CPU))
+    assert reg.unsupported("anywhere", _ctx(CPU)) is None
+
+
+def test_a_name_registers_once():
+    reg, _, _ = _registry()
+    with pytest.raises(ValueError, match="twice"):
+        reg.register("anywhere")(object)
+
+
+def test_sampler_family_has_both_backends():
+    assert SAMPLER.names() == ["hip", "reference"]
+
+
+def test_default_kernel_config_resolves_to_the_reference():
+    assert KernelConfig().sampler_backend == "reference"
+    assert isinstance(resolve_kernels(KernelConfig(), CPU, torch.float32).sampler, ReferenceSampler)
+
+
+def test_hip_backend_fails_at_startup_off_gpu():
+    with pytest.raises(ValueError, match="sampler backend 'hip' does not run on cpu"):
+        resolve_kernels(KernelConfig(sampler_backend="hip"), CPU, torch.bfloat16)
+    with pytest.raises(ValueError, match=r"does not support torch\.float16"):
+        SAMPLER.resolve("hip", _ctx(CUDA, torch.float16))
+    with pytest.raises(ValueError, match="unknown sampler backend 'triton'"):
+        resolve_kernels(KernelConfig(sampler_backend="triton"), CPU, torch.float32)  # type: ignore[arg-type]
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU reason")
+def test_hip_supports_reports_why_without_a_gpu():
+    reason = SAMPLER.unsupported("hip", _ctx(CUDA, torch.bfloat16))
+    assert reason is not None and ("no HIP device" in reason or "ROCm" in reason)
+
+
+def test_kernel_config_from_string():
+    assert KernelConfig.from_string(None) == KernelConfig() == KernelConfig.from_string("")
+    cfg = KernelConfig.from_string(" sampler_backend = hip ")
+    assert cfg.describe() == "sampler_backend=hip"
+    with pytest.raises(ValueError, match="unknown kernel setting"):
+        KernelConfig.from_string("sampler=x")
+    with pytest.raises(ValueError, match="key=value"):
+        KernelConfig.from_string("hip")
+
+
+def test_invalid_params_are_rejected():
+    for kw in (
+        {"temperature": -1},
+        {"top_p": 0},
+        {"top_k": -1},
+        {"max_tokens": 0},
+        {"repetition_penalty": 0},
+        {"min_p": 1.5},
+        {"presence_penalty": float("inf")},
+    ):
+        with pytest.raises(ValueError):
+            SamplingParams(**kw)
+
+
+def test_extension_fields_default_off_and_reference_fields_unchanged():
+    p = SamplingParams()
+    assert (p.max_tokens, p.temperature, p.top_k, p.top_p, p.seed) == (16, 1.0, 0, 1.0, None)
+    assert not p.penalized and p.min_p == 0.0
+
+
+def test_packing_rounds_reals_to_fp32_once():
+    pp = pack_params([SamplingParams(temperature=0.7, top_p=0.9, top_k=5), SamplingParams()])
+    assert pp.temperature.dtype == torch.float32 and pp.top_k.dtype == torch.int32
+    assert float(pp.temperature[0]) == float(torch.tensor(0.7, dtype=torch.float32))
+    ids, off = pack_history([[3, 1], [], [2]])
+    assert ids.tolist() == [3, 1, 2] and off.tolist() == [0, 2, 2, 3]
+
+
+def test_uniform_is_a_24_bit_fraction_and_depends_on_seed_and_position():
+    us = [uniform(7, p) for p in range(200)]
+    assert all(0 <= u < 1 and (u * 2**24).is_integer() for u in us)
+    assert len(set(us)) > 190 and uniform(7, 0) != uniform(8, 0)
+    assert [uniform(7, p) for p in range(50)] == us[:50]
+
+
+def test_reference_sample_keeps_the_engine_call():
+    s = ReferenceSampler(_ctx(CPU))
+    logits = torch.tensor([2.0, 1.0, 0.5, 0.0, -1.0, -3.0])
+    assert s.sample(torch.tensor([0.1, 3.0, -2.0]), SamplingParams(temperature=0), 0, 0) == 1
+    toks = [s.sample(logits, SamplingParams(top_k=2), 7, p) for p in range(30)]
+    assert toks == [s.sample(logits, SamplingParams(top_k=2), 7, p) for p in range(30)]
+    assert set(toks) <= {0, 1}
+    assert HipSampler is SAMPLER._entries["hip"].factory

@@ -1,0 +1,114 @@
+"""The C ABI library: it loads, exports exactly what include/vsampler.h declares, and rejects
+bad arguments with the documented codes before touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from vinfer_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "vsampler.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(vsamp_\w+)\s*\(", text, re.M)))
+
+
+def test_library_is_built_and_loads():
+    assert _lib.LIB_PATH.exists(), "run python -m vinfer_amd.csrc.build"
+    lib = _lib.load()
+    assert lib.vsamp_abi_version() == _lib.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared()
+    assert names == sorted(_lib.EXPORTS)
+    lib = _lib.load()
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_header_struct_matches_the_binding(tmp_path):
+    # Field names in order, and every offset and the size as the C compiler lays them out.
+    text = HEADER.read_text()
+    body = text[text.index("typedef struct vsamp_args") : text.index("} vsamp_args;")]
+    fields = re.findall(r"^\s*[\w\s\*]+?\b(\w+);", body, re.M)
+    assert fields == [f for f, _ in _lib.VsampArgs._fields_]
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = tmp_path / "layout.c"
+    lines = [f'printf("%zu\\n", offsetof(vsamp_args, {f}));' for f in fields]
+    src.write_text(
+        "#include <stdio.h>\n#include <stddef.h>\n#include \"vsampler.h\"\nint main(void){"
+        + "".join(lines)
+        + 'printf("%zu\\n", sizeof(vsamp_args));return 0;}\n'
+    )
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [getattr(_lib.VsampArgs, f).offset for f in fields] + [ctypes.sizeof(_lib.VsampArgs)]
+    assert got == want
+
+
+def test_workspace_size_formula():
+    lib = _lib.load()
+    assert lib.vsamp_workspace_bytes(0, 1, 0) > 0 or lib.vsamp_workspace_bytes(0, 1, 0) == 0
+    n = lib.vsamp_workspace_bytes(256, 151936, 256 * 4096)
+    assert n >= 256 * 4 + 3 * 4 * 256 * 4096 + 256 * (151936 // 8)
+    assert lib.vsamp_workspace_bytes(-1, 10, 0) == 0
+
+
+def _args(**kw):
+    a = _lib.VsampArgs()
+    a.logits, a.dtype, a.batch, a.vocab, a.row_stride = 0x1000, 0, 4, 100, 100
+    a.uniforms, a.out_ids = 0x2000, 0x3000
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "kw,code,msg",
+    [
+        ({"dtype": 7}, 2, "dtype"),
+        ({"vocab": 0}, 1, "vocab"),
+        ({"row_stride": 50}, 1, "row_stride"),
+        ({"batch": -1}, 1, "batch"),
+        ({"uniforms": None}, 1, "uniforms"),
+        ({"out_ids": None}, 1, "out_ids"),
+        ({"flags": 1}, 1, "flags"),
+        ({"draft_ids": 0x4000}, 1, "draft"),
+        ({"hist_ids": 0x5000, "hist_total": 10}, 1, "hist"),
+        ({"logits": None}, 1, "logits"),
+    ],
+)
+def test_bad_arguments_are_rejected_with_their_code(kw, code, msg):
+    lib = _lib.load()
+    rc = lib.vsamp_sample(ctypes.byref(_args(**kw)), None)
+    assert rc == code
+    assert msg in lib.vsamp_last_error().decode()
+    with pytest.raises(_lib.VsamplerError, match=msg):
+        _lib.check(rc)
+
+
+def test_empty_batch_is_a_no_op():
+    lib = _lib.load()
+    assert lib.vsamp_sample(ctypes.byref(_args(batch=0)), None) == 0
+    assert lib.vsamp_last_error() == b""
+
+
+def test_query_names_the_problem_without_a_gpu():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    reason = _lib.query(0)
+    assert reason and "device" in reason

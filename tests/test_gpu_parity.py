@@ -1,0 +1,244 @@
+"""Device parity: the ``hip`` backend, called through the C ABI, against the CPU oracle.
+
+Token ids must be identical on every row the oracle does not classify as a tie; greedy ids and
+penalty counts always; probabilities within 1e-5 relative (fp32 output of fp64 math)."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.sampler_oracle import classify_ties, penalize
+from tests.parity import compare_ids, oracle
+from vinfer_amd import _lib, workloads
+from vinfer_amd.registry import BackendContext
+from vinfer_amd.sampler import SAMPLER
+from vinfer_amd.sampling import SamplingParams, pack_history, pack_params, uniform
+from vinfer_amd.workloads import Workload
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+PROB_RTOL = 1e-5
+
+
+def hip(dtype=torch.bfloat16):
+    return SAMPLER.resolve("hip", BackendContext(DEV, dtype))
+
+
+def run(w: Workload):
+    d = w.to(DEV)
+    s = hip(w.logits.dtype)
+    ids, dp = s.sample_batch(d.logits, d.params, d.uniforms, d.hist_ids, d.hist_offsets, d.draft_ids)
+    torch.cuda.synchronize()
+    return ids.cpu(), None if dp is None else dp.cpu()
+
+
+def check(w: Workload, max_tie_frac: float = 0.05):
+    print(f"case {w.name} B={w.batch} V={w.vocab} dtype={w.logits.dtype}", flush=True)
+    ids, dp = run(w)
+    res = oracle(w)
+    ties, bad = compare_ids(ids, res, dp)
+    assert not bad, bad[:10]
+    assert ties <= max(1, max_tie_frac * w.batch), (ties, w.batch)
+    return ties
+
+
+def random_workload(seed, B, V, dtype, penalties=True, hist_len=64, name="random") -> Workload:
+    rng = np.random.default_rng(seed)
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(B, V, generator=g) * float(rng.choice([0.5, 2.0, 3.0]))).to(dtype)
+    params = [
+        SamplingParams(
+            temperature=float(rng.choice([0.0, 0.3, 0.7, 1.0, 1.5])),
+            top_k=int(rng.choice([0, 0, 1, 5, 50, V - 1, V, V + 7])),
+            top_p=float(rng.choice([1.0, 1.0, 0.5, 0.9, 0.99, 1e-6])),
+            min_p=float(rng.choice([0.0, 0.0, 0.05, 0.3, 1.0])),
+            repetition_penalty=float(rng.choice([1.0, 1.05, 1.3])) if penalties else 1.0,
+            presence_penalty=float(rng.choice([0.0, 0.5, -0.5])) if penalties else 0.0,
+            frequency_penalty=float(rng.choice([0.0, 0.2, 1.0])) if penalties else 0.0,
+        )
+        for _ in range(B)
+    ]
+    hist = [rng.integers(-2, V + 2, int(rng.integers(0, hist_len + 1))).tolist() for _ in range(B)]
+    hi, ho = pack_history(hist)
+    u = torch.from_numpy(rng.random(B, dtype=np.float32))
+    draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
+    return Workload(name, x, pack_params(params), u, hi, ho, draft)
+
+
+def test_device_is_supported():
+    assert _lib.query(0) is None
+    assert SAMPLER.unsupported("hip", BackendContext(DEV, torch.bfloat16)) is None
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("V", [1, 6, 96, 1000, 4099, 20000])
+def test_random_rows_match_the_oracle(dtype, V):
+    check(random_workload(V, 48, V, dtype), max_tie_frac=0.1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_probabilities_match_the_oracle(dtype):
+    w = random_workload(7, 32, 3000, dtype)
+    d = w.to(DEV)
+    pr = hip(dtype).probs(d.logits, d.params, d.hist_ids, d.hist_offsets).cpu().double().numpy()
+    for b, r in enumerate(oracle(w, want_probs=True)):
+        if classify_ties(r):
+            continue
+        assert ((pr[b] > 0) == r.kept).all(), b
+        np.testing.assert_allclose(pr[b], r.probs, rtol=PROB_RTOL, atol=1e-30)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_penalty_counts_and_values_are_exact(dtype):
+    w = random_workload(3, 16, 5000, dtype, hist_len=3000)
+    # one row with a single id repeated far past 2^16
+    hist = [list(range(5)) * 3] * 15 + [[17] * 70000 + [4999, -1, 5000]]
+    w.hist_ids, w.hist_offsets = pack_history(hist)
+    d = w.to(DEV)
+    xs, counts = hip(dtype).penalized_logits(d.logits, d.params, d.hist_ids, d.hist_offsets)
+    xs, counts = xs.cpu().numpy(), counts.cpu().numpy()
+    p = w.params
+    for b in range(w.batch):
+        h = np.array(hist[b])
+        x, c = penalize(
+            w.logits[b].float().numpy(),
+            h,
+            float(p.repetition_penalty[b]),
+            float(p.presence_penalty[b]),
+            float(p.frequency_penalty[b]),
+        )
+        assert np.array_equal(counts[b], c), b
+        if p.repetition_penalty[b] != 1 or p.presence_penalty[b] != 0 or p.frequency_penalty[b] != 0:
+            assert np.array_equal(xs[b].view(np.uint32), x.view(np.uint32)), b
+        else:
+            assert np.array_equal(xs[b], w.logits[b].float().numpy()), b
+
+
+@pytest.mark.parametrize("name,B", [("mixed_bf16", 64), ("peaked_flat", 64), ("verify_bf16", 24), ("large_fp32", 12), ("single_fp32", 1)])
+def test_workload_rows_match_the_oracle(name, B):
+    check(workloads.make(name, batch=B), max_tie_frac=0.1)
+
+
+def test_headline_shape_full_batch():
+    ties = check(workloads.make("peaked_flat"), max_tie_frac=0.1)
+    print("ties", ties)
+
+
+def test_single_row_many_steps():
+    # 200 steps of the single-row fp32 workload (new logits and uniform per step)
+    for step in range(0, 200, 40):
+        check(workloads.make("single_fp32", batch=40, seed=5000 + step))
+
+
+def test_degenerate_rows():
+    V = 37
+    nan, inf = float("nan"), float("inf")
+    rows = torch.randn(6, V)
+    rows[0, 5] = nan
+    rows[0, 9] = nan
+    rows[1, 3] = inf
+    rows[1, 30] = inf
+    rows[2, :] = -inf
+    rows[3, 11] = 3e38  # overflows to +inf at T = 1e-3
+    rows[4, :] = 0.0  # all equal: top-p cutoff inside one group
+    rows[5, 2] = nan
+    params = pack_params(
+        [
+            SamplingParams(temperature=1.0, top_p=0.9),
+            SamplingParams(temperature=0.7, top_k=3),
+            SamplingParams(temperature=1.0, min_p=0.1),
+            SamplingParams(temperature=1e-3),
+            SamplingParams(temperature=1.0, top_p=0.4),
+            SamplingParams(temperature=0.0),
+        ]
+    )
+    u = torch.tensor([0.3, 0.9, 0.5, 0.5, 0.99, 0.1])
+    for dtype in (torch.float32, torch.bfloat16):
+        w = Workload("degenerate", rows.to(dtype), params, u, None, None, torch.arange(6, dtype=torch.int32))
+        ids, _ = run(w)
+        assert ids.tolist() == [r.token for r in oracle(w)]
+        assert ids.tolist()[:3] == [5, 3, 0] and ids.tolist()[5] == 2
+
+
+def test_unaligned_and_padded_rows():
+    base = torch.randn(20, 1003)
+    for dtype in (torch.bfloat16, torch.float32):
+        x = base.to(dtype)[:, 1:1000]  # unaligned start, stride 1003
+        params = pack_params([SamplingParams(temperature=0.8, top_p=0.9)] * 20)
+        u = torch.rand(20)
+        s = hip(dtype)
+        ids, _ = s.sample_batch(x.to(DEV)[:, :], params.to(DEV), u.to(DEV))
+        w = Workload("strided", x.contiguous(), params, u, None, None, None)
+        ties, bad = compare_ids(ids, oracle(w))
+        assert not bad
+
+
+def test_temperature_division_merges_adjacent_fp32_values():
+    # T = 3 maps pairs of adjacent fp32 values to one z; top-k keeps every element whose z
+    # equals the kth z, which only a correctly rounded division reproduces.
+    rng = np.random.default_rng(11)
+    B, V = 32, 512
+    base = rng.normal(0, 2, (B, V // 2)).astype(np.float32)
+    x = np.concatenate([base, np.nextafter(base, np.float32(np.inf))], axis=1)
+    x = np.ascontiguousarray(x[:, rng.permutation(V)])
+    params = pack_params([SamplingParams(temperature=3.0, top_k=int(k)) for k in rng.integers(1, 60, B)])
+    w = Workload("merge", torch.from_numpy(x), params, torch.from_numpy(rng.random(B, dtype=np.float32)), None, None, None)
+    d = w.to(DEV)
+    pr = hip(torch.float32).probs(d.logits, d.params).cpu().numpy()
+    for b, r in enumerate(oracle(w, want_probs=True)):
+        assert ((pr[b] > 0) == r.kept).all(), b
+
+
+def test_draw_frequencies_match_the_distribution():
+    # 20,000 draws of one row with the package's uniforms: TV < 0.015 (test_sampler.py:24-38)
+    logits = torch.tensor([2.0, 1.0, 0.5, 0.0, -1.0, -3.0])
+    for sp in (SamplingParams(), SamplingParams(temperature=0.5), SamplingParams(top_k=3), SamplingParams(top_p=0.8)):
+        n = 20000
+        params = pack_params([sp] * n).to(DEV)
+        u = torch.tensor([uniform(1, p) for p in range(n)], dtype=torch.float32, device=DEV)
+        s = hip(torch.float32)
+        ids, _ = s.sample_batch(logits.expand(n, 6).contiguous().to(DEV), params, u)
+        freq = torch.bincount(ids.long().cpu(), minlength=6).double() / n
+        expected = s.probs(logits[None].to(DEV), pack_params([sp]).to(DEV))[0].double().cpu()
+        assert 0.5 * (freq - expected).abs().sum() < 0.015
+
+
+def test_per_token_call_matches_the_batch():
+    s = hip(torch.bfloat16)
+    logits = (torch.randn(1000) * 2).to(torch.bfloat16).to(DEV)
+    params = SamplingParams(temperature=0.9, top_p=0.9, repetition_penalty=1.2)
+    hist = [1, 2, 3, 3, 999]
+    for pos in range(10):
+        tok = s.sample(logits, params, 7, pos, history=hist)
+        u = torch.tensor([uniform(7, pos)], device=DEV)
+        hi, ho = pack_history([hist], DEV)
+        ids, _ = s.sample_batch(logits[None], pack_params([params], DEV), u, hi, ho)
+        assert tok == int(ids[0])
+    assert s.sample(torch.tensor([0.1, 3.0, -2.0], device=DEV), SamplingParams(temperature=0), 0, 0) == 1
+
+
+def test_deterministic_and_stream_safe():
+    w = workloads.make("mixed_bf16", batch=32).to(DEV)
+    s = hip()
+    a, _ = s.sample_batch(w.logits, w.params, w.uniforms, w.hist_ids, w.hist_offsets)
+    st = torch.cuda.Stream(DEV)
+    with torch.cuda.stream(st):
+        b, _ = s.sample_batch(w.logits, w.params, w.uniforms, w.hist_ids, w.hist_offsets)
+    st.synchronize()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_errors_are_raised_not_swallowed():
+    s = hip()
+    x = torch.randn(4, 100, device=DEV).to(torch.bfloat16)
+    p = pack_params([SamplingParams()] * 4, DEV)
+    with pytest.raises(ValueError, match="uniforms"):
+        s.sample_batch(x, p, torch.zeros(3, device=DEV))
+    with pytest.raises(ValueError):
+        s.sample_batch(x.half(), p, torch.zeros(4, device=DEV))
+    assert math.isfinite(float(s.probs(x, p).sum()))

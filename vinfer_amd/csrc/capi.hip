@@ -1,0 +1,285 @@
+// C ABI of the sampler library (declared in include/vsampler.h).
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/vsampler.h"
+#include "common.cuh"
+#include "penalty.cuh"
+#include "sample.cuh"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(VSAMP_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_dev_ok[kMaxDevices];  // 0 unknown, 1 gfx950, 2 not
+
+int check_device(int dev, char* why, size_t n) {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0) {
+    if (why && n) snprintf(why, n, "no HIP device available");
+    return VSAMP_E_DEVICE;
+  }
+  if (dev < 0 || dev >= count) {
+    if (why && n) snprintf(why, n, "device %d out of range (%d devices)", dev, count);
+    return VSAMP_E_DEVICE;
+  }
+  if (dev < kMaxDevices && g_dev_ok[dev].load() == 1) return VSAMP_OK;
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) {
+    if (why && n) snprintf(why, n, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    return VSAMP_E_HIP;
+  }
+  const bool ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  if (dev < kMaxDevices) g_dev_ok[dev].store(ok ? 1 : 2);
+  if (!ok) {
+    if (why && n) snprintf(why, n, "needs a gfx950 (MI355X) GPU, device %d is %s", dev, prop.gcnArchName);
+    return VSAMP_E_DEVICE;
+  }
+  return VSAMP_OK;
+}
+
+int check_current_device() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  char why[256];
+  int rc = check_device(dev, why, sizeof why);
+  if (rc) return fail(rc, "%s", why);
+  return VSAMP_OK;
+}
+
+size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+struct Layout {
+  size_t n_exc, exc_id, exc_val, exc_cnt, bitmap, total;
+  int nwords;
+};
+
+Layout layout(int64_t B, int64_t V, int64_t H) {
+  Layout L;
+  L.nwords = static_cast<int>((V + 31) / 32);
+  size_t o = 0;
+  L.n_exc = o;
+  o = align_up(o + 4 * static_cast<size_t>(B));
+  L.exc_id = o;
+  o = align_up(o + 4 * static_cast<size_t>(H));
+  L.exc_val = o;
+  o = align_up(o + 4 * static_cast<size_t>(H));
+  L.exc_cnt = o;
+  o = align_up(o + 4 * static_cast<size_t>(H));
+  L.bitmap = o;
+  o = align_up(o + 4 * static_cast<size_t>(B) * static_cast<size_t>(L.nwords));
+  L.total = o;
+  return L;
+}
+
+constexpr int64_t kMaxVocab = static_cast<int64_t>(vs::kMaxStripes) * vs::kThreads * vs::kBlk;
+
+int validate(const vsamp_args* a, bool need_draw) {
+  if (!a) return fail(VSAMP_E_ARG, "args is NULL");
+  if (a->flags != 0) return fail(VSAMP_E_ARG, "flags must be 0, got %u", a->flags);
+  if (a->dtype != VSAMP_BF16 && a->dtype != VSAMP_F32)
+    return fail(VSAMP_E_DTYPE, "unsupported logits dtype %d (VSAMP_BF16=0, VSAMP_F32=1)", a->dtype);
+  if (a->batch < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", a->batch);
+  if (a->vocab < 1 || a->vocab > kMaxVocab)
+    return fail(VSAMP_E_ARG, "vocab must be in [1, %lld], got %d", static_cast<long long>(kMaxVocab),
+                a->vocab);
+  if (a->row_stride < a->vocab)
+    return fail(VSAMP_E_ARG, "row_stride (%lld) must be >= vocab (%d)",
+                static_cast<long long>(a->row_stride), a->vocab);
+  if (a->batch > 0 && !a->logits) return fail(VSAMP_E_ARG, "logits is NULL");
+  if ((a->hist_ids == nullptr) != (a->hist_offsets == nullptr) && a->hist_total > 0)
+    return fail(VSAMP_E_ARG, "hist_ids and hist_offsets must both be set or both NULL");
+  if (a->hist_total < 0 || a->hist_total >= (int64_t(1) << 31))
+    return fail(VSAMP_E_ARG, "hist_total must be in [0, 2^31), got %lld",
+                static_cast<long long>(a->hist_total));
+  if (need_draw) {
+    if (a->batch > 0 && !a->out_ids) return fail(VSAMP_E_ARG, "out_ids is NULL");
+    if (a->batch > 0 && !a->uniforms) return fail(VSAMP_E_ARG, "uniforms is NULL");
+    if ((a->draft_ids == nullptr) != (a->out_draft_prob == nullptr))
+      return fail(VSAMP_E_ARG, "draft_ids and out_draft_prob must both be set or both NULL");
+  }
+  return VSAMP_OK;
+}
+
+bool wants_penalties(const vsamp_args* a) {
+  return a->hist_ids && a->hist_offsets && a->hist_total > 0 &&
+         (a->repetition_penalty || a->presence_penalty || a->frequency_penalty);
+}
+
+int check_workspace(const vsamp_args* a, const Layout& L) {
+  if (a->workspace_bytes < L.total || (L.total && !a->workspace))
+    return fail(VSAMP_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", a->workspace_bytes, L.total);
+  if (reinterpret_cast<uintptr_t>(a->workspace) & 255u)
+    return fail(VSAMP_E_WORKSPACE, "workspace must be 256-byte aligned");
+  return VSAMP_OK;
+}
+
+vs::Workspace workspace_of(const vsamp_args* a, const Layout& L) {
+  char* w = static_cast<char*>(a->workspace);
+  vs::Workspace ws;
+  ws.n_exc = reinterpret_cast<uint32_t*>(w + L.n_exc);
+  ws.exc_id = reinterpret_cast<int32_t*>(w + L.exc_id);
+  ws.exc_val = reinterpret_cast<float*>(w + L.exc_val);
+  ws.exc_cnt = reinterpret_cast<int32_t*>(w + L.exc_cnt);
+  ws.bitmap = reinterpret_cast<uint32_t*>(w + L.bitmap);
+  ws.nwords = L.nwords;
+  return ws;
+}
+
+vs::PenaltyArgs penalty_args(const vsamp_args* a, const vs::Workspace& ws) {
+  vs::PenaltyArgs p;
+  p.logits = a->logits;
+  p.stride = a->row_stride;
+  p.V = a->vocab;
+  p.rep = a->repetition_penalty;
+  p.pres = a->presence_penalty;
+  p.freq = a->frequency_penalty;
+  p.hist = a->hist_ids;
+  p.off = a->hist_offsets;
+  p.ws = ws;
+  p.dense_counts = nullptr;
+  p.counts_stride = 0;
+  return p;
+}
+
+template <class Tin>
+int launch_penalties(const vs::PenaltyArgs& p, int B, hipStream_t st) {
+  hipLaunchKernelGGL(vs::k_penalty_prep<Tin>, dim3(B), dim3(vs::kThreads), 0, st, p);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_penalty_prep");
+}
+
+template <class Tin>
+int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStream_t st) {
+  const bool pen = wants_penalties(a);
+  vs::SampleArgs s;
+  std::memset(&s, 0, sizeof s);
+  if (pen) {
+    const Layout L = layout(a->batch, a->vocab, a->hist_total);
+    if (int rc = check_workspace(a, L)) return rc;
+    s.ws = workspace_of(a, L);
+    s.pen = penalty_args(a, s.ws);
+    s.has_exc = 1;
+    s.off = a->hist_offsets;
+  }
+  s.logits = a->logits;
+  s.stride = a->row_stride;
+  s.V = a->vocab;
+  s.temp = a->temperature;
+  s.topk = a->top_k;
+  s.topp = a->top_p;
+  s.minp = a->min_p;
+  s.u = a->uniforms;
+  s.draft = a->draft_ids;
+  s.out_ids = a->out_ids;
+  s.out_dprob = a->out_draft_prob;
+  s.out_probs = probs;
+  s.probs_stride = probs_stride;
+  // One launch per step: the penalty phase runs at the start of the same kernel.
+  if (pen)
+    hipLaunchKernelGGL((vs::k_sample<Tin, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
+  else
+    hipLaunchKernelGGL((vs::k_sample<Tin, false>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_sample");
+}
+
+}  // namespace
+
+extern "C" {
+
+int vsamp_abi_version(void) { return VSAMP_ABI_VERSION; }
+
+int vsamp_query(int device, char* why, size_t n) {
+  if (why && n) why[0] = '\0';
+  return check_device(device, why, n);
+}
+
+size_t vsamp_workspace_bytes(int32_t batch, int32_t vocab, int64_t hist_total) {
+  if (batch < 0 || vocab < 1 || hist_total < 0) return 0;
+  return layout(batch, vocab, hist_total).total;
+}
+
+int vsamp_sample(const vsamp_args* a, void* stream) {
+  g_err.clear();
+  if (int rc = validate(a, true)) return rc;
+  if (a->batch == 0) return VSAMP_OK;
+  if (int rc = check_current_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return a->dtype == VSAMP_BF16 ? run_sample<uint16_t>(a, nullptr, 0, st)
+                                : run_sample<float>(a, nullptr, 0, st);
+}
+
+int vsamp_probs(const vsamp_args* a, float* out, int64_t out_stride, void* stream) {
+  g_err.clear();
+  if (int rc = validate(a, false)) return rc;
+  if (a->batch == 0) return VSAMP_OK;
+  if (!out) return fail(VSAMP_E_ARG, "out is NULL");
+  if (out_stride < a->vocab) return fail(VSAMP_E_ARG, "out_stride must be >= vocab");
+  if (int rc = check_current_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return a->dtype == VSAMP_BF16 ? run_sample<uint16_t>(a, out, out_stride, st)
+                                : run_sample<float>(a, out, out_stride, st);
+}
+
+int vsamp_penalized_logits(const vsamp_args* a, float* out, int32_t* counts, int64_t out_stride,
+                           void* stream) {
+  g_err.clear();
+  if (int rc = validate(a, false)) return rc;
+  if (a->batch == 0) return VSAMP_OK;
+  if (!out) return fail(VSAMP_E_ARG, "out is NULL");
+  if (out_stride < a->vocab) return fail(VSAMP_E_ARG, "out_stride must be >= vocab");
+  if (int rc = check_current_device()) return rc;
+  const Layout L = layout(a->batch, a->vocab, a->hist_total);
+  if (int rc = check_workspace(a, L)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  vs::PenaltyArgs p = penalty_args(a, workspace_of(a, L));
+  if (!wants_penalties(a)) {
+    p.rep = p.pres = p.freq = nullptr;  // every row off: exceptions stay empty
+  }
+  if (!(a->hist_ids && a->hist_offsets)) {
+    p.hist = nullptr;
+    p.off = nullptr;
+  }
+  p.dense_counts = counts;
+  p.counts_stride = out_stride;
+  int rc = a->dtype == VSAMP_BF16 ? launch_penalties<uint16_t>(p, a->batch, st)
+                                  : launch_penalties<float>(p, a->batch, st);
+  if (rc) return rc;
+  if (a->dtype == VSAMP_BF16)
+    hipLaunchKernelGGL(vs::k_penalized_out<uint16_t>, dim3(a->batch), dim3(vs::kThreads), 0, st, p, out,
+                       out_stride);
+  else
+    hipLaunchKernelGGL(vs::k_penalized_out<float>, dim3(a->batch), dim3(vs::kThreads), 0, st, p, out,
+                       out_stride);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_penalized_out");
+}
+
+const char* vsamp_last_error(void) { return g_err.c_str(); }
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+// Shared device helpers for the sampler kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vs {
+
+constexpr int kWave = 64;
+constexpr int kThreads = 1024;  // one workgroup per row
+constexpr int kWaves = kThreads / kWave;
+constexpr int kBlk = 8;  // elements per block: one 16-byte bf16 load, two for fp32
+constexpr int kMaxStripes = 64;  // V <= kMaxStripes * kThreads * kBlk = 524288
+constexpr int kMassShift = 42;   // masses are fixed-point: q = rint(p~ * 2^42), p~ <= 1
+constexpr double kMassScale = 4398046511104.0;  // 2^42
+
+typedef unsigned long long u64;
+
+// ---- ordered keys ---------------------------------------------------------------------------
+// A 32-bit key whose unsigned order is the numeric order of fp32 values, with -0.0 folded onto
+// +0.0 (they compare equal) and every NaN mapped above +inf.
+__device__ __forceinline__ uint32_t key_of(float x) {
+  if (x != x) return 0xFFFFFFFFu;
+  if (x == 0.0f) x = 0.0f;
+  uint32_t b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float val_of(uint32_t k) {
+  uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __uint_as_float(b);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// ---- fixed-point mass of one value ------------------------------------------------------------
+// p~ = exp(z - m) in fp64 with z = fl32(x / T) (IEEE division), m the row's max z.
+__device__ __forceinline__ double ptilde(float x, float T, float mz) {
+  float z = x / T;
+  return exp(static_cast<double>(z) - static_cast<double>(mz));
+}
+
+__device__ __forceinline__ u64 mass_q(double p) {
+  return static_cast<u64>(__builtin_rint(p * kMassScale));
+}
+
+// ---- wave primitives --------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+template <class T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ u64 wave_max_u64(u64 v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    u64 w = __shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// Inclusive prefix sum over the wave's lanes.
+template <class T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    T w = __shfl_up(v, o);
+    if (l >= o) v += w;
+  }
+  return v;
+}
+
+// ---- workgroup primitives (kThreads threads, all must call) ------------------------------------
+// `red` must hold kWaves entries of T.
+template <class T>
+__device__ __forceinline__ T block_sum(T v, T* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane_id() == 0) red[w] = v;
+  __syncthreads();
+  T s = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) s += red[i];
+  return s;
+}
+
+__device__ __forceinline__ u64 block_max_u64(u64 v, u64* red) {
+  v = wave_max_u64(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane_id() == 0) red[w] = v;
+  __syncthreads();
+  u64 s = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) s = red[i] > s ? red[i] : s;
+  return s;
+}
+
+// Exclusive prefix sum over the workgroup in thread order; returns the total in *total.
+template <class T>
+__device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
+  T inc = wave_incl_scan(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane_id() == kWave - 1) red[w] = inc;
+  __syncthreads();
+  T base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    base += (i < w) ? red[i] : T(0);
+    tot += red[i];
+  }
+  *total = tot;
+  return base + inc - v;
+}
+
+}  // namespace vs

@@ -1,0 +1,70 @@
+"""The sampler op family: its interface and its registry.
+
+``sample`` keeps the engine's per-token call unchanged (src/vinfer/runtime/sampler.py:68,
+called from runtime/generate.py:129): one 1-D ``[V]`` logits row in the model dtype, the
+request's ``SamplingParams``, its seed and the token position, returning a Python ``int``.
+Batched entry points are new methods of the interface, as the engine's convention for kernel
+families prescribes (kernels/gdn/base.py:7-8). Logits are caller-owned and never written.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from typing import Protocol
+
+import torch
+
+from vinfer_amd.registry import BackendRegistry
+from vinfer_amd.sampling import PackedParams, SamplingParams
+
+
+class SamplerBackend(Protocol):
+    def sample(
+        self,
+        logits: torch.Tensor,
+        params: SamplingParams,
+        seed: int,
+        position: int,
+        history: Sequence[int] | torch.Tensor | None = None,
+    ) -> int:
+        """One token id from ``logits`` (``[V]``) for the token at ``position``. ``history`` is
+        the request's token ids so far; it matters only when a penalty is on."""
+        ...
+
+    def sample_batch(
+        self,
+        logits: torch.Tensor,
+        params: PackedParams,
+        uniforms: torch.Tensor,
+        hist_ids: torch.Tensor | None = None,
+        hist_offsets: torch.Tensor | None = None,
+        draft_ids: torch.Tensor | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """One token per row of ``logits`` ``[B, V]``: ids int32 ``[B]`` and, when ``draft_ids``
+        (int32 ``[B]``) is given, the final probability of each draft id (fp32 ``[B]``).
+        ``uniforms`` fp32 ``[B]`` in [0, 1); histories in CSR form (int32)."""
+        ...
+
+    def probs(
+        self,
+        logits: torch.Tensor,
+        params: PackedParams,
+        hist_ids: torch.Tensor | None = None,
+        hist_offsets: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """The fp32 ``[B, V]`` distribution ``sample_batch`` draws from (``filtered_probs``,
+        sampler.py:50-65, plus penalties and min-p)."""
+        ...
+
+    def penalized_logits(
+        self,
+        logits: torch.Tensor,
+        params: PackedParams,
+        hist_ids: torch.Tensor | None = None,
+        hist_offsets: torch.Tensor | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Penalised fp32 logits ``[B, V]`` and the history count of every id (int32 ``[B, V]``)."""
+        ...
+
+
+SAMPLER: BackendRegistry[SamplerBackend] = BackendRegistry("sampler")

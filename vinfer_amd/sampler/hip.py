@@ -1,0 +1,219 @@
+"""The ``hip`` sampler backend: hand-written gfx950 kernels behind the C ABI of libvsampler.so.
+
+Registered for device type ``"cuda"`` (ROCm PyTorch reports HIP devices as ``cuda``) and the
+logits dtypes bf16 and fp32. ``supports`` checks, at engine build time, that this is a ROCm
+build of PyTorch, that the library loads and that the device is a gfx950 GPU
+(kernels/registry.py:38-43: an unsupported context is an error, never a fallback).
+
+Every call enqueues work on the current torch stream of the logits' device and returns without
+synchronising, except ``sample`` which returns a Python ``int`` as the engine's does
+(sampler.py:71, :77).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Sequence
+
+import torch
+
+from vinfer_amd import _lib
+from vinfer_amd.registry import BackendContext
+from vinfer_amd.sampler.base import SAMPLER
+from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params, uniform
+
+_DTYPES = {torch.bfloat16: _lib.VSAMP_BF16, torch.float32: _lib.VSAMP_F32}
+
+
+def _supports(ctx: BackendContext) -> str | None:
+    if torch.version.hip is None:
+        return "needs a ROCm build of PyTorch"
+    if not torch.cuda.is_available():
+        return "no HIP device is visible"
+    try:
+        _lib.load()
+    except Exception as e:  # the reason is reported, never swallowed into a fallback
+        return f"libvsampler.so does not load: {e}"
+    index = ctx.device.index if ctx.device.index is not None else torch.cuda.current_device()
+    return _lib.query(index)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+@SAMPLER.register("hip", devices={"cuda"}, dtypes={torch.bfloat16, torch.float32}, supports=_supports)
+class HipSampler:
+    def __init__(self, ctx: BackendContext) -> None:
+        self.ctx = ctx
+        self._lib = _lib.load()
+        self._workspace = torch.empty(0, dtype=torch.uint8)
+
+    # ---- argument checks ---------------------------------------------------------------------
+    def _device(self, logits: torch.Tensor) -> torch.device:
+        if logits.device.type != "cuda":
+            raise ValueError(f"hip sampler needs logits on a GPU, got {logits.device}")
+        if logits.dtype not in _DTYPES:
+            raise ValueError(f"hip sampler supports bf16 and fp32 logits, got {logits.dtype}")
+        if logits.dim() != 2 or logits.stride(1) != 1:
+            raise ValueError("logits must be [B, V] with unit stride along V")
+        return logits.device
+
+    @staticmethod
+    def _vec(t: torch.Tensor | None, n: int, dtype: torch.dtype, dev: torch.device, name: str):
+        if t is None:
+            return None
+        if t.dtype != dtype or t.device != dev or t.dim() != 1 or t.shape[0] != n:
+            raise ValueError(f"{name} must be a {dtype} [{n}] tensor on {dev}")
+        return t.contiguous()
+
+    def _args(self, logits, params, hist_ids, hist_offsets, uniforms=None, draft_ids=None):
+        dev = self._device(logits)
+        B, V = logits.shape
+        if params.batch != B:
+            raise ValueError(f"params describe {params.batch} rows, logits have {B}")
+        cols = {}
+        for name in (
+            "temperature",
+            "top_p",
+            "min_p",
+            "repetition_penalty",
+            "presence_penalty",
+            "frequency_penalty",
+        ):
+            cols[name] = self._vec(getattr(params, name), B, torch.float32, dev, name)
+        cols["top_k"] = self._vec(params.top_k, B, torch.int32, dev, "top_k")
+        if (hist_ids is None) != (hist_offsets is None):
+            raise ValueError("hist_ids and hist_offsets go together")
+        hist_total = 0
+        if hist_ids is not None:
+            hist_offsets = self._vec(hist_offsets, B + 1, torch.int32, dev, "hist_offsets")
+            if hist_ids.dtype != torch.int32 or hist_ids.device != dev or hist_ids.dim() != 1:
+                raise ValueError(f"hist_ids must be an int32 1-D tensor on {dev}")
+            hist_ids = hist_ids.contiguous()
+            hist_total = int(hist_ids.shape[0])
+        a = _lib.VsampArgs()
+        a.logits = logits.data_ptr()
+        a.dtype = _DTYPES[logits.dtype]
+        a.batch = B
+        a.vocab = V
+        a.row_stride = logits.stride(0) if B > 1 else V
+        for name, t in cols.items():
+            setattr(a, name, _ptr(t))
+        a.hist_ids = _ptr(hist_ids) if hist_total else None
+        a.hist_offsets = _ptr(hist_offsets) if hist_total else None
+        a.hist_total = hist_total
+        if uniforms is not None:
+            uniforms = self._vec(uniforms, B, torch.float32, dev, "uniforms")
+            a.uniforms = _ptr(uniforms)
+        if draft_ids is not None:
+            draft_ids = self._vec(draft_ids, B, torch.int32, dev, "draft_ids")
+            a.draft_ids = _ptr(draft_ids)
+        need = int(self._lib.vsamp_workspace_bytes(B, V, hist_total)) if hist_total else 0
+        if need:
+            if self._workspace.device != dev or self._workspace.numel() < need + 256:
+                self._workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+            base = self._workspace.data_ptr()
+            a.workspace = (base + 255) & ~255
+            a.workspace_bytes = need
+        keep = (logits, cols, hist_ids, hist_offsets, uniforms, draft_ids)
+        return a, keep
+
+    @staticmethod
+    def _stream(dev: torch.device) -> ctypes.c_void_p:
+        return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    # ---- the interface ----------------------------------------------------------------------
+    def prepare_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
+        """A reusable launch of ``sample_batch`` on fixed buffers: every check and the argument
+        block are done once; ``PreparedStep.launch()`` then only enqueues the kernel. Outputs
+        land in ``PreparedStep.ids`` / ``.draft_prob``; inputs may be refilled in place."""
+        a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids)
+        if a.workspace_bytes:  # a private workspace: steps prepared together may overlap
+            ws = torch.empty(a.workspace_bytes + 256, dtype=torch.uint8, device=logits.device)
+            a.workspace = (ws.data_ptr() + 255) & ~255
+            keep = keep + (ws,)
+        B = logits.shape[0]
+        ids = torch.empty(B, dtype=torch.int32, device=logits.device)
+        dprob = torch.empty(B, dtype=torch.float32, device=logits.device) if draft_ids is not None else None
+        a.out_ids = ids.data_ptr()
+        a.out_draft_prob = _ptr(dprob)
+        return PreparedStep(self._lib, a, keep, ids, dprob)
+
+    def sample_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
+        a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids)
+        dev = logits.device
+        B = logits.shape[0]
+        ids = torch.empty(B, dtype=torch.int32, device=dev)
+        dprob = torch.empty(B, dtype=torch.float32, device=dev) if draft_ids is not None else None
+        a.out_ids = ids.data_ptr()
+        a.out_draft_prob = _ptr(dprob)
+        _lib.check(self._lib.vsamp_sample(ctypes.byref(a), self._stream(dev)))
+        del keep
+        return ids, dprob
+
+    def probs(self, logits, params, hist_ids=None, hist_offsets=None):
+        a, keep = self._args(logits, params, hist_ids, hist_offsets)
+        B, V = logits.shape
+        out = torch.empty(B, V, dtype=torch.float32, device=logits.device)
+        _lib.check(self._lib.vsamp_probs(ctypes.byref(a), out.data_ptr(), V, self._stream(logits.device)))
+        del keep
+        return out
+
+    def penalized_logits(self, logits, params, hist_ids=None, hist_offsets=None):
+        a, keep = self._args(logits, params, hist_ids, hist_offsets)
+        B, V = logits.shape
+        dev = logits.device
+        need = int(self._lib.vsamp_workspace_bytes(B, V, a.hist_total))
+        if a.workspace_bytes < need:
+            if self._workspace.device != dev or self._workspace.numel() < need + 256:
+                self._workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+            a.workspace = (self._workspace.data_ptr() + 255) & ~255
+            a.workspace_bytes = need
+        out = torch.empty(B, V, dtype=torch.float32, device=dev)
+        counts = torch.empty(B, V, dtype=torch.int32, device=dev)
+        _lib.check(
+            self._lib.vsamp_penalized_logits(
+                ctypes.byref(a), out.data_ptr(), counts.data_ptr(), V, self._stream(dev)
+            )
+        )
+        del keep
+        return out, counts
+
+    def sample(
+        self,
+        logits: torch.Tensor,
+        params: SamplingParams,
+        seed: int,
+        position: int,
+        history: Sequence[int] | torch.Tensor | None = None,
+    ) -> int:
+        dev = logits.device
+        packed = pack_params([params], dev)
+        u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)
+        hist_ids = hist_offsets = None
+        if history is not None and params.penalized and len(history) > 0:
+            hist_ids = torch.as_tensor(history, dtype=torch.int32).to(dev)
+            hist_offsets = torch.tensor([0, hist_ids.shape[0]], dtype=torch.int32, device=dev)
+        ids, _ = self.sample_batch(logits.reshape(1, -1), packed, u, hist_ids, hist_offsets)
+        return int(ids[0])
+
+
+class PreparedStep:
+    """One batch's sampler launch with its argument block built (see ``prepare_batch``)."""
+
+    def __init__(self, lib, args, keep, ids, dprob) -> None:
+        self._lib, self._args, self._keep = lib, args, keep
+        self._ref = ctypes.byref(args)
+        self.ids, self.draft_prob = ids, dprob
+
+    def launch(self, stream: int | None = None) -> None:
+        """Enqueue the step on ``stream`` (a hipStream_t as int; default: torch's current)."""
+        if stream is None:
+            stream = torch.cuda.current_stream(self.ids.device).cuda_stream
+        code = self._lib.vsamp_sample(self._ref, ctypes.c_void_p(stream))
+        if code:
+            _lib.check(code)
+
+
+__all__ = ["HipSampler", "PackedParams", "PreparedStep"]

@@ -1,0 +1,169 @@
+"""The ``reference`` sampler backend: slow, readable torch code on any device.
+
+``sample`` is the engine's own sampler (src/vinfer/runtime/sampler.py:50-77): temperature,
+top-k, top-p and the exponential race ``argmax(p / E)`` with ``E`` drawn from a
+``torch.Generator`` seeded by ``position_seed(seed, position)``. It is what the engine runs
+with ``sampler_backend=reference``, the default. When a penalty or min-p is on it uses the
+batched path below instead, since the engine's sampler has neither.
+
+``sample_batch`` and ``probs`` restate the batched semantics the ``hip`` backend implements,
+row by row in torch: penalties, fp32 division by the temperature, top-k, fp64 softmax, min-p,
+top-p with ties broken by ascending id, and the inverse-CDF draw from the caller's uniform.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import torch
+
+from vinfer_amd.registry import BackendContext
+from vinfer_amd.sampler.base import SAMPLER
+from vinfer_amd.sampling import SamplingParams, pack_params, position_seed, uniform
+
+
+def filtered_probs(logits: torch.Tensor, params: SamplingParams) -> torch.Tensor:
+    """Probabilities after temperature, top-k and top-p, fp32 (sampler.py:50-65)."""
+    logits = logits.float() / params.temperature
+    if params.top_k and params.top_k < logits.shape[-1]:
+        kth = torch.topk(logits, params.top_k, dim=-1).values[..., -1:]
+        logits = logits.masked_fill(logits < kth, float("-inf"))
+    probs = torch.softmax(logits, dim=-1)
+    if params.top_p < 1:
+        sorted_probs, order = torch.sort(probs, dim=-1, descending=True)
+        before = sorted_probs.cumsum(-1) - sorted_probs
+        sorted_probs = sorted_probs.masked_fill(before >= params.top_p, 0.0)
+        probs = torch.zeros_like(probs).scatter(-1, order, sorted_probs)
+        probs = probs / probs.sum(-1, keepdim=True)
+    return probs
+
+
+def _penalize(x: torch.Tensor, hist: torch.Tensor, rep, pres, freq):
+    V = x.shape[0]
+    hist = hist.long()
+    hist = hist[(hist >= 0) & (hist < V)]
+    counts = torch.bincount(hist, minlength=V)
+    sel = counts > 0
+    xs = x[sel]
+    xs = torch.where(xs > 0, xs / rep, xs * rep)
+    xs = xs - freq * counts[sel].float()
+    xs = xs - pres
+    x = x.clone()
+    x[sel] = xs
+    return x, counts.int()
+
+
+def _row(x: torch.Tensor, T, k: int, tp, mp):
+    """Final fp64 probabilities of one penalised fp32 row (``T`` etc. are 0-dim fp32)."""
+    V = x.shape[0]
+    if not bool(T > 0):
+        out = torch.zeros(V, dtype=torch.float64, device=x.device)
+        out[int(torch.argmax(x))] = 1.0
+        return out
+    z = x / T
+    nan = torch.isnan(z)
+    m = z.max() if not bool(nan.any()) else None
+    point = None
+    if m is None:
+        point = int(torch.argmax(nan.int()))
+    elif bool(m == float("inf")):
+        point = int(torch.argmax((z == float("inf")).int()))
+    elif bool(m == float("-inf")):
+        point = 0
+    if point is not None:
+        out = torch.zeros(V, dtype=torch.float64, device=x.device)
+        out[point] = 1.0
+        return out
+    keep = torch.ones(V, dtype=torch.bool, device=x.device)
+    if 0 < k < V:
+        kth = torch.topk(z, k).values[-1]
+        keep &= z >= kth
+    pt = torch.where(keep, torch.exp(z.double() - m.double()), torch.zeros((), dtype=torch.float64))
+    if float(mp) > 0:
+        keep &= pt >= float(mp)
+    pt = torch.where(keep, pt, torch.zeros_like(pt))
+    if float(tp) < 1:
+        ids = torch.arange(V, device=x.device)
+        # descending p~, ascending id: sort by id first, then a stable sort by -p~
+        order = torch.sort(-pt[ids], stable=True).indices
+        sp = pt[order]
+        before = torch.cumsum(sp, 0) - sp
+        drop = order[(before >= float(tp) * pt.sum()) & (sp > 0)]
+        pt[drop] = 0.0
+    return pt / pt.sum()
+
+
+@SAMPLER.register("reference")
+class ReferenceSampler:
+    def __init__(self, ctx: BackendContext) -> None:
+        self.ctx = ctx
+
+    def _rows(self, logits, params, hist_ids, hist_offsets):
+        B, V = logits.shape
+        for b in range(B):
+            x = logits[b].float()
+            if hist_ids is not None:
+                h = hist_ids[int(hist_offsets[b]) : int(hist_offsets[b + 1])]
+            else:
+                h = torch.zeros(0, dtype=torch.int32, device=logits.device)
+            row = {k: getattr(params, k)[b] for k in params.__dataclass_fields__}
+            x, counts = _penalize(
+                x, h, row["repetition_penalty"], row["presence_penalty"], row["frequency_penalty"]
+            )
+            yield x, counts, row
+
+    def penalized_logits(self, logits, params, hist_ids=None, hist_offsets=None):
+        xs, cs = zip(*[(x, c) for x, c, _ in self._rows(logits, params, hist_ids, hist_offsets)])
+        return torch.stack(xs), torch.stack(cs)
+
+    def probs(self, logits, params, hist_ids=None, hist_offsets=None):
+        out = [
+            _row(x, r["temperature"], int(r["top_k"]), r["top_p"], r["min_p"])
+            for x, _, r in self._rows(logits, params, hist_ids, hist_offsets)
+        ]
+        return torch.stack(out).float()
+
+    def sample_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
+        ids, dps = [], []
+        for b, (x, _, r) in enumerate(self._rows(logits, params, hist_ids, hist_offsets)):
+            p = _row(x, r["temperature"], int(r["top_k"]), r["top_p"], r["min_p"])
+            kept = torch.nonzero(p > 0).flatten()
+            c = torch.cumsum(p[kept], 0)
+            j = int(torch.searchsorted(c, uniforms[b].double() * c[-1], right=True))
+            ids.append(int(kept[min(j, kept.numel() - 1)]))
+            if draft_ids is not None:
+                d = int(draft_ids[b])
+                dps.append(float(p[d]) if 0 <= d < p.numel() else 0.0)
+        dev = logits.device
+        out = torch.tensor(ids, dtype=torch.int32, device=dev)
+        dp = torch.tensor(dps, dtype=torch.float32, device=dev) if draft_ids is not None else None
+        return out, dp
+
+    def sample(
+        self,
+        logits: torch.Tensor,
+        params: SamplingParams,
+        seed: int,
+        position: int,
+        history: Sequence[int] | torch.Tensor | None = None,
+    ) -> int:
+        if params.penalized or params.min_p > 0:
+            dev = logits.device
+            hist = None
+            if history is not None and len(history) > 0:
+                hist = torch.as_tensor(history, dtype=torch.int32, device=dev)
+            off = None if hist is None else torch.tensor([0, hist.numel()], dtype=torch.int32, device=dev)
+            u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)
+            ids, _ = self.sample_batch(logits.reshape(1, -1), pack_params([params], dev), u, hist, off)
+            return int(ids[0])
+        # sampler.py:68-77
+        if params.greedy:
+            return int(torch.argmax(logits))
+        probs = filtered_probs(logits, params)
+        gen = torch.Generator(device=probs.device).manual_seed(position_seed(seed, position))
+        noise = torch.empty_like(probs).exponential_(generator=gen)
+        noise.clamp_min_(torch.finfo(noise.dtype).tiny)
+        return int(torch.argmax(probs / noise))
+
+
+__all__ = ["ReferenceSampler", "filtered_probs"]
