@@ -22,9 +22,10 @@ What it restates, row by row, in numpy (fp32 where the engine computes in fp32, 
 8. Top-p if ``< 1``: in descending ``p~`` order, ties by ascending id (the engine's sort is
    unstable there, sampler.py:60), drop a token when the mass strictly before it is
    ``>= top_p * S`` with ``S`` the kept mass (sampler.py:57-62, renormalised after min-p).
-9. Draw (replaces the exponential race of sampler.py:73-77): over kept tokens in ascending id
-   order, the first ``j`` with inclusive prefix ``C_j > u * S``; the last kept token if rounding
-   leaves none. Draft probability ``p~_d / S`` (0 if ``d`` was dropped).
+9. Draw (replaces the exponential race of sampler.py:73-77): over kept tokens in the order
+   top-p sorts them (descending ``p~``, ties by ascending id), the first ``j`` with inclusive
+   prefix ``C_j > u * S``; the last kept token with positive mass if rounding leaves none.
+   Draft probability ``p~_d / S`` (0 if ``d`` was dropped).
 
 ``classify_ties`` flags rows whose result two correct implementations may legitimately disagree
 on; the device kernels' masses are fixed-point with quantum ``2**-42`` (``p~ <= 1``), so a
@@ -132,14 +133,15 @@ def sample_row(
         pt[dropped] = 0.0
         info.update(P=P, before=before, order=order, n_top_p=nk, xs=x[order], sp=sp)
     kept = np.flatnonzero(keep)
+    korder = kept[np.argsort(-pt[kept], kind="stable")]  # p~ desc, id asc
     S = math.fsum(pt[kept])
-    C = np.cumsum(pt[kept])
+    C = np.cumsum(pt[korder])
     target = float(F32(u)) * S
     j = int(np.searchsorted(C, target, side="right"))  # first C_j > target
-    if j >= kept.size:  # rounding left none: the last kept token with positive mass
-        j = int(np.flatnonzero(pt[kept] > 0)[-1])
-    tok = int(kept[j])
-    info.update(S=S, C=C, target=target, j=j, n_kept=int(kept.size))
+    if j >= korder.size:  # rounding left none: the last kept token with positive mass
+        j = int(np.flatnonzero(pt[korder] > 0)[-1])
+    tok = int(korder[j])
+    info.update(S=S, C=C, target=target, j=j, n_kept=int(kept.size), korder=korder, x=x, pt=pt)
     dp = float(pt[draft] / S) if draft is not None and 0 <= draft < V else 0.0
     res = RowResult(tok, dp, "sampled", info=info)
     if want_probs:
@@ -190,6 +192,11 @@ def classify_ties(res: RowResult) -> list[str]:
     eps = (info["n_kept"] + 4) * MASS_QUANTUM + 1e-15 * info["S"]
     if abs(C[j] - target) <= eps or (j > 0 and abs(C[j - 1] - target) <= eps):
         reasons.append("draw")
+    # The drawn token's position inside its p~ group depends on the grouping (see above).
+    korder, pt, x = info["korder"], info["pt"], info["x"]
+    grp = korder[pt[korder] == pt[korder[j]]]
+    if grp.size > 1 and np.unique(x[grp]).size > 1:
+        reasons.append("merged_draw")
     return reasons
 
 

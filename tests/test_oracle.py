@@ -132,7 +132,7 @@ def test_penalty_steps_round_separately_in_fp32():
     assert out[0] == np.float32(x[0] - prod)
 
 
-# ---- the draw: inverse CDF in ascending id order ------------------------------------------------
+# ---- the draw: inverse CDF in descending-probability order ------------------------------------------------
 def test_uniform_sweep_reproduces_the_final_distribution_exactly():
     x = np.array([0.5, 2.0, -1.0, 1.5, 0.0, 1.9], np.float32)
     res = sample_row(x, 1.0, 4, 0.9, 0.0, 0.0, want_probs=True)
@@ -140,10 +140,14 @@ def test_uniform_sweep_reproduces_the_final_distribution_exactly():
     us = (np.arange(n) + 0.5) / n
     freq = np.bincount([sample_row(x, 1.0, 4, 0.9, 0.0, u).token for u in us[::16]], minlength=6)
     np.testing.assert_allclose(freq / freq.sum(), res.probs, atol=2 * 16 / n)
-    # ascending id order: the smallest u lands on the smallest kept id
+    # descending-probability order: the smallest u lands on the most likely token, the largest
+    # on the least likely kept one
     kept = np.flatnonzero(res.probs > 0)
-    assert sample_row(x, 1.0, 4, 0.9, 0.0, 0.0).token == kept[0]
-    assert sample_row(x, 1.0, 4, 0.9, 0.0, 1 - 2.0**-24).token == kept[-1]
+    assert sample_row(x, 1.0, 4, 0.9, 0.0, 0.0).token == int(np.argmax(x))
+    assert sample_row(x, 1.0, 4, 0.9, 0.0, 1 - 2.0**-24).token == kept[np.argmin(x[kept])]
+    # equal probabilities: ascending id
+    z = np.zeros(4, np.float32)
+    assert [sample_row(z, 1.0, 0, 1.0, 0.0, u).token for u in (0.1, 0.3, 0.6, 0.9)] == [0, 1, 2, 3]
 
 
 @pytest.mark.parametrize(

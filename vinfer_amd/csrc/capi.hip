@@ -74,13 +74,12 @@ int check_current_device() {
 size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 struct Layout {
-  size_t n_exc, exc_id, exc_val, exc_cnt, bitmap, total;
-  int nwords;
+  size_t n_exc, exc_id, exc_val, exc_cnt, total;
 };
 
 Layout layout(int64_t B, int64_t V, int64_t H) {
   Layout L;
-  L.nwords = static_cast<int>((V + 31) / 32);
+  (void)V;
   size_t o = 0;
   L.n_exc = o;
   o = align_up(o + 4 * static_cast<size_t>(B));
@@ -90,8 +89,6 @@ Layout layout(int64_t B, int64_t V, int64_t H) {
   o = align_up(o + 4 * static_cast<size_t>(H));
   L.exc_cnt = o;
   o = align_up(o + 4 * static_cast<size_t>(H));
-  L.bitmap = o;
-  o = align_up(o + 4 * static_cast<size_t>(B) * static_cast<size_t>(L.nwords));
   L.total = o;
   return L;
 }
@@ -145,8 +142,6 @@ vs::Workspace workspace_of(const vsamp_args* a, const Layout& L) {
   ws.exc_id = reinterpret_cast<int32_t*>(w + L.exc_id);
   ws.exc_val = reinterpret_cast<float*>(w + L.exc_val);
   ws.exc_cnt = reinterpret_cast<int32_t*>(w + L.exc_cnt);
-  ws.bitmap = reinterpret_cast<uint32_t*>(w + L.bitmap);
-  ws.nwords = L.nwords;
   return ws;
 }
 

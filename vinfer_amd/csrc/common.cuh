@@ -15,6 +15,8 @@ constexpr int kMassShift = 42;   // masses are fixed-point: q = rint(p~ * 2^42),
 constexpr double kMassScale = 4398046511104.0;  // 2^42
 
 typedef unsigned long long u64;
+typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ ushort2_t ones2() { return ushort2_t{1, 1}; }
 
 // ---- ordered keys ---------------------------------------------------------------------------
 // A 32-bit key whose unsigned order is the numeric order of fp32 values, with -0.0 folded onto
@@ -44,6 +46,16 @@ __device__ __forceinline__ double ptilde(float x, float T, float mz) {
 
 __device__ __forceinline__ u64 mass_q(double p) {
   return static_cast<u64>(__builtin_rint(p * kMassScale));
+}
+
+// ---- barriers ---------------------------------------------------------------------------------
+// A workgroup barrier that orders LDS only. __syncthreads() also releases global memory, which on
+// gfx950 waits for every outstanding global load and store of the wave (vmcnt counts both); use
+// this one wherever threads exchange data through LDS alone, so prefetches stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // ---- wave primitives --------------------------------------------------------------------------
@@ -83,9 +95,9 @@ template <class T>
 __device__ __forceinline__ T block_sum(T v, T* red) {
   v = wave_sum(v);
   const int w = threadIdx.x / kWave;
-  __syncthreads();
+  lds_barrier();
   if (lane_id() == 0) red[w] = v;
-  __syncthreads();
+  lds_barrier();
   T s = 0;
 #pragma unroll
   for (int i = 0; i < kWaves; ++i) s += red[i];
@@ -95,13 +107,34 @@ __device__ __forceinline__ T block_sum(T v, T* red) {
 __device__ __forceinline__ u64 block_max_u64(u64 v, u64* red) {
   v = wave_max_u64(v);
   const int w = threadIdx.x / kWave;
-  __syncthreads();
+  lds_barrier();
   if (lane_id() == 0) red[w] = v;
-  __syncthreads();
+  lds_barrier();
   u64 s = 0;
 #pragma unroll
   for (int i = 0; i < kWaves; ++i) s = red[i] > s ? red[i] : s;
   return s;
+}
+
+// A workgroup sum and max at once (one pair of barriers). `red` must hold 2 * kWaves entries.
+__device__ __forceinline__ void block_sum_max_u64(u64 sv, u64 mv, u64* red, u64* sum, u64* mx) {
+  sv = wave_sum(sv);
+  mv = wave_max_u64(mv);
+  const int w = threadIdx.x / kWave;
+  lds_barrier();
+  if (lane_id() == 0) {
+    red[w] = sv;
+    red[kWaves + w] = mv;
+  }
+  lds_barrier();
+  u64 s = 0, m = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    s += red[i];
+    m = red[kWaves + i] > m ? red[kWaves + i] : m;
+  }
+  *sum = s;
+  *mx = m;
 }
 
 // Exclusive prefix sum over the workgroup in thread order; returns the total in *total.
@@ -109,9 +142,9 @@ template <class T>
 __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
   T inc = wave_incl_scan(v);
   const int w = threadIdx.x / kWave;
-  __syncthreads();
+  lds_barrier();
   if (lane_id() == kWave - 1) red[w] = inc;
-  __syncthreads();
+  lds_barrier();
   T base = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < kWaves; ++i) {

@@ -4,12 +4,10 @@
 // arithmetic follows vLLM's order, one fp32 rounding per step and no fused multiply-add:
 //   x = x > 0 ? x / rep : x * rep;   x = x - freq * c;   x = x - pres       (for every c > 0)
 //
-// Layout produced in the workspace for row r (ids with c > 0 are the row's "exceptions"):
+// Workspace output for row r (ids with c > 0 are the row's "exceptions"), in no particular order:
 //   n_exc[r]                         number of distinct history ids in [0, V)
-//   exc_id/exc_val/exc_cnt[h0 + e]   e-th exception in ascending id order (h0 = hist_offsets[r];
-//                                    a row has at most L_r exceptions, so the slots never overlap)
-//   bitmap[r * nwords + w]           bit i of word w set iff id 32w + i is an exception; byte b
-//                                    (little-endian) is the lane mask of the 8-id block b
+//   exc_id/exc_val/exc_cnt[h0 + e]   e-th exception (h0 = hist_offsets[r]; a row has at most L_r
+//                                    of them, so the slots never overlap)
 #pragma once
 
 #include "common.cuh"
@@ -23,8 +21,6 @@ struct Workspace {
   int32_t* exc_id;   // [H]
   float* exc_val;    // [H]
   int32_t* exc_cnt;  // [H]
-  uint32_t* bitmap;  // [B][nwords]
-  int nwords;        // ceil(V / 32)
 };
 
 struct PenaltyArgs {
@@ -61,90 +57,221 @@ __device__ __forceinline__ float load_one<float>(const float* p, int64_t i) {
   return p[i];
 }
 
-__device__ __forceinline__ bool row_penalized(const PenaltyArgs& a, int r) {
-  const float rep = a.rep ? a.rep[r] : 1.0f;
-  const float pres = a.pres ? a.pres[r] : 0.0f;
-  const float freq = a.freq ? a.freq[r] : 0.0f;
-  return rep != 1.0f || pres != 0.0f || freq != 0.0f;
+// Where the penalty pass leaves the row's penalised ids and values in LDS, for a caller that
+// keeps them there (cap = 0: none). Rows with more than cap penalised ids are
+// still complete in the workspace.
+struct ExcCache {
+  int32_t* id;
+  float* val;
+  int cap;
+};
+
+// Counting: a row whose history has at most kHashMaxL ids counts them in an LDS hash table
+// (16384 slots of (id, count), at most 75 % full); longer histories count in windows of ids.
+constexpr int kHashSlots = 16384;
+constexpr int kHashMaxL = 12288;
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+// windowed counting: LDS words [0, 16384) counters (32768 ids as u16 pairs, or 16384 as u32),
+// [16384, 17408) presence bits, then cached history ids and staged (id, count) pairs
+constexpr int kCountWords = 16384;
+constexpr int kHistCache = kChunk - kCountWords - 1024;
+
+// The penalised values of exceptions [0, n) whose (id, count) pairs are in the workspace, or for
+// e < staged in LDS: all loads of a thread are issued before any value is computed.
+template <class Tin>
+__device__ void gather_values(const PenaltyArgs& a, const Tin* row, int h0, uint32_t n, const int2* stage,
+                              uint32_t staged, float rep, float pres, float freq, const ExcCache& ec) {
+  constexpr int kU = 4;
+  for (uint32_t e0 = threadIdx.x; e0 < n; e0 += kU * kThreads) {
+    int id[kU], c[kU];
+    float x[kU];
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+      const uint32_t e = e0 + k * kThreads;
+      id[k] = 0;
+      c[k] = 0;
+      if (e < n) {
+        if (e < staged) {
+          id[k] = stage[e].x;
+          c[k] = stage[e].y;
+        } else {
+          id[k] = a.ws.exc_id[h0 + e];
+          c[k] = a.ws.exc_cnt[h0 + e];
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kU; ++k) x[k] = e0 + k * kThreads < n ? load_one<Tin>(row, id[k]) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+      const uint32_t e = e0 + k * kThreads;
+      if (e >= n) continue;
+      const float xv = apply_penalty(x[k], c[k], rep, pres, freq);
+      a.ws.exc_val[h0 + e] = xv;
+      if (static_cast<int>(e) < ec.cap) {
+        ec.id[e] = id[k];
+        ec.val[e] = xv;
+      }
+    }
+  }
 }
 
-// Row r's penalty pass, run by a whole workgroup; `cnt` is kChunk words of LDS and `red`
-// kWaves words. Ends with the row's exceptions and bitmap written and visible to the workgroup.
+// Row r's penalty pass, run by a whole workgroup; `lds` is kChunk words and `red` kWaves words.
+// Writes the row's exceptions to the workspace (global memory: a reader in the same workgroup
+// needs a __syncthreads() first) and, up to ec.cap of them, to `ec` in LDS (visible on return).
+// With dense_counts set, also writes every id's count. Returns the number of exceptions.
 template <class Tin>
-__device__ void penalty_phase(const PenaltyArgs& a, int r, uint32_t* cnt, uint32_t* red) {
+__device__ uint32_t penalty_phase(const PenaltyArgs& a, int r, uint32_t* lds, uint32_t* red, ExcCache ec) {
   const int tid = threadIdx.x;
   const int V = a.V;
   const int h0 = a.off ? a.off[r] : 0;
   const int h1 = a.off ? a.off[r + 1] : 0;
-  const bool on = row_penalized(a, r) && a.hist != nullptr && h1 > h0;
-  if (!on && a.dense_counts == nullptr) {
-    if (tid == 0) a.ws.n_exc[r] = 0;
-    __threadfence();
-    __syncthreads();
-    return;
-  }
   const float rep = a.rep ? a.rep[r] : 1.0f;
   const float pres = a.pres ? a.pres[r] : 0.0f;
   const float freq = a.freq ? a.freq[r] : 0.0f;
+  const bool on = (rep != 1.0f || pres != 0.0f || freq != 0.0f) && a.hist != nullptr && h1 > h0;
+  const bool dense = a.dense_counts != nullptr;
+  if (!on && !dense) {
+    if (tid == 0) a.ws.n_exc[r] = 0;
+    return 0;
+  }
   const Tin* row = static_cast<const Tin*>(a.logits) + static_cast<int64_t>(r) * a.stride;
   const int32_t* hist = a.hist ? a.hist + h0 : nullptr;
-  const int L = h1 - h0;
-
+  const int L = hist ? h1 - h0 : 0;
+  int32_t* dc = dense ? a.dense_counts + static_cast<int64_t>(r) * a.counts_stride : nullptr;
+  if (dense) {
+    for (int i = tid; i < V; i += kThreads) dc[i] = 0;
+    __syncthreads();  // the zeros land before the counts below overwrite some of them
+  }
   uint32_t n_total = 0;
-  for (int base = 0; base < V; base += kChunk) {
-    for (int i = tid; i < kChunk; i += kThreads) cnt[i] = 0;
-    __syncthreads();
+  if (L <= kHashMaxL) {
+    // ---- one pass: an (id -> count) hash table in LDS ----
+    uint32_t* keys = lds;
+    uint32_t* cnts = lds + kHashSlots;
+    for (int i = tid; i < kHashSlots; i += kThreads) {
+      keys[i] = kEmpty;
+      cnts[i] = 0;
+    }
+    lds_barrier();
     for (int i = tid; i < L; i += kThreads) {
       const int id = hist[i];
-      const unsigned rel = static_cast<unsigned>(id - base);
-      if (id >= 0 && id < V && rel < static_cast<unsigned>(kChunk)) atomicAdd(&cnt[rel], 1u);
+      if (id < 0 || id >= V) continue;
+      uint32_t h = (static_cast<uint32_t>(id) * 2654435761u) >> (32 - 14);  // Fibonacci hashing
+      while (true) {
+        const uint32_t prev = atomicCAS(&keys[h], kEmpty, static_cast<uint32_t>(id));
+        if (prev == kEmpty || prev == static_cast<uint32_t>(id)) {
+          atomicAdd(&cnts[h], 1u);
+          break;
+        }
+        h = (h + 1) & (kHashSlots - 1);
+      }
     }
-    __syncthreads();
-    if (a.dense_counts) {
-      int32_t* dc = a.dense_counts + static_cast<int64_t>(r) * a.counts_stride + base;
-      for (int i = tid; i < kChunk && base + i < V; i += kThreads) dc[i] = static_cast<int32_t>(cnt[i]);
+    lds_barrier();
+    // compaction: thread t owns slots 16t .. 16t + 15
+    constexpr int kPer = kHashSlots / kThreads;
+    uint32_t mine = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) mine += keys[tid * kPer + k] != kEmpty ? 1u : 0u;
+    uint32_t e = block_excl_scan<uint32_t>(mine, red, &n_total);
+    // (id, count) pairs of this thread's slots, in registers while the table is overwritten
+    uint32_t sid[kPer], sc[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      sid[k] = keys[tid * kPer + k];
+      sc[k] = cnts[tid * kPer + k];
     }
-    // Thread t owns ids base + 32t .. base + 32t + 31. Reads start at a lane-dependent offset so
-    // a wave's 64 reads spread over the 32 LDS banks.
-    uint32_t mask = 0;
-    const int p0 = tid * 32;
-#pragma unroll 8
-    for (int s = 0; s < 32; ++s) {
-      const int i = (s + tid) & 31;
-      mask |= (cnt[p0 + i] != 0u ? 1u : 0u) << i;
+    lds_barrier();
+    int2* stage = reinterpret_cast<int2*>(lds);  // the table is dead: stage the pairs over it
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      if (sid[k] == kEmpty) continue;
+      if (dense) dc[sid[k]] = static_cast<int>(sc[k]);
+      if (on) {
+        a.ws.exc_id[h0 + e] = static_cast<int>(sid[k]);
+        a.ws.exc_cnt[h0 + e] = static_cast<int>(sc[k]);
+        stage[e] = make_int2(static_cast<int>(sid[k]), static_cast<int>(sc[k]));
+      }
+      ++e;
     }
-    const int word = (base >> 5) + tid;
-    if (word < a.ws.nwords) a.ws.bitmap[static_cast<int64_t>(r) * a.ws.nwords + word] = on ? mask : 0u;
-    uint32_t chunk_total;
-    const uint32_t my_off = block_excl_scan<uint32_t>(__popc(mask), red, &chunk_total);
-    if (on) {
-      uint32_t e = n_total + my_off;
-      uint32_t m = mask;
+    lds_barrier();
+    if (on) gather_values<Tin>(a, row, h0, n_total, stage, n_total, rep, pres, freq, ec);
+  } else {
+    // ---- long histories: count a window of ids at a time ----
+    uint32_t* cnt = lds;
+    uint32_t* present = lds + kCountWords;
+    int32_t* cache = reinterpret_cast<int32_t*>(lds + kCountWords + 1024);
+    const int Lc = L < kHistCache ? L : kHistCache;
+    const bool wide = L > 0xFFFF;  // u16 counters hold any count of a shorter history
+    const int window = wide ? kCountWords : 2 * kCountWords;
+    const int nwin_words = window / 32;
+    for (int i = tid; i < Lc; i += kThreads) cache[i] = hist[i];
+    for (int i = tid; i < kCountWords; i += kThreads) cnt[i] = 0;
+    for (int i = tid; i < 1024; i += kThreads) present[i] = 0;
+    lds_barrier();
+    for (int base = 0; base < V; base += window) {
+      for (int i = tid; i < L; i += kThreads) {
+        const int id = i < Lc ? cache[i] : hist[i];
+        const unsigned rel = static_cast<unsigned>(id - base);
+        if (id >= 0 && id < V && rel < static_cast<unsigned>(window)) {
+          if (wide) atomicAdd(&cnt[rel], 1u);
+          else atomicAdd(&cnt[rel >> 1], 1u << ((rel & 1u) << 4));
+          atomicOr(&present[rel >> 5], 1u << (rel & 31u));
+        }
+      }
+      lds_barrier();
+      // thread t owns presence word t: ids base + 32t .. base + 32t + 31
+      const uint32_t word = tid < nwin_words ? present[tid] : 0u;
+      auto count_of = [&](int rel) -> uint32_t {
+        return wide ? cnt[rel] : (cnt[rel >> 1] >> ((rel & 1) << 4)) & 0xFFFFu;
+      };
+      uint32_t chunk_total;
+      uint32_t e = n_total + block_excl_scan<uint32_t>(__popc(word), red, &chunk_total);
+      uint32_t m = word;
       while (m) {
         const int i = __ffs(m) - 1;
         m &= m - 1;
-        const int id = base + p0 + i;
-        const int c = static_cast<int>(cnt[p0 + i]);
-        const float x = load_one<Tin>(row, id);
-        a.ws.exc_id[h0 + e] = id;
-        a.ws.exc_val[h0 + e] = apply_penalty(x, c, rep, pres, freq);
-        a.ws.exc_cnt[h0 + e] = c;
+        const int id = base + 32 * tid + i;
+        const int c = static_cast<int>(count_of(32 * tid + i));
+        if (dense) dc[id] = c;
+        if (on) {
+          a.ws.exc_id[h0 + e] = id;
+          a.ws.exc_cnt[h0 + e] = c;
+        }
         ++e;
       }
+      lds_barrier();
+      // reset what this pass set: the counters of present ids and the presence words
+      if (tid < nwin_words && word) {
+        if (wide) {
+          uint32_t mm = word;
+          while (mm) {
+            const int i = __ffs(mm) - 1;
+            mm &= mm - 1;
+            cnt[32 * tid + i] = 0;
+          }
+        } else {
+          for (int pw = 0; pw < 16; ++pw)
+            if ((word >> (2 * pw)) & 3u) cnt[16 * tid + pw] = 0;
+        }
+        present[tid] = 0;
+      }
+      n_total += chunk_total;
+      lds_barrier();
     }
-    n_total += chunk_total;
+    // the (id, count) pairs were written by other threads of this workgroup: full barrier
     __syncthreads();
+    if (on) gather_values<Tin>(a, row, h0, n_total, nullptr, 0, rep, pres, freq, ec);
   }
   if (tid == 0) a.ws.n_exc[r] = on ? n_total : 0u;
-  __threadfence();
-  __syncthreads();
+  lds_barrier();
+  return on ? n_total : 0u;
 }
 
 template <class Tin>
 __global__ __launch_bounds__(kThreads) void k_penalty_prep(PenaltyArgs a) {
   __shared__ uint32_t cnt[kChunk];
   __shared__ uint32_t red[kWaves];
-  penalty_phase<Tin>(a, blockIdx.x, cnt, red);
+  penalty_phase<Tin>(a, blockIdx.x, cnt, red, ExcCache{nullptr, nullptr, 0});
 }
 
 // Penalised fp32 logits of every row: the bulk copy first, then the exceptions over it.

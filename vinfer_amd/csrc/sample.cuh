@@ -1,19 +1,27 @@
 // Per-row sampling kernel: one 1024-thread workgroup per row.
 //
-// Everything is decided in the space of penalised fp32 logits x. Temperature scaling
-// z = fl32(x / T) is monotone non-decreasing in x, so every filter is a threshold on x:
-//   top-k  : kth largest x by radix select over ordered keys, then the smallest x whose z
-//            reaches z(kth) (bisection over keys; handles division merging distinct x)
+// Everything is decided on penalised fp32 logits x. Temperature scaling z = fl32(x / T) is
+// monotone non-decreasing in x, so every filter is a threshold on x:
+//   top-k  : the kth largest x (exact order statistic), then the smallest x whose z reaches
+//            z(kth) (bisection over keys, which also covers division merging distinct x)
 //   min-p  : the smallest x with exp(z - max z) >= min_p (fp64), by bisection over keys
-//   top-p  : the cutoff value by a radix search over keys on fixed-point masses, with the
-//            tokens of the cutoff value kept in ascending id order up to the exact count
-// Masses are q = rint(p~ * 2^42) with p~ = exp(z - max z) in fp64, summed as integers, so every
-// sum is exact and order-independent. The draw is an inverse CDF over kept tokens in ascending
-// id order, found by a three-level search (stripe, thread, element) in the block-cyclic layout:
-// thread t reads blocks b = j * 1024 + t (8 ids each) for stripes j = 0, 1, ...
+//   top-p  : the cutoff value (the lowest value whose mass strictly above it is < P), and how
+//            many of its tokens are kept, in ascending id order
+//   draw   : the value group where the descending cumulative mass crosses u * S, and the
+//            member of that group (ascending id) it lands on
+// Masses are q = rint(p~ * 2^42) with p~ = exp(z - max z) in fp64, summed as integers: exact
+// and order-independent.
 //
-// Penalised tokens ("exceptions") are masked out of the logits reads by the row's bitmap and
-// visited from the exception list instead.
+// bf16 rows (fast path): one pass builds a histogram of the row's 65536 possible 16-bit keys
+// (u16 counts packed in pairs, 128 KB of LDS). Every threshold and the draw's value group are
+// then found from the histogram: per-chunk (64-key) counts and masses, a scan over chunks and a
+// wave-wide walk inside one chunk, with fp64 exps only for populated keys. A second,
+// compare-only pass finds the id of the drawn token. fp32 rows, and bf16 rows whose histogram
+// cannot hold them, take the generic path: radix descents over 32-bit ordered keys.
+//
+// Penalised tokens ("exceptions"): the generic path masks them out of logits reads by the row's
+// bitmap and visits them from the workspace's list; the fast path keeps the list in LDS and
+// takes their original keys back out of the histogram.
 #pragma once
 
 #include "common.cuh"
@@ -41,19 +49,57 @@ struct SampleArgs {
   PenaltyArgs pen;  // the penalty phase's inputs (used when the kernel runs it)
 };
 
-struct Smem {
+// Scratch of the id-order search.
+struct Search {
+  float vslot;
   u64 red64[kWaves];
-  uint32_t red32[kWaves];
   u64 cell[kWaves][kMaxStripes];
   u64 tw[kThreads];
-  uint32_t hcnt[256];
-  u64 hmass[256];
   u64 slot[kBlk];
   uint32_t slot_mask;
-  // broadcast scalars
   int bi[4];
   u64 bq[4];
+};
+
+// Scratch of the generic path's radix descents.
+struct Radix {
+  uint32_t hcnt[256];
+  u64 hmass[256];
   uint32_t bk[4];
+  u64 bq[4];
+};
+
+struct GenericSmem {
+  Search srch;
+  Radix rdx;
+};
+
+// After the histogram (or on the generic path) the 128 KB buffer holds, in words:
+//   [0, kBitmapOffset)                          Search and Radix scratch
+//   [kBitmapOffset, kBitmapOffset + 16384)      per-block lane masks of penalised ids (V / 8 bytes)
+//   [kMatchOffset, kMatchOffset + kMatchWords)  the draw's per-block count cells
+constexpr int kBitmapOffset = 5120;
+constexpr int kMatchOffset = kBitmapOffset + 16384;
+
+constexpr int kMaxL = 128;     // penalised values in one chunk the fast path can resolve
+constexpr int kExcCap = 2048;  // penalised ids per row the fast path keeps in LDS
+constexpr int kMatchWords = 8192;  // LDS words of the draw's per-block count cells (V <= 262144)
+
+struct FastSmem {
+  uint32_t ccnt[kThreads];  // per-chunk element counts
+  u64 cmass[kThreads];      // per-chunk masses of elements >= x0
+  int32_t eid[kExcCap];     // the row's penalised ids (ascending) and values
+  float eval[kExcCap];
+  uint32_t lkey[kMaxL];     // one chunk's penalised values: ordered key
+  u64 lq[kMaxL];            //   and mass
+  uint32_t binc[kWave];     // per-key counts / masses of penalised values inside that chunk
+  u64 binm[kWave];
+  uint32_t nl;
+  uint32_t red32[kWaves];
+  u64 red64[2 * kWaves];
+  uint32_t sk[8];
+  u64 sq[8];
+  int si[8];
 };
 
 template <class Tin>
@@ -135,6 +181,33 @@ __device__ __forceinline__ void for_each(const Row<Tin>& row, F f) {
   for (int e = threadIdx.x; e < row.nexc; e += kThreads) f(row.eval[e], row.eid[e]);
 }
 
+// The penalised logit of token d (bulk or exception); all threads call, all get the value.
+template <class Tin>
+__device__ __forceinline__ float value_of(const Row<Tin>& row, int d, float* slot) {
+  if (threadIdx.x == 0) *slot = load_one<Tin>(row.p, d);
+  lds_barrier();
+  for (int e = threadIdx.x; e < row.nexc; e += kThreads)
+    if (row.eid[e] == d) *slot = row.eval[e];
+  lds_barrier();
+  const float v = *slot;
+  lds_barrier();
+  return v;
+}
+
+// Fill `words` (V / 8 bytes, one lane mask per 8-id block) with the row's penalised ids.
+template <class Tin>
+__device__ __forceinline__ void build_bitmap(Row<Tin>& row, uint32_t* words) {
+  const int nw = (row.nblk + 3) / 4;
+  for (int i = threadIdx.x; i < nw; i += kThreads) words[i] = 0;
+  lds_barrier();
+  for (int e = threadIdx.x; e < row.nexc; e += kThreads) {
+    const uint32_t id = static_cast<uint32_t>(row.eid[e]);
+    atomicOr(&words[id >> 5], 1u << (id & 31u));
+  }
+  lds_barrier();
+  row.bm = reinterpret_cast<const uint8_t*>(words);
+}
+
 // Add 1 to hist[digit] for every lane with `valid`, pre-aggregating up to four repeated digits
 // per wave with ballots (the top digits of N(0, s) logits fall into a handful of bins).
 __device__ __forceinline__ void hist_count(uint32_t* hist, uint32_t digit, bool valid) {
@@ -186,26 +259,31 @@ __device__ uint32_t bisect_key(uint32_t lo, uint32_t hi, P pred) {
   return hi;
 }
 
-// First element index (ascending id) where the running sum of w(x, id) exceeds `target`
-// (clamped to total - 1); `target = UINT64_MAX` with `u >= 0` means floor(u * total).
-// Returns -1 when the total weight is 0; *total_out receives the total.
+// First element index (ascending id) where the running count of w(x, id) (0 or 1) exceeds
+// `target` (clamped to total - 1). Returns -1 when no element has w = 1.
 template <class Tin, class W>
-__device__ int find_first(const Row<Tin>& row, W wf, u64 target, float u, Smem& s, u64* total_out) {
+__device__ __noinline__ int find_first(const Row<Tin>& row, W wf, u64 target, Search& s) {
   const int tid = threadIdx.x;
   const int wv = tid / kWave;
-  // 1. per-(wave, stripe) sums
-  for (int j = 0; j < row.nstripes; ++j) {
-    const int b = j * kThreads + tid;
-    u64 w = 0;
-    if (b < row.nblk) {
-      float v[kBlk];
-      const uint32_t valid = row.load(b, v);
+  // 1. per-(wave, stripe) counts, four stripes' loads in flight per thread
+  for (int j0 = 0; j0 < row.nstripes; j0 += 4) {
+    uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int i = 0; i < kBlk; ++i)
-        if (valid & (1u << i)) w += wf(v[i], b * kBlk + i);
+    for (int k = 0; k < 4; ++k) {
+      const int b = (j0 + k) * kThreads + tid;
+      if (j0 + k < row.nstripes && b < row.nblk) {
+        float v[kBlk];
+        const uint32_t valid = row.load(b, v);
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i)
+          if (valid & (1u << i)) w[k] += static_cast<uint32_t>(wf(v[i], b * kBlk + i));
+      }
     }
-    w = wave_sum<u64>(w);
-    if (lane_id() == 0) s.cell[wv][j] = w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t ws = wave_sum<uint32_t>(w[k]);
+      if (lane_id() == 0 && j0 + k < row.nstripes) s.cell[wv][j0 + k] = ws;
+    }
   }
   __syncthreads();
   for (int e = tid; e < row.nexc; e += kThreads) {
@@ -217,7 +295,7 @@ __device__ int find_first(const Row<Tin>& row, W wf, u64 target, float u, Smem& 
     }
   }
   __syncthreads();
-  // 2. stripe totals, prefix over stripes, the stripe where the sum crosses the target
+  // 2. stripe totals, prefix over stripes, the stripe where the count crosses the target
   if (wv == 0) {
     const int j = lane_id();
     u64 t = 0;
@@ -226,7 +304,6 @@ __device__ int find_first(const Row<Tin>& row, W wf, u64 target, float u, Smem& 
     const u64 inc = wave_incl_scan<u64>(t);
     const u64 total = __shfl(inc, kWave - 1);
     u64 tg = target;
-    if (u >= 0.0f) tg = static_cast<u64>(static_cast<double>(u) * static_cast<double>(total));
     if (total > 0 && tg > total - 1) tg = total - 1;
     const bool hit = total > 0 && inc > tg && (inc - t) <= tg;
     const u64 hm = __ballot(hit);
@@ -235,11 +312,10 @@ __device__ int find_first(const Row<Tin>& row, W wf, u64 target, float u, Smem& 
       s.bq[1] = tg;
       s.bi[0] = hm ? (__ffsll(static_cast<long long>(hm)) - 1) : -1;
     }
-    if (hit) s.bq[2] = inc - t;  // sum before stripe j*
+    if (hit) s.bq[2] = inc - t;  // count before stripe js
   }
   __syncthreads();
   const u64 total = s.bq[0];
-  *total_out = total;
   if (total == 0) {
     __syncthreads();
     return -1;
@@ -247,7 +323,7 @@ __device__ int find_first(const Row<Tin>& row, W wf, u64 target, float u, Smem& 
   const u64 tg = s.bq[1];
   const int js = s.bi[0] < 0 ? 0 : s.bi[0];
   const u64 base = s.bi[0] < 0 ? 0ull : s.bq[2];
-  // 3. per-thread sums inside stripe js, prefix over threads
+  // 3. per-thread counts inside stripe js, prefix over threads
   {
     const int b = js * kThreads + tid;
     u64 w = 0;
@@ -321,14 +397,20 @@ __device__ int find_first(const Row<Tin>& row, W wf, u64 target, float u, Smem& 
   return res;
 }
 
-// Radix descent over ordered keys on counts: the key of the kth largest element (k >= 1).
+// ---- generic path: radix descents over 32-bit ordered keys ------------------------------------
+
+// The key of the kth largest element (k >= 1).
 template <class Tin>
-__device__ uint32_t radix_kth(const Row<Tin>& row, uint32_t k, Smem& s) {
+__device__ uint32_t radix_kth(const Row<Tin>& row, uint32_t k, Radix& s) {
   uint32_t prefix = 0;
   uint32_t kk = k;
   for (int lvl = 0; lvl < 4; ++lvl) {
     const int shift = 24 - 8 * lvl;
     for (int i = threadIdx.x; i < 256; i += kThreads) s.hcnt[i] = 0;
+    if (threadIdx.x == 0) {
+      s.bk[0] = 0;
+      s.bk[1] = 0;
+    }
     __syncthreads();
     const bool all = lvl == 0;
     const uint32_t pfx = prefix;
@@ -380,11 +462,15 @@ __device__ uint32_t radix_kth(const Row<Tin>& row, uint32_t k, Smem& s) {
   return prefix;
 }
 
-// Radix descent over ordered keys on masses, among elements with x >= x0: the cutoff value of
-// top-p (the lowest value whose mass strictly above it is < P), its count and that mass above.
+enum MassMode { kCutoff = 0, kCross = 1 };
+
+// Radix descent on masses among elements with x >= x0.
+//   kCutoff: the lowest value whose mass strictly above is < target (the top-p cutoff)
+//   kCross : the value whose group holds the target: above <= target < above + group mass
+// Returns the value's key; *n_c its count, *mass_c its group mass, *m_above the mass above it.
 template <class Tin>
-__device__ uint32_t radix_cutoff(const Row<Tin>& row, float x0, float T, float mz, double P, Smem& s,
-                                 uint32_t* n_c, u64* mass_c, u64* m_above) {
+__device__ uint32_t radix_mass(const Row<Tin>& row, int mode, float x0, float T, float mz,
+                               double target, Radix& s, uint32_t* n_c, u64* mass_c, u64* m_above) {
   uint32_t prefix = 0;
   u64 mprev = 0;
   for (int lvl = 0; lvl < 4; ++lvl) {
@@ -392,6 +478,12 @@ __device__ uint32_t radix_cutoff(const Row<Tin>& row, float x0, float T, float m
     for (int i = threadIdx.x; i < 256; i += kThreads) {
       s.hcnt[i] = 0;
       s.hmass[i] = 0;
+    }
+    if (threadIdx.x == 0) {
+      s.bk[0] = 0;
+      s.bk[1] = 0;
+      s.bq[0] = mprev;
+      s.bq[1] = 0;
     }
     __syncthreads();
     auto one = [&](float x, bool valid) {
@@ -402,7 +494,7 @@ __device__ uint32_t radix_cutoff(const Row<Tin>& row, float x0, float T, float m
     };
     for (int b = threadIdx.x, j = 0; j < row.nstripes; ++j, b += kThreads) {
       float v[kBlk];
-      uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
+      const uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
 #pragma unroll
       for (int i = 0; i < kBlk; ++i) one(v[i], valid & (1u << i));
     }
@@ -427,21 +519,28 @@ __device__ uint32_t radix_cutoff(const Row<Tin>& row, float x0, float T, float m
       u64 above = mprev + inc - ms;
       int cand = -1;
       u64 cand_above = 0;
+      uint32_t cand_c = 0;
+      u64 cand_m = 0;
       for (int i = 0; i < 4; ++i) {
-        if (static_cast<double>(above) < P && c[i] > 0) {
+        const double ab = static_cast<double>(above);
+        const bool ok = mode == kCutoff ? (ab < target && c[i] > 0)
+                                        : (c[i] > 0 && ab <= target && target < static_cast<double>(above + mm[i]));
+        if (ok) {
           cand = 255 - 4 * l - i;
           cand_above = above;
+          cand_c = c[i];
+          cand_m = mm[i];
         }
         above += mm[i];
       }
-      // lowest candidate digit = highest lane with a candidate
+      // kCutoff: the lowest candidate digit = the highest lane with one; kCross: the unique one
       const u64 hm = __ballot(cand >= 0);
       const int lw = hm ? 63 - __clzll(static_cast<long long>(hm)) : -1;
       if (l == lw) {
         s.bk[0] = static_cast<uint32_t>(cand);
         s.bq[0] = cand_above;
-        s.bk[1] = c[255 - 4 * l - cand];
-        s.bq[1] = mm[255 - 4 * l - cand];
+        s.bk[1] = cand_c;
+        s.bq[1] = cand_m;
       }
     }
     __syncthreads();
@@ -455,42 +554,116 @@ __device__ uint32_t radix_cutoff(const Row<Tin>& row, float x0, float T, float m
   return prefix;
 }
 
-template <class Tin, bool PEN>
-__global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
-  __shared__ Smem s;
-  const int r = blockIdx.x;
+// What a row's filters left: kept(x, id) = x >= x0 && (!partial || x > vc || (x == vc && id <=
+// idr)); S the kept mass; a point mass at `point` for greedy and degenerate rows.
+struct Kept {
+  float x0 = -INFINITY;
+  float vc = 0.0f;
+  bool partial = false;
+  int idr = 0;
+  uint32_t r = 0;    // kept members of the cutoff group
+  u64 mabove_c = 0;  // mass strictly above the cutoff value
+  u64 qc = 0;        // mass of one member of the cutoff group
+  bool has_cut = false;
+  u64 S = 0;
+  int point = -1;
+
+  __device__ __forceinline__ bool keep(float x, int id) const {
+    if (!(x >= x0)) return false;
+    if (!partial) return true;
+    return x > vc || (x == vc && id <= idr);
+  }
+};
+
+struct RowParams {
+  float T, tp, mp, u;
+  int K, draft;
+};
+
+// Greedy rows and rows whose scaled logits are not all finite: a point mass. Shared by both
+// paths; returns true when the row is such a row (and sets k.point).
+template <class Tin>
+__device__ bool degenerate(const Row<Tin>& row, const RowParams& p, uint32_t mkey, int imax, float mz,
+                           Search& s, Kept& k) {
+  if (!(p.T > 0.0f) || mkey == 0xFFFFFFFFu) {
+    k.point = imax;  // greedy (sampler.py:70-71), or a NaN logit: its first index
+    return true;
+  }
+  const float T = p.T;
+  if (mz != mz) {  // x = +inf with T = +inf: the first index where z is NaN
+    k.point = find_first(row, [&](float x, int) -> u64 { const float z = x / T; return z != z; }, 0ull, s);
+    return true;
+  }
+  if (mz == INFINITY) {
+    k.point = find_first(row, [&](float x, int) -> u64 { return x / T == INFINITY; }, 0ull, s);
+    return true;
+  }
+  if (mz == -INFINITY) {
+    k.point = 0;
+    return true;
+  }
+  return false;
+}
+
+// Writes the row's outputs: probabilities (probs mode) or the sampled id and draft probability.
+// `draw` is the drawn token (ignored for point rows).
+template <class Tin>
+__device__ __forceinline__ void finish(const SampleArgs& a, const Row<Tin>& row, const RowParams& p, float mz,
+                       const Kept& k, int draw, float* vslot) {
   const int tid = threadIdx.x;
-  const int V = a.V;
-  if (PEN) {
-    __shared__ uint32_t cnt[kChunk];
-    penalty_phase<Tin>(a.pen, r, cnt, s.red32);
+  const int r = blockIdx.x;
+  if (a.out_probs) {
+    float* o = a.out_probs + static_cast<int64_t>(r) * a.probs_stride;
+    if (k.point >= 0) {
+      for (int i = tid; i < row.V; i += kThreads) o[i] = i == k.point ? 1.0f : 0.0f;
+      return;
+    }
+    const double inv = kMassScale / static_cast<double>(k.S);
+    const float T = p.T;
+    for_each(row, [&](float x, int id) {
+      o[id] = k.keep(x, id) ? static_cast<float>(ptilde(x, T, mz) * inv) : 0.0f;
+    });
+    return;
   }
-
-  Row<Tin> row;
-  row.p = static_cast<const Tin*>(a.logits) + static_cast<int64_t>(r) * a.stride;
-  row.V = V;
-  row.nblk = (V + kBlk - 1) / kBlk;
-  row.nstripes = (row.nblk + kThreads - 1) / kThreads;
-  row.vec = (reinterpret_cast<uintptr_t>(row.p) & 15u) == 0;
-  row.nexc = a.has_exc ? static_cast<int>(a.ws.n_exc[r]) : 0;
-  if (row.nexc > 0) {
-    const int h0 = a.off[r];
-    row.bm = reinterpret_cast<const uint8_t*>(a.ws.bitmap + static_cast<int64_t>(r) * a.ws.nwords);
-    row.eid = a.ws.exc_id + h0;
-    row.eval = a.ws.exc_val + h0;
+  int tok;
+  double dprob = 0.0;
+  if (k.point >= 0) {
+    tok = k.point;
+    dprob = p.draft == tok ? 1.0 : 0.0;
   } else {
-    row.bm = nullptr;
-    row.eid = nullptr;
-    row.eval = nullptr;
+    tok = draw;
+    if (p.draft >= 0 && p.draft < row.V && a.out_dprob) {
+      const float xd = value_of(row, p.draft, vslot);
+      if (k.keep(xd, p.draft)) dprob = ptilde(xd, p.T, mz) * kMassScale / static_cast<double>(k.S);
+    }
   }
+  if (tid == 0) {
+    a.out_ids[r] = tok;
+    if (a.out_dprob) a.out_dprob[r] = static_cast<float>(dprob);
+  }
+}
 
-  const float T = a.temp ? a.temp[r] : 1.0f;
-  const int K = a.topk ? a.topk[r] : 0;
-  const float tp = a.topp ? a.topp[r] : 1.0f;
-  const float mp = a.minp ? a.minp[r] : 0.0f;
-  const int draft = a.draft ? a.draft[r] : -1;
+// With the cutoff group partial, the id of its r-th member (what kept() needs): only probs mode
+// and a draft token inside that group ask for it.
+template <class Tin>
+__device__ __forceinline__ void resolve_idr(const SampleArgs& a, const Row<Tin>& row, const RowParams& p, Kept& k,
+                            Search& s) {
+  if (!k.partial) return;
+  bool need = a.out_probs != nullptr;
+  if (!need && p.draft >= 0 && p.draft < row.V && a.out_dprob) need = value_of(row, p.draft, &s.vslot) == k.vc;
+  if (need) {
+    const float vc = k.vc;
+    k.idr = find_first(row, [&](float x, int) -> u64 { return x == vc; }, static_cast<u64>(k.r - 1), s);
+  }
+}
 
-  // ---- max (and first index of the max; NaN counts as the max) ----------------------------
+// ---- generic path -----------------------------------------------------------------------------
+template <class Tin>
+__device__ __noinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g) {
+  const int V = row.V;
+  Search& s = g.srch;
+  if (row.nexc > 0) build_bitmap(row, reinterpret_cast<uint32_t*>(&g) + kBitmapOffset);
+  // max (and first index of the max; NaN counts as the max)
   u64 best = 0;
   for_each(row, [&](float x, int id) {
     const u64 kq = (static_cast<u64>(key_of(x)) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(id));
@@ -500,140 +673,759 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
   const uint32_t mkey = static_cast<uint32_t>(best >> 32);
   const int imax = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
   const float xmax = val_of(mkey);
-
-  // kept(x, id) after all filters, described by (x0, vc, idr, partial)
-  float x0 = -INFINITY;
-  float vc = 0.0f;
-  int idr = 0;
-  bool partial = false;
-  int point = -1;  // greedy / degenerate rows: a point mass at this index
-
+  const float T = p.T;
   const float mz = xmax / T;
-  if (!(T > 0.0f) || mkey == 0xFFFFFFFFu) {
-    point = imax;  // greedy (sampler.py:70-71), or a NaN logit: its first index
-  } else if (mz != mz) {
-    // x = +inf with T = +inf: the first index where z is NaN
-    u64 tot;
-    point = find_first(row, [&](float x, int) -> u64 { const float z = x / T; return z != z; }, 0ull,
-                       -1.0f, s, &tot);
-  } else if (mz == INFINITY) {
-    u64 tot;
-    point = find_first(row, [&](float x, int) -> u64 { return x / T == INFINITY; }, 0ull, -1.0f, s,
-                       &tot);
-  } else if (mz == -INFINITY) {
-    point = 0;
-  }
-
-  if (point < 0) {
-    // ---- top-k: keep z >= kth largest z (sampler.py:53-55) --------------------------------
-    const uint32_t lo_key = key_of(-INFINITY);
-    if (K > 0 && K < V) {
-      const uint32_t kkey = radix_kth(row, static_cast<uint32_t>(K), s);
-      if (tid == 0) {
-        const float kz = val_of(kkey) / T;
-        s.bk[2] = bisect_key(lo_key, kkey, [&](float x) { return x / T >= kz; });
-      }
-      __syncthreads();
-      x0 = val_of(s.bk[2]);
-      __syncthreads();
-    }
-    // ---- min-p: keep exp(z - max z) >= min_p --------------------------------------------
-    if (mp > 0.0f) {
-      if (tid == 0) {
-        const double dmp = static_cast<double>(mp);
-        s.bk[3] = bisect_key(lo_key, mkey, [&](float x) { return ptilde(x, T, mz) >= dmp; });
-      }
-      __syncthreads();
-      const float xm = val_of(s.bk[3]);
-      x0 = xm > x0 ? xm : x0;
-      __syncthreads();
-    }
-    // ---- top-p (sampler.py:57-64) ----------------------------------------------------------
-    if (tp < 1.0f) {
-      u64 S0 = 0;
-      for_each(row, [&](float x, int) {
-        if (x >= x0) S0 += mass_q(ptilde(x, T, mz));
-      });
-      S0 = block_sum<u64>(S0, s.red64);
-      const double P = static_cast<double>(tp) * static_cast<double>(S0);
-      uint32_t nc;
-      u64 massc, mabove;
-      const uint32_t ck = radix_cutoff(row, x0, T, mz, P, s, &nc, &massc, &mabove);
-      vc = val_of(ck);
-      const u64 qc = nc ? massc / nc : 0ull;
-      uint32_t rr = nc;
-      if (qc > 0) {
-        const double need = (P - static_cast<double>(mabove)) / static_cast<double>(qc);
-        const double cr = ceil(need);
-        rr = cr < 1.0 ? 1u : (cr >= static_cast<double>(nc) ? nc : static_cast<uint32_t>(cr));
-      }
-      if (rr >= nc) {
-        x0 = vc;
-      } else {
-        u64 tot;
-        idr = find_first(row, [&](float x, int) -> u64 { return x == vc; },
-                         static_cast<u64>(rr - 1), -1.0f, s, &tot);
-        partial = true;
-      }
-    }
-  }
-
-  auto kept = [&](float x, int id) -> bool {
-    if (!(x >= x0)) return false;
-    if (!partial) return true;
-    return x > vc || (x == vc && id <= idr);
-  };
-
-  if (a.out_probs) {
-    float* o = a.out_probs + static_cast<int64_t>(r) * a.probs_stride;
-    if (point >= 0) {
-      for (int i = tid; i < V; i += kThreads) o[i] = i == point ? 1.0f : 0.0f;
-      return;
-    }
-    u64 S = 0;
-    for_each(row, [&](float x, int id) {
-      if (kept(x, id)) S += mass_q(ptilde(x, T, mz));
-    });
-    S = block_sum<u64>(S, s.red64);
-    const double inv = kMassScale / static_cast<double>(S);
-    for_each(row, [&](float x, int id) {
-      o[id] = kept(x, id) ? static_cast<float>(ptilde(x, T, mz) * inv) : 0.0f;
-    });
+  Kept k;
+  if (degenerate(row, p, mkey, imax, mz, s, k)) {
+    finish(a, row, p, mz, k, 0, &s.vslot);
     return;
   }
+  const uint32_t lo_key = key_of(-INFINITY);
+  if (p.K > 0 && p.K < V) {  // top-k: keep z >= kth largest z (sampler.py:53-55)
+    const uint32_t kkey = radix_kth(row, static_cast<uint32_t>(p.K), g.rdx);
+    if (threadIdx.x == 0) {
+      const float kz = val_of(kkey) / T;
+      g.rdx.bk[2] = bisect_key(lo_key, kkey, [&](float x) { return x / T >= kz; });
+    }
+    __syncthreads();
+    k.x0 = val_of(g.rdx.bk[2]);
+    __syncthreads();
+  }
+  if (p.mp > 0.0f) {  // min-p: keep exp(z - max z) >= min_p
+    if (threadIdx.x == 0) {
+      const double dmp = static_cast<double>(p.mp);
+      g.rdx.bk[3] = bisect_key(lo_key, mkey, [&](float x) { return ptilde(x, T, mz) >= dmp; });
+    }
+    __syncthreads();
+    const float xm = val_of(g.rdx.bk[3]);
+    k.x0 = xm > k.x0 ? xm : k.x0;
+    __syncthreads();
+  }
+  u64 S0 = 0;
+  {
+    const float x0 = k.x0;
+    for_each(row, [&](float x, int) {
+      if (x >= x0) S0 += mass_q(ptilde(x, T, mz));
+    });
+    S0 = block_sum<u64>(S0, s.red64);
+  }
+  k.S = S0;
+  if (p.tp < 1.0f) {  // top-p (sampler.py:57-64)
+    const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
+    uint32_t nc;
+    u64 massc, mabove;
+    const uint32_t ck = radix_mass(row, kCutoff, k.x0, T, mz, P, g.rdx, &nc, &massc, &mabove);
+    k.has_cut = true;
+    k.vc = val_of(ck);
+    k.qc = nc ? massc / nc : 0ull;
+    k.mabove_c = mabove;
+    uint32_t rr = nc;
+    if (k.qc > 0) {
+      const double cr = ceil((P - static_cast<double>(mabove)) / static_cast<double>(k.qc));
+      rr = cr < 1.0 ? 1u : (cr >= static_cast<double>(nc) ? nc : static_cast<uint32_t>(cr));
+    }
+    k.r = rr;
+    k.partial = rr < nc;
+    if (!k.partial) k.x0 = k.vc;
+    k.S = mabove + static_cast<u64>(rr) * k.qc;
+  }
+  resolve_idr(a, row, p, k, s);
+  int draw = 0;
+  if (!a.out_probs) {
+    // the draw: descending value, ascending id within a value
+    const u64 td = static_cast<u64>(static_cast<double>(p.u) * static_cast<double>(k.S));
+    const u64 tdc = td < k.S ? td : k.S - 1;
+    float vd;
+    u64 j;
+    if (k.has_cut && tdc >= k.mabove_c && k.qc > 0) {
+      vd = k.vc;
+      j = (tdc - k.mabove_c) / k.qc;
+    } else {
+      uint32_t nd;
+      u64 massd, maboved;
+      const uint32_t dk = radix_mass(row, kCross, k.x0, T, mz, static_cast<double>(tdc), g.rdx, &nd, &massd,
+                                     &maboved);
+      vd = val_of(dk);
+      const u64 qd = nd ? massd / nd : 0ull;
+      j = qd ? (tdc - maboved) / qd : 0ull;
+      if (j >= nd) j = nd ? nd - 1 : 0;
+    }
+    draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, s);
+  }
+  finish(a, row, p, mz, k, draw, &s.vslot);
+}
 
-  int tok;
-  double dprob = 0.0;
-  if (point >= 0) {
-    tok = point;
-    dprob = draft == tok ? 1.0 : 0.0;
-  } else {
-    const float u = a.u[r];
-    u64 S;
-    tok = find_first(row, [&](float x, int id) -> u64 {
-      return kept(x, id) ? mass_q(ptilde(x, T, mz)) : 0ull;
-    }, ~0ull, u >= 0.0f ? u : 0.0f, s, &S);
-    if (draft >= 0 && draft < V && tid == 0) {
-      float xd;
-      const int b = draft / kBlk;
-      if (row.bm && (row.bm[b] >> (draft % kBlk)) & 1u) {
-        int lo = 0, hi = row.nexc - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (row.eid[mid] < draft) lo = mid + 1;
-          else hi = mid;
-        }
-        xd = row.eval[lo];
-      } else {
-        xd = load_one<Tin>(row.p, draft);
-      }
-      if (kept(xd, draft)) dprob = ptilde(xd, T, mz) * kMassScale / static_cast<double>(S);
+// ---- bf16 fast path: a 16-bit key histogram -----------------------------------------------------
+// Ordered 16-bit key of raw bf16 bits (unsigned order = numeric order; -0.0 sits just below
+// +0.0 and is folded onto it after the histogram is built).
+__device__ __forceinline__ uint32_t ok16(uint32_t raw) {
+  return raw ^ ((raw & 0x8000u) ? 0xFFFFu : 0x8000u);
+}
+__device__ __forceinline__ float val16(uint32_t ok) {
+  const uint32_t raw = (ok & 0x8000u) ? (ok & 0x7FFFu) : (~ok & 0xFFFFu);
+  return __uint_as_float(raw << 16);
+}
+__device__ __forceinline__ uint32_t hcount(const uint32_t* h, uint32_t ok) {
+  return (h[ok >> 1] >> ((ok & 1u) << 4)) & 0xFFFFu;
+}
+// Chunk c holds keys 65535 - 64c - 63 .. 65535 - 64c; lane l of a chunk walk is key 65535-64c-l.
+__device__ __forceinline__ int chunk_of16(uint32_t ok) { return static_cast<int>((65535u - ok) >> 6); }
+
+enum WalkMode { kWalkCount = 0, kWalkCutoff = 1, kWalkCross = 2 };
+
+struct WalkResult {
+  uint32_t key;  // 32-bit ordered key of the value found
+  uint32_t n;    // its group count (kept members)
+  u64 q;         // mass of one member
+  u64 above;     // count (kWalkCount) or mass strictly above it
+  int ok;        // 0 if the chunk holds too many penalised values to resolve
+};
+
+// Resolve a value inside chunk c (all threads call; wave 0 walks). `above` is the count or mass
+// strictly above the chunk, `target` the 1-based rank (count) or the mass target. `ne` penalised
+// values are in f.eid / f.eval.
+__device__ __forceinline__ WalkResult walk_chunk(const uint32_t* hist, FastSmem& f, int ne, int c, int mode, u64 above,
+                                 double target, float x0, float T, float mz) {
+  const int tid = threadIdx.x;
+  if (tid < kWave) {
+    f.binc[tid] = 0;
+    f.binm[tid] = 0;
+  }
+  if (tid == 0) f.nl = 0;
+  lds_barrier();
+  // the chunk's penalised values
+  for (int e = tid; e < ne; e += kThreads) {
+    const float x = f.eval[e];
+    const uint32_t key = key_of(x);
+    const uint32_t top = key >> 16;
+    if (chunk_of16(top) != c) continue;
+    if (mode != kWalkCount && !(x >= x0)) continue;
+    const u64 q = mode == kWalkCount ? 0ull : mass_q(ptilde(x, T, mz));
+    const int lane = static_cast<int>(65535u - 64u * static_cast<uint32_t>(c) - top);
+    atomicAdd(&f.binc[lane], 1u);
+    atomicAdd(&f.binm[lane], q);
+    const uint32_t i = atomicAdd(&f.nl, 1u);
+    if (i < kMaxL) {
+      f.lkey[i] = key;
+      f.lq[i] = q;
     }
   }
-  if (tid == 0) {
-    a.out_ids[r] = tok;
-    if (a.out_dprob) a.out_dprob[r] = static_cast<float>(dprob);
+  lds_barrier();
+  WalkResult res;
+  res.ok = f.nl <= kMaxL;
+  res.key = 0;
+  res.n = 0;
+  res.q = 0;
+  res.above = 0;
+  if (!res.ok) return res;
+  if (tid < kWave) {
+    const int l = tid;
+    const uint32_t K = 65535u - 64u * static_cast<uint32_t>(c) - l;
+    const uint32_t cnt = hcount(hist, K);
+    const float v = val16(K);
+    const bool inb = mode == kWalkCount || v >= x0;
+    const uint32_t cb = inb ? cnt : 0u;
+    const u64 qb = (mode != kWalkCount && cb) ? mass_q(ptilde(v, T, mz)) : 0ull;
+    const uint32_t cl = cb + f.binc[l];
+    const u64 ml = (mode == kWalkCount ? static_cast<u64>(cl) : cb * qb + f.binm[l]);
+    const u64 inc = wave_incl_scan<u64>(ml);
+    const u64 ab = above + inc - ml;  // strictly above this key
+    bool hit;
+    if (mode == kWalkCount) hit = static_cast<double>(ab) < target && target <= static_cast<double>(ab + ml);
+    else if (mode == kWalkCutoff) hit = cl > 0 && static_cast<double>(ab) < target;
+    else hit = ml > 0 && static_cast<double>(ab) <= target && target < static_cast<double>(ab + ml);
+    const u64 hm = __ballot(hit);
+    const int lw = hm ? (mode == kWalkCutoff ? 63 - __clzll(static_cast<long long>(hm))
+                                             : __ffsll(static_cast<long long>(hm)) - 1)
+                      : 0;
+    if (l == lw) {
+      f.si[0] = l;
+      f.sk[0] = cb;
+      f.sq[0] = qb;
+      f.sq[1] = ab;
+      f.sk[1] = f.binc[l];
+    }
   }
+  lds_barrier();
+  const int l = f.si[0];
+  const uint32_t K = 65535u - 64u * static_cast<uint32_t>(c) - l;
+  const uint32_t cb = f.sk[0];
+  const u64 qb = f.sq[0];
+  const u64 ab = f.sq[1];
+  const uint32_t nx = f.sk[1];
+  const uint32_t bkey = key_of(val16(K));
+  if (nx == 0) {
+    res.key = bkey;
+    res.n = cb;
+    res.q = qb;
+    res.above = ab;
+    lds_barrier();
+    return res;
+  }
+  // The key mixes its bf16 value with penalised values: walk its items in descending order.
+  if (tid == 0) {
+    // move this key's penalised values to the front of the list, then sort them (descending)
+    int n = 0;
+    for (uint32_t i = 0; i < f.nl; ++i) {
+      if ((f.lkey[i] >> 16) == K) {
+        const uint32_t tk = f.lkey[n];
+        const u64 tq = f.lq[n];
+        f.lkey[n] = f.lkey[i];
+        f.lq[n] = f.lq[i];
+        f.lkey[i] = tk;
+        f.lq[i] = tq;
+        ++n;
+      }
+    }
+    for (int i = 1; i < n; ++i) {
+      const uint32_t kk = f.lkey[i];
+      const u64 qq = f.lq[i];
+      int j = i - 1;
+      while (j >= 0 && f.lkey[j] < kk) {
+        f.lkey[j + 1] = f.lkey[j];
+        f.lq[j + 1] = f.lq[j];
+        --j;
+      }
+      f.lkey[j + 1] = kk;
+      f.lq[j + 1] = qq;
+    }
+    // merge with the bulk value (cb members of mass qb each), walking distinct values
+    u64 acc = ab;
+    int ie = 0;
+    bool bulk_done = cb == 0;
+    uint32_t rkey = bkey, rn = 0;
+    u64 rq = 0, rab = ab;
+    while (ie < n || !bulk_done) {
+      uint32_t vkey;
+      if (bulk_done) vkey = f.lkey[ie];
+      else if (ie < n && f.lkey[ie] > bkey) vkey = f.lkey[ie];
+      else vkey = bkey;
+      uint32_t gn = 0;
+      u64 gm = 0, gq = 0;
+      if (!bulk_done && vkey == bkey) {
+        gn += cb;
+        gm += cb * qb;
+        gq = qb;
+        bulk_done = true;
+      }
+      while (ie < n && f.lkey[ie] == vkey) {
+        gn += 1;
+        gm += f.lq[ie];
+        gq = f.lq[ie];
+        ++ie;
+      }
+      const u64 gw = mode == kWalkCount ? static_cast<u64>(gn) : gm;
+      bool hit;
+      if (mode == kWalkCount) hit = static_cast<double>(acc) < target && target <= static_cast<double>(acc + gw);
+      else if (mode == kWalkCutoff) hit = gn > 0 && static_cast<double>(acc) < target;
+      else hit = gw > 0 && static_cast<double>(acc) <= target && target < static_cast<double>(acc + gw);
+      if (hit) {
+        rkey = vkey;
+        rn = gn;
+        rq = gq;
+        rab = acc;
+        if (mode != kWalkCutoff) break;
+      }
+      acc += gw;
+    }
+    f.sk[2] = rkey;
+    f.sk[3] = rn;
+    f.sq[2] = rq;
+    f.sq[3] = rab;
+  }
+  lds_barrier();
+  res.key = f.sk[2];
+  res.n = f.sk[3];
+  res.q = f.sq[2];
+  res.above = f.sq[3];
+  lds_barrier();
+  return res;
+}
+
+// Smallest key K in [lo, hi] with pred(val_of(K)) (pred(val_of(hi)) must hold), searched by
+// wave 0 with 64 probes per round; the result is returned to every thread.
+template <class P>
+__device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, P pred, FastSmem& f) {
+  if (threadIdx.x < kWave) {
+    const uint32_t l = lane_id();
+    while (lo < hi) {
+      // probes lo + step*(l+1) - 1 for l = 0..63 split [lo, hi] into 64 pieces
+      const u64 span = static_cast<u64>(hi) - lo;
+      const u64 step = (span + 63) / 64;
+      const u64 probe64 = static_cast<u64>(lo) + step * (l + 1) - 1;
+      const uint32_t probe = probe64 < hi ? static_cast<uint32_t>(probe64) : hi;
+      const bool ok = pred(val_of(probe));
+      const u64 hm = __ballot(ok);
+      // the first probe that holds bounds the answer from above; the one before it from below
+      const int first = hm ? __ffsll(static_cast<long long>(hm)) - 1 : 64;
+      const uint32_t nhi = first < 64 ? __shfl(probe, first) : hi;
+      const uint32_t nlo = first > 0 ? __shfl(probe, first - 1) + 1 : lo;
+      lo = nlo;
+      hi = nhi;
+    }
+    if (threadIdx.x == 0) f.sk[7] = hi;
+  }
+  lds_barrier();
+  const uint32_t res = f.sk[7];
+  lds_barrier();
+  return res;
+}
+
+// The id of the j-th (0-based, ascending id) token whose penalised value is vd: bulk positions
+// holding vd that are not penalised, and penalised ids whose new value is vd.
+// One pass counts, per 8-id block, the tokens whose bf16 value is vd into a byte per (stripe,
+// thread) cell (`cells`, nstripes * kThreads bytes of LDS); penalised positions then move their
+// cell by -1 (original value vd) or +1 (new value vd). A scan over the cells in id order finds
+// the block, and one thread the lane. `orig` holds this thread's penalised tokens' original
+// raw values (entries e = tid + k * kThreads). Needs row.bm (penalised positions) built.
+__device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, const uint32_t* orig, float vd,
+                              u64 j, uint8_t* cells) {
+  const int tid = threadIdx.x;
+  const uint32_t vb = __float_as_uint(vd);
+  const bool bf = (vb & 0xFFFFu) == 0u;  // vd is a bf16 value: bulk tokens can hold it
+  const uint32_t t16 = bf ? vb >> 16 : 0x10000u;  // 0x10000: matches no raw value
+  const uint32_t t16b = vd == 0.0f ? (t16 ^ 0x8000u) : t16;  // -0.0 and +0.0 are one value
+  const uint16_t* base = row.p;
+  const int V = row.V;
+  const int ncells = row.nstripes * kThreads;
+  uint32_t* cw = reinterpret_cast<uint32_t*>(cells);
+  for (int i = tid; i < ncells / 4; i += kThreads) cw[i] = 0;
+  lds_barrier();
+  auto cell_add = [&](int id, int delta) {
+    const int cidx = (id / kBlk / kThreads) * kThreads + (id / kBlk) % kThreads;
+    atomicAdd(&cw[cidx >> 2], static_cast<uint32_t>(delta) << (8 * (cidx & 3)));
+  };
+  if (bf) {
+    const uint32_t pat = t16 * 0x10001u, patb = t16b * 0x10001u;
+    // zero 16-bit halves of x, counted
+    auto z2 = [](uint32_t x) -> uint32_t { return ((x & 0xFFFFu) == 0u ? 1u : 0u) + (x < 0x10000u ? 1u : 0u); };
+    const int nfull = row.vec ? V / kBlk : 0;
+    for (int b0 = tid; b0 < nfull; b0 += 8 * kThreads) {
+      uint4 d[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int b = b0 + k * kThreads;
+        d[k] = b < nfull ? *reinterpret_cast<const uint4*>(base + b * kBlk) : make_uint4(~pat, ~pat, ~pat, ~pat);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int b = b0 + k * kThreads;
+        if (b >= nfull) break;
+        uint32_t c = z2(d[k].x ^ pat) + z2(d[k].y ^ pat) + z2(d[k].z ^ pat) + z2(d[k].w ^ pat);
+        if (t16b != t16) c += z2(d[k].x ^ patb) + z2(d[k].y ^ patb) + z2(d[k].z ^ patb) + z2(d[k].w ^ patb);
+        // block b = stripe * kThreads + thread is cell b: each is written by its own thread
+        cells[b] = static_cast<uint8_t>(c);
+      }
+    }
+    lds_barrier();
+    // the rest: a ragged tail, or every element of an unaligned row
+    for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
+      const uint32_t raw = base[i];
+      if (raw == t16 || raw == t16b) cell_add(i, 1);
+    }
+    // penalised positions whose original value was vd are not members
+#pragma unroll
+    for (int k = 0; k < kExcCap / kThreads; ++k) {
+      const int e = tid + k * kThreads;
+      if (e < ne && (orig[k] == t16 || orig[k] == t16b)) cell_add(f.eid[e], -1);
+    }
+  }
+  // penalised ids whose new value is vd are members
+  for (int e = tid; e < ne; e += kThreads)
+    if (f.eval[e] == vd) cell_add(f.eid[e], 1);
+  lds_barrier();
+  // the cell holding the j-th member: per-thread sums of consecutive cells, then a scan
+  const int per = (ncells + kThreads - 1) / kThreads;
+  const int c0 = tid * per;
+  uint32_t mine = 0;
+  for (int c = c0; c < c0 + per && c < ncells; ++c) mine += cells[c];
+  uint32_t total;
+  const uint32_t before = block_excl_scan<uint32_t>(mine, f.red32, &total);
+  if (tid == 0) f.si[6] = -1;
+  lds_barrier();
+  if (total > 0 && j < total && before <= j && j < before + mine) {
+    uint32_t acc = before;
+    for (int c = c0; c < c0 + per && c < ncells; ++c) {
+      if (j < acc + cells[c]) {
+        f.si[5] = c;  // block id = (c / kThreads) * kThreads + c % kThreads = c
+        f.sq[5] = acc;
+        break;
+      }
+      acc += cells[c];
+    }
+    f.si[6] = 0;
+  }
+  lds_barrier();
+  if (f.si[6] < 0) {
+    lds_barrier();
+    return -1;
+  }
+  const int b = f.si[5];
+  const u64 acc0 = f.sq[5];
+  // penalised lanes of block b whose new value is vd
+  if (tid == 0) f.sk[4] = 0;
+  lds_barrier();
+  for (int e = tid; e < ne; e += kThreads) {
+    const int id = f.eid[e];
+    if (id / kBlk == b && f.eval[e] == vd) atomicOr(&f.sk[4], 1u << (id % kBlk));
+  }
+  lds_barrier();
+  if (tid == 0) {
+    const uint32_t pen = row.bm ? row.bm[b] : 0u;
+    u64 acc = acc0;
+    int found = b * kBlk;
+    for (int i = 0; i < kBlk && b * kBlk + i < V; ++i) {
+      const int id = b * kBlk + i;
+      bool member;
+      if ((pen >> i) & 1u) member = (f.sk[4] >> i) & 1u;
+      else {
+        const uint32_t raw = base[id];
+        member = raw == t16 || raw == t16b;
+      }
+      if (member) {
+        if (acc == j) {
+          found = id;
+          break;
+        }
+        ++acc;
+      }
+    }
+    f.si[6] = found;
+  }
+  lds_barrier();
+  const int res = f.si[6];
+  lds_barrier();
+  return res;
+}
+
+// The bf16 fast path. Returns false (before writing any output) when the row needs the generic
+// path: a key count past 65535, more penalised ids than the LDS list holds, or a chunk with
+// more than kMaxL penalised values. `srch` and the match list alias `hist`: they are used only
+// once the histogram is no longer read.
+__device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row, const RowParams& p, uint32_t* hist,
+                         FastSmem& f, Search& srch, int ne) {
+  const int tid = threadIdx.x;
+  const int V = row.V;
+  const float T = p.T;
+  if (ne > kExcCap) return false;
+  // ---- 1. histogram of every key, then the penalised tokens' original keys taken out ----------
+  // (u16 halves of a word wrap and borrow exactly: only the final counts must stay below 2^16)
+  uint32_t orig[kExcCap / kThreads];
+#pragma unroll
+  for (int k = 0; k < kExcCap / kThreads; ++k) {
+    const int e = tid + k * kThreads;
+    orig[k] = e < ne ? row.p[f.eid[e]] : 0u;
+  }
+  for (int i = tid; i < kChunk / 4; i += kThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0, 0, 0, 0);
+  lds_barrier();
+  {
+    const uint16_t* base = row.p;
+    const int nfull = row.vec ? V / kBlk : 0;  // blocks read as one 16-byte load
+    auto add2 = [&](uint32_t w) {
+      // ordered keys of both halves at once: xor with (sign ? 0xFFFF : 0x8000)
+      const uint32_t s2 = (w >> 15) & 0x00010001u;
+      const uint32_t k2 = w ^ (s2 * 0x7FFFu | 0x80008000u);
+      const uint32_t klo = k2 & 0xFFFFu, khi = k2 >> 16;
+      atomicAdd(&hist[klo >> 1], 1u << ((klo & 1u) << 4));
+      atomicAdd(&hist[khi >> 1], 1u << ((khi & 1u) << 4));
+    };
+    for (int b0 = tid; b0 < nfull; b0 += 8 * kThreads) {
+      uint4 d[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int b = b0 + k * kThreads;
+        d[k] = b < nfull ? *reinterpret_cast<const uint4*>(base + b * kBlk) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (b0 + k * kThreads >= nfull) break;
+        add2(d[k].x);
+        add2(d[k].y);
+        add2(d[k].z);
+        add2(d[k].w);
+      }
+    }
+    // the rest: a ragged tail, or every element of an unaligned row
+    for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
+      const uint32_t ko = ok16(base[i]);
+      atomicAdd(&hist[ko >> 1], 1u << ((ko & 1u) << 4));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kExcCap / kThreads; ++k) {
+    if (tid + k * kThreads < ne) {
+      const uint32_t ko = ok16(orig[k]);
+      atomicAdd(&hist[ko >> 1], 0u - (1u << ((ko & 1u) << 4)));
+    }
+  }
+  lds_barrier();
+  // fold -0.0 (key 0x7FFF, high half of word 0x3FFF) onto +0.0 (key 0x8000, low half of 0x4000)
+  if (tid == 0) {
+    const uint32_t neg0 = hist[0x3FFF] >> 16;
+    const uint32_t pos0 = hist[0x4000] & 0xFFFFu;
+    f.si[1] = 0;
+    if (neg0) {
+      if (pos0 + neg0 > 0xFFFFu) f.si[1] = 1;  // would overflow: generic path
+      hist[0x3FFF] &= 0xFFFFu;
+      hist[0x4000] += neg0;
+    }
+  }
+  lds_barrier();
+  // ---- 2. per-chunk counts, the row max, NaNs, overflow --------------------------------
+  uint32_t cnt = 0, nan = 0;
+  {
+    const int w0 = 32768 - 32 * tid - 32;  // the chunk's 32 words: keys 2*w0 .. 2*w0 + 63
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int piece = (s + tid) & 7;  // rotate so a wave's 16-byte reads spread over the banks
+      const uint4 q4 = *reinterpret_cast<const uint4*>(&hist[w0 + 4 * piece]);
+      // lo + hi of each word in one v_dot2_u32_u16
+      cnt = __builtin_amdgcn_udot2(__builtin_bit_cast(ushort2_t, q4.x), ones2(), cnt, false);
+      cnt = __builtin_amdgcn_udot2(__builtin_bit_cast(ushort2_t, q4.y), ones2(), cnt, false);
+      cnt = __builtin_amdgcn_udot2(__builtin_bit_cast(ushort2_t, q4.z), ones2(), cnt, false);
+      cnt = __builtin_amdgcn_udot2(__builtin_bit_cast(ushort2_t, q4.w), ones2(), cnt, false);
+    }
+    // NaN keys: all of chunks 0 and 1023 (keys >= 0xFFC0, <= 0x003F), and chunks 1 and 1022
+    // but for +inf (0xFF80) and -inf (0x007F)
+    if (tid == 0 || tid == 1023) nan = cnt;
+    if (tid == 1) nan = cnt - hcount(hist, 0xFF80u);
+    if (tid == 1022) nan = cnt - hcount(hist, 0x007Fu);
+    f.ccnt[tid] = cnt;
+  }
+  // penalised values: the max and NaNs
+  uint32_t emax = 0;
+  for (int e = tid; e < ne; e += kThreads) {
+    const uint32_t key = key_of(f.eval[e]);
+    if (key == 0xFFFFFFFFu) ++nan;
+    emax = key > emax ? key : emax;
+  }
+  // one reduction: count | NaNs, and max of (highest populated chunk | penalised max)
+  u64 tot, mx;
+  const u64 code = cnt ? static_cast<u64>(1024 - tid) : 0ull;  // higher = a chunk of larger keys
+  block_sum_max_u64((static_cast<u64>(cnt) << 32) | nan, (static_cast<u64>(emax) << 11) | code, f.red64, &tot, &mx);
+  const uint32_t total = static_cast<uint32_t>(tot >> 32);
+  const uint32_t nnan = static_cast<uint32_t>(tot);
+  if (f.si[1] || total != static_cast<uint32_t>(V - ne)) return false;
+  // the bulk max: the top populated key of the top populated chunk (wave 0 looks it up)
+  {
+    u64 cm = 0;
+    // (emax is packed above the chunk code, so recover the chunk code separately)
+    if (tid == 0) f.sq[7] = 0;
+    lds_barrier();
+    if (cnt) atomicMax(reinterpret_cast<unsigned long long*>(&f.sq[7]), code);
+    lds_barrier();
+    cm = f.sq[7];
+    if (tid < kWave) {
+      uint32_t K = 0;
+      bool has = false;
+      if (cm) {
+        const int c = 1024 - static_cast<int>(cm);
+        K = 65535u - 64u * static_cast<uint32_t>(c) - tid;
+        has = hcount(hist, K) != 0;
+      }
+      const u64 hb = __ballot(has);
+      if (tid == 0) {
+        u64 mk = 0;
+        if (hb) {
+          const int c = 1024 - static_cast<int>(cm);
+          mk = key_of(val16(65535u - 64u * static_cast<uint32_t>(c) - (__ffsll(static_cast<long long>(hb)) - 1)));
+        }
+        const u64 em = mx >> 11;
+        f.sq[6] = em > mk ? em : mk;
+      }
+    }
+    lds_barrier();
+  }
+  const u64 mk = f.sq[6];
+  lds_barrier();
+  const uint32_t mkey = static_cast<uint32_t>(mk);
+  const float xmax = val_of(mkey);
+  const float mz = xmax / T;
+  Kept k;
+  if (nnan || mz != mz || mz == INFINITY || mz == -INFINITY) {
+    // the histogram is dead: the id searches use its memory
+    if (ne > 0) build_bitmap(row, hist + kBitmapOffset);
+    // point rows: the first NaN, the first +inf z, or index 0 (all -inf)
+    if (nnan) k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
+    else if (!degenerate(row, p, mkey, 0, mz, srch, k)) k.point = 0;
+    finish(a, row, p, mz, k, 0, &srch.vslot);
+    return true;
+  }
+  const uint32_t lo_key = key_of(-INFINITY);
+  // ---- 3. top-k ----------------------------------------------------------------------
+  if (p.K > 0 && p.K < V) {
+    if (tid == 0) f.si[2] = -1;
+    for (int e = tid; e < ne; e += kThreads) atomicAdd(&f.ccnt[chunk_of16(key_of(f.eval[e]) >> 16)], 1u);
+    lds_barrier();
+    uint32_t ctot;
+    const uint32_t ex = block_excl_scan<uint32_t>(f.ccnt[tid], f.red32, &ctot);
+    if (ex < static_cast<uint32_t>(p.K) && static_cast<uint32_t>(p.K) <= ex + f.ccnt[tid]) {
+      f.si[2] = tid;
+      f.sq[6] = ex;
+    }
+    lds_barrier();
+    const int ck = f.si[2];
+    const u64 cab = f.sq[6];
+    lds_barrier();
+    if (ck < 0) return false;
+    const WalkResult wr = walk_chunk(hist, f, ne, ck, kWalkCount, cab, static_cast<double>(p.K), -INFINITY, T, mz);
+    if (!wr.ok) return false;
+    const float kz = val_of(wr.key) / T;
+    k.x0 = val_of(wave_bisect(lo_key, wr.key, [&](float x) { return x / T >= kz; }, f));
+  }
+  // ---- 4. min-p ----------------------------------------------------------------------
+  if (p.mp > 0.0f) {
+    const double dmp = static_cast<double>(p.mp);
+    const float xm = val_of(wave_bisect(lo_key, mkey, [&](float x) { return ptilde(x, T, mz) >= dmp; }, f));
+    k.x0 = xm > k.x0 ? xm : k.x0;
+  }
+  // ---- 5. per-chunk masses of elements >= x0 ------------------------------------------
+  const float x0 = k.x0;
+  const uint32_t x0top = key_of(x0) >> 16;
+  {
+    f.cmass[tid] = 0;
+    lds_barrier();
+    // wave w takes chunks w + 16 l (lane l says which need work), then a lane per key of each:
+    // fp64 exps for populated keys only
+    const int wv = tid / kWave, l = lane_id();
+    const int cl = wv + kWaves * l;
+    const bool need = f.ccnt[cl] > 0 && 65535u - 64u * static_cast<uint32_t>(cl) >= x0top;
+    u64 todo = __ballot(need);
+    while (todo) {
+      const int i = __ffsll(static_cast<long long>(todo)) - 1;
+      todo &= todo - 1;
+      const int c = wv + kWaves * i;
+      const uint32_t K = 65535u - 64u * static_cast<uint32_t>(c) - l;
+      const uint32_t n = hcount(hist, K);
+      const float v = val16(K);
+      const u64 m = (n && v >= x0) ? n * mass_q(ptilde(v, T, mz)) : 0ull;
+      const u64 sm = wave_sum<u64>(m);
+      if (l == 0) f.cmass[c] = sm;
+    }
+    lds_barrier();
+    for (int e = tid; e < ne; e += kThreads) {
+      const float x = f.eval[e];
+      if (x >= x0) atomicAdd(&f.cmass[chunk_of16(key_of(x) >> 16)], mass_q(ptilde(x, T, mz)));
+    }
+    lds_barrier();
+  }
+  u64 S0;
+  const u64 cab = block_excl_scan<u64>(f.cmass[tid], f.red64, &S0);  // mass above chunk tid
+  k.S = S0;
+  // ---- 6. top-p cutoff ----------------------------------------------------------------
+  if (p.tp < 1.0f) {
+    const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
+    // the lowest chunk holding mass whose mass above is < P
+    const u64 cand = (f.cmass[tid] > 0 && static_cast<double>(cab) < P) ? static_cast<u64>(tid) + 1 : 0ull;
+    const u64 cm = block_max_u64(cand, f.red64);
+    const int c = static_cast<int>(cm) - 1;
+    if (tid == c) f.sq[4] = cab;
+    lds_barrier();
+    const u64 ab = f.sq[4];
+    lds_barrier();
+    if (c < 0) return false;
+    const WalkResult wr = walk_chunk(hist, f, ne, c, kWalkCutoff, ab, P, x0, T, mz);
+    if (!wr.ok) return false;
+    k.has_cut = true;
+    k.vc = val_of(wr.key);
+    k.qc = wr.q;
+    k.mabove_c = wr.above;
+    uint32_t rr = wr.n;
+    if (k.qc > 0) {
+      const double cr = ceil((P - static_cast<double>(wr.above)) / static_cast<double>(k.qc));
+      rr = cr < 1.0 ? 1u : (cr >= static_cast<double>(wr.n) ? wr.n : static_cast<uint32_t>(cr));
+    }
+    k.r = rr;
+    k.partial = rr < wr.n;
+    if (!k.partial) k.x0 = k.vc;
+    k.S = wr.above + static_cast<u64>(rr) * k.qc;
+  }
+  // ---- 7. the draw's value group: descending value, ascending id within a value -----------
+  float vd = 0.0f;
+  u64 j = 0;
+  if (!a.out_probs) {
+    const u64 td0 = static_cast<u64>(static_cast<double>(p.u) * static_cast<double>(k.S));
+    const u64 td = td0 < k.S ? td0 : k.S - 1;
+    if (k.has_cut && td >= k.mabove_c && k.qc > 0) {
+      vd = k.vc;
+      j = (td - k.mabove_c) / k.qc;
+    } else {
+      // the chunk holding the target, then the value inside it
+      if (tid == 0) f.si[3] = -1;
+      lds_barrier();
+      if (f.cmass[tid] > 0 && cab <= td && td < cab + f.cmass[tid]) {
+        f.si[3] = tid;
+        f.sq[5] = cab;
+      }
+      lds_barrier();
+      const int cd = f.si[3];
+      const u64 abd = f.sq[5];
+      lds_barrier();
+      if (cd < 0) return false;
+      const WalkResult wr = walk_chunk(hist, f, ne, cd, kWalkCross, abd, static_cast<double>(td), x0, T, mz);
+      if (!wr.ok) return false;
+      vd = val_of(wr.key);
+      j = wr.q ? (td - wr.above) / wr.q : 0ull;
+      if (j >= wr.n) j = wr.n ? wr.n - 1 : 0;
+    }
+  }
+  // the histogram is dead: the id searches below use its memory
+  if (ne > 0) build_bitmap(row, hist + kBitmapOffset);
+  resolve_idr(a, row, p, k, srch);
+  int draw = 0;
+  if (!a.out_probs) {
+    draw = row.nstripes * kThreads <= 4 * kMatchWords
+               ? select_member(row, f, ne, orig, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset))
+               : -1;
+    if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
+  }
+  finish(a, row, p, mz, k, draw, &srch.vslot);
+  return true;
+}
+
+template <class Tin, bool PEN>
+__global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
+  // 128 KB: the penalty counts, then the key histogram, then the id-search / radix scratch
+  __shared__ __align__(16) uint32_t big[kChunk];
+  __shared__ FastSmem f;
+  static_assert(sizeof(GenericSmem) <= sizeof(uint32_t) * kBitmapOffset, "scratch must fit below the bitmap");
+  static_assert(kMatchOffset + kMatchWords <= kChunk, "count cells must fit");
+  const int r = blockIdx.x;
+  // every per-row parameter load is issued before the penalty pass waits on its own
+  RowParams p;
+  p.T = a.temp ? a.temp[r] : 1.0f;
+  p.K = a.topk ? a.topk[r] : 0;
+  p.tp = a.topp ? a.topp[r] : 1.0f;
+  p.mp = a.minp ? a.minp[r] : 0.0f;
+  p.u = a.u ? a.u[r] : 0.0f;
+  p.draft = a.draft ? a.draft[r] : -1;
+  int ne = 0;
+  if (PEN) ne = static_cast<int>(penalty_phase<Tin>(a.pen, r, big, f.red32, ExcCache{f.eid, f.eval, kExcCap}));
+  p.u = p.u >= 0.0f ? p.u : 0.0f;
+
+  Row<Tin> row;
+  row.p = static_cast<const Tin*>(a.logits) + static_cast<int64_t>(r) * a.stride;
+  row.V = a.V;
+  row.nblk = (a.V + kBlk - 1) / kBlk;
+  row.nstripes = (row.nblk + kThreads - 1) / kThreads;
+  row.vec = (reinterpret_cast<uintptr_t>(row.p) & 15u) == 0;
+  row.nexc = ne;
+  row.bm = nullptr;  // built in LDS by the path that masks penalised positions
+  row.eid = f.eid;   // the fast path reads the penalised ids from LDS
+  row.eval = f.eval;
+  GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
+  if constexpr (sizeof(Tin) == 2) {
+    if (p.T > 0.0f && ne <= kExcCap) {
+      if (fast_row(a, row, p, big, f, g.srch, ne)) return;
+    }
+  }
+  // the generic path reads the penalised ids from the workspace the penalty pass wrote
+  __syncthreads();
+  if (ne > 0) {
+    row.eid = a.ws.exc_id + a.off[r];
+    row.eval = a.ws.exc_val + a.off[r];
+  }
+  generic_row(a, row, p, g);
 }
 
 }  // namespace vs

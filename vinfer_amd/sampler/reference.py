@@ -8,7 +8,8 @@ batched path below instead, since the engine's sampler has neither.
 
 ``sample_batch`` and ``probs`` restate the batched semantics the ``hip`` backend implements,
 row by row in torch: penalties, fp32 division by the temperature, top-k, fp64 softmax, min-p,
-top-p with ties broken by ascending id, and the inverse-CDF draw from the caller's uniform.
+top-p with ties broken by ascending id, and the inverse-CDF draw from the caller's uniform over
+the kept tokens in that same order (descending probability, ties by ascending id).
 """
 
 from __future__ import annotations
@@ -127,7 +128,8 @@ class ReferenceSampler:
         ids, dps = [], []
         for b, (x, _, r) in enumerate(self._rows(logits, params, hist_ids, hist_offsets)):
             p = _row(x, r["temperature"], int(r["top_k"]), r["top_p"], r["min_p"])
-            kept = torch.nonzero(p > 0).flatten()
+            # kept tokens by descending probability, ties by ascending id
+            kept = torch.sort(-p, stable=True).indices[: int((p > 0).sum())]
             c = torch.cumsum(p[kept], 0)
             j = int(torch.searchsorted(c, uniforms[b].double() * c[-1], right=True))
             ids.append(int(kept[min(j, kept.numel() - 1)]))
