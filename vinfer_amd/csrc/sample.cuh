@@ -86,10 +86,11 @@ constexpr int kExcCap = 2048;  // penalised ids per row the fast path keeps in L
 constexpr int kMatchWords = 8192;  // LDS words of the draw's per-block count cells (V <= 262144)
 
 struct FastSmem {
+  // ccnt, cmass and eval also hold the history's hash table while the row's histogram is built
   uint32_t ccnt[kThreads];  // per-chunk element counts
   u64 cmass[kThreads];      // per-chunk masses of elements >= x0
-  int32_t eid[kExcCap];     // the row's penalised ids (ascending) and values
-  float eval[kExcCap];
+  float eval[kExcCap];      // the row's penalised values and ids (in no particular order)
+  int32_t eid[kExcCap];
   uint32_t lkey[kMaxL];     // one chunk's penalised values: ordered key
   u64 lq[kMaxL];            //   and mass
   uint32_t binc[kWave];     // per-key counts / masses of penalised values inside that chunk
@@ -100,7 +101,41 @@ struct FastSmem {
   uint32_t sk[8];
   u64 sq[8];
   int si[8];
+  uint32_t hfail;  // the history's hash table overflowed a probe sequence
 };
+
+// ---- the fast path's history count ----------------------------------------------------------
+// A history of at most kFastMaxL ids is counted in a kFastSlots-word LDS hash table over
+// ccnt/cmass/eval (dead until the histogram is complete) whose words pack (id << 13 | count):
+// ids are below 2^19 and counts below 8191, so a word is never kEmpty. Linear probing; a probe
+// sequence longer than kFastProbes sends the row to the generic path.
+constexpr int kFastSlots = 4096;
+constexpr int kFastHistPer = 8;  // history ids per thread
+constexpr int kFastMaxL = kFastHistPer * kThreads - 2;
+constexpr int kFastProbes = 64;
+static_assert(offsetof(FastSmem, cmass) == sizeof(uint32_t) * kThreads &&
+                  offsetof(FastSmem, eval) == offsetof(FastSmem, cmass) + sizeof(u64) * kThreads &&
+                  offsetof(FastSmem, eval) + sizeof(float) * kExcCap >= sizeof(uint32_t) * kFastSlots,
+              "the hash table must fit over ccnt, cmass and eval");
+static_assert(kMaxStripes * kThreads * kBlk <= (1 << 19) && kFastMaxL < 8191, "hash word fields");
+
+__device__ __forceinline__ uint32_t* fast_htab(FastSmem& f) { return f.ccnt; }
+
+// Counts one occurrence of `id`; false if its probe sequence found neither it nor a free slot.
+__device__ __forceinline__ bool fast_insert(uint32_t* htab, uint32_t id) {
+  uint32_t h = (id * 2654435761u) >> (32 - 12);  // Fibonacci hashing onto 4096 slots
+  const uint32_t tag = id << 13;
+  for (int n = 0; n < kFastProbes; ++n) {
+    const uint32_t prev = atomicCAS(&htab[h], kEmpty, tag | 1u);
+    if (prev == kEmpty) return true;
+    if ((prev & 0xFFFFE000u) == tag) {
+      atomicAdd(&htab[h], 1u);
+      return true;
+    }
+    h = (h + 1) & (kFastSlots - 1);
+  }
+  return false;
+}
 
 template <class Tin>
 struct Row {
@@ -578,6 +613,8 @@ struct Kept {
 struct RowParams {
   float T, tp, mp, u;
   int K, draft;
+  float rep, pres, freq;  // penalties
+  int h0, h1;             // the row's history: hist_ids[h0, h1)
 };
 
 // Greedy rows and rows whose scaled logits are not all finite: a point mass. Shared by both
@@ -976,10 +1013,11 @@ __device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, P pred
 // One pass counts, per 8-id block, the tokens whose bf16 value is vd into a byte per (stripe,
 // thread) cell (`cells`, nstripes * kThreads bytes of LDS); penalised positions then move their
 // cell by -1 (original value vd) or +1 (new value vd). A scan over the cells in id order finds
-// the block, and one thread the lane. `orig` holds this thread's penalised tokens' original
-// raw values (entries e = tid + k * kThreads). Needs row.bm (penalised positions) built.
-__device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, const uint32_t* orig, float vd,
-                              u64 j, uint8_t* cells) {
+// the block, and one thread the lane. Needs row.bm (penalised positions) built.
+// The pass reads the row's blocks last to first: the end of the row, read last by the
+// histogram pass, is the part most likely still in L2.
+__device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, float vd, u64 j,
+                                            uint8_t* cells) {
   const int tid = threadIdx.x;
   const uint32_t vb = __float_as_uint(vd);
   const bool bf = (vb & 0xFFFFu) == 0u;  // vd is a bf16 value: bulk tokens can hold it
@@ -997,24 +1035,36 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   };
   if (bf) {
     const uint32_t pat = t16 * 0x10001u, patb = t16b * 0x10001u;
+    // the penalised ids' original values (bulk blocks count them as they were)
+    uint32_t orig[kExcCap / kThreads];
+#pragma unroll
+    for (int k = 0; k < kExcCap / kThreads; ++k) {
+      const int e = tid + k * kThreads;
+      orig[k] = e < ne ? base[f.eid[e]] : 0u;
+    }
     // zero 16-bit halves of x, counted
     auto z2 = [](uint32_t x) -> uint32_t { return ((x & 0xFFFFu) == 0u ? 1u : 0u) + (x < 0x10000u ? 1u : 0u); };
     const int nfull = row.vec ? V / kBlk : 0;
-    for (int b0 = tid; b0 < nfull; b0 += 8 * kThreads) {
-      uint4 d[8];
+    // rolling prefetch over blocks nfull - 1 - i, i = tid + (D * round + k) * kThreads
+    constexpr int D = 4;
+    uint4 d[D];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int b = b0 + k * kThreads;
-        d[k] = b < nfull ? *reinterpret_cast<const uint4*>(base + b * kBlk) : make_uint4(~pat, ~pat, ~pat, ~pat);
-      }
+    for (int k = 0; k < D; ++k) {
+      const int i = tid + k * kThreads;
+      d[k] = i < nfull ? *reinterpret_cast<const uint4*>(base + (nfull - 1 - i) * kBlk) : make_uint4(0, 0, 0, 0);
+    }
+    for (int i0 = tid; i0 < nfull; i0 += D * kThreads) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int b = b0 + k * kThreads;
-        if (b >= nfull) break;
-        uint32_t c = z2(d[k].x ^ pat) + z2(d[k].y ^ pat) + z2(d[k].z ^ pat) + z2(d[k].w ^ pat);
-        if (t16b != t16) c += z2(d[k].x ^ patb) + z2(d[k].y ^ patb) + z2(d[k].z ^ patb) + z2(d[k].w ^ patb);
-        // block b = stripe * kThreads + thread is cell b: each is written by its own thread
-        cells[b] = static_cast<uint8_t>(c);
+      for (int k = 0; k < D; ++k) {
+        const int i = i0 + k * kThreads;
+        if (i >= nfull) break;
+        const uint4 w = d[k];
+        const int in = i + D * kThreads;
+        if (in < nfull) d[k] = *reinterpret_cast<const uint4*>(base + (nfull - 1 - in) * kBlk);
+        uint32_t c = z2(w.x ^ pat) + z2(w.y ^ pat) + z2(w.z ^ pat) + z2(w.w ^ pat);
+        if (t16b != t16) c += z2(w.x ^ patb) + z2(w.y ^ patb) + z2(w.z ^ patb) + z2(w.w ^ patb);
+        // block b is cell b (b = stripe * kThreads + thread), written by the one thread reading it
+        cells[nfull - 1 - i] = static_cast<uint8_t>(c);
       }
     }
     lds_barrier();
@@ -1099,65 +1149,131 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
 }
 
 // The bf16 fast path. Returns false (before writing any output) when the row needs the generic
-// path: a key count past 65535, more penalised ids than the LDS list holds, or a chunk with
-// more than kMaxL penalised values. `srch` and the match list alias `hist`: they are used only
-// once the histogram is no longer read.
+// path: a history longer than kFastMaxL or with more than kExcCap distinct ids, a key count past
+// 65535, or a chunk with more than kMaxL penalised values. `srch` and the match list alias
+// `hist`: they are used only once the histogram is no longer read.
+//
+// With PEN the row's history is counted here, between the first rounds of the histogram pass,
+// and the penalised ids' original values are gathered while the pass streams the row; the
+// penalised ids and values end in f.eid / f.eval.
+template <bool PEN>
 __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row, const RowParams& p, uint32_t* hist,
-                         FastSmem& f, Search& srch, int ne) {
+                                         FastSmem& f, Search& srch) {
   const int tid = threadIdx.x;
   const int V = row.V;
   const float T = p.T;
-  if (ne > kExcCap) return false;
+  const int L = PEN ? p.h1 - p.h0 : 0;
+  const bool pen = PEN && L > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
+  if (pen && L > kFastMaxL) return false;
   // ---- 1. histogram of every key, then the penalised tokens' original keys taken out ----------
   // (u16 halves of a word wrap and borrow exactly: only the final counts must stay below 2^16)
-  uint32_t orig[kExcCap / kThreads];
+  const uint16_t* base = row.p;
+  const int nfull = row.vec ? V / kBlk : 0;  // blocks read as one 16-byte load
+  // A rolling prefetch: slot k of d holds block tid + (D * round + k) * kThreads and is reloaded
+  // for the next round as soon as it is consumed, so D loads per thread are always in flight.
+  constexpr int D = 4;
+  uint4 d[D];
 #pragma unroll
-  for (int k = 0; k < kExcCap / kThreads; ++k) {
-    const int e = tid + k * kThreads;
-    orig[k] = e < ne ? row.p[f.eid[e]] : 0u;
+  for (int k = 0; k < D; ++k) {
+    const int b = tid + k * kThreads;
+    d[k] = b < nfull ? *reinterpret_cast<const uint4*>(base + b * kBlk) : make_uint4(0, 0, 0, 0);
   }
+  uint32_t hid[kFastHistPer];
+  if (pen) {
+    const int32_t* h = a.pen.hist + p.h0;
+#pragma unroll
+    for (int k = 0; k < kFastHistPer; ++k) {
+      const int i = tid + k * kThreads;
+      hid[k] = i < L ? static_cast<uint32_t>(h[i]) : kEmpty;  // ids outside [0, V) are skipped
+    }
+  }
+  uint32_t* htab = fast_htab(f);
   for (int i = tid; i < kChunk / 4; i += kThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0, 0, 0, 0);
+  if (pen) reinterpret_cast<uint4*>(htab)[tid] = make_uint4(kEmpty, kEmpty, kEmpty, kEmpty);
+  static_assert(kFastSlots == 4 * kThreads, "one uint4 of slots per thread");
+  if (tid == 0) f.hfail = 0;
   lds_barrier();
-  {
-    const uint16_t* base = row.p;
-    const int nfull = row.vec ? V / kBlk : 0;  // blocks read as one 16-byte load
-    auto add2 = [&](uint32_t w) {
-      // ordered keys of both halves at once: xor with (sign ? 0xFFFF : 0x8000)
-      const uint32_t s2 = (w >> 15) & 0x00010001u;
-      const uint32_t k2 = w ^ (s2 * 0x7FFFu | 0x80008000u);
-      const uint32_t klo = k2 & 0xFFFFu, khi = k2 >> 16;
-      atomicAdd(&hist[klo >> 1], 1u << ((klo & 1u) << 4));
-      atomicAdd(&hist[khi >> 1], 1u << ((khi & 1u) << 4));
-    };
-    for (int b0 = tid; b0 < nfull; b0 += 8 * kThreads) {
-      uint4 d[8];
+  auto add2 = [&](uint32_t w) {
+    // ordered keys of both halves at once: xor with (sign ? 0xFFFF : 0x8000)
+    const uint32_t s2 = (w >> 15) & 0x00010001u;
+    const uint32_t k2 = w ^ (s2 * 0x7FFFu | 0x80008000u);
+    const uint32_t klo = k2 & 0xFFFFu, khi = k2 >> 16;
+    atomicAdd(&hist[klo >> 1], 1u << ((klo & 1u) << 4));
+    atomicAdd(&hist[khi >> 1], 1u << ((khi & 1u) << 4));
+  };
+  // the history: stage 0 inserts this thread's ids, stage 1 compacts the table (thread t keeps
+  // slots 4t .. 4t + 3 in sl, their ids' original values in og) and gathers the originals
+  int stage = pen ? 0 : 2;
+  uint32_t sl[4] = {kEmpty, kEmpty, kEmpty, kEmpty}, og[4] = {0u, 0u, 0u, 0u};
+  uint32_t e0 = 0, nexc = 0;
+  auto pen_step = [&]() {
+    if (stage == 0) {
+      bool ok = true;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int b = b0 + k * kThreads;
-        d[k] = b < nfull ? *reinterpret_cast<const uint4*>(base + b * kBlk) : make_uint4(0, 0, 0, 0);
-      }
+      for (int k = 0; k < kFastHistPer; ++k)
+        if (hid[k] < static_cast<uint32_t>(V)) ok = fast_insert(htab, hid[k]) && ok;
+      if (!ok) f.hfail = 1;
+    } else {
+      lds_barrier();
+      const uint4 s4 = reinterpret_cast<const uint4*>(htab)[tid];
+      sl[0] = s4.x;
+      sl[1] = s4.y;
+      sl[2] = s4.z;
+      sl[3] = s4.w;
+      uint32_t n = 0;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if (b0 + k * kThreads >= nfull) break;
-        add2(d[k].x);
-        add2(d[k].y);
-        add2(d[k].z);
-        add2(d[k].w);
+      for (int k = 0; k < 4; ++k) n += sl[k] != kEmpty ? 1u : 0u;
+      e0 = block_excl_scan<uint32_t>(n, f.red32, &nexc);  // (its barriers end every read of htab)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) og[k] = sl[k] != kEmpty ? base[sl[k] >> 13] : 0u;
+    }
+    ++stage;
+  };
+  const int rounds = (nfull + D * kThreads - 1) / (D * kThreads);
+  for (int it = 0; it < rounds; ++it) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const int b = tid + (it * D + k) * kThreads;
+      if (b < nfull) {
+        const uint4 w = d[k];
+        const int bn = b + D * kThreads;
+        if (bn < nfull) d[k] = *reinterpret_cast<const uint4*>(base + bn * kBlk);
+        add2(w.x);
+        add2(w.y);
+        add2(w.z);
+        add2(w.w);
       }
     }
-    // the rest: a ragged tail, or every element of an unaligned row
-    for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
-      const uint32_t ko = ok16(base[i]);
-      atomicAdd(&hist[ko >> 1], 1u << ((ko & 1u) << 4));
+    if (stage < 2) {  // (uniform: `it` and `stage` are the same in every thread)
+      pen_step();
+      if (stage == 2 && (f.hfail || nexc > static_cast<uint32_t>(kExcCap))) return false;
     }
   }
+  while (stage < 2) {
+    pen_step();
+    if (stage == 2 && (f.hfail || nexc > static_cast<uint32_t>(kExcCap))) return false;
+  }
+  // the rest: a ragged tail, or every element of an unaligned row
+  for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
+    const uint32_t ko = ok16(base[i]);
+    atomicAdd(&hist[ko >> 1], 1u << ((ko & 1u) << 4));
+  }
+  // the penalised ids: original keys out of the histogram, penalised values into the list
+  if (pen) {
+    uint32_t e = e0;
 #pragma unroll
-  for (int k = 0; k < kExcCap / kThreads; ++k) {
-    if (tid + k * kThreads < ne) {
-      const uint32_t ko = ok16(orig[k]);
+    for (int k = 0; k < 4; ++k) {
+      if (sl[k] == kEmpty) continue;
+      const uint32_t ko = ok16(og[k]);
       atomicAdd(&hist[ko >> 1], 0u - (1u << ((ko & 1u) << 4)));
+      f.eid[e] = static_cast<int32_t>(sl[k] >> 13);
+      f.eval[e] = apply_penalty(bf16_to_f32(static_cast<uint16_t>(og[k])), static_cast<int>(sl[k] & 0x1FFFu),
+                                p.rep, p.pres, p.freq);
+      ++e;
     }
   }
+  const int ne = static_cast<int>(nexc);
+  row.nexc = ne;
   lds_barrier();
   // fold -0.0 (key 0x7FFF, high half of word 0x3FFF) onto +0.0 (key 0x8000, low half of 0x4000)
   if (tid == 0) {
@@ -1375,7 +1491,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   int draw = 0;
   if (!a.out_probs) {
     draw = row.nstripes * kThreads <= 4 * kMatchWords
-               ? select_member(row, f, ne, orig, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset))
+               ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset))
                : -1;
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
   }
@@ -1385,13 +1501,13 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
 
 template <class Tin, bool PEN>
 __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
-  // 128 KB: the penalty counts, then the key histogram, then the id-search / radix scratch
+  // 128 KB: the key histogram (or the generic path's penalty counts), then the id-search /
+  // radix scratch
   __shared__ __align__(16) uint32_t big[kChunk];
   __shared__ FastSmem f;
   static_assert(sizeof(GenericSmem) <= sizeof(uint32_t) * kBitmapOffset, "scratch must fit below the bitmap");
   static_assert(kMatchOffset + kMatchWords <= kChunk, "count cells must fit");
   const int r = blockIdx.x;
-  // every per-row parameter load is issued before the penalty pass waits on its own
   RowParams p;
   p.T = a.temp ? a.temp[r] : 1.0f;
   p.K = a.topk ? a.topk[r] : 0;
@@ -1399,8 +1515,11 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
   p.mp = a.minp ? a.minp[r] : 0.0f;
   p.u = a.u ? a.u[r] : 0.0f;
   p.draft = a.draft ? a.draft[r] : -1;
-  int ne = 0;
-  if (PEN) ne = static_cast<int>(penalty_phase<Tin>(a.pen, r, big, f.red32, ExcCache{f.eid, f.eval, kExcCap}));
+  p.rep = PEN && a.pen.rep ? a.pen.rep[r] : 1.0f;
+  p.pres = PEN && a.pen.pres ? a.pen.pres[r] : 0.0f;
+  p.freq = PEN && a.pen.freq ? a.pen.freq[r] : 0.0f;
+  p.h0 = PEN ? a.off[r] : 0;
+  p.h1 = PEN ? a.off[r + 1] : 0;
   p.u = p.u >= 0.0f ? p.u : 0.0f;
 
   Row<Tin> row;
@@ -1409,21 +1528,25 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
   row.nblk = (a.V + kBlk - 1) / kBlk;
   row.nstripes = (row.nblk + kThreads - 1) / kThreads;
   row.vec = (reinterpret_cast<uintptr_t>(row.p) & 15u) == 0;
-  row.nexc = ne;
+  row.nexc = 0;
   row.bm = nullptr;  // built in LDS by the path that masks penalised positions
-  row.eid = f.eid;   // the fast path reads the penalised ids from LDS
+  row.eid = f.eid;   // the fast path keeps the penalised ids and values in LDS
   row.eval = f.eval;
   GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
   if constexpr (sizeof(Tin) == 2) {
-    if (p.T > 0.0f && ne <= kExcCap) {
-      if (fast_row(a, row, p, big, f, g.srch, ne)) return;
+    if (p.T > 0.0f) {
+      if (fast_row<PEN>(a, row, p, big, f, g.srch)) return;
+      lds_barrier();  // (every thread is done with the fast path's LDS)
     }
   }
-  // the generic path reads the penalised ids from the workspace the penalty pass wrote
+  // the generic path: the penalty pass writes the penalised ids and values to the workspace
+  int ne = 0;
+  if (PEN) ne = static_cast<int>(penalty_phase<Tin>(a.pen, r, big, f.red32, ExcCache{nullptr, nullptr, 0}));
   __syncthreads();
   if (ne > 0) {
-    row.eid = a.ws.exc_id + a.off[r];
-    row.eval = a.ws.exc_val + a.off[r];
+    row.nexc = ne;
+    row.eid = a.ws.exc_id + p.h0;
+    row.eval = a.ws.exc_val + p.h0;
   }
   generic_row(a, row, p, g);
 }
