@@ -18,6 +18,16 @@ typedef unsigned long long u64;
 typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ ushort2_t ones2() { return ushort2_t{1, 1}; }
 
+// ---- global pointers --------------------------------------------------------------------------
+// Pointers that reach a kernel inside an argument struct are generic: loads through them compile
+// to flat loads, which count against both the vector-memory and the LDS wait counters, so every
+// LDS wait would also wait for the row loads in flight. Casting through the global address
+// space lets the compiler emit global (and, for uniform addresses, scalar) loads instead.
+template <class T>
+__device__ __forceinline__ T* as_global(T* p) {
+  return (T*)((__attribute__((address_space(1))) T*)p);
+}
+
 // ---- ordered keys ---------------------------------------------------------------------------
 // A 32-bit key whose unsigned order is the numeric order of fp32 values, with -0.0 folded onto
 // +0.0 (they compare equal) and every NaN mapped above +inf.

@@ -37,6 +37,27 @@ struct PenaltyArgs {
   int64_t counts_stride;
 };
 
+// The same arguments with every pointer cast to the global address space.
+__device__ __forceinline__ Workspace globalized(Workspace w) {
+  w.n_exc = as_global(w.n_exc);
+  w.exc_id = as_global(w.exc_id);
+  w.exc_val = as_global(w.exc_val);
+  w.exc_cnt = as_global(w.exc_cnt);
+  return w;
+}
+
+__device__ __forceinline__ PenaltyArgs globalized(PenaltyArgs a) {
+  a.logits = as_global(a.logits);
+  a.rep = as_global(a.rep);
+  a.pres = as_global(a.pres);
+  a.freq = as_global(a.freq);
+  a.hist = as_global(a.hist);
+  a.off = as_global(a.off);
+  a.ws = globalized(a.ws);
+  a.dense_counts = as_global(a.dense_counts);
+  return a;
+}
+
 __device__ __forceinline__ float apply_penalty(float x, int c, float rep, float pres, float freq) {
   // Compiled with -ffp-contract=off: every operation below rounds on its own.
   x = (x > 0.0f) ? x / rep : x * rep;
@@ -79,7 +100,7 @@ constexpr int kHistCache = kChunk - kCountWords - 1024;
 // The penalised values of exceptions [0, n) whose (id, count) pairs are in the workspace, or for
 // e < staged in LDS: all loads of a thread are issued before any value is computed.
 template <class Tin>
-__device__ void gather_values(const PenaltyArgs& a, const Tin* row, int h0, uint32_t n, const int2* stage,
+__device__ __forceinline__ void gather_values(const PenaltyArgs& a, const Tin* row, int h0, uint32_t n, const int2* stage,
                               uint32_t staged, float rep, float pres, float freq, const ExcCache& ec) {
   constexpr int kU = 4;
   for (uint32_t e0 = threadIdx.x; e0 < n; e0 += kU * kThreads) {
@@ -121,7 +142,7 @@ __device__ void gather_values(const PenaltyArgs& a, const Tin* row, int h0, uint
 // needs a __syncthreads() first) and, up to ec.cap of them, to `ec` in LDS (visible on return).
 // With dense_counts set, also writes every id's count. Returns the number of exceptions.
 template <class Tin>
-__device__ uint32_t penalty_phase(const PenaltyArgs& a, int r, uint32_t* lds, uint32_t* red, ExcCache ec) {
+__device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, uint32_t* lds, uint32_t* red, ExcCache ec) {
   const int tid = threadIdx.x;
   const int V = a.V;
   const int h0 = a.off ? a.off[r] : 0;
@@ -268,7 +289,8 @@ __device__ uint32_t penalty_phase(const PenaltyArgs& a, int r, uint32_t* lds, ui
 }
 
 template <class Tin>
-__global__ __launch_bounds__(kThreads) void k_penalty_prep(PenaltyArgs a) {
+__global__ __launch_bounds__(kThreads) void k_penalty_prep(PenaltyArgs a_) {
+  const PenaltyArgs a = globalized(a_);
   __shared__ uint32_t cnt[kChunk];
   __shared__ uint32_t red[kWaves];
   penalty_phase<Tin>(a, blockIdx.x, cnt, red, ExcCache{nullptr, nullptr, 0});
@@ -276,8 +298,10 @@ __global__ __launch_bounds__(kThreads) void k_penalty_prep(PenaltyArgs a) {
 
 // Penalised fp32 logits of every row: the bulk copy first, then the exceptions over it.
 template <class Tin>
-__global__ __launch_bounds__(kThreads) void k_penalized_out(PenaltyArgs a, float* out,
+__global__ __launch_bounds__(kThreads) void k_penalized_out(PenaltyArgs a_, float* out_,
                                                             int64_t out_stride) {
+  const PenaltyArgs a = globalized(a_);
+  float* out = as_global(out_);
   const int r = blockIdx.x;
   const Tin* row = static_cast<const Tin*>(a.logits) + static_cast<int64_t>(r) * a.stride;
   float* o = out + static_cast<int64_t>(r) * out_stride;

@@ -85,6 +85,16 @@ constexpr int kMaxL = 128;     // penalised values in one chunk the fast path ca
 constexpr int kExcCap = 2048;  // penalised ids per row the fast path keeps in LDS
 constexpr int kMatchWords = 8192;  // LDS words of the draw's per-block count cells (V <= 262144)
 
+// A row's parameters, as 32-bit words in this order (absent columns take the defaults below).
+struct RowParams {
+  float T, tp, mp, u;
+  int K, draft;
+  float rep, pres, freq;  // penalties
+  int h0, h1;             // the row's history: hist_ids[h0, h1)
+};
+constexpr int kParamWords = 11;
+static_assert(sizeof(RowParams) == 4 * kParamWords, "RowParams is 32-bit words");
+
 struct FastSmem {
   // ccnt, cmass and eval also hold the history's hash table while the row's histogram is built
   uint32_t ccnt[kThreads];  // per-chunk element counts
@@ -102,7 +112,52 @@ struct FastSmem {
   u64 sq[8];
   int si[8];
   uint32_t hfail;  // the history's hash table overflowed a probe sequence
+  RowParams prm;   // this row's parameters
 };
+
+// A load through an explicitly global pointer (never a flat load).
+template <class T>
+__device__ __forceinline__ T ld_global(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+
+// 16-byte block b of a bf16 row.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_block(const uint16_t* base, int b) {
+  const u32x4_t v = ld_global(reinterpret_cast<const u32x4_t*>(base + b * kBlk));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// defaults of the parameter words (RowParams order): T 1, top-p 1, min-p 0, u 0, top-k 0,
+// draft -1, repetition 1, presence 0, frequency 0, history [0, 0)
+__device__ const uint32_t kParamDefaults[16] = {0x3F800000u, 0x3F800000u, 0u, 0u, 0u, 0xFFFFFFFFu, 0x3F800000u,
+                                                0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+
+// Parameter word w of row r (w >= kParamWords: a default, unused): every column is loaded
+// (uniform addresses, one load each) and the lane picks its word; selecting the column per lane
+// instead would index the argument struct, which then has to live in scratch memory.
+template <bool PEN>
+__device__ __forceinline__ uint32_t param_word(const SampleArgs& a, int r, int w) {
+  auto col = [&](const void* c, int i, int d) -> uint32_t {
+    return ld_global(c ? static_cast<const uint32_t*>(c) + i : &kParamDefaults[d]);
+  };
+  uint32_t v[kParamWords];
+  v[0] = col(a.temp, r, 0);
+  v[1] = col(a.topp, r, 1);
+  v[2] = col(a.minp, r, 2);
+  v[3] = col(a.u, r, 3);
+  v[4] = col(a.topk, r, 4);
+  v[5] = col(a.draft, r, 5);
+  v[6] = col(PEN ? a.pen.rep : nullptr, r, 6);
+  v[7] = col(PEN ? a.pen.pres : nullptr, r, 7);
+  v[8] = col(PEN ? a.pen.freq : nullptr, r, 8);
+  v[9] = col(PEN ? a.off : nullptr, r, 9);
+  v[10] = col(PEN ? a.off : nullptr, r + 1, 10);
+  uint32_t x = 0;
+#pragma unroll
+  for (int k = 0; k < kParamWords; ++k) x = w == k ? v[k] : x;
+  return x;
+}
 
 // ---- the fast path's history count ----------------------------------------------------------
 // A history of at most kFastMaxL ids is counted in a kFastSlots-word LDS hash table over
@@ -297,7 +352,7 @@ __device__ uint32_t bisect_key(uint32_t lo, uint32_t hi, P pred) {
 // First element index (ascending id) where the running count of w(x, id) (0 or 1) exceeds
 // `target` (clamped to total - 1). Returns -1 when no element has w = 1.
 template <class Tin, class W>
-__device__ __noinline__ int find_first(const Row<Tin>& row, W wf, u64 target, Search& s) {
+__device__ __forceinline__ int find_first(const Row<Tin>& row, W wf, u64 target, Search& s) {
   const int tid = threadIdx.x;
   const int wv = tid / kWave;
   // 1. per-(wave, stripe) counts, four stripes' loads in flight per thread
@@ -610,17 +665,11 @@ struct Kept {
   }
 };
 
-struct RowParams {
-  float T, tp, mp, u;
-  int K, draft;
-  float rep, pres, freq;  // penalties
-  int h0, h1;             // the row's history: hist_ids[h0, h1)
-};
 
 // Greedy rows and rows whose scaled logits are not all finite: a point mass. Shared by both
 // paths; returns true when the row is such a row (and sets k.point).
 template <class Tin>
-__device__ bool degenerate(const Row<Tin>& row, const RowParams& p, uint32_t mkey, int imax, float mz,
+__device__ __forceinline__ bool degenerate(const Row<Tin>& row, const RowParams& p, uint32_t mkey, int imax, float mz,
                            Search& s, Kept& k) {
   if (!(p.T > 0.0f) || mkey == 0xFFFFFFFFu) {
     k.point = imax;  // greedy (sampler.py:70-71), or a NaN logit: its first index
@@ -696,7 +745,7 @@ __device__ __forceinline__ void resolve_idr(const SampleArgs& a, const Row<Tin>&
 
 // ---- generic path -----------------------------------------------------------------------------
 template <class Tin>
-__device__ __noinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g) {
+__device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g) {
   const int V = row.V;
   Search& s = g.srch;
   if (row.nexc > 0) build_bitmap(row, reinterpret_cast<uint32_t*>(&g) + kBitmapOffset);
@@ -1040,7 +1089,8 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
 #pragma unroll
     for (int k = 0; k < kExcCap / kThreads; ++k) {
       const int e = tid + k * kThreads;
-      orig[k] = e < ne ? base[f.eid[e]] : 0u;
+      const int id = f.eid[e < ne ? e : 0];
+      orig[k] = ld_global(base + (e < ne ? id : 0));
     }
     // zero 16-bit halves of x, counted
     auto z2 = [](uint32_t x) -> uint32_t { return ((x & 0xFFFFu) == 0u ? 1u : 0u) + (x < 0x10000u ? 1u : 0u); };
@@ -1048,23 +1098,21 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     // rolling prefetch over blocks nfull - 1 - i, i = tid + (D * round + k) * kThreads
     constexpr int D = 4;
     uint4 d[D];
+    if (nfull > 0) {
 #pragma unroll
-    for (int k = 0; k < D; ++k) {
-      const int i = tid + k * kThreads;
-      d[k] = i < nfull ? *reinterpret_cast<const uint4*>(base + (nfull - 1 - i) * kBlk) : make_uint4(0, 0, 0, 0);
+      for (int k = 0; k < D; ++k) d[k] = ld_block(base, nfull - 1 - min(tid + k * kThreads, nfull - 1));
     }
-    for (int i0 = tid; i0 < nfull; i0 += D * kThreads) {
+    const int rounds = (nfull + D * kThreads - 1) / (D * kThreads);
+    for (int it = 0; it < rounds; ++it) {
 #pragma unroll
       for (int k = 0; k < D; ++k) {
-        const int i = i0 + k * kThreads;
-        if (i >= nfull) break;
+        const int i = tid + (it * D + k) * kThreads;
         const uint4 w = d[k];
-        const int in = i + D * kThreads;
-        if (in < nfull) d[k] = *reinterpret_cast<const uint4*>(base + (nfull - 1 - in) * kBlk);
         uint32_t c = z2(w.x ^ pat) + z2(w.y ^ pat) + z2(w.z ^ pat) + z2(w.w ^ pat);
         if (t16b != t16) c += z2(w.x ^ patb) + z2(w.y ^ patb) + z2(w.z ^ patb) + z2(w.w ^ patb);
+        d[k] = ld_block(base, nfull - 1 - min(i + D * kThreads, nfull - 1));
         // block b is cell b (b = stripe * kThreads + thread), written by the one thread reading it
-        cells[nfull - 1 - i] = static_cast<uint8_t>(c);
+        if (i < nfull) cells[nfull - 1 - i] = static_cast<uint8_t>(c);
       }
     }
     lds_barrier();
@@ -1148,51 +1196,57 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   return res;
 }
 
-// The bf16 fast path. Returns false (before writing any output) when the row needs the generic
-// path: a history longer than kFastMaxL or with more than kExcCap distinct ids, a key count past
-// 65535, or a chunk with more than kMaxL penalised values. `srch` and the match list alias
+// The bf16 fast path (every temperature: T <= 0 is greedy). Returns false (before writing any
+// output) when the row needs the generic path: a history longer than kFastMaxL or with more
+// than kExcCap distinct ids, a key count past 65535, or a chunk with more than kMaxL penalised
+// values. `srch` and the match list alias
 // `hist`: they are used only once the histogram is no longer read.
 //
 // With PEN the row's history is counted here, between the first rounds of the histogram pass,
 // and the penalised ids' original values are gathered while the pass streams the row; the
 // penalised ids and values end in f.eid / f.eval.
+//
+// `pw` is parameter word tid of the row (threads below kParamWords), loaded by the caller; the
+// parameters reach f.prm (read through `p`) once the row's first loads are issued.
+//
+// Loads here sit outside divergent branches (a lane past the end rereads a valid block whose
+// data it ignores): a load inside one needs a copy at the join, and that copy waits for every
+// load in flight.
 template <bool PEN>
 __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row, const RowParams& p, uint32_t* hist,
-                                         FastSmem& f, Search& srch) {
+                                         FastSmem& f, Search& srch, uint32_t pw) {
   const int tid = threadIdx.x;
   const int V = row.V;
-  const float T = p.T;
-  const int L = PEN ? p.h1 - p.h0 : 0;
-  const bool pen = PEN && L > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
-  if (pen && L > kFastMaxL) return false;
   // ---- 1. histogram of every key, then the penalised tokens' original keys taken out ----------
   // (u16 halves of a word wrap and borrow exactly: only the final counts must stay below 2^16)
   const uint16_t* base = row.p;
   const int nfull = row.vec ? V / kBlk : 0;  // blocks read as one 16-byte load
   // A rolling prefetch: slot k of d holds block tid + (D * round + k) * kThreads and is reloaded
-  // for the next round as soon as it is consumed, so D loads per thread are always in flight.
+  // for the next round as soon as it is consumed (into the same registers: loading before the
+  // old value is consumed would need a copy at the loop's end, which waits for every load).
   constexpr int D = 4;
   uint4 d[D];
+  if (nfull > 0) {
 #pragma unroll
-  for (int k = 0; k < D; ++k) {
-    const int b = tid + k * kThreads;
-    d[k] = b < nfull ? *reinterpret_cast<const uint4*>(base + b * kBlk) : make_uint4(0, 0, 0, 0);
+    for (int k = 0; k < D; ++k) d[k] = ld_block(base, min(tid + k * kThreads, nfull - 1));
   }
-  uint32_t hid[kFastHistPer];
-  if (pen) {
-    const int32_t* h = a.pen.hist + p.h0;
-#pragma unroll
-    for (int k = 0; k < kFastHistPer; ++k) {
-      const int i = tid + k * kThreads;
-      hid[k] = i < L ? static_cast<uint32_t>(h[i]) : kEmpty;  // ids outside [0, V) are skipped
-    }
-  }
+  if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
   uint32_t* htab = fast_htab(f);
   for (int i = tid; i < kChunk / 4; i += kThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0, 0, 0, 0);
-  if (pen) reinterpret_cast<uint4*>(htab)[tid] = make_uint4(kEmpty, kEmpty, kEmpty, kEmpty);
+  reinterpret_cast<uint4*>(htab)[tid] = make_uint4(kEmpty, kEmpty, kEmpty, kEmpty);
   static_assert(kFastSlots == 4 * kThreads, "one uint4 of slots per thread");
   if (tid == 0) f.hfail = 0;
   lds_barrier();
+  const float T = p.T;
+  const int L = PEN ? p.h1 - p.h0 : 0;
+  const bool on = PEN && L > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
+  const bool pen = on && L <= kFastMaxL;  // a longer history is counted by the generic path
+  uint32_t hid[kFastHistPer];  // history positions tid + k * kThreads (clamped to the last)
+  if (pen) {
+    const int32_t* h = a.pen.hist + p.h0;
+#pragma unroll
+    for (int k = 0; k < kFastHistPer; ++k) hid[k] = static_cast<uint32_t>(ld_global(h + min(tid + k * kThreads, L - 1)));
+  }
   auto add2 = [&](uint32_t w) {
     // ordered keys of both halves at once: xor with (sign ? 0xFFFF : 0x8000)
     const uint32_t s2 = (w >> 15) & 0x00010001u;
@@ -1202,16 +1256,17 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     atomicAdd(&hist[khi >> 1], 1u << ((khi & 1u) << 4));
   };
   // the history: stage 0 inserts this thread's ids, stage 1 compacts the table (thread t keeps
-  // slots 4t .. 4t + 3 in sl, their ids' original values in og) and gathers the originals
+  // slots 4t .. 4t + 3 in sl); the ids' original values are gathered after the pass (a load
+  // here would be carried round the loop by a copy that waits for the row loads in flight)
   int stage = pen ? 0 : 2;
-  uint32_t sl[4] = {kEmpty, kEmpty, kEmpty, kEmpty}, og[4] = {0u, 0u, 0u, 0u};
+  uint32_t sl[4] = {kEmpty, kEmpty, kEmpty, kEmpty};
   uint32_t e0 = 0, nexc = 0;
   auto pen_step = [&]() {
     if (stage == 0) {
       bool ok = true;
 #pragma unroll
-      for (int k = 0; k < kFastHistPer; ++k)
-        if (hid[k] < static_cast<uint32_t>(V)) ok = fast_insert(htab, hid[k]) && ok;
+      for (int k = 0; k < kFastHistPer; ++k)  // (ids outside [0, V) are skipped)
+        if (tid + k * kThreads < L && hid[k] < static_cast<uint32_t>(V)) ok = fast_insert(htab, hid[k]) && ok;
       if (!ok) f.hfail = 1;
     } else {
       lds_barrier();
@@ -1224,8 +1279,6 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
 #pragma unroll
       for (int k = 0; k < 4; ++k) n += sl[k] != kEmpty ? 1u : 0u;
       e0 = block_excl_scan<uint32_t>(n, f.red32, &nexc);  // (its barriers end every read of htab)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) og[k] = sl[k] != kEmpty ? base[sl[k] >> 13] : 0u;
     }
     ++stage;
   };
@@ -1235,14 +1288,12 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     for (int k = 0; k < D; ++k) {
       const int b = tid + (it * D + k) * kThreads;
       if (b < nfull) {
-        const uint4 w = d[k];
-        const int bn = b + D * kThreads;
-        if (bn < nfull) d[k] = *reinterpret_cast<const uint4*>(base + bn * kBlk);
-        add2(w.x);
-        add2(w.y);
-        add2(w.z);
-        add2(w.w);
+        add2(d[k].x);
+        add2(d[k].y);
+        add2(d[k].z);
+        add2(d[k].w);
       }
+      d[k] = ld_block(base, min(b + D * kThreads, nfull - 1));
     }
     if (stage < 2) {  // (uniform: `it` and `stage` are the same in every thread)
       pen_step();
@@ -1253,6 +1304,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     pen_step();
     if (stage == 2 && (f.hfail || nexc > static_cast<uint32_t>(kExcCap))) return false;
   }
+  if (on && !pen) return false;
+  uint32_t og[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) og[k] = ld_global(base + (sl[k] != kEmpty ? sl[k] >> 13 : 0u));
   // the rest: a ragged tail, or every element of an unaligned row
   for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
     const uint32_t ko = ok16(base[i]);
@@ -1358,11 +1413,12 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   const float xmax = val_of(mkey);
   const float mz = xmax / T;
   Kept k;
-  if (nnan || mz != mz || mz == INFINITY || mz == -INFINITY) {
+  if (nnan || !(T > 0.0f) || mz != mz || mz == INFINITY || mz == -INFINITY) {
     // the histogram is dead: the id searches use its memory
     if (ne > 0) build_bitmap(row, hist + kBitmapOffset);
-    // point rows: the first NaN, the first +inf z, or index 0 (all -inf)
+    // point rows: the first NaN, the first max (greedy), the first +inf z, or index 0 (all -inf)
     if (nnan) k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
+    else if (!(T > 0.0f)) k.point = find_first(row, [&](float x, int) -> u64 { return x == xmax; }, 0ull, srch);
     else if (!degenerate(row, p, mkey, 0, mz, srch, k)) k.point = 0;
     finish(a, row, p, mz, k, 0, &srch.vslot);
     return true;
@@ -1460,7 +1516,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   float vd = 0.0f;
   u64 j = 0;
   if (!a.out_probs) {
-    const u64 td0 = static_cast<u64>(static_cast<double>(p.u) * static_cast<double>(k.S));
+    const float u = p.u >= 0.0f ? p.u : 0.0f;
+    const u64 td0 = static_cast<u64>(static_cast<double>(u) * static_cast<double>(k.S));
     const u64 td = td0 < k.S ? td0 : k.S - 1;
     if (k.has_cut && td >= k.mabove_c && k.qc > 0) {
       vd = k.vc;
@@ -1499,8 +1556,26 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   return true;
 }
 
+__device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
+  a.logits = as_global(a.logits);
+  a.temp = as_global(a.temp);
+  a.topk = as_global(a.topk);
+  a.topp = as_global(a.topp);
+  a.minp = as_global(a.minp);
+  a.u = as_global(a.u);
+  a.draft = as_global(a.draft);
+  a.out_ids = as_global(a.out_ids);
+  a.out_dprob = as_global(a.out_dprob);
+  a.out_probs = as_global(a.out_probs);
+  a.ws = globalized(a.ws);
+  a.off = as_global(a.off);
+  a.pen = globalized(a.pen);
+  return a;
+}
+
 template <class Tin, bool PEN>
-__global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
+__global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
+  const SampleArgs a = globalized(a_);
   // 128 KB: the key histogram (or the generic path's penalty counts), then the id-search /
   // radix scratch
   __shared__ __align__(16) uint32_t big[kChunk];
@@ -1508,19 +1583,10 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
   static_assert(sizeof(GenericSmem) <= sizeof(uint32_t) * kBitmapOffset, "scratch must fit below the bitmap");
   static_assert(kMatchOffset + kMatchWords <= kChunk, "count cells must fit");
   const int r = blockIdx.x;
-  RowParams p;
-  p.T = a.temp ? a.temp[r] : 1.0f;
-  p.K = a.topk ? a.topk[r] : 0;
-  p.tp = a.topp ? a.topp[r] : 1.0f;
-  p.mp = a.minp ? a.minp[r] : 0.0f;
-  p.u = a.u ? a.u[r] : 0.0f;
-  p.draft = a.draft ? a.draft[r] : -1;
-  p.rep = PEN && a.pen.rep ? a.pen.rep[r] : 1.0f;
-  p.pres = PEN && a.pen.pres ? a.pen.pres[r] : 0.0f;
-  p.freq = PEN && a.pen.freq ? a.pen.freq[r] : 0.0f;
-  p.h0 = PEN ? a.off[r] : 0;
-  p.h1 = PEN ? a.off[r + 1] : 0;
-  p.u = p.u >= 0.0f ? p.u : 0.0f;
+  const int tid = threadIdx.x;
+  // the row's parameters: lane w of wave 0 loads word w, all in one vector load
+  uint32_t pw = 0;
+  if (tid < kWave) pw = param_word<PEN>(a, r, tid);
 
   Row<Tin> row;
   row.p = static_cast<const Tin*>(a.logits) + static_cast<int64_t>(r) * a.stride;
@@ -1534,11 +1600,14 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a) {
   row.eval = f.eval;
   GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
   if constexpr (sizeof(Tin) == 2) {
-    if (p.T > 0.0f) {
-      if (fast_row<PEN>(a, row, p, big, f, g.srch)) return;
-      lds_barrier();  // (every thread is done with the fast path's LDS)
-    }
+    if (fast_row<PEN>(a, row, f.prm, big, f, g.srch, pw)) return;
+    lds_barrier();  // (every thread is done with the fast path's LDS; f.prm is set)
+  } else {
+    if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
+    lds_barrier();
   }
+  RowParams p = f.prm;
+  p.u = p.u >= 0.0f ? p.u : 0.0f;
   // the generic path: the penalty pass writes the penalised ids and values to the workspace
   int ne = 0;
   if (PEN) ne = static_cast<int>(penalty_phase<Tin>(a.pen, r, big, f.red32, ExcCache{nullptr, nullptr, 0}));
