@@ -69,33 +69,80 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // ---- wave primitives --------------------------------------------------------------------------
+// Cross-lane steps use DPP (data-parallel primitives: a VALU operand read from another lane of
+// the same 16-lane row, or broadcast across rows) rather than ds_bpermute shuffles, which go
+// through the LDS crossbar and cost a round trip each.
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+namespace dpp {
+constexpr int kXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kShr1 = 0x111;        // row_shr:1 (+ n - 1 for row_shr:n)
+constexpr int kMirror = 0x140;      // row_mirror: lane 15 - i of the row
+constexpr int kHalfMirror = 0x141;  // row_half_mirror: lane 7 - i of the half-row
+constexpr int kBcast15 = 0x142;     // lane 15 of each row into the next row (row_mask picks rows)
+constexpr int kBcast31 = 0x143;     // lane 31 into rows 2 and 3
+
+// Lane-moved copy of x; lanes the control leaves without a source (or rows outside row_mask)
+// read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t mov(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROW_MASK, 0xF, true));
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ u64 mov(u64 x) {
+  const uint32_t lo = mov<CTRL, ROW_MASK>(static_cast<uint32_t>(x));
+  const uint32_t hi = mov<CTRL, ROW_MASK>(static_cast<uint32_t>(x >> 32));
+  return (static_cast<u64>(hi) << 32) | lo;
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int mov(int x) {
+  return static_cast<int>(mov<CTRL, ROW_MASK>(static_cast<uint32_t>(x)));
+}
+
+// Lane 63's value, in every lane.
+__device__ __forceinline__ uint32_t last(uint32_t x) { return __builtin_amdgcn_readlane(x, 63); }
+__device__ __forceinline__ int last(int x) { return __builtin_amdgcn_readlane(x, 63); }
+__device__ __forceinline__ u64 last(u64 x) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), 63);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(x >> 32), 63);
+  return (static_cast<u64>(hi) << 32) | lo;
+}
+
+// Reduction with an associative, commutative op: every 16-lane row ends with its row total in
+// all lanes, then rows 1 and 3 fold in rows 0 and 2, then row 3 folds in rows 0 + 1.
+template <class T, class Op>
+__device__ __forceinline__ T reduce(T v, Op op) {
+  v = op(v, mov<kXor1>(v));
+  v = op(v, mov<kXor2>(v));
+  v = op(v, mov<kHalfMirror>(v));
+  v = op(v, mov<kMirror>(v));
+  v = op(v, mov<kBcast15, 0xA>(v));
+  v = op(v, mov<kBcast31, 0xC>(v));
+  return last(v);
+}
+}  // namespace dpp
+
+// Sum over the wave's 64 lanes, in every lane (32/64-bit integers).
 template <class T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  return dpp::reduce(v, [](T a, T b) { return a + b; });
 }
 
 __device__ __forceinline__ u64 wave_max_u64(u64 v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    u64 w = __shfl_xor(v, o);
-    v = w > v ? w : v;
-  }
-  return v;
+  return dpp::reduce(v, [](u64 a, u64 b) { return a > b ? a : b; });
 }
 
-// Inclusive prefix sum over the wave's lanes.
+// Inclusive prefix sum over the wave's lanes (32/64-bit integers): Hillis-Steele steps of 1, 2,
+// 4 and 8 lanes inside each 16-lane row, then the row carries.
 template <class T>
 __device__ __forceinline__ T wave_incl_scan(T v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    T w = __shfl_up(v, o);
-    if (l >= o) v += w;
-  }
+  v += dpp::mov<dpp::kShr1>(v);
+  v += dpp::mov<dpp::kShr1 + 1>(v);
+  v += dpp::mov<dpp::kShr1 + 3>(v);
+  v += dpp::mov<dpp::kShr1 + 7>(v);
+  v += dpp::mov<dpp::kBcast15, 0xA>(v);
+  v += dpp::mov<dpp::kBcast31, 0xC>(v);
   return v;
 }
 

@@ -306,7 +306,7 @@ __device__ __forceinline__ void hist_count(uint32_t* hist, uint32_t digit, bool 
   for (int it = 0; it < 4; ++it) {
     if (!active) break;
     const int leader = __ffsll(static_cast<long long>(active)) - 1;
-    const uint32_t d0 = __shfl(digit, leader);
+    const uint32_t d0 = __builtin_amdgcn_readlane(digit, leader);
     const u64 same = __ballot(valid && digit == d0);
     if (lane_id() == leader) atomicAdd(&hist[d0], static_cast<uint32_t>(__popcll(same)));
     if (digit == d0) valid = false;
@@ -321,7 +321,7 @@ __device__ __forceinline__ void hist_mass(uint32_t* hc, u64* hm, uint32_t digit,
   for (int it = 0; it < 4; ++it) {
     if (!active) break;
     const int leader = __ffsll(static_cast<long long>(active)) - 1;
-    const uint32_t d0 = __shfl(digit, leader);
+    const uint32_t d0 = __builtin_amdgcn_readlane(digit, leader);
     const bool mine = valid && digit == d0;
     const u64 same = __ballot(mine);
     const u64 s = wave_sum<u64>(mine ? q : 0ull);
@@ -392,7 +392,7 @@ __device__ __forceinline__ int find_first(const Row<Tin>& row, W wf, u64 target,
     if (j < row.nstripes)
       for (int w = 0; w < kWaves; ++w) t += s.cell[w][j];
     const u64 inc = wave_incl_scan<u64>(t);
-    const u64 total = __shfl(inc, kWave - 1);
+    const u64 total = dpp::last(inc);
     u64 tg = target;
     if (total > 0 && tg > total - 1) tg = total - 1;
     const bool hit = total > 0 && inc > tg && (inc - t) <= tg;
@@ -1044,8 +1044,9 @@ __device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, P pred
       const u64 hm = __ballot(ok);
       // the first probe that holds bounds the answer from above; the one before it from below
       const int first = hm ? __ffsll(static_cast<long long>(hm)) - 1 : 64;
-      const uint32_t nhi = first < 64 ? __shfl(probe, first) : hi;
-      const uint32_t nlo = first > 0 ? __shfl(probe, first - 1) + 1 : lo;
+      // (first comes from a ballot: the same in every lane, so the lanes are read directly)
+      const uint32_t nhi = first < 64 ? __builtin_amdgcn_readlane(probe, first) : hi;
+      const uint32_t nlo = first > 0 ? __builtin_amdgcn_readlane(probe, first - 1) + 1 : lo;
       lo = nlo;
       hi = nhi;
     }
