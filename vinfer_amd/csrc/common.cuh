@@ -50,7 +50,7 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 // ---- fixed-point mass of one value ------------------------------------------------------------
 // p~ = exp(z - m) in fp64 with z = fl32(x / T) (IEEE division), m the row's max z.
 __device__ __forceinline__ double ptilde(float x, float T, float mz) {
-  float z = x / T;
+  const float z = T == 1.0f ? x : x / T;  // (x / 1 is x: skip the division)
   return exp(static_cast<double>(z) - static_cast<double>(mz));
 }
 
@@ -144,6 +144,23 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
   v += dpp::mov<dpp::kBcast15, 0xA>(v);
   v += dpp::mov<dpp::kBcast31, 0xC>(v);
   return v;
+}
+
+// For every lane with `valid`, acc[key] op= v through `at(key, value)`, lanes sharing a key
+// combined first: one LDS atomic per distinct key in the wave instead of one per lane (keys
+// that many lanes share would otherwise serialise). All 64 lanes must be active.
+template <class T, class Op, class At>
+__device__ __forceinline__ void wave_grouped(uint32_t key, T v, bool valid, Op op, At at) {
+  u64 act = __ballot(valid);
+  while (act) {
+    const int leader = __ffsll(static_cast<long long>(act)) - 1;
+    const uint32_t k0 = __builtin_amdgcn_readlane(key, leader);
+    const bool mine = valid && key == k0;
+    const u64 same = __ballot(mine);
+    const T s = dpp::reduce(mine ? v : T(0), op);
+    if (lane_id() == leader) at(k0, s);
+    act &= ~same;
+  }
 }
 
 // ---- workgroup primitives (kThreads threads, all must call) ------------------------------------

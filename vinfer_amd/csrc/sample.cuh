@@ -95,7 +95,20 @@ struct RowParams {
 constexpr int kParamWords = 11;
 static_assert(sizeof(RowParams) == 4 * kParamWords, "RowParams is 32-bit words");
 
-struct FastSmem {
+// What wave 0 decides between the fast path's parallel phases (one LDS copy, read by all).
+struct FastPlan {
+  int status;  // kPlanFast, kPlanGeneric or kPlanPoint
+  uint32_t mkey, nnan;
+  float x0, mz;
+  // the kept set (Kept's fields) and the draw
+  float vc, vd;
+  int partial, has_cut;
+  uint32_t r;
+  u64 mabove_c, qc, S, j;
+};
+constexpr int kPlanFast = 0, kPlanGeneric = 1, kPlanPoint = 2;
+
+struct __align__(16) FastSmem {
   // ccnt, cmass and eval also hold the history's hash table while the row's histogram is built
   uint32_t ccnt[kThreads];  // per-chunk element counts
   u64 cmass[kThreads];      // per-chunk masses of elements >= x0
@@ -106,6 +119,7 @@ struct FastSmem {
   uint32_t binc[kWave];     // per-key counts / masses of penalised values inside that chunk
   u64 binm[kWave];
   uint32_t nl;
+  uint32_t pchunk[2];  // the chunks that hold penalised values lie in [pchunk[0], pchunk[1]]
   uint32_t red32[kWaves];
   u64 red64[2 * kWaves];
   uint32_t sk[8];
@@ -113,6 +127,8 @@ struct FastSmem {
   int si[8];
   uint32_t hfail;  // the history's hash table overflowed a probe sequence
   RowParams prm;   // this row's parameters
+  uint4 wp[kWaves];  // per-wave partials: count, NaNs, top chunk code, penalised max key
+  FastPlan plan;
 };
 
 // A load through an explicitly global pointer (never a flat load).
@@ -867,20 +883,25 @@ struct WalkResult {
   int ok;        // 0 if the chunk holds too many penalised values to resolve
 };
 
-// Resolve a value inside chunk c (all threads call; wave 0 walks). `above` is the count or mass
-// strictly above the chunk, `target` the 1-based rank (count) or the mass target. `ne` penalised
-// values are in f.eid / f.eval.
-__device__ __forceinline__ WalkResult walk_chunk(const uint32_t* hist, FastSmem& f, int ne, int c, int mode, u64 above,
-                                 double target, float x0, float T, float mz) {
-  const int tid = threadIdx.x;
-  if (tid < kWave) {
-    f.binc[tid] = 0;
-    f.binm[tid] = 0;
-  }
-  if (tid == 0) f.nl = 0;
-  lds_barrier();
-  // the chunk's penalised values
-  for (int e = tid; e < ne; e += kThreads) {
+__device__ __forceinline__ u64 readlane64(u64 x, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(x >> 32), lane);
+  return (static_cast<u64>(hi) << 32) | lo;
+}
+
+// Resolve a value inside chunk c, by the 64 lanes of one wave and no workgroup barrier (the
+// wave's LDS operations complete in order). `above` is the count or mass strictly above the
+// chunk, `target` the 1-based rank (count) or the mass target. `ne` penalised values are in
+// f.eid / f.eval. Every lane returns the result.
+__device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& f, int ne, int c, int mode, u64 above,
+                                                double target, float x0, float T, float mz) {
+  const int l = lane_id();
+  f.binc[l] = 0;
+  f.binm[l] = 0;
+  if (l == 0) f.nl = 0;
+  // the chunk's penalised values: per-key counts and masses, and a list of (key, mass)
+  const bool has_pen = static_cast<uint32_t>(c) >= f.pchunk[0] && static_cast<uint32_t>(c) <= f.pchunk[1];
+  for (int e = l; has_pen && e < ne; e += kWave) {
     const float x = f.eval[e];
     const uint32_t key = key_of(x);
     const uint32_t top = key >> 16;
@@ -896,7 +917,6 @@ __device__ __forceinline__ WalkResult walk_chunk(const uint32_t* hist, FastSmem&
       f.lq[i] = q;
     }
   }
-  lds_barrier();
   WalkResult res;
   res.ok = f.nl <= kMaxL;
   res.key = 0;
@@ -904,56 +924,47 @@ __device__ __forceinline__ WalkResult walk_chunk(const uint32_t* hist, FastSmem&
   res.q = 0;
   res.above = 0;
   if (!res.ok) return res;
-  if (tid < kWave) {
-    const int l = tid;
-    const uint32_t K = 65535u - 64u * static_cast<uint32_t>(c) - l;
-    const uint32_t cnt = hcount(hist, K);
-    const float v = val16(K);
-    const bool inb = mode == kWalkCount || v >= x0;
-    const uint32_t cb = inb ? cnt : 0u;
-    const u64 qb = (mode != kWalkCount && cb) ? mass_q(ptilde(v, T, mz)) : 0ull;
-    const uint32_t cl = cb + f.binc[l];
-    const u64 ml = (mode == kWalkCount ? static_cast<u64>(cl) : cb * qb + f.binm[l]);
-    const u64 inc = wave_incl_scan<u64>(ml);
-    const u64 ab = above + inc - ml;  // strictly above this key
-    bool hit;
-    if (mode == kWalkCount) hit = static_cast<double>(ab) < target && target <= static_cast<double>(ab + ml);
-    else if (mode == kWalkCutoff) hit = cl > 0 && static_cast<double>(ab) < target;
-    else hit = ml > 0 && static_cast<double>(ab) <= target && target < static_cast<double>(ab + ml);
-    const u64 hm = __ballot(hit);
-    const int lw = hm ? (mode == kWalkCutoff ? 63 - __clzll(static_cast<long long>(hm))
-                                             : __ffsll(static_cast<long long>(hm)) - 1)
-                      : 0;
-    if (l == lw) {
-      f.si[0] = l;
-      f.sk[0] = cb;
-      f.sq[0] = qb;
-      f.sq[1] = ab;
-      f.sk[1] = f.binc[l];
-    }
-  }
-  lds_barrier();
-  const int l = f.si[0];
   const uint32_t K = 65535u - 64u * static_cast<uint32_t>(c) - l;
-  const uint32_t cb = f.sk[0];
-  const u64 qb = f.sq[0];
-  const u64 ab = f.sq[1];
-  const uint32_t nx = f.sk[1];
-  const uint32_t bkey = key_of(val16(K));
+  const uint32_t cnt = hcount(hist, K);
+  const float v = val16(K);
+  const bool inb = mode == kWalkCount || v >= x0;
+  const uint32_t cb = inb ? cnt : 0u;
+  const u64 qb = (mode != kWalkCount && cb) ? mass_q(ptilde(v, T, mz)) : 0ull;
+  const uint32_t bl = f.binc[l];
+  const uint32_t cl = cb + bl;
+  const u64 ml = (mode == kWalkCount ? static_cast<u64>(cl) : cb * qb + f.binm[l]);
+  const u64 inc = wave_incl_scan<u64>(ml);
+  const u64 ab = above + inc - ml;  // strictly above this key
+  bool hit;
+  if (mode == kWalkCount) hit = static_cast<double>(ab) < target && target <= static_cast<double>(ab + ml);
+  else if (mode == kWalkCutoff) hit = cl > 0 && static_cast<double>(ab) < target;
+  else hit = ml > 0 && static_cast<double>(ab) <= target && target < static_cast<double>(ab + ml);
+  const u64 hm = __ballot(hit);
+  const int lw = hm ? (mode == kWalkCutoff ? 63 - __clzll(static_cast<long long>(hm))
+                                           : __ffsll(static_cast<long long>(hm)) - 1)
+                    : 0;
+  const uint32_t cbw = __builtin_amdgcn_readlane(cb, lw);
+  const u64 qbw = readlane64(qb, lw);
+  const u64 abw = readlane64(ab, lw);
+  const uint32_t nx = __builtin_amdgcn_readlane(bl, lw);
+  const uint32_t Kw = 65535u - 64u * static_cast<uint32_t>(c) - lw;
+  const uint32_t bkey = key_of(val16(Kw));
   if (nx == 0) {
     res.key = bkey;
-    res.n = cb;
-    res.q = qb;
-    res.above = ab;
-    lds_barrier();
+    res.n = cbw;
+    res.q = qbw;
+    res.above = abw;
     return res;
   }
-  // The key mixes its bf16 value with penalised values: walk its items in descending order.
-  if (tid == 0) {
+  // The key mixes its bf16 value with penalised values: lane 0 walks its items in descending
+  // order.
+  uint32_t rkey = bkey, rn = 0;
+  u64 rq = 0, rab = abw;
+  if (l == 0) {
     // move this key's penalised values to the front of the list, then sort them (descending)
     int n = 0;
     for (uint32_t i = 0; i < f.nl; ++i) {
-      if ((f.lkey[i] >> 16) == K) {
+      if ((f.lkey[i] >> 16) == Kw) {
         const uint32_t tk = f.lkey[n];
         const u64 tq = f.lq[n];
         f.lkey[n] = f.lkey[i];
@@ -966,21 +977,19 @@ __device__ __forceinline__ WalkResult walk_chunk(const uint32_t* hist, FastSmem&
     for (int i = 1; i < n; ++i) {
       const uint32_t kk = f.lkey[i];
       const u64 qq = f.lq[i];
-      int j = i - 1;
-      while (j >= 0 && f.lkey[j] < kk) {
-        f.lkey[j + 1] = f.lkey[j];
-        f.lq[j + 1] = f.lq[j];
-        --j;
+      int jj = i - 1;
+      while (jj >= 0 && f.lkey[jj] < kk) {
+        f.lkey[jj + 1] = f.lkey[jj];
+        f.lq[jj + 1] = f.lq[jj];
+        --jj;
       }
-      f.lkey[j + 1] = kk;
-      f.lq[j + 1] = qq;
+      f.lkey[jj + 1] = kk;
+      f.lq[jj + 1] = qq;
     }
-    // merge with the bulk value (cb members of mass qb each), walking distinct values
-    u64 acc = ab;
+    // merge with the bulk value (cbw members of mass qbw each), walking distinct values
+    u64 acc = abw;
     int ie = 0;
-    bool bulk_done = cb == 0;
-    uint32_t rkey = bkey, rn = 0;
-    u64 rq = 0, rab = ab;
+    bool bulk_done = cbw == 0;
     while (ie < n || !bulk_done) {
       uint32_t vkey;
       if (bulk_done) vkey = f.lkey[ie];
@@ -989,9 +998,9 @@ __device__ __forceinline__ WalkResult walk_chunk(const uint32_t* hist, FastSmem&
       uint32_t gn = 0;
       u64 gm = 0, gq = 0;
       if (!bulk_done && vkey == bkey) {
-        gn += cb;
-        gm += cb * qb;
-        gq = qb;
+        gn += cbw;
+        gm += cbw * qbw;
+        gq = qbw;
         bulk_done = true;
       }
       while (ie < n && f.lkey[ie] == vkey) {
@@ -1001,11 +1010,11 @@ __device__ __forceinline__ WalkResult walk_chunk(const uint32_t* hist, FastSmem&
         ++ie;
       }
       const u64 gw = mode == kWalkCount ? static_cast<u64>(gn) : gm;
-      bool hit;
-      if (mode == kWalkCount) hit = static_cast<double>(acc) < target && target <= static_cast<double>(acc + gw);
-      else if (mode == kWalkCutoff) hit = gn > 0 && static_cast<double>(acc) < target;
-      else hit = gw > 0 && static_cast<double>(acc) <= target && target < static_cast<double>(acc + gw);
-      if (hit) {
+      bool h;
+      if (mode == kWalkCount) h = static_cast<double>(acc) < target && target <= static_cast<double>(acc + gw);
+      else if (mode == kWalkCutoff) h = gn > 0 && static_cast<double>(acc) < target;
+      else h = gw > 0 && static_cast<double>(acc) <= target && target < static_cast<double>(acc + gw);
+      if (h) {
         rkey = vkey;
         rn = gn;
         rq = gq;
@@ -1014,60 +1023,63 @@ __device__ __forceinline__ WalkResult walk_chunk(const uint32_t* hist, FastSmem&
       }
       acc += gw;
     }
-    f.sk[2] = rkey;
-    f.sk[3] = rn;
-    f.sq[2] = rq;
-    f.sq[3] = rab;
   }
-  lds_barrier();
-  res.key = f.sk[2];
-  res.n = f.sk[3];
-  res.q = f.sq[2];
-  res.above = f.sq[3];
-  lds_barrier();
+  res.key = __builtin_amdgcn_readlane(rkey, 0);
+  res.n = __builtin_amdgcn_readlane(rn, 0);
+  res.q = readlane64(rq, 0);
+  res.above = readlane64(rab, 0);
   return res;
 }
 
-// Smallest key K in [lo, hi] with pred(val_of(K)) (pred(val_of(hi)) must hold), searched by
-// wave 0 with 64 probes per round; the result is returned to every thread.
+// Smallest key K in [lo, hi] with pred(val_of(K)) (pred(val_of(hi)) must hold; pred is false
+// below the answer and true from it on), by the 64 lanes of one wave: 64 probes per round.
+// `guess` is an estimate of the answer: the first round probes the 64 keys around it.
 template <class P>
-__device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, P pred, FastSmem& f) {
-  if (threadIdx.x < kWave) {
-    const uint32_t l = lane_id();
-    while (lo < hi) {
-      // probes lo + step*(l+1) - 1 for l = 0..63 split [lo, hi] into 64 pieces
-      const u64 span = static_cast<u64>(hi) - lo;
-      const u64 step = (span + 63) / 64;
-      const u64 probe64 = static_cast<u64>(lo) + step * (l + 1) - 1;
-      const uint32_t probe = probe64 < hi ? static_cast<uint32_t>(probe64) : hi;
-      const bool ok = pred(val_of(probe));
-      const u64 hm = __ballot(ok);
-      // the first probe that holds bounds the answer from above; the one before it from below
-      const int first = hm ? __ffsll(static_cast<long long>(hm)) - 1 : 64;
-      // (first comes from a ballot: the same in every lane, so the lanes are read directly)
-      const uint32_t nhi = first < 64 ? __builtin_amdgcn_readlane(probe, first) : hi;
-      const uint32_t nlo = first > 0 ? __builtin_amdgcn_readlane(probe, first - 1) + 1 : lo;
-      lo = nlo;
-      hi = nhi;
-    }
-    if (threadIdx.x == 0) f.sk[7] = hi;
+__device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, uint32_t guess, P pred) {
+  const uint32_t l = lane_id();
+  if (lo < hi) {
+    const uint32_t g = guess < lo ? lo : (guess > hi ? hi : guess);
+    const uint32_t g0 = g - lo >= 32u ? g - 32u : lo;  // probes g0 .. g0 + 63, clamped to hi
+    const u64 p64 = static_cast<u64>(g0) + l;
+    const uint32_t probe = p64 < hi ? static_cast<uint32_t>(p64) : hi;
+    const u64 hm = __ballot(pred(val_of(probe)));
+    const int first = hm ? __ffsll(static_cast<long long>(hm)) - 1 : 64;
+    // (first comes from a ballot: the same in every lane, so the lanes are read directly)
+    if (first < 64) hi = __builtin_amdgcn_readlane(probe, first);
+    if (first > 0) lo = __builtin_amdgcn_readlane(probe, first - 1) + 1;
+    if (first == 0) lo = lo < hi ? lo : hi;
   }
-  lds_barrier();
-  const uint32_t res = f.sk[7];
-  lds_barrier();
-  return res;
+  while (lo < hi) {
+    // probes lo + step*(l+1) - 1 for l = 0..63 split [lo, hi] into 64 pieces
+    const u64 span = static_cast<u64>(hi) - lo;
+    const u64 step = (span + 63) / 64;
+    const u64 probe64 = static_cast<u64>(lo) + step * (l + 1) - 1;
+    const uint32_t probe = probe64 < hi ? static_cast<uint32_t>(probe64) : hi;
+    const u64 hm = __ballot(pred(val_of(probe)));
+    // the first probe that holds bounds the answer from above; the one before it from below
+    const int first = hm ? __ffsll(static_cast<long long>(hm)) - 1 : 64;
+    const uint32_t nhi = first < 64 ? __builtin_amdgcn_readlane(probe, first) : hi;
+    const uint32_t nlo = first > 0 ? __builtin_amdgcn_readlane(probe, first - 1) + 1 : lo;
+    lo = nlo;
+    hi = nhi;
+  }
+  return hi;
 }
 
 // The id of the j-th (0-based, ascending id) token whose penalised value is vd: bulk positions
 // holding vd that are not penalised, and penalised ids whose new value is vd.
-// One pass counts, per 8-id block, the tokens whose bf16 value is vd into a byte per (stripe,
-// thread) cell (`cells`, nstripes * kThreads bytes of LDS); penalised positions then move their
-// cell by -1 (original value vd) or +1 (new value vd). A scan over the cells in id order finds
-// the block, and one thread the lane. Needs row.bm (penalised positions) built.
-// The pass reads the row's blocks last to first: the end of the row, read last by the
-// histogram pass, is the part most likely still in L2.
+// One pass counts, per 8-id block, the unpenalised tokens whose bf16 value is vd into a byte
+// cell (`cells`: cell b is block b, kThreads * cells_per(row) bytes of LDS); penalised ids whose
+// new value is vd add 1 to theirs. A scan over the cells in id order finds the block, and one
+// thread the lane. Needs row.bm (penalised positions) built when the row has any.
+// Thread t reads the blocks it read in the histogram pass (t + m * kThreads, and the tail
+// elements t + n * kThreads), last to first: the end of the row, read last, is the part most
+// likely still in L2. `mxk` is the largest key the thread saw there: a thread whose largest key
+// is below vd's holds no member and reads nothing.
+__device__ __forceinline__ int cells_per(const Row<uint16_t>& row) { return (row.nstripes + 3) & ~3; }
+
 __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, float vd, u64 j,
-                                            uint8_t* cells) {
+                                            uint8_t* cells, uint32_t mxk) {
   const int tid = threadIdx.x;
   const uint32_t vb = __float_as_uint(vd);
   const bool bf = (vb & 0xFFFFu) == 0u;  // vd is a bf16 value: bulk tokens can hold it
@@ -1075,78 +1087,78 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   const uint32_t t16b = vd == 0.0f ? (t16 ^ 0x8000u) : t16;  // -0.0 and +0.0 are one value
   const uint16_t* base = row.p;
   const int V = row.V;
-  const int ncells = row.nstripes * kThreads;
+  const int per = cells_per(row);  // cells per thread in the scan (a multiple of 4)
   uint32_t* cw = reinterpret_cast<uint32_t*>(cells);
-  for (int i = tid; i < ncells / 4; i += kThreads) cw[i] = 0;
+  for (int i = tid; i < per * kThreads / 4; i += kThreads) cw[i] = 0;
   lds_barrier();
-  auto cell_add = [&](int id, int delta) {
-    const int cidx = (id / kBlk / kThreads) * kThreads + (id / kBlk) % kThreads;
-    atomicAdd(&cw[cidx >> 2], static_cast<uint32_t>(delta) << (8 * (cidx & 3)));
+  auto cell_add = [&](int id, uint32_t delta) {
+    const int b = id / kBlk;
+    atomicAdd(&cw[b >> 2], delta << (8 * (b & 3)));
+  };
+  auto penalised = [&](int id) -> bool { return row.bm && ((row.bm[id / kBlk] >> (id % kBlk)) & 1u); };
+  // lanes of an 8-element block (4 words, 2 halves each) whose raw value is vd's
+  auto match8 = [&](uint4 w) -> uint32_t {
+    uint32_t m = 0;
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = ws[q] & 0xFFFFu, hi = ws[q] >> 16;
+      m |= ((lo == t16 || lo == t16b) ? 1u : 0u) << (2 * q);
+      m |= ((hi == t16 || hi == t16b) ? 1u : 0u) << (2 * q + 1);
+    }
+    return m;
   };
   if (bf) {
-    const uint32_t pat = t16 * 0x10001u, patb = t16b * 0x10001u;
-    // the penalised ids' original values (bulk blocks count them as they were)
-    uint32_t orig[kExcCap / kThreads];
-#pragma unroll
-    for (int k = 0; k < kExcCap / kThreads; ++k) {
-      const int e = tid + k * kThreads;
-      const int id = f.eid[e < ne ? e : 0];
-      orig[k] = ld_global(base + (e < ne ? id : 0));
-    }
-    // zero 16-bit halves of x, counted
-    auto z2 = [](uint32_t x) -> uint32_t { return ((x & 0xFFFFu) == 0u ? 1u : 0u) + (x < 0x10000u ? 1u : 0u); };
     const int nfull = row.vec ? V / kBlk : 0;
-    // rolling prefetch over blocks nfull - 1 - i, i = tid + (D * round + k) * kThreads
-    constexpr int D = 4;
-    uint4 d[D];
-    if (nfull > 0) {
+    const uint32_t ka = ok16(t16), kb = ok16(t16b);
+    const bool cand = mxk >= (ka < kb ? ka : kb);
+    // this thread's blocks tid + m * kThreads, m < nm, read from the last with a rolling
+    // prefetch (slot k: m = m0 - k)
+    const int nm = tid < nfull ? (nfull - 1 - tid) / kThreads + 1 : 0;
+    if (cand && nm > 0) {
+      constexpr int D = 4;
+      uint4 d[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) d[k] = ld_block(base, nfull - 1 - min(tid + k * kThreads, nfull - 1));
-    }
-    const int rounds = (nfull + D * kThreads - 1) / (D * kThreads);
-    for (int it = 0; it < rounds; ++it) {
+      for (int k = 0; k < D; ++k) d[k] = ld_block(base, tid + max(nm - 1 - k, 0) * kThreads);
+      for (int m0 = nm - 1; m0 >= 0; m0 -= D) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) {
-        const int i = tid + (it * D + k) * kThreads;
-        const uint4 w = d[k];
-        uint32_t c = z2(w.x ^ pat) + z2(w.y ^ pat) + z2(w.z ^ pat) + z2(w.w ^ pat);
-        if (t16b != t16) c += z2(w.x ^ patb) + z2(w.y ^ patb) + z2(w.z ^ patb) + z2(w.w ^ patb);
-        d[k] = ld_block(base, nfull - 1 - min(i + D * kThreads, nfull - 1));
-        // block b is cell b (b = stripe * kThreads + thread), written by the one thread reading it
-        if (i < nfull) cells[nfull - 1 - i] = static_cast<uint8_t>(c);
+        for (int k = 0; k < D; ++k) {
+          const int m = m0 - k;
+          const int b = tid + (m < 0 ? 0 : m) * kThreads;
+          uint32_t mask = match8(d[k]);
+          d[k] = ld_block(base, tid + max(m - D, 0) * kThreads);
+          if (row.bm) mask &= ~static_cast<uint32_t>(row.bm[b]);
+          // block b is written by the one thread reading it
+          if (m >= 0) cells[b] = static_cast<uint8_t>(__popc(mask));
+        }
       }
     }
-    lds_barrier();
     // the rest: a ragged tail, or every element of an unaligned row
-    for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
-      const uint32_t raw = base[i];
-      if (raw == t16 || raw == t16b) cell_add(i, 1);
-    }
-    // penalised positions whose original value was vd are not members
-#pragma unroll
-    for (int k = 0; k < kExcCap / kThreads; ++k) {
-      const int e = tid + k * kThreads;
-      if (e < ne && (orig[k] == t16 || orig[k] == t16b)) cell_add(f.eid[e], -1);
+    if (cand) {
+      for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
+        const uint32_t raw = base[i];
+        if ((raw == t16 || raw == t16b) && !penalised(i)) cell_add(i, 1u);
+      }
     }
   }
   // penalised ids whose new value is vd are members
   for (int e = tid; e < ne; e += kThreads)
-    if (f.eval[e] == vd) cell_add(f.eid[e], 1);
+    if (f.eval[e] == vd) cell_add(f.eid[e], 1u);
   lds_barrier();
-  // the cell holding the j-th member: per-thread sums of consecutive cells, then a scan
-  const int per = (ncells + kThreads - 1) / kThreads;
+  // the cell holding the j-th member: per-thread sums of `per` consecutive cells (4 at a time,
+  // one v_dot4_u32_u8 each), then a scan
   const int c0 = tid * per;
   uint32_t mine = 0;
-  for (int c = c0; c < c0 + per && c < ncells; ++c) mine += cells[c];
+  for (int c = c0; c < c0 + per; c += 4) mine = __builtin_amdgcn_udot4(cw[c >> 2], 0x01010101u, mine, false);
   uint32_t total;
   const uint32_t before = block_excl_scan<uint32_t>(mine, f.red32, &total);
   if (tid == 0) f.si[6] = -1;
   lds_barrier();
   if (total > 0 && j < total && before <= j && j < before + mine) {
     uint32_t acc = before;
-    for (int c = c0; c < c0 + per && c < ncells; ++c) {
+    for (int c = c0; c < c0 + per; ++c) {
       if (j < acc + cells[c]) {
-        f.si[5] = c;  // block id = (c / kThreads) * kThreads + c % kThreads = c
+        f.si[5] = c;  // the block
         f.sq[5] = acc;
         break;
       }
@@ -1171,12 +1183,15 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   lds_barrier();
   if (tid == 0) {
     const uint32_t pen = row.bm ? row.bm[b] : 0u;
+    const bool full = row.vec && (b + 1) * kBlk <= V;
+    const uint32_t bulk = full ? match8(ld_block(base, b)) : 0u;  // (one load for a full block)
     u64 acc = acc0;
     int found = b * kBlk;
     for (int i = 0; i < kBlk && b * kBlk + i < V; ++i) {
       const int id = b * kBlk + i;
       bool member;
       if ((pen >> i) & 1u) member = (f.sk[4] >> i) & 1u;
+      else if (full) member = (bulk >> i) & 1u;
       else {
         const uint32_t raw = base[id];
         member = raw == t16 || raw == t16b;
@@ -1237,6 +1252,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   reinterpret_cast<uint4*>(htab)[tid] = make_uint4(kEmpty, kEmpty, kEmpty, kEmpty);
   static_assert(kFastSlots == 4 * kThreads, "one uint4 of slots per thread");
   if (tid == 0) f.hfail = 0;
+  if (tid == 0) {
+    f.pchunk[0] = kThreads;
+    f.pchunk[1] = 0;
+  }
   lds_barrier();
   const float T = p.T;
   const int L = PEN ? p.h1 - p.h0 : 0;
@@ -1248,6 +1267,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
 #pragma unroll
     for (int k = 0; k < kFastHistPer; ++k) hid[k] = static_cast<uint32_t>(ld_global(h + min(tid + k * kThreads, L - 1)));
   }
+  // mx2: the largest key this thread has seen, per 16-bit half (the member search skips the
+  // threads whose largest key is below the value it looks for)
+  ushort2_t mx2 = ushort2_t{0, 0};
   auto add2 = [&](uint32_t w) {
     // ordered keys of both halves at once: xor with (sign ? 0xFFFF : 0x8000)
     const uint32_t s2 = (w >> 15) & 0x00010001u;
@@ -1255,36 +1277,17 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     const uint32_t klo = k2 & 0xFFFFu, khi = k2 >> 16;
     atomicAdd(&hist[klo >> 1], 1u << ((klo & 1u) << 4));
     atomicAdd(&hist[khi >> 1], 1u << ((khi & 1u) << 4));
+    mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(ushort2_t, k2));
   };
-  // the history: stage 0 inserts this thread's ids, stage 1 compacts the table (thread t keeps
-  // slots 4t .. 4t + 3 in sl); the ids' original values are gathered after the pass (a load
-  // here would be carried round the loop by a copy that waits for the row loads in flight)
-  int stage = pen ? 0 : 2;
+  // the history: after round 0 each thread inserts its ids; after round 1 the table is
+  // compacted (thread t keeps slots 4t .. 4t + 3 in sl) and the ids' original values are
+  // loaded, in flight through the remaining rounds. (Rounds 0 and 1 are peeled off the loop:
+  // a value defined inside a loop and carried round it takes a copy that waits for every load
+  // in flight.)
   uint32_t sl[4] = {kEmpty, kEmpty, kEmpty, kEmpty};
   uint32_t e0 = 0, nexc = 0;
-  auto pen_step = [&]() {
-    if (stage == 0) {
-      bool ok = true;
-#pragma unroll
-      for (int k = 0; k < kFastHistPer; ++k)  // (ids outside [0, V) are skipped)
-        if (tid + k * kThreads < L && hid[k] < static_cast<uint32_t>(V)) ok = fast_insert(htab, hid[k]) && ok;
-      if (!ok) f.hfail = 1;
-    } else {
-      lds_barrier();
-      const uint4 s4 = reinterpret_cast<const uint4*>(htab)[tid];
-      sl[0] = s4.x;
-      sl[1] = s4.y;
-      sl[2] = s4.z;
-      sl[3] = s4.w;
-      uint32_t n = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) n += sl[k] != kEmpty ? 1u : 0u;
-      e0 = block_excl_scan<uint32_t>(n, f.red32, &nexc);  // (its barriers end every read of htab)
-    }
-    ++stage;
-  };
-  const int rounds = (nfull + D * kThreads - 1) / (D * kThreads);
-  for (int it = 0; it < rounds; ++it) {
+  const int rounds = (nfull + D * kThreads - 1) / (D * kThreads);  // (uniform)
+  auto round = [&](int it) {
 #pragma unroll
     for (int k = 0; k < D; ++k) {
       const int b = tid + (it * D + k) * kThreads;
@@ -1296,23 +1299,40 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
       }
       d[k] = ld_block(base, min(b + D * kThreads, nfull - 1));
     }
-    if (stage < 2) {  // (uniform: `it` and `stage` are the same in every thread)
-      pen_step();
-      if (stage == 2 && (f.hfail || nexc > static_cast<uint32_t>(kExcCap))) return false;
-    }
+  };
+  if (rounds > 0) round(0);
+  if (pen) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < kFastHistPer; ++k)  // (ids outside [0, V) are skipped)
+      if (tid + k * kThreads < L && hid[k] < static_cast<uint32_t>(V)) ok = fast_insert(htab, hid[k]) && ok;
+    if (!ok) f.hfail = 1;
   }
-  while (stage < 2) {
-    pen_step();
-    if (stage == 2 && (f.hfail || nexc > static_cast<uint32_t>(kExcCap))) return false;
+  if (rounds > 1) round(1);
+  if (pen) {
+    lds_barrier();
+    const uint4 s4 = reinterpret_cast<const uint4*>(htab)[tid];
+    sl[0] = s4.x;
+    sl[1] = s4.y;
+    sl[2] = s4.z;
+    sl[3] = s4.w;
+    uint32_t n = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) n += sl[k] != kEmpty ? 1u : 0u;
+    e0 = block_excl_scan<uint32_t>(n, f.red32, &nexc);  // (its barriers end every read of htab)
+    if (f.hfail || nexc > static_cast<uint32_t>(kExcCap)) return false;
   }
   if (on && !pen) return false;
   uint32_t og[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) og[k] = ld_global(base + (sl[k] != kEmpty ? sl[k] >> 13 : 0u));
+  for (int it = 2; it < rounds; ++it) round(it);
   // the rest: a ragged tail, or every element of an unaligned row
+  uint32_t mxk = mx2.x > mx2.y ? mx2.x : mx2.y;
   for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
     const uint32_t ko = ok16(base[i]);
     atomicAdd(&hist[ko >> 1], 1u << ((ko & 1u) << 4));
+    mxk = ko > mxk ? ko : mxk;
   }
   // the penalised ids: original keys out of the histogram, penalised values into the list
   if (pen) {
@@ -1343,9 +1363,11 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     }
   }
   lds_barrier();
-  // ---- 2. per-chunk counts, the row max, NaNs, overflow --------------------------------
-  uint32_t cnt = 0, nan = 0;
+  // The rest alternates parallel phases (all threads, one barrier each) with decisions taken by
+  // wave 0 alone (no workgroup barrier inside), which it publishes in f.plan.
+  // ---- 2. [all] per-chunk counts, NaNs, the top chunk, the penalised max ---------------------
   {
+    uint32_t cnt = 0, nan = 0;
     const int w0 = 32768 - 32 * tid - 32;  // the chunk's 32 words: keys 2*w0 .. 2*w0 + 63
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -1363,193 +1385,309 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     if (tid == 1) nan = cnt - hcount(hist, 0xFF80u);
     if (tid == 1022) nan = cnt - hcount(hist, 0x007Fu);
     f.ccnt[tid] = cnt;
-  }
-  // penalised values: the max and NaNs
-  uint32_t emax = 0;
-  for (int e = tid; e < ne; e += kThreads) {
-    const uint32_t key = key_of(f.eval[e]);
-    if (key == 0xFFFFFFFFu) ++nan;
-    emax = key > emax ? key : emax;
-  }
-  // one reduction: count | NaNs, and max of (highest populated chunk | penalised max)
-  u64 tot, mx;
-  const u64 code = cnt ? static_cast<u64>(1024 - tid) : 0ull;  // higher = a chunk of larger keys
-  block_sum_max_u64((static_cast<u64>(cnt) << 32) | nan, (static_cast<u64>(emax) << 11) | code, f.red64, &tot, &mx);
-  const uint32_t total = static_cast<uint32_t>(tot >> 32);
-  const uint32_t nnan = static_cast<uint32_t>(tot);
-  if (f.si[1] || total != static_cast<uint32_t>(V - ne)) return false;
-  // the bulk max: the top populated key of the top populated chunk (wave 0 looks it up)
-  {
-    u64 cm = 0;
-    // (emax is packed above the chunk code, so recover the chunk code separately)
-    if (tid == 0) f.sq[7] = 0;
-    lds_barrier();
-    if (cnt) atomicMax(reinterpret_cast<unsigned long long*>(&f.sq[7]), code);
-    lds_barrier();
-    cm = f.sq[7];
-    if (tid < kWave) {
-      uint32_t K = 0;
-      bool has = false;
-      if (cm) {
-        const int c = 1024 - static_cast<int>(cm);
-        K = 65535u - 64u * static_cast<uint32_t>(c) - tid;
-        has = hcount(hist, K) != 0;
-      }
-      const u64 hb = __ballot(has);
-      if (tid == 0) {
-        u64 mk = 0;
-        if (hb) {
-          const int c = 1024 - static_cast<int>(cm);
-          mk = key_of(val16(65535u - 64u * static_cast<uint32_t>(c) - (__ffsll(static_cast<long long>(hb)) - 1)));
-        }
-        const u64 em = mx >> 11;
-        f.sq[6] = em > mk ? em : mk;
+    f.cmass[tid] = 0;
+    // penalised values: their max and NaNs
+    uint32_t emax = 0, emin = 0xFFFFFFFFu;
+    for (int e = tid; e < ne; e += kThreads) {
+      const uint32_t key = key_of(f.eval[e]);
+      if (key == 0xFFFFFFFFu) ++nan;
+      emax = key > emax ? key : emax;
+      emin = key < emin ? key : emin;
+    }
+    const uint32_t code = cnt ? static_cast<uint32_t>(1024 - tid) : 0u;  // higher = larger keys
+    auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+    const uint4 wpart = make_uint4(wave_sum<uint32_t>(cnt), wave_sum<uint32_t>(nan), dpp::reduce(code, umax),
+                                   dpp::reduce(emax, umax));
+    // the penalised values' chunk range (wave_walk skips the list outside it)
+    const uint32_t wmin = ~dpp::reduce(~emin, umax);
+    if (lane_id() == 0) {
+      f.wp[tid / kWave] = wpart;
+      if (wpart.w) {
+        atomicMin(&f.pchunk[0], static_cast<uint32_t>(chunk_of16(wpart.w >> 16)));
+        atomicMax(&f.pchunk[1], static_cast<uint32_t>(chunk_of16(wmin >> 16)));
       }
     }
-    lds_barrier();
   }
-  const u64 mk = f.sq[6];
   lds_barrier();
-  const uint32_t mkey = static_cast<uint32_t>(mk);
-  const float xmax = val_of(mkey);
-  const float mz = xmax / T;
+  // ---- 3. [wave 0] totals, the max, point rows, top-k and min-p thresholds -----------------
+  const uint32_t lo_key = key_of(-INFINITY);
+  if (tid < kWave) {
+    const int l = tid;
+    const uint4 wq = l < kWaves ? f.wp[l] : make_uint4(0, 0, 0, 0);
+    auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+    const uint32_t total = wave_sum<uint32_t>(wq.x);
+    const uint32_t nnan = wave_sum<uint32_t>(wq.y);
+    const uint32_t cm = dpp::reduce(wq.z, umax);
+    const uint32_t em = dpp::reduce(wq.w, umax);
+    int status = kPlanFast;
+    uint32_t mkey = 0;
+    float x0 = -INFINITY, mz = 0.0f;
+    if (f.si[1] || total != static_cast<uint32_t>(V - ne)) {
+      status = kPlanGeneric;  // a key count past 65535
+    } else {
+      // the bulk max: the top populated key of the top populated chunk
+      uint32_t mk = 0;
+      if (cm) {
+        const uint32_t top = 65535u - 64u * (1024u - cm);
+        const u64 hb = __ballot(hcount(hist, top - l) != 0);
+        if (hb) mk = key_of(val16(top - (__ffsll(static_cast<long long>(hb)) - 1)));
+      }
+      mkey = em > mk ? em : mk;
+      const float xmax = val_of(mkey);
+      mz = xmax / T;
+      if (nnan || !(T > 0.0f) || mz != mz || mz == INFINITY || mz == -INFINITY) {
+        status = kPlanPoint;
+      } else {
+        // top-k: the K-th largest value's chunk (penalised values join their chunks' counts),
+        // its value, then the smallest x with fl32(x / T) >= its z
+        if (p.K > 0 && p.K < V) {
+          for (int e = l; e < ne; e += kWave) atomicAdd(&f.ccnt[chunk_of16(key_of(f.eval[e]) >> 16)], 1u);
+          uint32_t cc[16];
+          uint32_t sum = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint4 v4 = *reinterpret_cast<const uint4*>(&f.ccnt[16 * l + 4 * q]);
+            cc[4 * q] = v4.x;
+            cc[4 * q + 1] = v4.y;
+            cc[4 * q + 2] = v4.z;
+            cc[4 * q + 3] = v4.w;
+            sum += v4.x + v4.y + v4.z + v4.w;
+          }
+          uint32_t ex = wave_incl_scan<uint32_t>(sum) - sum;
+          const uint32_t Kq = static_cast<uint32_t>(p.K);
+          int ck = -1;
+          uint32_t cab = 0;
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            if (ck < 0 && ex < Kq && Kq <= ex + cc[q]) {
+              ck = 16 * l + q;
+              cab = ex;
+            }
+            ex += cc[q];
+          }
+          const u64 hm = __ballot(ck >= 0);
+          if (!hm) {
+            status = kPlanGeneric;
+          } else {
+            const int lw = __ffsll(static_cast<long long>(hm)) - 1;
+            ck = __builtin_amdgcn_readlane(ck, lw);
+            cab = __builtin_amdgcn_readlane(cab, lw);
+            const WalkResult wr = wave_walk(hist, f, ne, ck, kWalkCount, cab, static_cast<double>(p.K), -INFINITY, T, mz);
+            if (!wr.ok) {
+              status = kPlanGeneric;
+            } else {
+              const float kz = val_of(wr.key) / T;
+              x0 = val_of(wave_bisect(lo_key, wr.key, key_of(kz * T), [&](float x) { return x / T >= kz; }));
+            }
+          }
+        }
+        // min-p: the smallest x with exp(fl32(x / T) - max z) >= min_p
+        if (status == kPlanFast && p.mp > 0.0f) {
+          const double dmp = static_cast<double>(p.mp);
+          const float guess = static_cast<float>(static_cast<double>(T) * (static_cast<double>(mz) + log(dmp)));
+          const float xm = val_of(wave_bisect(lo_key, mkey, key_of(guess), [&](float x) { return ptilde(x, T, mz) >= dmp; }));
+          x0 = xm > x0 ? xm : x0;
+        }
+      }
+    }
+    if (l == 0) {
+      f.plan.status = status;
+      f.plan.mkey = mkey;
+      f.plan.nnan = nnan;
+      f.plan.x0 = x0;
+      f.plan.mz = mz;
+    }
+  }
+  lds_barrier();
+  const int status = f.plan.status;
+  if (status == kPlanGeneric) return false;
+  const uint32_t mkey = f.plan.mkey;
+  const float mz = f.plan.mz;
   Kept k;
-  if (nnan || !(T > 0.0f) || mz != mz || mz == INFINITY || mz == -INFINITY) {
+  if (status == kPlanPoint) {
+    const float xmax = val_of(mkey);
     // the histogram is dead: the id searches use its memory
     if (ne > 0) build_bitmap(row, hist + kBitmapOffset);
     // point rows: the first NaN, the first max (greedy), the first +inf z, or index 0 (all -inf)
-    if (nnan) k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
+    if (f.plan.nnan) k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
     else if (!(T > 0.0f)) k.point = find_first(row, [&](float x, int) -> u64 { return x == xmax; }, 0ull, srch);
     else if (!degenerate(row, p, mkey, 0, mz, srch, k)) k.point = 0;
     finish(a, row, p, mz, k, 0, &srch.vslot);
     return true;
   }
-  const uint32_t lo_key = key_of(-INFINITY);
-  // ---- 3. top-k ----------------------------------------------------------------------
-  if (p.K > 0 && p.K < V) {
-    if (tid == 0) f.si[2] = -1;
-    for (int e = tid; e < ne; e += kThreads) atomicAdd(&f.ccnt[chunk_of16(key_of(f.eval[e]) >> 16)], 1u);
-    lds_barrier();
-    uint32_t ctot;
-    const uint32_t ex = block_excl_scan<uint32_t>(f.ccnt[tid], f.red32, &ctot);
-    if (ex < static_cast<uint32_t>(p.K) && static_cast<uint32_t>(p.K) <= ex + f.ccnt[tid]) {
-      f.si[2] = tid;
-      f.sq[6] = ex;
-    }
-    lds_barrier();
-    const int ck = f.si[2];
-    const u64 cab = f.sq[6];
-    lds_barrier();
-    if (ck < 0) return false;
-    const WalkResult wr = walk_chunk(hist, f, ne, ck, kWalkCount, cab, static_cast<double>(p.K), -INFINITY, T, mz);
-    if (!wr.ok) return false;
-    const float kz = val_of(wr.key) / T;
-    k.x0 = val_of(wave_bisect(lo_key, wr.key, [&](float x) { return x / T >= kz; }, f));
-  }
-  // ---- 4. min-p ----------------------------------------------------------------------
-  if (p.mp > 0.0f) {
-    const double dmp = static_cast<double>(p.mp);
-    const float xm = val_of(wave_bisect(lo_key, mkey, [&](float x) { return ptilde(x, T, mz) >= dmp; }, f));
-    k.x0 = xm > k.x0 ? xm : k.x0;
-  }
-  // ---- 5. per-chunk masses of elements >= x0 ------------------------------------------
-  const float x0 = k.x0;
-  const uint32_t x0top = key_of(x0) >> 16;
+  // ---- 5. [all] per-chunk masses of elements >= x0 ---------------------------------------
   {
-    f.cmass[tid] = 0;
-    lds_barrier();
+    const float x0 = f.plan.x0;
+    const uint32_t x0top = key_of(x0) >> 16;
     // wave w takes chunks w + 16 l (lane l says which need work), then a lane per key of each:
     // fp64 exps for populated keys only
     const int wv = tid / kWave, l = lane_id();
     const int cl = wv + kWaves * l;
     const bool need = f.ccnt[cl] > 0 && 65535u - 64u * static_cast<uint32_t>(cl) >= x0top;
     u64 todo = __ballot(need);
-    while (todo) {
-      const int i = __ffsll(static_cast<long long>(todo)) - 1;
-      todo &= todo - 1;
-      const int c = wv + kWaves * i;
+    auto key_mass = [&](int c) -> u64 {
       const uint32_t K = 65535u - 64u * static_cast<uint32_t>(c) - l;
       const uint32_t n = hcount(hist, K);
       const float v = val16(K);
-      const u64 m = (n && v >= x0) ? n * mass_q(ptilde(v, T, mz)) : 0ull;
-      const u64 sm = wave_sum<u64>(m);
-      if (l == 0) f.cmass[c] = sm;
+      return (n && v >= x0) ? n * mass_q(ptilde(v, T, mz)) : 0ull;
+    };
+    // two chunks per round: their exp chains overlap
+    while (todo) {
+      const int i1 = __ffsll(static_cast<long long>(todo)) - 1;
+      todo &= todo - 1;
+      const int i2 = todo ? __ffsll(static_cast<long long>(todo)) - 1 : -1;
+      todo &= todo - 1;
+      const int c1 = wv + kWaves * i1;
+      const int c2 = wv + kWaves * (i2 < 0 ? i1 : i2);
+      const u64 m1 = key_mass(c1);
+      const u64 m2 = i2 < 0 ? 0ull : key_mass(c2);
+      const u64 s1 = wave_sum<u64>(m1);
+      const u64 s2 = wave_sum<u64>(m2);
+      if (l == 0) {
+        atomicAdd(&f.cmass[c1], s1);
+        if (i2 >= 0) atomicAdd(&f.cmass[c2], s2);
+      }
     }
-    lds_barrier();
     for (int e = tid; e < ne; e += kThreads) {
       const float x = f.eval[e];
       if (x >= x0) atomicAdd(&f.cmass[chunk_of16(key_of(x) >> 16)], mass_q(ptilde(x, T, mz)));
     }
-    lds_barrier();
   }
-  u64 S0;
-  const u64 cab = block_excl_scan<u64>(f.cmass[tid], f.red64, &S0);  // mass above chunk tid
-  k.S = S0;
-  // ---- 6. top-p cutoff ----------------------------------------------------------------
-  if (p.tp < 1.0f) {
-    const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
-    // the lowest chunk holding mass whose mass above is < P
-    const u64 cand = (f.cmass[tid] > 0 && static_cast<double>(cab) < P) ? static_cast<u64>(tid) + 1 : 0ull;
-    const u64 cm = block_max_u64(cand, f.red64);
-    const int c = static_cast<int>(cm) - 1;
-    if (tid == c) f.sq[4] = cab;
-    lds_barrier();
-    const u64 ab = f.sq[4];
-    lds_barrier();
-    if (c < 0) return false;
-    const WalkResult wr = walk_chunk(hist, f, ne, c, kWalkCutoff, ab, P, x0, T, mz);
-    if (!wr.ok) return false;
-    k.has_cut = true;
-    k.vc = val_of(wr.key);
-    k.qc = wr.q;
-    k.mabove_c = wr.above;
-    uint32_t rr = wr.n;
-    if (k.qc > 0) {
-      const double cr = ceil((P - static_cast<double>(wr.above)) / static_cast<double>(k.qc));
-      rr = cr < 1.0 ? 1u : (cr >= static_cast<double>(wr.n) ? wr.n : static_cast<uint32_t>(cr));
+  lds_barrier();
+  // ---- 6/7. [wave 0] the total, the top-p cutoff, the draw ---------------------------------
+  if (tid < kWave) {
+    const int l = tid;
+    int status2 = kPlanFast;
+    float x0 = f.plan.x0;
+    // lane l holds chunks 16l .. 16l + 15
+    u64 m[16];
+    u64 sum = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint4 v4 = *reinterpret_cast<const uint4*>(&f.cmass[16 * l + 2 * q]);
+      m[2 * q] = (static_cast<u64>(v4.y) << 32) | v4.x;
+      m[2 * q + 1] = (static_cast<u64>(v4.w) << 32) | v4.z;
+      sum += m[2 * q] + m[2 * q + 1];
     }
-    k.r = rr;
-    k.partial = rr < wr.n;
-    if (!k.partial) k.x0 = k.vc;
-    k.S = wr.above + static_cast<u64>(rr) * k.qc;
-  }
-  // ---- 7. the draw's value group: descending value, ascending id within a value -----------
-  float vd = 0.0f;
-  u64 j = 0;
-  if (!a.out_probs) {
-    const float u = p.u >= 0.0f ? p.u : 0.0f;
-    const u64 td0 = static_cast<u64>(static_cast<double>(u) * static_cast<double>(k.S));
-    const u64 td = td0 < k.S ? td0 : k.S - 1;
-    if (k.has_cut && td >= k.mabove_c && k.qc > 0) {
-      vd = k.vc;
-      j = (td - k.mabove_c) / k.qc;
-    } else {
-      // the chunk holding the target, then the value inside it
-      if (tid == 0) f.si[3] = -1;
-      lds_barrier();
-      if (f.cmass[tid] > 0 && cab <= td && td < cab + f.cmass[tid]) {
-        f.si[3] = tid;
-        f.sq[5] = cab;
+    const u64 incl = wave_incl_scan<u64>(sum);
+    const u64 S0 = dpp::last(incl);
+    const u64 base = incl - sum;  // mass above chunk 16l
+    Kept kk;
+    kk.x0 = x0;
+    kk.S = S0;
+    if (p.tp < 1.0f) {
+      const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
+      // the lowest chunk holding mass whose mass above is < P
+      int c = -1;
+      u64 ab = 0, run = base;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        if (m[q] > 0 && static_cast<double>(run) < P) {
+          c = 16 * l + q;
+          ab = run;
+        }
+        run += m[q];
       }
-      lds_barrier();
-      const int cd = f.si[3];
-      const u64 abd = f.sq[5];
-      lds_barrier();
-      if (cd < 0) return false;
-      const WalkResult wr = walk_chunk(hist, f, ne, cd, kWalkCross, abd, static_cast<double>(td), x0, T, mz);
-      if (!wr.ok) return false;
-      vd = val_of(wr.key);
-      j = wr.q ? (td - wr.above) / wr.q : 0ull;
-      if (j >= wr.n) j = wr.n ? wr.n - 1 : 0;
+      const u64 hm = __ballot(c >= 0);
+      if (!hm) {
+        status2 = kPlanGeneric;
+      } else {
+        const int lw = 63 - __clzll(static_cast<long long>(hm));
+        c = __builtin_amdgcn_readlane(c, lw);
+        ab = readlane64(ab, lw);
+        const WalkResult wr = wave_walk(hist, f, ne, c, kWalkCutoff, ab, P, x0, T, mz);
+        if (!wr.ok) {
+          status2 = kPlanGeneric;
+        } else {
+          kk.has_cut = true;
+          kk.vc = val_of(wr.key);
+          kk.qc = wr.q;
+          kk.mabove_c = wr.above;
+          uint32_t rr = wr.n;
+          if (kk.qc > 0) {
+            const double cr = ceil((P - static_cast<double>(wr.above)) / static_cast<double>(kk.qc));
+            rr = cr < 1.0 ? 1u : (cr >= static_cast<double>(wr.n) ? wr.n : static_cast<uint32_t>(cr));
+          }
+          kk.r = rr;
+          kk.partial = rr < wr.n;
+          if (!kk.partial) kk.x0 = kk.vc;
+          kk.S = wr.above + static_cast<u64>(rr) * kk.qc;
+        }
+      }
+    }
+    // the draw's value group: descending value, ascending id within a value
+    float vd = 0.0f;
+    u64 j = 0;
+    if (status2 == kPlanFast && !a.out_probs) {
+      const float u = p.u >= 0.0f ? p.u : 0.0f;
+      const u64 td0 = static_cast<u64>(static_cast<double>(u) * static_cast<double>(kk.S));
+      const u64 td = td0 < kk.S ? td0 : kk.S - 1;
+      if (kk.has_cut && td >= kk.mabove_c && kk.qc > 0) {
+        vd = kk.vc;
+        j = (td - kk.mabove_c) / kk.qc;
+      } else {
+        // the chunk holding the target, then the value inside it
+        int cd = -1;
+        u64 abd = 0, run = base;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          if (m[q] > 0 && run <= td && td < run + m[q]) {
+            cd = 16 * l + q;
+            abd = run;
+          }
+          run += m[q];
+        }
+        const u64 hm = __ballot(cd >= 0);
+        if (!hm) {
+          status2 = kPlanGeneric;
+        } else {
+          const int lw = __ffsll(static_cast<long long>(hm)) - 1;
+          cd = __builtin_amdgcn_readlane(cd, lw);
+          abd = readlane64(abd, lw);
+          const WalkResult wr = wave_walk(hist, f, ne, cd, kWalkCross, abd, static_cast<double>(td), x0, T, mz);
+          if (!wr.ok) {
+            status2 = kPlanGeneric;
+          } else {
+            vd = val_of(wr.key);
+            j = wr.q ? (td - wr.above) / wr.q : 0ull;
+            if (j >= wr.n) j = wr.n ? wr.n - 1 : 0;
+          }
+        }
+      }
+    }
+    if (l == 0) {
+      f.plan.status = status2;
+      f.plan.x0 = kk.x0;
+      f.plan.vc = kk.vc;
+      f.plan.partial = kk.partial;
+      f.plan.has_cut = kk.has_cut;
+      f.plan.r = kk.r;
+      f.plan.mabove_c = kk.mabove_c;
+      f.plan.qc = kk.qc;
+      f.plan.S = kk.S;
+      f.plan.vd = vd;
+      f.plan.j = j;
     }
   }
+  lds_barrier();
+  if (f.plan.status == kPlanGeneric) return false;
+  k.x0 = f.plan.x0;
+  k.vc = f.plan.vc;
+  k.partial = f.plan.partial;
+  k.has_cut = f.plan.has_cut;
+  k.r = f.plan.r;
+  k.mabove_c = f.plan.mabove_c;
+  k.qc = f.plan.qc;
+  k.S = f.plan.S;
+  const float vd = f.plan.vd;
+  const u64 j = f.plan.j;
   // the histogram is dead: the id searches below use its memory
   if (ne > 0) build_bitmap(row, hist + kBitmapOffset);
   resolve_idr(a, row, p, k, srch);
   int draw = 0;
   if (!a.out_probs) {
-    draw = row.nstripes * kThreads <= 4 * kMatchWords
-               ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset))
+    draw = cells_per(row) * kThreads <= 4 * kMatchWords
+               ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk)
                : -1;
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
   }
