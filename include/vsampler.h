@@ -100,8 +100,9 @@ int vsamp_query(int device, char* why, size_t n);
 size_t vsamp_workspace_bytes(int32_t batch, int32_t vocab, int64_t hist_total);
 
 /* Sample one token per row: penalties, temperature, top-k, softmax, min-p, top-p, then the
- * inverse-CDF draw over kept tokens in ascending id order. Replaces `sample(logits, params,
- * seed, position)` (sampler.py:68-77) for B rows at once. */
+ * inverse-CDF draw with u over the kept tokens taken in descending probability (equal
+ * probabilities: ascending id). Replaces `sample(logits, params, seed, position)`
+ * (sampler.py:68-77) for B rows at once. */
 int vsamp_sample(const vsamp_args* args, void* stream);
 
 /* The final per-token probabilities [B, V] fp32 that vsamp_sample draws from (0 for dropped

@@ -13,11 +13,14 @@
 // and order-independent.
 //
 // bf16 rows (fast path): one pass builds a histogram of the row's 65536 possible 16-bit keys
-// (u16 counts packed in pairs, 128 KB of LDS). Every threshold and the draw's value group are
-// then found from the histogram: per-chunk (64-key) counts and masses, a scan over chunks and a
-// wave-wide walk inside one chunk, with fp64 exps only for populated keys. A second,
-// compare-only pass finds the id of the drawn token. fp32 rows, and bf16 rows whose histogram
-// cannot hold them, take the generic path: radix descents over 32-bit ordered keys.
+// (u16 counts packed in pairs, 128 KB of LDS) while it counts the row's token history in an LDS
+// hash table. Every threshold and the draw's value group are then found from the histogram:
+// per-chunk (64-key) counts and masses computed by all waves, and the decisions (totals, top-k,
+// min-p, top-p, the draw) taken by wave 0 alone from a scan over chunks and a walk inside one
+// chunk, with fp64 exps only for populated keys. A second, compare-only pass over the blocks
+// of the threads that can hold the drawn value finds the id of the drawn token. fp32 rows, and
+// bf16 rows whose histogram or history table cannot hold them, take the generic path: a
+// workspace penalty pass, then radix descents over 32-bit ordered keys.
 //
 // Penalised tokens ("exceptions"): the generic path masks them out of logits reads by the row's
 // bitmap and visits them from the workspace's list; the fast path keeps the list in LDS and
@@ -216,7 +219,7 @@ struct Row {
   int nstripes;
   bool vec;
   const uint8_t* bm;   // per-block lane masks of exceptions, or null
-  const int32_t* eid;  // exceptions of this row, ascending id
+  const int32_t* eid;  // exceptions of this row (in no particular order)
   const float* eval;
   int nexc;
 
