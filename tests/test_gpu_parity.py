@@ -164,6 +164,36 @@ def test_degenerate_rows():
         assert ids.tolist()[:3] == [5, 3, 0] and ids.tolist()[5] == 2
 
 
+def _colliding_ids(V: int, first_bucket: int, buckets: int, per_bucket: int) -> list[int]:
+    """Ids whose 4096-slot Fibonacci hash lands in `buckets` consecutive buckets, `per_bucket`
+    of each: inserted together they form one long probe run in the kernel's history table."""
+    h = (np.arange(V, dtype=np.uint64) * np.uint64(2654435761)) % np.uint64(1 << 32) >> np.uint64(20)
+    out = []
+    for b in range(first_bucket, first_bucket + buckets):
+        out += np.flatnonzero(h == b)[:per_bucket].tolist()
+    return out
+
+
+def test_bf16_rows_the_histogram_path_hands_to_the_generic_path():
+    # histories the bf16 histogram path does not count itself: longer than its table takes,
+    # more distinct ids than its list holds, one probe run past its limit; beside normal rows
+    V, B = 151936, 8
+    rng = np.random.default_rng(11)
+    w = random_workload(21, B, V, torch.bfloat16, hist_len=100)
+    hist = [rng.integers(0, V, 200).tolist() for _ in range(B)]
+    hist[1] = rng.integers(0, V, 9000).tolist()  # longer than 8190 ids
+    hist[3] = rng.permutation(V)[:3000].tolist()  # 3000 distinct ids
+    hist[5] = _colliding_ids(V, 100, 72, 2) * 2  # a 144-slot probe run
+    hist[6] = rng.permutation(V)[:2048].tolist() * 2  # exactly the list's capacity
+    w.hist_ids, w.hist_offsets = pack_history(hist)
+    p = w.params
+    for t in (p.repetition_penalty, p.presence_penalty, p.frequency_penalty):
+        t.fill_(0.0)
+    p.repetition_penalty.fill_(1.1)
+    p.temperature[1::2] = 0.0  # greedy rows take the same paths
+    check(w, max_tie_frac=0.25)
+
+
 def test_unaligned_and_padded_rows():
     base = torch.randn(20, 1003)
     for dtype in (torch.bfloat16, torch.float32):
