@@ -150,6 +150,20 @@ def test_uniform_sweep_reproduces_the_final_distribution_exactly():
     assert [sample_row(z, 1.0, 0, 1.0, 0.0, u).token for u in (0.1, 0.3, 0.6, 0.9)] == [0, 1, 2, 3]
 
 
+def test_draft_probability_is_the_draw_frequency_of_that_id():
+    # the reported probability of a draft id is the share of uniforms whose draw lands on it
+    x = np.array([0.5, 2.0, -1.0, 1.5, 0.0, 1.9, -0.2], np.float32)
+    n = 1 << 14
+    us = (np.arange(n) + 0.5) / n
+    for T, k, p, mp in ((1.0, 0, 1.0, 0.0), (0.7, 5, 0.9, 0.0), (1.3, 0, 0.95, 0.2)):
+        toks = np.array([sample_row(x, T, k, p, mp, u).token for u in us])
+        for d in range(len(x)):
+            dp = sample_row(x, T, k, p, mp, 0.5, draft=d).draft_prob
+            assert abs(np.mean(toks == d) - dp) <= 1.0 / n, (T, k, p, mp, d)
+    # greedy: probability 1 for the argmax, 0 otherwise
+    assert [sample_row(x, 0.0, 0, 1.0, 0.0, 0.5, draft=d).draft_prob for d in range(7)] == [0, 1, 0, 0, 0, 0, 0]
+
+
 @pytest.mark.parametrize(
     "params",
     [
