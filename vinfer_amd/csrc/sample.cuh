@@ -1071,18 +1071,19 @@ __device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, uint32
 
 // The id of the j-th (0-based, ascending id) token whose penalised value is vd: bulk positions
 // holding vd that are not penalised, and penalised ids whose new value is vd.
-// One pass counts, per 8-id block, the unpenalised tokens whose bf16 value is vd into a byte
-// cell (`cells`: cell b is block b, kThreads * cells_per(row) bytes of LDS); penalised ids whose
-// new value is vd add 1 to theirs. A scan over the cells in id order finds the block, and one
-// thread the lane. Needs row.bm (penalised positions) built when the row has any.
+// One pass writes, per 8-id block, the mask of its members into a byte cell (`cells`: cell b
+// is block b, kThreads * cells_per(row) bytes of LDS): unpenalised lanes whose bf16 value is vd
+// (penalised lanes masked out by the position bitmap), then penalised ids whose new value is
+// vd. Per-thread popcounts of consecutive cells and a scan find the block; its mask, the lane.
 // Thread t reads the blocks it read in the histogram pass (t + m * kThreads, and the tail
-// elements t + n * kThreads), last to first: the end of the row, read last, is the part most
-// likely still in L2. `mxk` is the largest key the thread saw there: a thread whose largest key
-// is below vd's holds no member and reads nothing.
+// elements t + n * kThreads): the first 2 * 4 from `keep` (registers), the rest from memory,
+// last to first (the end of the row, read last, is the part most likely still in L2). `mxk` is
+// the largest key the thread saw in that pass: a thread whose largest key is below vd's holds
+// no member and reads nothing. Needs row.bm built when the row has penalised ids.
 __device__ __forceinline__ int cells_per(const Row<uint16_t>& row) { return (row.nstripes + 3) & ~3; }
 
 __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, float vd, u64 j,
-                                            uint8_t* cells, uint32_t mxk) {
+                                            uint8_t* cells, uint32_t mxk, const uint4 (&keep)[8]) {
   const int tid = threadIdx.x;
   const uint32_t vb = __float_as_uint(vd);
   const bool bf = (vb & 0xFFFFu) == 0u;  // vd is a bf16 value: bulk tokens can hold it
@@ -1094,9 +1095,9 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   uint32_t* cw = reinterpret_cast<uint32_t*>(cells);
   for (int i = tid; i < per * kThreads / 4; i += kThreads) cw[i] = 0;
   lds_barrier();
-  auto cell_add = [&](int id, uint32_t delta) {
+  auto cell_or = [&](int id) {
     const int b = id / kBlk;
-    atomicAdd(&cw[b >> 2], delta << (8 * (b & 3)));
+    atomicOr(&cw[b >> 2], 1u << (8 * (b & 3) + id % kBlk));
   };
   auto penalised = [&](int id) -> bool { return row.bm && ((row.bm[id / kBlk] >> (id % kBlk)) & 1u); };
   // lanes of an 8-element block (4 words, 2 halves each) whose raw value is vd's
@@ -1115,44 +1116,54 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     const int nfull = row.vec ? V / kBlk : 0;
     const uint32_t ka = ok16(t16), kb = ok16(t16b);
     const bool cand = mxk >= (ka < kb ? ka : kb);
-    // this thread's blocks tid + m * kThreads, m < nm, read from the last with a rolling
-    // prefetch (slot k: m = m0 - k)
+    // this thread's blocks tid + m * kThreads, m < nm; m >= 8 from memory with a rolling
+    // prefetch (slot k: m = m0 - k), m < 8 from `keep`
     const int nm = tid < nfull ? (nfull - 1 - tid) / kThreads + 1 : 0;
-    if (cand && nm > 0) {
+    if (cand && nm > 8) {
       constexpr int D = 4;
       uint4 d[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) d[k] = ld_block(base, tid + max(nm - 1 - k, 0) * kThreads);
-      for (int m0 = nm - 1; m0 >= 0; m0 -= D) {
+      for (int k = 0; k < D; ++k) d[k] = ld_block(base, tid + max(nm - 1 - k, 8) * kThreads);
+      for (int m0 = nm - 1; m0 >= 8; m0 -= D) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
           const int m = m0 - k;
-          const int b = tid + (m < 0 ? 0 : m) * kThreads;
+          const int b = tid + (m < 8 ? 8 : m) * kThreads;
           uint32_t mask = match8(d[k]);
-          d[k] = ld_block(base, tid + max(m - D, 0) * kThreads);
+          d[k] = ld_block(base, tid + max(m - D, 8) * kThreads);
           if (row.bm) mask &= ~static_cast<uint32_t>(row.bm[b]);
           // block b is written by the one thread reading it
-          if (m >= 0) cells[b] = static_cast<uint8_t>(__popc(mask));
+          if (m >= 8) cells[b] = static_cast<uint8_t>(mask);
         }
       }
     }
+    if (cand) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const int b = tid + m * kThreads;
+        uint32_t mask = match8(keep[m]);
+        if (row.bm && m < nm) mask &= ~static_cast<uint32_t>(row.bm[b]);
+        if (m < nm) cells[b] = static_cast<uint8_t>(mask);
+      }
+    }
+    lds_barrier();  // (the byte stores above land before the word atomics below)
     // the rest: a ragged tail, or every element of an unaligned row
     if (cand) {
       for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
         const uint32_t raw = base[i];
-        if ((raw == t16 || raw == t16b) && !penalised(i)) cell_add(i, 1u);
+        if ((raw == t16 || raw == t16b) && !penalised(i)) cell_or(i);
       }
     }
   }
   // penalised ids whose new value is vd are members
   for (int e = tid; e < ne; e += kThreads)
-    if (f.eval[e] == vd) cell_add(f.eid[e], 1u);
+    if (f.eval[e] == vd) cell_or(f.eid[e]);
   lds_barrier();
-  // the cell holding the j-th member: per-thread sums of `per` consecutive cells (4 at a time,
-  // one v_dot4_u32_u8 each), then a scan
+  // the cell holding the j-th member: per-thread member counts of `per` consecutive cells (one
+  // popcount per 4 cells), then a scan
   const int c0 = tid * per;
   uint32_t mine = 0;
-  for (int c = c0; c < c0 + per; c += 4) mine = __builtin_amdgcn_udot4(cw[c >> 2], 0x01010101u, mine, false);
+  for (int c = c0; c < c0 + per; c += 4) mine += __popc(cw[c >> 2]);
   uint32_t total;
   const uint32_t before = block_excl_scan<uint32_t>(mine, f.red32, &total);
   if (tid == 0) f.si[6] = -1;
@@ -1160,54 +1171,17 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   if (total > 0 && j < total && before <= j && j < before + mine) {
     uint32_t acc = before;
     for (int c = c0; c < c0 + per; ++c) {
-      if (j < acc + cells[c]) {
-        f.si[5] = c;  // the block
-        f.sq[5] = acc;
+      const uint32_t mask = cells[c];
+      const uint32_t n = __popc(mask);
+      if (j < acc + n) {
+        // the (j - acc)-th set lane of block c
+        uint32_t m = mask;
+        for (uint32_t r = static_cast<uint32_t>(j - acc); r > 0; --r) m &= m - 1;
+        f.si[6] = c * kBlk + __ffs(m) - 1;
         break;
       }
-      acc += cells[c];
+      acc += n;
     }
-    f.si[6] = 0;
-  }
-  lds_barrier();
-  if (f.si[6] < 0) {
-    lds_barrier();
-    return -1;
-  }
-  const int b = f.si[5];
-  const u64 acc0 = f.sq[5];
-  // penalised lanes of block b whose new value is vd
-  if (tid == 0) f.sk[4] = 0;
-  lds_barrier();
-  for (int e = tid; e < ne; e += kThreads) {
-    const int id = f.eid[e];
-    if (id / kBlk == b && f.eval[e] == vd) atomicOr(&f.sk[4], 1u << (id % kBlk));
-  }
-  lds_barrier();
-  if (tid == 0) {
-    const uint32_t pen = row.bm ? row.bm[b] : 0u;
-    const bool full = row.vec && (b + 1) * kBlk <= V;
-    const uint32_t bulk = full ? match8(ld_block(base, b)) : 0u;  // (one load for a full block)
-    u64 acc = acc0;
-    int found = b * kBlk;
-    for (int i = 0; i < kBlk && b * kBlk + i < V; ++i) {
-      const int id = b * kBlk + i;
-      bool member;
-      if ((pen >> i) & 1u) member = (f.sk[4] >> i) & 1u;
-      else if (full) member = (bulk >> i) & 1u;
-      else {
-        const uint32_t raw = base[id];
-        member = raw == t16 || raw == t16b;
-      }
-      if (member) {
-        if (acc == j) {
-          found = id;
-          break;
-        }
-        ++acc;
-      }
-    }
-    f.si[6] = found;
   }
   lds_barrier();
   const int res = f.si[6];
@@ -1290,6 +1264,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   uint32_t sl[4] = {kEmpty, kEmpty, kEmpty, kEmpty};
   uint32_t e0 = 0, nexc = 0;
   const int rounds = (nfull + D * kThreads - 1) / (D * kThreads);  // (uniform)
+  uint4 kb[2 * D];  // this thread's first 2*D blocks, kept for the member search
   auto round = [&](int it) {
 #pragma unroll
     for (int k = 0; k < D; ++k) {
@@ -1300,6 +1275,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
         add2(d[k].z);
         add2(d[k].w);
       }
+      if (it < 2) kb[it * D + k] = d[k];
       d[k] = ld_block(base, min(b + D * kThreads, nfull - 1));
     }
   };
@@ -1690,7 +1666,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   int draw = 0;
   if (!a.out_probs) {
     draw = cells_per(row) * kThreads <= 4 * kMatchWords
-               ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk)
+               ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb)
                : -1;
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
   }
