@@ -47,15 +47,55 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
+// ---- exp(d), d <= 0, in fp64 -------------------------------------------------------------------
+// d = (16k + j) ln2/16 + r with |r| <= ln2/32, so exp(d) = 2^k (t_j + t_j (e^r - 1)) with
+// t_j = 2^(j/16) (correctly rounded, below) and e^r - 1 from its Taylor series through r^7
+// (the first omitted term is below 2e-18). The last fma rounds once; t_j's own rounding adds at
+// most half an ulp. About 15 fp64 operations where the library exp takes about 35: the masses
+// evaluate one per populated key and are bound by VALU issue.
+constexpr double kExp2Sixteenths[16] = {
+    0x1.0000000000000p+0, 0x1.0b5586cf9890fp+0, 0x1.172b83c7d517bp+0, 0x1.2387a6e756238p+0,
+    0x1.306fe0a31b715p+0, 0x1.3dea64c123422p+0, 0x1.4bfdad5362a27p+0, 0x1.5ab07dd485429p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.7a11473eb0187p+0, 0x1.8ace5422aa0dbp+0, 0x1.9c49182a3f090p+0,
+    0x1.ae89f995ad3adp+0, 0x1.c199bdd85529cp+0, 0x1.d5818dcfba487p+0, 0x1.ea4afa2a490dap+0};
+constexpr double kSixteenOverLn2 = 0x1.71547652b82fep+4;
+constexpr double kLn2Over16Hi = 0x1.62e42fefa0000p-5;  // 36 bits: k * hi is exact for |k| < 2^17
+constexpr double kLn2Over16Lo = 0x1.cf79abc9e3b3ap-44;
+
+// The table in LDS (a lane-indexed read); exp_table_init() fills it, before a barrier.
+__shared__ double g_exp2_16[16];
+__device__ __forceinline__ void exp_table_init() {
+  if (threadIdx.x < 16) g_exp2_16[threadIdx.x] = kExp2Sixteenths[threadIdx.x];
+}
+
+__device__ __forceinline__ double exp_nonpos(double d) {
+  if (!(d >= -745.5)) return 0.0;  // below the smallest subnormal (and -inf, NaN)
+  const double kd = __builtin_rint(d * kSixteenOverLn2);
+  double r = __builtin_fma(-kd, kLn2Over16Hi, d);
+  r = __builtin_fma(-kd, kLn2Over16Lo, r);
+  double q = __builtin_fma(r, 1.0 / 5040.0, 1.0 / 720.0);
+  q = __builtin_fma(r, q, 1.0 / 120.0);
+  q = __builtin_fma(r, q, 1.0 / 24.0);
+  q = __builtin_fma(r, q, 1.0 / 6.0);
+  q = __builtin_fma(r, q, 0.5);
+  const double em1 = __builtin_fma(r * r, q, r);  // e^r - 1
+  const int k = static_cast<int>(kd);
+  const double t = g_exp2_16[k & 15];
+  return __builtin_ldexp(__builtin_fma(t, em1, t), k >> 4);
+}
+
 // ---- fixed-point mass of one value ------------------------------------------------------------
 // p~ = exp(z - m) in fp64 with z = fl32(x / T) (IEEE division), m the row's max z.
 __device__ __forceinline__ double ptilde(float x, float T, float mz) {
   const float z = T == 1.0f ? x : x / T;  // (x / 1 is x: skip the division)
-  return exp(static_cast<double>(z) - static_cast<double>(mz));
+  return exp_nonpos(static_cast<double>(z) - static_cast<double>(mz));
 }
 
+// q = rint(p * 2^42) for p in [0, 1]: adding 2^52 rounds to an integer (ties to even, as rint)
+// and leaves it in the low mantissa bits.
 __device__ __forceinline__ u64 mass_q(double p) {
-  return static_cast<u64>(__builtin_rint(p * kMassScale));
+  const double b = __builtin_fma(p, kMassScale, 4503599627370496.0);  // + 2^52
+  return static_cast<u64>(__double_as_longlong(b)) - 0x4330000000000000ull;
 }
 
 // ---- barriers ---------------------------------------------------------------------------------
@@ -67,6 +107,15 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+
+// ---- uniform values ----------------------------------------------------------------------------
+// A value every lane holds the same copy of (read from LDS, say), moved to a scalar register:
+// branches on it are scalar branches and arithmetic with it takes a scalar operand.
+__device__ __forceinline__ float uniform_f(float x) {
+  return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(x)));
+}
+__device__ __forceinline__ uint32_t uniform_u(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int uniform_i(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // ---- wave primitives --------------------------------------------------------------------------
 // Cross-lane steps use DPP (data-parallel primitives: a VALU operand read from another lane of
@@ -87,6 +136,10 @@ constexpr int kBcast31 = 0x143;     // lane 31 into rows 2 and 3
 // read 0.
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ uint32_t mov(uint32_t x) {
+  if constexpr (ROW_MASK == 0xF && (CTRL < 0x100 || CTRL == kMirror || CTRL == kHalfMirror)) {
+    // every lane has a source lane: no old value to keep
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), CTRL, 0xF, 0xF, false));
+  }
   return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROW_MASK, 0xF, true));
 }
 template <int CTRL, int ROW_MASK = 0xF>

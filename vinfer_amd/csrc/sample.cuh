@@ -1076,14 +1076,18 @@ __device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, uint32
 // (penalised lanes masked out by the position bitmap), then penalised ids whose new value is
 // vd. Per-thread popcounts of consecutive cells and a scan find the block; its mask, the lane.
 // Thread t reads the blocks it read in the histogram pass (t + m * kThreads, and the tail
-// elements t + n * kThreads): the first 2 * 4 from `keep` (registers), the rest from memory,
+// elements t + n * kThreads): the first kKeep from `keep` (registers), the rest from memory,
 // last to first (the end of the row, read last, is the part most likely still in L2). `mxk` is
 // the largest key the thread saw in that pass: a thread whose largest key is below vd's holds
 // no member and reads nothing. Needs row.bm built when the row has penalised ids.
 __device__ __forceinline__ int cells_per(const Row<uint16_t>& row) { return (row.nstripes + 3) & ~3; }
 
+// Histogram rounds (of 4 blocks per thread) whose blocks stay in registers for the member search.
+constexpr int kKeepRounds = 2;
+constexpr int kKeep = 4 * kKeepRounds;
+
 __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, float vd, u64 j,
-                                            uint8_t* cells, uint32_t mxk, const uint4 (&keep)[8]) {
+                                            uint8_t* cells, uint32_t mxk, const uint4 (&keep)[kKeep]) {
   const int tid = threadIdx.x;
   const uint32_t vb = __float_as_uint(vd);
   const bool bf = (vb & 0xFFFFu) == 0u;  // vd is a bf16 value: bulk tokens can hold it
@@ -1100,46 +1104,51 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     atomicOr(&cw[b >> 2], 1u << (8 * (b & 3) + id % kBlk));
   };
   auto penalised = [&](int id) -> bool { return row.bm && ((row.bm[id / kBlk] >> (id % kBlk)) & 1u); };
-  // lanes of an 8-element block (4 words, 2 halves each) whose raw value is vd's
-  auto match8 = [&](uint4 w) -> uint32_t {
-    uint32_t m = 0;
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t lo = ws[q] & 0xFFFFu, hi = ws[q] >> 16;
-      m |= ((lo == t16 || lo == t16b) ? 1u : 0u) << (2 * q);
-      m |= ((hi == t16 || hi == t16b) ? 1u : 0u) << (2 * q + 1);
-    }
-    return m;
+  // The member lanes of an 8-element block: xor with the pattern zeroes the matching 16-bit
+  // halves, v_pk_min_u16(x, 1) leaves 0 (match) or 1 per half, and three shifted ors gather the
+  // halves of the 4 words into bits 0, 2, 4, 6 (low halves) and 16, 18, 20, 22 (high halves).
+  // (The ones come through an opaque scalar register, or the compiler expands the min into
+  // compares.)
+  uint32_t ones_word;
+  asm("s_mov_b32 %0, 0x10001" : "=s"(ones_word));
+  const ushort2_t one2 = __builtin_bit_cast(ushort2_t, ones_word);
+  auto nz2 = [&](uint32_t w, uint32_t pat) -> uint32_t {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(ushort2_t, w ^ pat), one2));
+  };
+  auto match1 = [&](uint4 w, uint32_t pat) -> uint32_t {
+    const uint32_t a = nz2(w.x, pat) | (nz2(w.y, pat) << 2) | (nz2(w.z, pat) << 4) | (nz2(w.w, pat) << 6);
+    return ~(a | (a >> 15)) & 0xFFu;
   };
   if (bf) {
+    const uint32_t pat = t16 * 0x10001u, patb = t16b * 0x10001u;
+    auto match8 = [&](uint4 w) -> uint32_t { return match1(w, pat) | (t16b != t16 ? match1(w, patb) : 0u); };
     const int nfull = row.vec ? V / kBlk : 0;
     const uint32_t ka = ok16(t16), kb = ok16(t16b);
     const bool cand = mxk >= (ka < kb ? ka : kb);
-    // this thread's blocks tid + m * kThreads, m < nm; m >= 8 from memory with a rolling
-    // prefetch (slot k: m = m0 - k), m < 8 from `keep`
+    // this thread's blocks tid + m * kThreads, m < nm; m >= kKeep from memory with a rolling
+    // prefetch (slot k: m = m0 - k), m < kKeep from `keep`
     const int nm = tid < nfull ? (nfull - 1 - tid) / kThreads + 1 : 0;
-    if (cand && nm > 8) {
+    if (cand && nm > kKeep) {
       constexpr int D = 4;
       uint4 d[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) d[k] = ld_block(base, tid + max(nm - 1 - k, 8) * kThreads);
-      for (int m0 = nm - 1; m0 >= 8; m0 -= D) {
+      for (int k = 0; k < D; ++k) d[k] = ld_block(base, tid + max(nm - 1 - k, kKeep) * kThreads);
+      for (int m0 = nm - 1; m0 >= kKeep; m0 -= D) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
           const int m = m0 - k;
-          const int b = tid + (m < 8 ? 8 : m) * kThreads;
+          const int b = tid + (m < kKeep ? kKeep : m) * kThreads;
           uint32_t mask = match8(d[k]);
-          d[k] = ld_block(base, tid + max(m - D, 8) * kThreads);
+          d[k] = ld_block(base, tid + max(m - D, kKeep) * kThreads);
           if (row.bm) mask &= ~static_cast<uint32_t>(row.bm[b]);
           // block b is written by the one thread reading it
-          if (m >= 8) cells[b] = static_cast<uint8_t>(mask);
+          if (m >= kKeep) cells[b] = static_cast<uint8_t>(mask);
         }
       }
     }
     if (cand) {
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
+      for (int m = 0; m < kKeep; ++m) {
         const int b = tid + m * kThreads;
         uint32_t mask = match8(keep[m]);
         if (row.bm && m < nm) mask &= ~static_cast<uint32_t>(row.bm[b]);
@@ -1234,7 +1243,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     f.pchunk[1] = 0;
   }
   lds_barrier();
-  const float T = p.T;
+  const float T = uniform_f(p.T);
   const int L = PEN ? p.h1 - p.h0 : 0;
   const bool on = PEN && L > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
   const bool pen = on && L <= kFastMaxL;  // a longer history is counted by the generic path
@@ -1264,7 +1273,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   uint32_t sl[4] = {kEmpty, kEmpty, kEmpty, kEmpty};
   uint32_t e0 = 0, nexc = 0;
   const int rounds = (nfull + D * kThreads - 1) / (D * kThreads);  // (uniform)
-  uint4 kb[2 * D];  // this thread's first 2*D blocks, kept for the member search
+  uint4 kb[kKeepRounds * D];  // this thread's first blocks, kept for the member search
   auto round = [&](int it) {
 #pragma unroll
     for (int k = 0; k < D; ++k) {
@@ -1275,7 +1284,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
         add2(d[k].z);
         add2(d[k].w);
       }
-      if (it < 2) kb[it * D + k] = d[k];
+      if (it < kKeepRounds) kb[it * D + k] = d[k];
       d[k] = ld_block(base, min(b + D * kThreads, nfull - 1));
     }
   };
@@ -1305,7 +1314,11 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   uint32_t og[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) og[k] = ld_global(base + (sl[k] != kEmpty ? sl[k] >> 13 : 0u));
-  for (int it = 2; it < rounds; ++it) round(it);
+  static_assert(kKeepRounds >= 2, "rounds 0 and 1 are peeled for the history stages");
+#pragma unroll
+  for (int it = 2; it < kKeepRounds; ++it)  // (peeled too: `kb` is indexed by constants only)
+    if (it < rounds) round(it);
+  for (int it = kKeepRounds; it < rounds; ++it) round(it);
   // the rest: a ragged tail, or every element of an unaligned row
   uint32_t mxk = mx2.x > mx2.y ? mx2.x : mx2.y;
   for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
@@ -1480,8 +1493,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   lds_barrier();
   const int status = f.plan.status;
   if (status == kPlanGeneric) return false;
-  const uint32_t mkey = f.plan.mkey;
-  const float mz = f.plan.mz;
+  const uint32_t mkey = uniform_u(f.plan.mkey);
+  const float mz = uniform_f(f.plan.mz);
   Kept k;
   if (status == kPlanPoint) {
     const float xmax = val_of(mkey);
@@ -1496,7 +1509,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   }
   // ---- 5. [all] per-chunk masses of elements >= x0 ---------------------------------------
   {
-    const float x0 = f.plan.x0;
+    const float x0 = uniform_f(f.plan.x0);
     const uint32_t x0top = key_of(x0) >> 16;
     // wave w takes chunks w + 16 l (lane l says which need work), then a lane per key of each:
     // fp64 exps for populated keys only
@@ -1702,6 +1715,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   static_assert(kMatchOffset + kMatchWords <= kChunk, "count cells must fit");
   const int r = blockIdx.x;
   const int tid = threadIdx.x;
+  exp_table_init();  // (published by the first barrier of either path)
   // the row's parameters: lane w of wave 0 loads word w, all in one vector load
   uint32_t pw = 0;
   if (tid < kWave) pw = param_word<PEN>(a, r, tid);
