@@ -174,17 +174,23 @@ def _colliding_ids(V: int, first_bucket: int, buckets: int, per_bucket: int) -> 
     return out
 
 
-def test_bf16_rows_the_histogram_path_hands_to_the_generic_path():
+@pytest.mark.parametrize("V", [151936, 200000])  # history counted in a presence bitmap / a hash table
+def test_bf16_rows_the_histogram_path_hands_to_the_generic_path(V):
     # histories the bf16 histogram path does not count itself: longer than its table takes,
     # more distinct ids than its list holds, one probe run past its limit; beside normal rows
-    V, B = 151936, 8
+    # and histories of dense id ranges, the vocabulary's ends and ids outside it
+    B = 10
     rng = np.random.default_rng(11)
     w = random_workload(21, B, V, torch.bfloat16, hist_len=100)
     hist = [rng.integers(0, V, 200).tolist() for _ in range(B)]
+    hist[0] = list(range(2048)) + list(range(0, 2048, 3))  # dense: whole bitmap words
     hist[1] = rng.integers(0, V, 9000).tolist()  # longer than 8190 ids
+    hist[2] = [0, V - 1, -5, V + 3, V - 1, 0, 2**31 - 1, 64, 63]
     hist[3] = rng.permutation(V)[:3000].tolist()  # 3000 distinct ids
+    hist[4] = list(range(V - 2048, V)) * 3  # the top of the vocabulary, exactly the capacity
     hist[5] = _colliding_ids(V, 100, 72, 2) * 2  # a 144-slot probe run
     hist[6] = rng.permutation(V)[:2048].tolist() * 2  # exactly the list's capacity
+    hist[8] = rng.permutation(V)[:2049].tolist()  # one past it
     w.hist_ids, w.hist_offsets = pack_history(hist)
     p = w.params
     for t in (p.repetition_penalty, p.presence_penalty, p.frequency_penalty):

@@ -62,14 +62,22 @@ constexpr double kSixteenOverLn2 = 0x1.71547652b82fep+4;
 constexpr double kLn2Over16Hi = 0x1.62e42fefa0000p-5;  // 36 bits: k * hi is exact for |k| < 2^17
 constexpr double kLn2Over16Lo = 0x1.cf79abc9e3b3ap-44;
 
-// The table in LDS (a lane-indexed read); exp_table_init() fills it, before a barrier.
+// The table in LDS (a lane-indexed read); exp_table_init() fills it, before a barrier. Thread 0
+// stores the 16 constants as immediates: a lane-indexed read of a constant array would be a
+// global load at the kernel's start, which the next wait for any load waits for.
 __shared__ double g_exp2_16[16];
 __device__ __forceinline__ void exp_table_init() {
-  if (threadIdx.x < 16) g_exp2_16[threadIdx.x] = kExp2Sixteenths[threadIdx.x];
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) g_exp2_16[i] = kExp2Sixteenths[i];
+  }
 }
 
-__device__ __forceinline__ double exp_nonpos(double d) {
-  if (!(d >= -745.5)) return 0.0;  // below the smallest subnormal (and -inf, NaN)
+__device__ __forceinline__ double exp_nonpos(double d0) {
+  // (branch-free, so that independent evaluations interleave: below the smallest subnormal,
+  // and for -inf and NaN, the result is selected to 0 at the end)
+  const bool tiny = !(d0 >= -745.5);
+  const double d = tiny ? 0.0 : d0;
   const double kd = __builtin_rint(d * kSixteenOverLn2);
   double r = __builtin_fma(-kd, kLn2Over16Hi, d);
   r = __builtin_fma(-kd, kLn2Over16Lo, r);
@@ -81,7 +89,8 @@ __device__ __forceinline__ double exp_nonpos(double d) {
   const double em1 = __builtin_fma(r * r, q, r);  // e^r - 1
   const int k = static_cast<int>(kd);
   const double t = g_exp2_16[k & 15];
-  return __builtin_ldexp(__builtin_fma(t, em1, t), k >> 4);
+  const double y = __builtin_ldexp(__builtin_fma(t, em1, t), k >> 4);
+  return tiny ? 0.0 : y;
 }
 
 // ---- fixed-point mass of one value ------------------------------------------------------------

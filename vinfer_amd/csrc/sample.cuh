@@ -142,6 +142,8 @@ __device__ __forceinline__ T ld_global(const T* p) {
 
 // 16-byte block b of a bf16 row.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __align__(16) uint16_t g_unused_block[kBlk];  // (read, never written)
+
 __device__ __forceinline__ uint4 ld_block(const uint16_t* base, int b) {
   const u32x4_t v = ld_global(reinterpret_cast<const u32x4_t*>(base + b * kBlk));
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -155,27 +157,19 @@ __device__ const uint32_t kParamDefaults[16] = {0x3F800000u, 0x3F800000u, 0u, 0u
 // Parameter word w of row r (w >= kParamWords: a default, unused): every column is loaded
 // (uniform addresses, one load each) and the lane picks its word; selecting the column per lane
 // instead would index the argument struct, which then has to live in scratch memory.
+// Word w of row r's parameters, one load per lane: the lane picks its column's address (or the
+// default's) first, so nothing waits for the load until the word is used.
 template <bool PEN>
 __device__ __forceinline__ uint32_t param_word(const SampleArgs& a, int r, int w) {
-  auto col = [&](const void* c, int i, int d) -> uint32_t {
-    return ld_global(c ? static_cast<const uint32_t*>(c) + i : &kParamDefaults[d]);
-  };
-  uint32_t v[kParamWords];
-  v[0] = col(a.temp, r, 0);
-  v[1] = col(a.topp, r, 1);
-  v[2] = col(a.minp, r, 2);
-  v[3] = col(a.u, r, 3);
-  v[4] = col(a.topk, r, 4);
-  v[5] = col(a.draft, r, 5);
-  v[6] = col(PEN ? a.pen.rep : nullptr, r, 6);
-  v[7] = col(PEN ? a.pen.pres : nullptr, r, 7);
-  v[8] = col(PEN ? a.pen.freq : nullptr, r, 8);
-  v[9] = col(PEN ? a.off : nullptr, r, 9);
-  v[10] = col(PEN ? a.off : nullptr, r + 1, 10);
-  uint32_t x = 0;
+  const void* cols[kParamWords] = {a.temp, a.topp, a.minp, a.u, a.topk, a.draft,
+                                   PEN ? a.pen.rep : nullptr, PEN ? a.pen.pres : nullptr,
+                                   PEN ? a.pen.freq : nullptr, PEN ? a.off : nullptr, PEN ? a.off : nullptr};
+  const void* c = nullptr;
 #pragma unroll
-  for (int k = 0; k < kParamWords; ++k) x = w == k ? v[k] : x;
-  return x;
+  for (int k = 0; k < kParamWords; ++k) c = w == k ? cols[k] : c;
+  const int i = w == kParamWords - 1 ? r + 1 : r;
+  const uint32_t* q = c ? static_cast<const uint32_t*>(c) + i : &kParamDefaults[w];
+  return ld_global(q);
 }
 
 // ---- the fast path's history count ----------------------------------------------------------
@@ -210,6 +204,26 @@ __device__ __forceinline__ bool fast_insert(uint32_t* htab, uint32_t id) {
   }
   return false;
 }
+
+// Up to kPresMaxV ids the history is counted without hashing, in the same LDS (words of
+// ccnt .. eid, in order): a presence bitmap of the vocabulary (one bit per id, 64-bit words
+// from word kPresBits), the exclusive prefix of the bitmap words' popcounts (u16, after the
+// bitmap) and u16 counts indexed by the rank of an id among the distinct ids (words 0 ..
+// kThreads - 1). Setting the bits takes one non-returning atomic per id; ranks come from the
+// prefix and a popcount; a rank's id is written by the thread that owns its bitmap word (words
+// kPresPer * t .. + kPresPer - 1 belong to thread t) into words kPresBits .. (over the dead
+// bitmap). Distinct ids end in ascending id order.
+constexpr int kPresBits = kThreads;  // first word of the bitmap (and of the ids in rank order)
+constexpr int kPresRegion = kThreads + 2 * kThreads + 2 * kExcCap;  // words of ccnt .. eid
+constexpr int kPresPer = 3;          // bitmap words per thread
+constexpr int kPresMaxWords = (2 * (kPresRegion - kPresBits)) / 5;  // 64-bit words: 2 + 1/2 u32 each
+constexpr int kPresMaxV = 64 * kPresMaxWords;
+static_assert(kPresMaxWords <= kPresPer * kThreads && kPresBits + kExcCap <= offsetof(FastSmem, eval) / 4,
+              "bitmap words per thread; the ids in rank order must lie below eval");
+static_assert(offsetof(FastSmem, eid) == offsetof(FastSmem, eval) + sizeof(float) * kExcCap &&
+                  offsetof(FastSmem, lkey) == 4 * kPresRegion,
+              "ccnt .. eid must be contiguous");
+static_assert(kExcCap <= 2 * kThreads, "two ranks per thread");
 
 template <class Tin>
 struct Row {
@@ -1226,17 +1240,29 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   // A rolling prefetch: slot k of d holds block tid + (D * round + k) * kThreads and is reloaded
   // for the next round as soon as it is consumed (into the same registers: loading before the
   // old value is consumed would need a copy at the loop's end, which waits for every load).
+  // (A row with no full block loads a constant block instead, unused: loads issued on one branch
+  // only would make the first wait for the parameters wait for every load in flight.)
   constexpr int D = 4;
   uint4 d[D];
-  if (nfull > 0) {
+  {
+    const uint16_t* src = nfull > 0 ? base : g_unused_block;
 #pragma unroll
-    for (int k = 0; k < D; ++k) d[k] = ld_block(base, min(tid + k * kThreads, nfull - 1));
+    for (int k = 0; k < D; ++k) d[k] = ld_block(src, min(tid + k * kThreads, max(nfull - 1, 0)));
   }
   if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
   uint32_t* htab = fast_htab(f);
   for (int i = tid; i < kChunk / 4; i += kThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0, 0, 0, 0);
-  reinterpret_cast<uint4*>(htab)[tid] = make_uint4(kEmpty, kEmpty, kEmpty, kEmpty);
-  static_assert(kFastSlots == 4 * kThreads, "one uint4 of slots per thread");
+  // (uniform) the history is counted in a presence bitmap, else in the hash table
+  const bool presence = PEN && V <= kPresMaxV;
+  const int nw64 = (V + 63) / 64;
+  if (presence) {
+    // the counts and the bitmap
+    for (int i = tid; i < (kPresBits + 2 * nw64 + 3) / 4; i += kThreads)
+      reinterpret_cast<uint4*>(htab)[i] = make_uint4(0, 0, 0, 0);
+  } else {
+    reinterpret_cast<uint4*>(htab)[tid] = make_uint4(kEmpty, kEmpty, kEmpty, kEmpty);
+  }
+  static_assert(kFastSlots == 4 * kThreads && kPresBits % 4 == 0, "one uint4 of slots per thread");
   if (tid == 0) f.hfail = 0;
   if (tid == 0) {
     f.pchunk[0] = kThreads;
@@ -1247,11 +1273,16 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   const int L = PEN ? p.h1 - p.h0 : 0;
   const bool on = PEN && L > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
   const bool pen = on && L <= kFastMaxL;  // a longer history is counted by the generic path
-  uint32_t hid[kFastHistPer];  // history positions tid + k * kThreads (clamped to the last)
-  if (pen) {
-    const int32_t* h = a.pen.hist + p.h0;
+  // history positions tid + k * kThreads (clamped to the last). With PEN they are loaded whether
+  // or not the row counts a history (a row that does not reads the batch's first history id and
+  // ignores it): loads issued on one branch only make the first use of the row's blocks wait for
+  // every load.
+  uint32_t hid[kFastHistPer];
+  if constexpr (PEN) {
+    const int32_t* h = a.pen.hist + (pen ? p.h0 : 0);
+    const int hl = pen ? L - 1 : 0;
 #pragma unroll
-    for (int k = 0; k < kFastHistPer; ++k) hid[k] = static_cast<uint32_t>(ld_global(h + min(tid + k * kThreads, L - 1)));
+    for (int k = 0; k < kFastHistPer; ++k) hid[k] = static_cast<uint32_t>(ld_global(h + min(tid + k * kThreads, hl)));
   }
   // mx2: the largest key this thread has seen, per 16-bit half (the member search skips the
   // threads whose largest key is below the value it looks for)
@@ -1289,15 +1320,56 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     }
   };
   if (rounds > 0) round(0);
-  if (pen) {
+  // The presence path's four steps follow rounds 0 .. 3, each while the next round's blocks
+  // arrive: the bits and their prefix; ranks and counts; the ids in rank order; each thread's two
+  // entries (ranks tid and tid + kThreads), whose original values are then loaded.
+  uint32_t estep = 1;  // list positions of this thread's entries: e0, e0 + estep, ...
+  uint32_t* bm32 = htab + kPresBits;
+  const u64* bm64 = reinterpret_cast<const u64*>(bm32);
+  uint16_t* pre16 = reinterpret_cast<uint16_t*>(bm32 + 2 * nw64);
+  auto valid = [&](int k) { return tid + k * kThreads < L && hid[k] < static_cast<uint32_t>(V); };  // (ids outside [0, V) are skipped)
+  u64 bw[kPresPer] = {0, 0, 0};
+  uint32_t pw3[kPresPer] = {0, 0, 0};
+  static_assert(kPresPer == 3, "three words per thread");
+  if (pen && presence) {
+#pragma unroll
+    for (int k = 0; k < kFastHistPer; ++k)
+      if (valid(k)) atomicOr(&bm32[hid[k] >> 5], 1u << (hid[k] & 31u));
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < kPresPer; ++i) {
+      const int w = kPresPer * tid + i;
+      bw[i] = w < nw64 ? bm64[w] : 0ull;
+    }
+    const uint32_t n0 = __popcll(bw[0]), n1 = __popcll(bw[1]), n2 = __popcll(bw[2]);
+    e0 = block_excl_scan<uint32_t>(n0 + n1 + n2, f.red32, &nexc);
+    if (nexc > static_cast<uint32_t>(kExcCap)) return false;  // (uniform)
+    pw3[0] = e0;
+    pw3[1] = e0 + n0;
+    pw3[2] = e0 + n0 + n1;
+#pragma unroll
+    for (int i = 0; i < kPresPer; ++i)
+      if (kPresPer * tid + i < nw64) pre16[kPresPer * tid + i] = static_cast<uint16_t>(pw3[i]);
+  }
+  if (pen && !presence) {
     bool ok = true;
 #pragma unroll
-    for (int k = 0; k < kFastHistPer; ++k)  // (ids outside [0, V) are skipped)
-      if (tid + k * kThreads < L && hid[k] < static_cast<uint32_t>(V)) ok = fast_insert(htab, hid[k]) && ok;
+    for (int k = 0; k < kFastHistPer; ++k)
+      if (valid(k)) ok = fast_insert(htab, hid[k]) && ok;
     if (!ok) f.hfail = 1;
   }
   if (rounds > 1) round(1);
-  if (pen) {
+  if (pen && presence) {
+    lds_barrier();
+#pragma unroll
+    for (int k = 0; k < kFastHistPer; ++k) {
+      if (!valid(k)) continue;
+      const uint32_t w = hid[k] >> 6;
+      const uint32_t rank = pre16[w] + static_cast<uint32_t>(__popcll(bm64[w] & ((1ull << (hid[k] & 63u)) - 1ull)));
+      atomicAdd(&htab[rank >> 1], 1u << ((rank & 1u) << 4));
+    }
+  }
+  if (pen && !presence) {
     lds_barrier();
     const uint4 s4 = reinterpret_cast<const uint4*>(htab)[tid];
     sl[0] = s4.x;
@@ -1311,14 +1383,31 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     if (f.hfail || nexc > static_cast<uint32_t>(kExcCap)) return false;
   }
   if (on && !pen) return false;
+  if (rounds > 2) round(2);
+  uint32_t* ids = htab + kPresBits;
+  if (pen && presence) {
+    lds_barrier();  // (every read of the bitmap and the prefix is done: the ids go over them)
+#pragma unroll
+    for (int i = 0; i < kPresPer; ++i) {
+      uint32_t rk = pw3[i];
+      for (u64 m = bw[i]; m; m &= m - 1) ids[rk++] = 64u * (kPresPer * tid + i) + static_cast<uint32_t>(__builtin_ctzll(m));
+    }
+  }
+  if (rounds > 3) round(3);
+  if (pen && presence) {
+    lds_barrier();
+    const uint16_t* cnt16 = reinterpret_cast<const uint16_t*>(htab);
+    const uint32_t ra = tid, rb = tid + kThreads;
+    sl[0] = ra < nexc ? (ids[ra] << 13) | cnt16[ra] : kEmpty;  // (id << 13 | count)
+    sl[1] = rb < nexc ? (ids[rb] << 13) | cnt16[rb] : kEmpty;
+    e0 = tid;
+    estep = kThreads;
+  }
   uint32_t og[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) og[k] = ld_global(base + (sl[k] != kEmpty ? sl[k] >> 13 : 0u));
-  static_assert(kKeepRounds >= 2, "rounds 0 and 1 are peeled for the history stages");
-#pragma unroll
-  for (int it = 2; it < kKeepRounds; ++it)  // (peeled too: `kb` is indexed by constants only)
-    if (it < rounds) round(it);
-  for (int it = kKeepRounds; it < rounds; ++it) round(it);
+  static_assert(kKeepRounds <= 4, "the rounds whose blocks are kept are among the four peeled ones");
+  for (int it = 4; it < rounds; ++it) round(it);
   // the rest: a ragged tail, or every element of an unaligned row
   uint32_t mxk = mx2.x > mx2.y ? mx2.x : mx2.y;
   for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
@@ -1331,13 +1420,13 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     uint32_t e = e0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      if (sl[k] == kEmpty) continue;
+      if (sl[k] == kEmpty) continue;  // (the presence path fills sl[0] and sl[1] only)
       const uint32_t ko = ok16(og[k]);
       atomicAdd(&hist[ko >> 1], 0u - (1u << ((ko & 1u) << 4)));
       f.eid[e] = static_cast<int32_t>(sl[k] >> 13);
       f.eval[e] = apply_penalty(bf16_to_f32(static_cast<uint16_t>(og[k])), static_cast<int>(sl[k] & 0x1FFFu),
                                 p.rep, p.pres, p.freq);
-      ++e;
+      e += estep;
     }
   }
   const int ne = static_cast<int>(nexc);
@@ -1521,7 +1610,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
       const uint32_t K = 65535u - 64u * static_cast<uint32_t>(c) - l;
       const uint32_t n = hcount(hist, K);
       const float v = val16(K);
-      return (n && v >= x0) ? n * mass_q(ptilde(v, T, mz)) : 0ull;
+      return static_cast<u64>(v >= x0 ? n : 0u) * mass_q(ptilde(v, T, mz));  // (no branch)
     };
     // two chunks per round: their exp chains overlap
     while (todo) {
@@ -1716,9 +1805,10 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   const int r = blockIdx.x;
   const int tid = threadIdx.x;
   exp_table_init();  // (published by the first barrier of either path)
-  // the row's parameters: lane w of wave 0 loads word w, all in one vector load
-  uint32_t pw = 0;
-  if (tid < kWave) pw = param_word<PEN>(a, r, tid);
+  // the row's parameters: thread w < kParamWords loads word w, the others word 0 (every thread
+  // loads: a load on one branch only would make later waits wait for every load in flight)
+  const uint32_t pw = param_word<PEN>(a, r, tid < kParamWords ? tid : 0);
+  __builtin_amdgcn_sched_barrier(0);  // (issued before the row's first loads)
 
   Row<Tin> row;
   row.p = static_cast<const Tin*>(a.logits) + static_cast<int64_t>(r) * a.stride;
