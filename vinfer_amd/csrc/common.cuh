@@ -117,6 +117,19 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// ---- lanes of one wave exchanging LDS words without a workgroup barrier -------------------------
+// A wave's LDS operations complete in program order, so lanes can pass words to each other
+// through LDS with no barrier; but to the compiler the lanes are separate threads, and it may
+// forward a lane's own earlier store to a later read of the same word (on a path where the lane
+// did no atomic there itself) or move reads across the other lanes' updates. wave_lds_sync()
+// keeps LDS reads and writes from moving or being forwarded across it (a wavefront-scope fence:
+// no instruction), and lds_peek() reads a word as a relaxed atomic, which is never forwarded.
+__device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
+template <class T>
+__device__ __forceinline__ T lds_peek(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+
 // ---- uniform values ----------------------------------------------------------------------------
 // A value every lane holds the same copy of (read from LDS, say), moved to a scalar register:
 // branches on it are scalar branches and arithmetic with it takes a scalar operand.

@@ -934,8 +934,9 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
       f.lq[i] = q;
     }
   }
+  wave_lds_sync();  // (the lanes' counts, masses and list entries are in)
   WalkResult res;
-  res.ok = f.nl <= kMaxL;
+  res.ok = lds_peek(&f.nl) <= kMaxL;
   res.key = 0;
   res.n = 0;
   res.q = 0;
@@ -947,9 +948,9 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
   const bool inb = mode == kWalkCount || v >= x0;
   const uint32_t cb = inb ? cnt : 0u;
   const u64 qb = (mode != kWalkCount && cb) ? mass_q(ptilde(v, T, mz)) : 0ull;
-  const uint32_t bl = f.binc[l];
+  const uint32_t bl = lds_peek(&f.binc[l]);
   const uint32_t cl = cb + bl;
-  const u64 ml = (mode == kWalkCount ? static_cast<u64>(cl) : cb * qb + f.binm[l]);
+  const u64 ml = (mode == kWalkCount ? static_cast<u64>(cl) : cb * qb + lds_peek(&f.binm[l]));
   const u64 inc = wave_incl_scan<u64>(ml);
   const u64 ab = above + inc - ml;  // strictly above this key
   bool hit;
@@ -980,7 +981,8 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
   if (l == 0) {
     // move this key's penalised values to the front of the list, then sort them (descending)
     int n = 0;
-    for (uint32_t i = 0; i < f.nl; ++i) {
+    const uint32_t nl = lds_peek(&f.nl);
+    for (uint32_t i = 0; i < nl; ++i) {
       if ((f.lkey[i] >> 16) == Kw) {
         const uint32_t tk = f.lkey[n];
         const u64 tq = f.lq[n];
@@ -1146,7 +1148,12 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
       constexpr int D = 4;
       uint4 d[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) d[k] = ld_block(base, tid + max(nm - 1 - k, kKeep) * kThreads);
+      for (int k = 0; k < D; ++k) {
+        d[k] = ld_block(base, tid + max(nm - 1 - k, kKeep) * kThreads);
+        // (issued in slot order, the order they are used in: the loop's first wait is then for
+        // one load, not all four)
+        __builtin_amdgcn_sched_barrier(0);
+      }
       for (int m0 = nm - 1; m0 >= kKeep; m0 -= D) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
@@ -1406,8 +1413,11 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   uint32_t og[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) og[k] = ld_global(base + (sl[k] != kEmpty ? sl[k] >> 13 : 0u));
-  static_assert(kKeepRounds <= 4, "the rounds whose blocks are kept are among the four peeled ones");
-  for (int it = 4; it < rounds; ++it) round(it);
+  static_assert(kKeepRounds <= 4, "the rounds whose blocks are kept are among the peeled ones");
+  // (round 4 is peeled too: the first use of its blocks then waits for them alone, not for the
+  // original values just requested, as a wait at a loop's head would)
+  if (rounds > 4) round(4);
+  for (int it = 5; it < rounds; ++it) round(it);
   // the rest: a ragged tail, or every element of an unaligned row
   uint32_t mxk = mx2.x > mx2.y ? mx2.x : mx2.y;
   for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
@@ -1523,6 +1533,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
         // its value, then the smallest x with fl32(x / T) >= its z
         if (p.K > 0 && p.K < V) {
           for (int e = l; e < ne; e += kWave) atomicAdd(&f.ccnt[chunk_of16(key_of(f.eval[e]) >> 16)], 1u);
+          wave_lds_sync();
           uint32_t cc[16];
           uint32_t sum = 0;
 #pragma unroll
