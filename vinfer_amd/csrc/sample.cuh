@@ -1191,27 +1191,53 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   lds_barrier();
   // the cell holding the j-th member: per-thread member counts of `per` consecutive cells (one
   // popcount per 4 cells), then a scan
+  // (the thread's cells stay in registers: the thread holding the j-th member finds it there)
   const int c0 = tid * per;
+  constexpr int kCellWords = 8;  // per <= 32 (the caller's bound on cells_per)
+  uint32_t cv[kCellWords];
   uint32_t mine = 0;
-  for (int c = c0; c < c0 + per; c += 4) mine += __popc(cw[c >> 2]);
+#pragma unroll
+  for (int i = 0; i < kCellWords; ++i) {
+    cv[i] = 4 * i < per ? cw[(c0 >> 2) + i] : 0u;
+    mine += __popc(cv[i]);
+  }
   uint32_t total;
   const uint32_t before = block_excl_scan<uint32_t>(mine, f.red32, &total);
   if (tid == 0) f.si[6] = -1;
   lds_barrier();
   if (total > 0 && j < total && before <= j && j < before + mine) {
-    uint32_t acc = before;
-    for (int c = c0; c < c0 + per; ++c) {
-      const uint32_t mask = cells[c];
-      const uint32_t n = __popc(mask);
-      if (j < acc + n) {
-        // the (j - acc)-th set lane of block c
-        uint32_t m = mask;
-        for (uint32_t r = static_cast<uint32_t>(j - acc); r > 0; --r) m &= m - 1;
-        f.si[6] = c * kBlk + __ffs(m) - 1;
-        break;
+    // the word, then the cell (byte) within it, then the lane within the cell
+    uint32_t r = static_cast<uint32_t>(j - before), word = 0;
+    int wi = -1;
+#pragma unroll
+    for (int i = 0; i < kCellWords; ++i) {
+      const uint32_t n = __popc(cv[i]);
+      if (wi < 0) {
+        if (r < n) {
+          wi = i;
+          word = cv[i];
+        } else {
+          r -= n;
+        }
       }
-      acc += n;
     }
+    int bi = -1;
+    uint32_t mask = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t m8 = (word >> (8 * b)) & 0xFFu;
+      const uint32_t n = __popc(m8);
+      if (bi < 0) {
+        if (r < n) {
+          bi = b;
+          mask = m8;
+        } else {
+          r -= n;
+        }
+      }
+    }
+    for (; r > 0; --r) mask &= mask - 1;
+    f.si[6] = (c0 + 4 * wi + bi) * kBlk + __ffs(mask) - 1;
   }
   lds_barrier();
   const int res = f.si[6];
