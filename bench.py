@@ -92,64 +92,6 @@ def cpu_baseline(w, budget_s: float = 12.0):
     }
 
 
-def measured_traffic() -> int | None:
-    """HBM bytes per launch of the sampler kernel, from the counter summary's
-    `traffic_bytes_per_launch:` line (None when the summary has none)."""
-    try:
-        with open(PROFILE) as fh:
-            for line in fh:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip().replace(",", ""))
-    except OSError:
-        return None
-    return None
-
-
-def copy_probe() -> int:
-    """A plain device copy of COPY_PROBE_BYTES (bf16), launched 5 times: the reference the
-    FETCH_SIZE / WRITE_SIZE counters are scaled by."""
-    import torch
-
-    dev = torch.device("cuda", 0)
-    src = torch.empty(COPY_PROBE_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
-    dst = torch.empty_like(src)
-    torch.cuda.synchronize()
-    for _ in range(5):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "launches": 5}), flush=True)
-    return 0
-
-
-def cpu_baseline(w, budget_s: float = 12.0, max_rows: int = 256):
-    """The CPU oracle on rows of the same workload until ``budget_s`` of CPU work."""
-    from oracle.sampler_oracle import sample_batch  # the checker, timed here as the baseline
-
-    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
-    p = w.params
-    logits = f(w.logits)
-    cols = [f(getattr(p, k)) for k in ("temperature", "top_k", "top_p", "min_p")]
-    pens = [f(getattr(p, k)) for k in ("repetition_penalty", "presence_penalty", "frequency_penalty")]
-    hist, off, u = w.hist_ids.numpy(), w.hist_offsets.numpy(), f(w.uniforms)
-    rows, step, t0 = 0, 8, time.perf_counter()
-    while rows < max_rows and time.perf_counter() - t0 < budget_s:
-        sl = slice(rows, rows + step)
-        sample_batch(
-            logits[sl], *[c[sl] for c in cols], *[c[sl] for c in pens],
-            hist, off[rows : rows + step + 1], u[sl],
-        )
-        rows += step
-    dt = time.perf_counter() - t0
-    return {
-        "value": rows / dt,
-        "unit": "rows/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"first {rows} rows of the same workload ({rows // 2} peaked, {rows // 2} flat) "
-        f"with penalties, min-p and top-p; numpy fp64 oracle on one thread; {dt:.1f} s",
-    }
-
-
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
