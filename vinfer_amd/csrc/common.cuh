@@ -221,6 +221,18 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
   return v;
 }
 
+// Inclusive scan within each half of the wave (lanes 0-31, 32-63): lane 31 holds the sum of the
+// first half, lane 63 of the second.
+template <class T>
+__device__ __forceinline__ T half_incl_scan(T v) {
+  v += dpp::mov<dpp::kShr1>(v);
+  v += dpp::mov<dpp::kShr1 + 1>(v);
+  v += dpp::mov<dpp::kShr1 + 3>(v);
+  v += dpp::mov<dpp::kShr1 + 7>(v);
+  v += dpp::mov<dpp::kBcast15, 0xA>(v);
+  return v;
+}
+
 // For every lane with `valid`, acc[key] op= v through `at(key, value)`, lanes sharing a key
 // combined first: one LDS atomic per distinct key in the wave instead of one per lane (keys
 // that many lanes share would otherwise serialise). All 64 lanes must be active.

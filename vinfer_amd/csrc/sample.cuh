@@ -1637,34 +1637,32 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   {
     const float x0 = uniform_f(f.plan.x0);
     const uint32_t x0top = key_of(x0) >> 16;
-    // wave w takes chunks w + 16 l (lane l says which need work), then a lane per key of each:
-    // fp64 exps for populated keys only
+    // wave w takes chunks w + 16 l (lane l says which need work) two at a time: lanes 0-31 the
+    // first, lanes 32-63 the second, lane l the keys 2(l mod 32) and 2(l mod 32) + 1 of its chunk
+    // (one histogram word holds both counts); fp64 exps for populated keys only
     const int wv = tid / kWave, l = lane_id();
     const int cl = wv + kWaves * l;
     const bool need = f.ccnt[cl] > 0 && 65535u - 64u * static_cast<uint32_t>(cl) >= x0top;
     u64 todo = __ballot(need);
-    auto key_mass = [&](int c) -> u64 {
-      const uint32_t K = 65535u - 64u * static_cast<uint32_t>(c) - l;
-      const uint32_t n = hcount(hist, K);
-      const float v = val16(K);
-      return static_cast<u64>(v >= x0 ? n : 0u) * mass_q(ptilde(v, T, mz));  // (no branch)
-    };
-    // two chunks per round: their exp chains overlap
-    while (todo) {
+    const bool second = l >= 32;
+    const uint32_t l2 = static_cast<uint32_t>(l & 31);
+    while (todo) {  // (uniform)
       const int i1 = __ffsll(static_cast<long long>(todo)) - 1;
       todo &= todo - 1;
       const int i2 = todo ? __ffsll(static_cast<long long>(todo)) - 1 : -1;
       todo &= todo - 1;
-      const int c1 = wv + kWaves * i1;
-      const int c2 = wv + kWaves * (i2 < 0 ? i1 : i2);
-      const u64 m1 = key_mass(c1);
-      const u64 m2 = i2 < 0 ? 0ull : key_mass(c2);
-      const u64 s1 = wave_sum<u64>(m1);
-      const u64 s2 = wave_sum<u64>(m2);
-      if (l == 0) {
-        atomicAdd(&f.cmass[c1], s1);
-        if (i2 >= 0) atomicAdd(&f.cmass[c2], s2);
-      }
+      const bool live = !second || i2 >= 0;
+      const int c = wv + kWaves * (second && i2 >= 0 ? i2 : i1);
+      // keys Ka (odd: the word's high half) and Ka - 1
+      const uint32_t Ka = 65535u - 64u * static_cast<uint32_t>(c) - 2u * l2;
+      const uint32_t hw = hist[Ka >> 1];
+      const uint32_t na = live ? hw >> 16 : 0u, nb = live ? hw & 0xFFFFu : 0u;
+      const float va = val16(Ka), vb = val16(Ka - 1u);
+      // (no branch: both exps of a lane interleave; keys below x0 count 0)
+      u64 mq = static_cast<u64>(va >= x0 ? na : 0u) * mass_q(ptilde(va, T, mz)) +
+               static_cast<u64>(vb >= x0 ? nb : 0u) * mass_q(ptilde(vb, T, mz));
+      mq = half_incl_scan<u64>(mq);
+      if (l2 == 31u && live) atomicAdd(&f.cmass[c], mq);
     }
     for (int e = tid; e < ne; e += kThreads) {
       const float x = f.eval[e];
