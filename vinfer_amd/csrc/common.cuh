@@ -221,6 +221,16 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
   return v;
 }
 
+// Inclusive scan within each row of 16 lanes.
+template <class T>
+__device__ __forceinline__ T row_incl_scan(T v) {
+  v += dpp::mov<dpp::kShr1>(v);
+  v += dpp::mov<dpp::kShr1 + 1>(v);
+  v += dpp::mov<dpp::kShr1 + 3>(v);
+  v += dpp::mov<dpp::kShr1 + 7>(v);
+  return v;
+}
+
 // Inclusive scan within each half of the wave (lanes 0-31, 32-63): lane 31 holds the sum of the
 // first half, lane 63 of the second.
 template <class T>

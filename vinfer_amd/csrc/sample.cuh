@@ -1675,42 +1675,50 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     const int l = tid;
     int status2 = kPlanFast;
     float x0 = f.plan.x0;
-    // lane l holds chunks 16l .. 16l + 15
-    u64 m[16];
+    // lane l sums chunks 16l .. 16l + 15; a search inside the chunks of one lane L then gives
+    // lane i of every 16-lane row chunk 16L + i and the mass above it
     u64 sum = 0;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const uint4 v4 = *reinterpret_cast<const uint4*>(&f.cmass[16 * l + 2 * q]);
-      m[2 * q] = (static_cast<u64>(v4.y) << 32) | v4.x;
-      m[2 * q + 1] = (static_cast<u64>(v4.w) << 32) | v4.z;
-      sum += m[2 * q] + m[2 * q + 1];
+      sum += ((static_cast<u64>(v4.y) << 32) | v4.x) + ((static_cast<u64>(v4.w) << 32) | v4.z);
     }
     const u64 incl = wave_incl_scan<u64>(sum);
     const u64 S0 = dpp::last(incl);
     const u64 base = incl - sum;  // mass above chunk 16l
+    auto lane_chunks = [&](int L, u64& mq, u64& run) {
+      mq = f.cmass[16 * L + (l & 15)];
+      run = readlane64(base, L) + row_incl_scan<u64>(mq) - mq;
+    };
     Kept kk;
     kk.x0 = x0;
     kk.S = S0;
     if (p.tp < 1.0f) {
       const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
-      // the lowest chunk holding mass whose mass above is < P
+      // the last chunk holding mass whose mass above is < P: the chunks with mass above < P are
+      // a prefix, so it is in the last lane whose first chunk has mass above < P when that lane
+      // holds mass (its first chunk holding mass has that lane's mass above), else it is the
+      // last chunk holding mass of the lanes before
       int c = -1;
-      u64 ab = 0, run = base;
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        if (m[q] > 0 && static_cast<double>(run) < P) {
-          c = 16 * l + q;
-          ab = run;
+      u64 ab = 0;
+      const u64 below = __ballot(static_cast<double>(base) < P);
+      if (below) {
+        const int lb = 63 - __clzll(static_cast<long long>(below));
+        const bool in_lb = readlane64(sum, lb) > 0;
+        const u64 held = __ballot(sum > 0 && l < lb);
+        const int L = in_lb ? lb : (held ? 63 - __clzll(static_cast<long long>(held)) : -1);
+        if (L >= 0) {
+          u64 mq, run;
+          lane_chunks(L, mq, run);
+          const u64 hm = __ballot(mq > 0 && (!in_lb || static_cast<double>(run) < P)) & 0xFFFFull;
+          const int q = 63 - __clzll(static_cast<long long>(hm));  // (hm != 0: the lane holds mass)
+          c = 16 * L + q;
+          ab = readlane64(run, q);
         }
-        run += m[q];
       }
-      const u64 hm = __ballot(c >= 0);
-      if (!hm) {
+      if (c < 0) {
         status2 = kPlanGeneric;
       } else {
-        const int lw = 63 - __clzll(static_cast<long long>(hm));
-        c = __builtin_amdgcn_readlane(c, lw);
-        ab = readlane64(ab, lw);
         const WalkResult wr = wave_walk(hist, f, ne, c, kWalkCutoff, ab, P, x0, T, mz);
         if (!wr.ok) {
           status2 = kPlanGeneric;
@@ -1742,24 +1750,25 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
         vd = kk.vc;
         j = (td - kk.mabove_c) / kk.qc;
       } else {
-        // the chunk holding the target, then the value inside it
+        // the chunk holding the target (in the lane whose mass range holds it), then the value
+        // inside it
         int cd = -1;
-        u64 abd = 0, run = base;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          if (m[q] > 0 && run <= td && td < run + m[q]) {
-            cd = 16 * l + q;
-            abd = run;
+        u64 abd = 0;
+        const u64 hl = __ballot(sum > 0 && base <= td && td < base + sum);
+        if (hl) {
+          const int L = __ffsll(static_cast<long long>(hl)) - 1;
+          u64 mq, run;
+          lane_chunks(L, mq, run);
+          const u64 hm = __ballot(mq > 0 && run <= td && td < run + mq) & 0xFFFFull;
+          if (hm) {
+            const int q = __ffsll(static_cast<long long>(hm)) - 1;
+            cd = 16 * L + q;
+            abd = readlane64(run, q);
           }
-          run += m[q];
         }
-        const u64 hm = __ballot(cd >= 0);
-        if (!hm) {
+        if (cd < 0) {
           status2 = kPlanGeneric;
         } else {
-          const int lw = __ffsll(static_cast<long long>(hm)) - 1;
-          cd = __builtin_amdgcn_readlane(cd, lw);
-          abd = readlane64(abd, lw);
           const WalkResult wr = wave_walk(hist, f, ne, cd, kWalkCross, abd, static_cast<double>(td), x0, T, mz);
           if (!wr.ok) {
             status2 = kPlanGeneric;
