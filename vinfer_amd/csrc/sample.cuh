@@ -172,6 +172,16 @@ __device__ __forceinline__ uint32_t param_word(const SampleArgs& a, int r, int w
   return ld_global(q);
 }
 
+// floor(n / d), d > 0, for quotients below 2^32 (a member index): the double quotient is within
+// one of it (each operand and the division round by at most 2^-53), so one step up or down in
+// integers makes it exact -- a fraction of the 64-bit integer division's instructions.
+__device__ __forceinline__ u64 div_index(u64 n, u64 d) {
+  u64 q = static_cast<u64>(static_cast<double>(n) / static_cast<double>(d));
+  if (q * d > n) --q;
+  else if (n - q * d >= d) ++q;
+  return q;
+}
+
 // ---- the fast path's history count ----------------------------------------------------------
 // A history of at most kFastMaxL ids is counted in a kFastSlots-word LDS hash table over
 // ccnt/cmass/eval (dead until the histogram is complete) whose words pack (id << 13 | count):
@@ -1602,7 +1612,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
         // min-p: the smallest x with exp(fl32(x / T) - max z) >= min_p
         if (status == kPlanFast && p.mp > 0.0f) {
           const double dmp = static_cast<double>(p.mp);
-          const float guess = static_cast<float>(static_cast<double>(T) * (static_cast<double>(mz) + log(dmp)));
+          // (only a starting point for the bisection, which tests every step exactly)
+          const float guess = T * (mz + __logf(p.mp));
           const float xm = val_of(wave_bisect(lo_key, mkey, key_of(guess), [&](float x) { return ptilde(x, T, mz) >= dmp; }));
           x0 = xm > x0 ? xm : x0;
         }
@@ -1748,7 +1759,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
       const u64 td = td0 < kk.S ? td0 : kk.S - 1;
       if (kk.has_cut && td >= kk.mabove_c && kk.qc > 0) {
         vd = kk.vc;
-        j = (td - kk.mabove_c) / kk.qc;
+        j = div_index(td - kk.mabove_c, kk.qc);
       } else {
         // the chunk holding the target (in the lane whose mass range holds it), then the value
         // inside it
@@ -1774,7 +1785,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
             status2 = kPlanGeneric;
           } else {
             vd = val_of(wr.key);
-            j = wr.q ? (td - wr.above) / wr.q : 0ull;
+            j = wr.q ? div_index(td - wr.above, wr.q) : 0ull;
             if (j >= wr.n) j = wr.n ? wr.n - 1 : 0;
           }
         }
