@@ -1103,7 +1103,9 @@ __device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, uint32
 // vd. Per-thread popcounts of consecutive cells and a scan find the block; its mask, the lane.
 // Thread t reads the blocks it read in the histogram pass (t + m * kThreads, and the tail
 // elements t + n * kThreads): the first kKeep from `keep` (registers), the rest from memory,
-// last to first (the end of the row, read last, is the part most likely still in L2). `mxk` is
+// last to first (the end of the row, read last, is the part most likely still in L2); `first`
+// holds the first four of those, requested by the caller before the draw was known (see
+// member_prefetch). `mxk` is
 // the largest key the thread saw in that pass: a thread whose largest key is below vd's holds
 // no member and reads nothing. Needs row.bm built when the row has penalised ids.
 __device__ __forceinline__ int cells_per(const Row<uint16_t>& row) { return (row.nstripes + 3) & ~3; }
@@ -1112,8 +1114,24 @@ __device__ __forceinline__ int cells_per(const Row<uint16_t>& row) { return (row
 constexpr int kKeepRounds = 2;
 constexpr int kKeep = 4 * kKeepRounds;
 
+// The member search's first four reads (this thread's last four blocks beyond the kept ones,
+// clamped into the row), requested before the draw is known so that they arrive during the
+// cutoff and draw walks. Every thread requests them (no branch), used or not.
+__device__ __forceinline__ void member_prefetch(const Row<uint16_t>& row, uint4 (&first)[4]) {
+  const int tid = threadIdx.x;
+  const int nfull = row.vec ? row.V / kBlk : 0;
+  const int nm = tid < nfull ? (nfull - 1 - tid) / kThreads + 1 : 0;
+  const uint16_t* src = nfull > 0 ? row.p : g_unused_block;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    first[k] = ld_block(src, min(tid + max(nm - 1 - k, kKeep) * kThreads, max(nfull - 1, 0)));
+    __builtin_amdgcn_sched_barrier(0);  // (issued in slot order, the order they are used in)
+  }
+}
+
 __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, float vd, u64 j,
-                                            uint8_t* cells, uint32_t mxk, const uint4 (&keep)[kKeep]) {
+                                            uint8_t* cells, uint32_t mxk, const uint4 (&keep)[kKeep],
+                                            const uint4 (&first)[4]) {
   const int tid = threadIdx.x;
   const uint32_t vb = __float_as_uint(vd);
   const bool bf = (vb & 0xFFFFu) == 0u;  // vd is a bf16 value: bulk tokens can hold it
@@ -1156,14 +1174,10 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     const int nm = tid < nfull ? (nfull - 1 - tid) / kThreads + 1 : 0;
     if (cand && nm > kKeep) {
       constexpr int D = 4;
+      static_assert(D == 4, "the first four blocks come in `first`");
       uint4 d[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) {
-        d[k] = ld_block(base, tid + max(nm - 1 - k, kKeep) * kThreads);
-        // (issued in slot order, the order they are used in: the loop's first wait is then for
-        // one load, not all four)
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int k = 0; k < D; ++k) d[k] = first[k];
       for (int m0 = nm - 1; m0 >= kKeep; m0 -= D) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
@@ -1681,6 +1695,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     }
   }
   lds_barrier();
+  uint4 first[4];
+  member_prefetch(row, first);
   // ---- 6/7. [wave 0] the total, the top-p cutoff, the draw ---------------------------------
   if (tid < kWave) {
     const int l = tid;
@@ -1823,7 +1839,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   int draw = 0;
   if (!a.out_probs) {
     draw = cells_per(row) * kThreads <= 4 * kMatchWords
-               ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb)
+               ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb, first)
                : -1;
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
   }
