@@ -174,7 +174,30 @@ def _colliding_ids(V: int, first_bucket: int, buckets: int, per_bucket: int) -> 
     return out
 
 
-@pytest.mark.parametrize("V", [151936, 200000])  # history counted in a presence bitmap / a hash table
+def test_few_penalised_values_inside_the_walked_chunk():
+    # every logit is one of the 64 bf16 values 1 + k/128 (one chunk of 64 keys), so the cutoff
+    # and draw walks both run in that chunk; three penalised ids move by 2^-9 and stay in it, at
+    # keys whose lanes lie past the penalised list's length (the walk's per-key counts are then
+    # written only by other lanes)
+    rng = np.random.default_rng(5)
+    B, V = 16, 2048
+    vals = (1.0 + np.arange(64) / 128.0).astype(np.float32)
+    x = torch.from_numpy(vals[rng.integers(0, 64, (B, V))]).to(torch.bfloat16)
+    hist = []
+    for _ in range(B):
+        k = rng.integers(16, 60, 3)  # value indices: mid-chunk keys
+        ids = [int(rng.choice(np.flatnonzero(np.isclose(x[len(hist)].float().numpy(), vals[i])))) for i in k]
+        hist.append(ids)
+    hi, ho = pack_history(hist)
+    params = pack_params(
+        [SamplingParams(temperature=1.0, top_p=float(rng.choice([0.3, 0.5, 0.8])), presence_penalty=2.0**-9)
+         for _ in range(B)]
+    )
+    u = torch.from_numpy(rng.random(B, dtype=np.float32))
+    check(Workload("walk_chunk", x, params, u, hi, ho, None), max_tie_frac=0.25)
+
+
+@pytest.mark.parametrize("V", [151936, 157248, 157249, 200000])  # presence bitmap up to 157248, then hash
 def test_bf16_rows_the_histogram_path_hands_to_the_generic_path(V):
     # histories the bf16 histogram path does not count itself: longer than its table takes,
     # more distinct ids than its list holds, one probe run past its limit; beside normal rows
