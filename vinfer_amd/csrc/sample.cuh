@@ -1140,9 +1140,7 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   const uint16_t* base = row.p;
   const int V = row.V;
   const int per = cells_per(row);  // cells per thread in the scan (a multiple of 4)
-  uint32_t* cw = reinterpret_cast<uint32_t*>(cells);
-  for (int i = tid; i < per * kThreads / 4; i += kThreads) cw[i] = 0;
-  lds_barrier();
+  uint32_t* cw = reinterpret_cast<uint32_t*>(cells);  // (zeroed by the caller, f.si[6] = -1)
   auto cell_or = [&](int id) {
     const int b = id / kBlk;
     atomicOr(&cw[b >> 2], 1u << (8 * (b & 3) + id % kBlk));
@@ -1227,8 +1225,6 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   }
   uint32_t total;
   const uint32_t before = block_excl_scan<uint32_t>(mine, f.red32, &total);
-  if (tid == 0) f.si[6] = -1;
-  lds_barrier();
   if (total > 0 && j < total && before <= j && j < before + mine) {
     // the word, then the cell (byte) within it, then the lane within the cell
     uint32_t r = static_cast<uint32_t>(j - before), word = 0;
@@ -1264,9 +1260,7 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     f.si[6] = (c0 + 4 * wi + bi) * kBlk + __ffs(mask) - 1;
   }
   lds_barrier();
-  const int res = f.si[6];
-  lds_barrier();
-  return res;
+  return f.si[6];  // (nothing writes f.si[6] again in this launch)
 }
 
 // The bf16 fast path (every temperature: T <= 0 is greedy). Returns false (before writing any
@@ -1833,14 +1827,31 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   k.S = f.plan.S;
   const float vd = f.plan.vd;
   const u64 j = f.plan.j;
-  // the histogram is dead: the id searches below use its memory
-  if (ne > 0) build_bitmap(row, hist + kBitmapOffset);
+  // the histogram is dead: the id searches below use its memory. One pass zeroes the position
+  // bitmap of the penalised ids and the member search's cells.
+  const bool cells_fit = !a.out_probs && cells_per(row) * kThreads <= 4 * kMatchWords;
+  {
+    uint32_t* bmw = hist + kBitmapOffset;
+    const int nbw = ne > 0 ? (row.nblk + 3) / 4 : 0;
+    const int ncw = cells_fit ? cells_per(row) * kThreads / 4 : 0;
+    for (int i = tid; i < nbw; i += kThreads) bmw[i] = 0;
+    for (int i = tid; i < ncw; i += kThreads) hist[kMatchOffset + i] = 0;
+    if (tid == 0) f.si[6] = -1;
+    lds_barrier();
+    if (ne > 0) {
+      for (int e = tid; e < ne; e += kThreads) {
+        const uint32_t id = static_cast<uint32_t>(f.eid[e]);
+        atomicOr(&bmw[id >> 5], 1u << (id & 31u));
+      }
+      lds_barrier();
+      row.bm = reinterpret_cast<const uint8_t*>(bmw);
+    }
+  }
   resolve_idr(a, row, p, k, srch);
   int draw = 0;
   if (!a.out_probs) {
-    draw = cells_per(row) * kThreads <= 4 * kMatchWords
-               ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb, first)
-               : -1;
+    draw = cells_fit ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb, first)
+                     : -1;
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
   }
   finish(a, row, p, mz, k, draw, &srch.vslot);
