@@ -174,6 +174,31 @@ def _colliding_ids(V: int, first_bucket: int, buckets: int, per_bucket: int) -> 
     return out
 
 
+@pytest.mark.parametrize("V", [4096, 151936])
+def test_signed_zeros_are_one_value(V):
+    # -0.0 and +0.0 are one value: the bf16 histogram counts them under one key (a count past
+    # 65535 sends the row to the generic path), and the member search takes both bit patterns
+    rng = np.random.default_rng(17)
+    B = 8
+    x = (torch.randn(B, V, generator=torch.Generator().manual_seed(17)) * 0.5).to(torch.bfloat16)
+    zero = torch.from_numpy(rng.random((B, V)) < 0.5)
+    sign = torch.from_numpy(rng.random((B, V)) < 0.5)
+    z = torch.where(sign, torch.tensor(-0.0), torch.tensor(0.0)).to(torch.bfloat16)
+    x = torch.where(zero, z, x)
+    x[1] = torch.where(sign[1], torch.tensor(-0.0), torch.tensor(0.0)).to(torch.bfloat16)  # all zero
+    x[2] = torch.full((V,), -0.0).to(torch.bfloat16)  # all -0.0 but one +0.0
+    x[2, V // 3] = 0.0
+    x[3] = -x[3].abs()  # max 0 (either sign): greedy takes the first zero
+    params = pack_params(
+        [SamplingParams(temperature=float(t), top_p=float(tp), presence_penalty=0.5)
+         for t, tp in zip([1.0, 1.0, 1.0, 0.0, 0.7, 1.0, 0.0, 1.3], [0.9, 1.0, 0.5, 1.0, 0.95, 0.3, 1.0, 0.99])]
+    )
+    hist = [rng.integers(0, V, 50).tolist() for _ in range(B)]
+    hi, ho = pack_history(hist)
+    u = torch.from_numpy(rng.random(B, dtype=np.float32))
+    check(Workload("signed_zero", x, params, u, hi, ho, None), max_tie_frac=0.5)
+
+
 def test_few_penalised_values_inside_the_walked_chunk():
     # every logit is one of the 64 bf16 values 1 + k/128 (one chunk of 64 keys), so the cutoff
     # and draw walks both run in that chunk; three penalised ids move by 2^-9 and stay in it, at
