@@ -70,6 +70,20 @@ struct Radix {
   u64 hmass[256];
   uint32_t bk[4];
   u64 bq[4];
+  uint32_t ncand;  // elements >= x0 (the candidate list's length when it fits)
+};
+
+// The generic path's candidates: the elements >= x0 (bulk values and penalised values), copied
+// to LDS when at most kCandCap of them, so that the top-p cutoff and the draw descend over the
+// list instead of re-reading the row (two 4-level descents: eight passes over the row).
+struct Cand {
+  float x;
+  int32_t id;
+};
+constexpr int kCandCap = 4096;
+struct CandList {
+  const Cand* c;
+  int n;
 };
 
 struct GenericSmem {
@@ -602,7 +616,7 @@ enum MassMode { kCutoff = 0, kCross = 1 };
 //   kCross : the value whose group holds the target: above <= target < above + group mass
 // Returns the value's key; *n_c its count, *mass_c its group mass, *m_above the mass above it.
 template <class Tin>
-__device__ uint32_t radix_mass(const Row<Tin>& row, int mode, float x0, float T, float mz,
+__device__ uint32_t radix_mass(const Row<Tin>& row, const CandList* list, int mode, float x0, float T, float mz,
                                double target, Radix& s, uint32_t* n_c, u64* mass_c, u64* m_above) {
   uint32_t prefix = 0;
   u64 mprev = 0;
@@ -625,16 +639,25 @@ __device__ uint32_t radix_mass(const Row<Tin>& row, int mode, float x0, float T,
       const u64 q = m ? mass_q(ptilde(x, T, mz)) : 0ull;
       hist_mass(s.hcnt, s.hmass, (key >> shift) & 255u, q, m);
     };
-    for (int b = threadIdx.x, j = 0; j < row.nstripes; ++j, b += kThreads) {
-      float v[kBlk];
-      const uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
+    // (every lane calls `one` each round: its ballots and wave sums need the whole wave)
+    if (list) {
+      for (int i0 = 0; i0 < list->n; i0 += kThreads) {
+        const int i = i0 + threadIdx.x;
+        const bool ok = i < list->n;
+        one(ok ? list->c[i].x : 0.0f, ok);
+      }
+    } else {
+      for (int b = threadIdx.x, j = 0; j < row.nstripes; ++j, b += kThreads) {
+        float v[kBlk];
+        const uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
 #pragma unroll
-      for (int i = 0; i < kBlk; ++i) one(v[i], valid & (1u << i));
-    }
-    for (int e0 = 0; e0 < row.nexc; e0 += kThreads) {
-      const int e = e0 + threadIdx.x;
-      const bool ok = e < row.nexc;
-      one(ok ? row.eval[e] : 0.0f, ok);
+        for (int i = 0; i < kBlk; ++i) one(v[i], valid & (1u << i));
+      }
+      for (int e0 = 0; e0 < row.nexc; e0 += kThreads) {
+        const int e = e0 + threadIdx.x;
+        const bool ok = e < row.nexc;
+        one(ok ? row.eval[e] : 0.0f, ok);
+      }
     }
     __syncthreads();
     if (threadIdx.x < kWave) {
@@ -831,19 +854,38 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     __syncthreads();
   }
   u64 S0 = 0;
+  Cand* cand = reinterpret_cast<Cand*>(reinterpret_cast<uint32_t*>(&g) + kMatchOffset);
+  static_assert(kMatchOffset + 2 * kCandCap <= kChunk, "the candidate list must fit");
+  const bool listable = k.x0 > -INFINITY;  // (uniform) a threshold: usually few candidates
+  if (threadIdx.x == 0) g.rdx.ncand = 0;
+  __syncthreads();
   {
     const float x0 = k.x0;
-    for_each(row, [&](float x, int) {
-      if (x >= x0) S0 += mass_q(ptilde(x, T, mz));
+    for_each(row, [&](float x, int id) {
+      const bool c = x >= x0;
+      if (c) S0 += mass_q(ptilde(x, T, mz));
+      // the candidates of this round of the wave: one counter update per wave
+      const u64 bal = __ballot(listable && c);
+      if (bal) {
+        const int leader = __ffsll(static_cast<long long>(bal)) - 1;
+        uint32_t at = 0;
+        if (lane_id() == leader) at = atomicAdd(&g.rdx.ncand, static_cast<uint32_t>(__popcll(bal)));
+        at = __builtin_amdgcn_readlane(at, leader) +
+             static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
+        if (listable && c && at < static_cast<uint32_t>(kCandCap)) cand[at] = Cand{x, id};
+      }
     });
-    S0 = block_sum<u64>(S0, s.red64);
+    S0 = block_sum<u64>(S0, s.red64);  // (its barriers also publish the list)
   }
+  const uint32_t ncand = g.rdx.ncand;
+  const CandList cl{cand, static_cast<int>(ncand)};
+  const CandList* list = listable && ncand <= static_cast<uint32_t>(kCandCap) ? &cl : nullptr;
   k.S = S0;
   if (p.tp < 1.0f) {  // top-p (sampler.py:57-64)
     const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
     uint32_t nc;
     u64 massc, mabove;
-    const uint32_t ck = radix_mass(row, kCutoff, k.x0, T, mz, P, g.rdx, &nc, &massc, &mabove);
+    const uint32_t ck = radix_mass(row, list, kCutoff, k.x0, T, mz, P, g.rdx, &nc, &massc, &mabove);
     k.has_cut = true;
     k.vc = val_of(ck);
     k.qc = nc ? massc / nc : 0ull;
@@ -872,7 +914,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     } else {
       uint32_t nd;
       u64 massd, maboved;
-      const uint32_t dk = radix_mass(row, kCross, k.x0, T, mz, static_cast<double>(tdc), g.rdx, &nd, &massd,
+      const uint32_t dk = radix_mass(row, list, kCross, k.x0, T, mz, static_cast<double>(tdc), g.rdx, &nd, &massd,
                                      &maboved);
       vd = val_of(dk);
       const u64 qd = nd ? massd / nd : 0ull;
