@@ -548,7 +548,7 @@ __device__ __forceinline__ int find_first(const Row<Tin>& row, W wf, u64 target,
 
 // The key of the kth largest element (k >= 1).
 template <class Tin>
-__device__ uint32_t radix_kth(const Row<Tin>& row, uint32_t k, Radix& s) {
+__device__ uint32_t radix_kth(const Row<Tin>& row, const CandList* list, uint32_t k, Radix& s) {
   uint32_t prefix = 0;
   uint32_t kk = k;
   for (int lvl = 0; lvl < 4; ++lvl) {
@@ -561,22 +561,32 @@ __device__ uint32_t radix_kth(const Row<Tin>& row, uint32_t k, Radix& s) {
     __syncthreads();
     const bool all = lvl == 0;
     const uint32_t pfx = prefix;
-    for (int b = threadIdx.x, j = 0; j < row.nstripes; ++j, b += kThreads) {
-      float v[kBlk];
-      const uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
+    // (every lane calls hist_count each round: its ballots need the whole wave)
+    if (list) {
+      for (int i0 = 0; i0 < list->n; i0 += kThreads) {
+        const int i = i0 + threadIdx.x;
+        const bool ok = i < list->n;
+        const uint32_t key = key_of(ok ? list->c[i].x : 0.0f);
+        hist_count(s.hcnt, (key >> shift) & 255u, ok && (all || (key >> (shift + 8)) == pfx));
+      }
+    } else {
+      for (int b = threadIdx.x, j = 0; j < row.nstripes; ++j, b += kThreads) {
+        float v[kBlk];
+        const uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
 #pragma unroll
-      for (int i = 0; i < kBlk; ++i) {
-        const uint32_t key = key_of(v[i]);
-        const bool m = (valid & (1u << i)) && (all || (key >> (shift + 8)) == pfx);
+        for (int i = 0; i < kBlk; ++i) {
+          const uint32_t key = key_of(v[i]);
+          const bool m = (valid & (1u << i)) && (all || (key >> (shift + 8)) == pfx);
+          hist_count(s.hcnt, (key >> shift) & 255u, m);
+        }
+      }
+      for (int e0 = 0; e0 < row.nexc; e0 += kThreads) {
+        const int e = e0 + threadIdx.x;
+        const bool ok = e < row.nexc;
+        const uint32_t key = key_of(ok ? row.eval[e] : 0.0f);
+        const bool m = ok && (all || (key >> (shift + 8)) == pfx);
         hist_count(s.hcnt, (key >> shift) & 255u, m);
       }
-    }
-    for (int e0 = 0; e0 < row.nexc; e0 += kThreads) {
-      const int e = e0 + threadIdx.x;
-      const bool ok = e < row.nexc;
-      const uint32_t key = key_of(ok ? row.eval[e] : 0.0f);
-      const bool m = ok && (all || (key >> (shift + 8)) == pfx);
-      hist_count(s.hcnt, (key >> shift) & 255u, m);
     }
     __syncthreads();
     if (threadIdx.x < kWave) {
@@ -815,13 +825,24 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
   const int V = row.V;
   Search& s = g.srch;
   if (row.nexc > 0) build_bitmap(row, reinterpret_cast<uint32_t*>(&g) + kBitmapOffset);
-  // max (and first index of the max; NaN counts as the max)
+  // max (and first index of the max; NaN counts as the max); with top-k, in the same pass, a
+  // histogram of the keys' top 13 bits
+  const bool topk = p.K > 0 && p.K < V;  // (uniform)
+  uint32_t* h13 = reinterpret_cast<uint32_t*>(&g) + kMatchOffset;
+  constexpr int kTopBins = 8192;
+  static_assert(kMatchOffset + kTopBins <= kChunk && kTopBins == 8 * kThreads, "top-k bins: eight per thread");
+  if (topk) {
+    for (int i = threadIdx.x; i < kTopBins; i += kThreads) h13[i] = 0;
+    __syncthreads();
+  }
   u64 best = 0;
   for_each(row, [&](float x, int id) {
-    const u64 kq = (static_cast<u64>(key_of(x)) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(id));
+    const uint32_t key = key_of(x);
+    const u64 kq = (static_cast<u64>(key) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(id));
     best = kq > best ? kq : best;
+    if (topk) atomicAdd(&h13[key >> 19], 1u);
   });
-  best = block_max_u64(best, s.red64);
+  best = block_max_u64(best, s.red64);  // (its barriers also end the histogram)
   const uint32_t mkey = static_cast<uint32_t>(best >> 32);
   const int imax = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
   const float xmax = val_of(mkey);
@@ -833,8 +854,50 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     return;
   }
   const uint32_t lo_key = key_of(-INFINITY);
-  if (p.K > 0 && p.K < V) {  // top-k: keep z >= kth largest z (sampler.py:53-55)
-    const uint32_t kkey = radix_kth(row, static_cast<uint32_t>(p.K), g.rdx);
+  if (topk) {  // top-k: keep z >= kth largest z (sampler.py:53-55)
+    // the bin of the K-th largest key (thread t sums bins 8191 - 8t .. 8184 - 8t, descending),
+    // then the K'-th largest of that bin's elements, copied to LDS when they fit
+    const uint32_t K = static_cast<uint32_t>(p.K);
+    uint32_t c8[8], s8 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      c8[i] = h13[kTopBins - 1 - 8 * threadIdx.x - i];
+      s8 += c8[i];
+    }
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan<uint32_t>(s8, g.rdx.hcnt, &tot);  // (hcnt: free until the descent)
+    if (ex < K && K <= ex + s8) {
+      uint32_t above = ex;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (above < K && K <= above + c8[i]) {
+          g.rdx.bk[0] = static_cast<uint32_t>(kTopBins - 1 - 8 * threadIdx.x - i);
+          g.rdx.bk[1] = above;
+        }
+        above += c8[i];
+      }
+    }
+    if (threadIdx.x == 0) g.rdx.ncand = 0;
+    __syncthreads();  // (every read of the bins is done: the candidates go over them)
+    const uint32_t bin = g.rdx.bk[0], kin = K - g.rdx.bk[1];
+    Cand* cand = reinterpret_cast<Cand*>(h13);
+    for_each(row, [&](float x, int id) {
+      const bool c = (key_of(x) >> 19) == bin;
+      const u64 bal = __ballot(c);  // (one counter update per wave round)
+      if (bal) {
+        const int leader = __ffsll(static_cast<long long>(bal)) - 1;
+        uint32_t at = 0;
+        if (lane_id() == leader) at = atomicAdd(&g.rdx.ncand, static_cast<uint32_t>(__popcll(bal)));
+        at = __builtin_amdgcn_readlane(at, leader) +
+             static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
+        if (c && at < static_cast<uint32_t>(kCandCap)) cand[at] = Cand{x, id};
+      }
+    });
+    __syncthreads();
+    const uint32_t nb = g.rdx.ncand;
+    const CandList bl{cand, static_cast<int>(nb)};
+    const uint32_t kkey = nb <= static_cast<uint32_t>(kCandCap) ? radix_kth(row, &bl, kin, g.rdx)
+                                                                : radix_kth(row, nullptr, K, g.rdx);
     if (threadIdx.x == 0) {
       const float kz = val_of(kkey) / T;
       g.rdx.bk[2] = bisect_key(lo_key, kkey, [&](float x) { return x / T >= kz; });
