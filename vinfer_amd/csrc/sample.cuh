@@ -854,6 +854,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     return;
   }
   const uint32_t lo_key = key_of(-INFINITY);
+  uint32_t topbin = 0, ntop = kCandCap + 1u;  // the top-k candidates: bins >= topbin, ntop of them
   if (topk) {  // top-k: keep z >= kth largest z (sampler.py:53-55)
     // the bin of the K-th largest key (thread t sums bins 8191 - 8t .. 8184 - 8t, descending),
     // then the K'-th largest of that bin's elements, copied to LDS when they fit
@@ -879,10 +880,13 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     }
     if (threadIdx.x == 0) g.rdx.ncand = 0;
     __syncthreads();  // (every read of the bins is done: the candidates go over them)
-    const uint32_t bin = g.rdx.bk[0], kin = K - g.rdx.bk[1];
+    // every element of that bin and the bins above (at most K - 1 of those): the K-th largest of
+    // them is the row's; they hold every element >= x0 when x0 falls in those bins
+    const uint32_t bin = g.rdx.bk[0];
+    topbin = bin;
     Cand* cand = reinterpret_cast<Cand*>(h13);
     for_each(row, [&](float x, int id) {
-      const bool c = (key_of(x) >> 19) == bin;
+      const bool c = (key_of(x) >> 19) >= bin;
       const u64 bal = __ballot(c);  // (one counter update per wave round)
       if (bal) {
         const int leader = __ffsll(static_cast<long long>(bal)) - 1;
@@ -895,8 +899,9 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     });
     __syncthreads();
     const uint32_t nb = g.rdx.ncand;
+    ntop = nb;
     const CandList bl{cand, static_cast<int>(nb)};
-    const uint32_t kkey = nb <= static_cast<uint32_t>(kCandCap) ? radix_kth(row, &bl, kin, g.rdx)
+    const uint32_t kkey = nb <= static_cast<uint32_t>(kCandCap) ? radix_kth(row, &bl, K, g.rdx)
                                                                 : radix_kth(row, nullptr, K, g.rdx);
     if (threadIdx.x == 0) {
       const float kz = val_of(kkey) / T;
@@ -919,7 +924,15 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
   u64 S0 = 0;
   Cand* cand = reinterpret_cast<Cand*>(reinterpret_cast<uint32_t*>(&g) + kMatchOffset);
   static_assert(kMatchOffset + 2 * kCandCap <= kChunk, "the candidate list must fit");
+  // (uniform) the top-k candidates already hold every element >= x0: no pass over the row
+  const bool reuse = ntop <= static_cast<uint32_t>(kCandCap) && (key_of(k.x0) >> 19) >= topbin;
   const bool listable = k.x0 > -INFINITY;  // (uniform) a threshold: usually few candidates
+  if (reuse) {
+    const float x0 = k.x0;
+    for (int i = threadIdx.x; i < static_cast<int>(ntop); i += kThreads)
+      if (cand[i].x >= x0) S0 += mass_q(ptilde(cand[i].x, T, mz));
+    S0 = block_sum<u64>(S0, s.red64);
+  } else {
   if (threadIdx.x == 0) g.rdx.ncand = 0;
   __syncthreads();
   {
@@ -940,9 +953,10 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     });
     S0 = block_sum<u64>(S0, s.red64);  // (its barriers also publish the list)
   }
-  const uint32_t ncand = g.rdx.ncand;
+  }
+  const uint32_t ncand = reuse ? ntop : g.rdx.ncand;
   const CandList cl{cand, static_cast<int>(ncand)};
-  const CandList* list = listable && ncand <= static_cast<uint32_t>(kCandCap) ? &cl : nullptr;
+  const CandList* list = (reuse || listable) && ncand <= static_cast<uint32_t>(kCandCap) ? &cl : nullptr;
   k.S = S0;
   if (p.tp < 1.0f) {  // top-p (sampler.py:57-64)
     const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
