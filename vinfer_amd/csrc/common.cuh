@@ -123,11 +123,16 @@ __device__ __forceinline__ void lds_barrier() {
 // forward a lane's own earlier store to a later read of the same word (on a path where the lane
 // did no atomic there itself) or move reads across the other lanes' updates. wave_lds_sync()
 // keeps LDS reads and writes from moving or being forwarded across it (a wavefront-scope fence:
-// no instruction), and lds_peek() reads a word as a relaxed atomic, which is never forwarded.
+// no instruction); lds_peek() / lds_poke() read and write a word as relaxed atomics, which are
+// never forwarded.
 __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
 template <class T>
 __device__ __forceinline__ T lds_peek(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+template <class T>
+__device__ __forceinline__ void lds_poke(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 
 // ---- uniform values ----------------------------------------------------------------------------

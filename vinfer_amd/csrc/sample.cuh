@@ -998,7 +998,38 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
       j = qd ? (tdc - maboved) / qd : 0ull;
       if (j >= nd) j = nd ? nd - 1 : 0;
     }
-    draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, s);
+    // the j-th (ascending id) element equal to vd: from the candidate list when it holds at
+    // most 64 of them (wave 0 ranks their ids), else from the row
+    draw = -1;
+    if (list) {
+      if (threadIdx.x < kWave) {
+        const int l = lane_id();
+        uint32_t* ids = g.rdx.hcnt;  // (free: the descents are done)
+        uint32_t cnt = 0;  // (uniform)
+        for (int i0 = 0; i0 < list->n; i0 += kWave) {
+          const int i = i0 + l;
+          const bool m = i < list->n && list->c[i].x == vd;
+          const u64 bal = __ballot(m);
+          const uint32_t pos = cnt + static_cast<uint32_t>(__popcll(bal & ((1ull << l) - 1ull)));
+          if (m && pos < static_cast<uint32_t>(kWave)) lds_poke(&ids[pos], static_cast<uint32_t>(list->c[i].id));
+          cnt += static_cast<uint32_t>(__popcll(bal));
+        }
+        int res = -1;
+        if (cnt <= static_cast<uint32_t>(kWave) && j < cnt) {
+          wave_lds_sync();
+          const uint32_t mine = static_cast<uint32_t>(l) < cnt ? lds_peek(&ids[l]) : 0xFFFFFFFFu;
+          uint32_t rank = 0;
+          for (uint32_t q = 0; q < cnt; ++q) rank += __builtin_amdgcn_readlane(mine, q) < mine ? 1u : 0u;
+          const u64 hit = __ballot(static_cast<uint32_t>(l) < cnt && rank == j);
+          if (hit) res = static_cast<int>(__builtin_amdgcn_readlane(mine, __ffsll(static_cast<long long>(hit)) - 1));
+        }
+        if (l == 0) g.rdx.bk[2] = static_cast<uint32_t>(res);
+      }
+      __syncthreads();
+      draw = static_cast<int>(g.rdx.bk[2]);
+      __syncthreads();
+    }
+    if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, s);
   }
   finish(a, row, p, mz, k, draw, &s.vslot);
 }
