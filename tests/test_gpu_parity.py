@@ -93,6 +93,34 @@ def test_probabilities_match_the_oracle(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_long_history_counts_are_exact(dtype):
+    # histories past the hash table's length: counted through a presence bitmap of the
+    # vocabulary, or in windows of ids when the distinct ids do not fit beside it (60000 here)
+    V = 151936
+    rng = np.random.default_rng(8)
+    w = random_workload(4, 4, V, dtype, hist_len=10)
+    perm = rng.permutation(V)
+    hist = [
+        workloads.zipf_ids(rng, 20000, V, 1.05, perm).tolist(),
+        rng.permutation(V)[:60000].tolist(),  # 60000 distinct ids
+        (workloads.zipf_ids(rng, 30000, V, 1.1, perm).tolist() + [-3, V, V + 9]),
+        rng.integers(0, V, 65535).tolist(),
+    ]
+    w.hist_ids, w.hist_offsets = pack_history(hist)
+    p = w.params
+    p.presence_penalty.fill_(0.5)
+    d = w.to(DEV)
+    xs, counts = hip(dtype).penalized_logits(d.logits, d.params, d.hist_ids, d.hist_offsets)
+    xs, counts = xs.cpu().numpy(), counts.cpu().numpy()
+    for b in range(w.batch):
+        x, c = penalize(w.logits[b].float().numpy(), np.array(hist[b]), float(p.repetition_penalty[b]),
+                        float(p.presence_penalty[b]), float(p.frequency_penalty[b]))
+        assert np.array_equal(counts[b], c), b
+        assert np.array_equal(xs[b].view(np.uint32), x.view(np.uint32)), b
+    check(w, max_tie_frac=0.5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
 def test_penalty_counts_and_values_are_exact(dtype):
     w = random_workload(3, 16, 5000, dtype, hist_len=3000)
     # one row with a single id repeated far past 2^16

@@ -137,6 +137,86 @@ __device__ __forceinline__ void gather_values(const PenaltyArgs& a, const Tin* r
   }
 }
 
+// Long histories (more than kHashMaxL ids, at most 65535) over a vocabulary of at most kBmMaxV
+// ids: a presence bitmap of the vocabulary (one non-returning atomic per history id), the
+// exclusive prefix of its 64-bit words' popcounts, then u16 counts indexed by the rank of an id
+// among the distinct ids (prefix + popcount below it; a second pass over the history). Thread t
+// owns bitmap words kBmPer * t .. + kBmPer - 1 and writes their ids' (id, count) pairs in rank
+// order. Returns false (having written nothing) when the distinct ids do not fit: the caller
+// then counts in windows.
+constexpr int kBmPer = 4;                       // 64-bit bitmap words per thread
+constexpr int kBmMaxV = 64 * kBmPer * kThreads;  // 262144
+template <class Tin>
+__device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, int r, uint32_t* lds, uint32_t* red, ExcCache ec,
+                                             int h0, int L, int V, bool on, int32_t* dc, float rep, float pres,
+                                             float freq, const Tin* row, const int32_t* hist, uint32_t* n_out) {
+  const int tid = threadIdx.x;
+  const int nw = (V + 63) / 64;  // 64-bit bitmap words
+  u64* bm = reinterpret_cast<u64*>(lds);
+  uint16_t* pre = reinterpret_cast<uint16_t*>(lds + 2 * nw);  // u16 prefix per word
+  uint32_t* cnt = lds + 2 * nw + (nw + 1) / 2;                 // u16 counts by rank, in pairs
+  const int cap = 2 * (kChunk - (2 * nw + (nw + 1) / 2));       // ranks that fit
+  for (int i = tid; i < 2 * nw; i += kThreads) lds[i] = 0;
+  lds_barrier();
+  for (int i = tid; i < L; i += kThreads) {
+    const int id = hist[i];
+    if (id >= 0 && id < V) atomicOr(&lds[id >> 5], 1u << (id & 31));
+  }
+  lds_barrier();
+  u64 w[kBmPer];
+  uint32_t n = 0;
+#pragma unroll
+  for (int k = 0; k < kBmPer; ++k) {
+    const int wi = kBmPer * tid + k;
+    w[k] = wi < nw ? bm[wi] : 0ull;
+    n += __popcll(w[k]);
+  }
+  uint32_t total;
+  const uint32_t e0 = block_excl_scan<uint32_t>(n, red, &total);
+  if (total > static_cast<uint32_t>(cap) || total > 0xFFFFu) return false;  // (uniform)
+  uint32_t pw[kBmPer];
+  {
+    uint32_t e = e0;
+#pragma unroll
+    for (int k = 0; k < kBmPer; ++k) {
+      pw[k] = e;
+      const int wi = kBmPer * tid + k;
+      if (wi < nw) pre[wi] = static_cast<uint16_t>(e);
+      e += __popcll(w[k]);
+    }
+  }
+  for (int i = tid; i < static_cast<int>((total + 1) / 2); i += kThreads) cnt[i] = 0;
+  lds_barrier();
+  for (int i = tid; i < L; i += kThreads) {
+    const int id = hist[i];
+    if (id < 0 || id >= V) continue;
+    const int wi = id >> 6;
+    const uint32_t rank = pre[wi] + static_cast<uint32_t>(__popcll(bm[wi] & ((1ull << (id & 63)) - 1ull)));
+    atomicAdd(&cnt[rank >> 1], 1u << ((rank & 1u) << 4));
+  }
+  lds_barrier();
+  // (id, count) pairs in rank order
+#pragma unroll
+  for (int k = 0; k < kBmPer; ++k) {
+    uint32_t e = pw[k];
+    for (u64 m = w[k]; m; m &= m - 1) {
+      const int id = 64 * (kBmPer * tid + k) + static_cast<int>(__builtin_ctzll(m));
+      const int c = static_cast<int>((cnt[e >> 1] >> ((e & 1u) << 4)) & 0xFFFFu);
+      if (dc) dc[id] = c;
+      if (on) {
+        a.ws.exc_id[h0 + e] = id;
+        a.ws.exc_cnt[h0 + e] = c;
+      }
+      ++e;
+    }
+  }
+  // the (id, count) pairs were written by other threads of this workgroup: full barrier
+  __syncthreads();
+  if (on) gather_values<Tin>(a, row, h0, total, nullptr, 0, rep, pres, freq, ec);
+  *n_out = total;
+  return true;
+}
+
 // Row r's penalty pass, run by a whole workgroup; `lds` is kChunk words and `red` kWaves words.
 // Writes the row's exceptions to the workspace (global memory: a reader in the same workgroup
 // needs a __syncthreads() first) and, up to ec.cap of them, to `ec` in LDS (visible on return).
@@ -216,6 +296,9 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
     }
     lds_barrier();
     if (on) gather_values<Tin>(a, row, h0, n_total, stage, n_total, rep, pres, freq, ec);
+  } else if (V <= kBmMaxV && L <= 0xFFFF && bitmap_count<Tin>(a, r, lds, red, ec, h0, L, V, on, dc, rep, pres, freq,
+                                                                row, hist, &n_total)) {
+    // (counted through a presence bitmap: two passes over the history)
   } else {
     // ---- long histories: count a window of ids at a time ----
     uint32_t* cnt = lds;
