@@ -226,6 +226,13 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
   return v;
 }
 
+// A 64-bit value of one lane, in every lane.
+__device__ __forceinline__ u64 readlane64(u64 x, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(x >> 32), lane);
+  return (static_cast<u64>(hi) << 32) | lo;
+}
+
 // Inclusive scan within each row of 16 lanes.
 template <class T>
 __device__ __forceinline__ T row_incl_scan(T v) {

@@ -627,11 +627,17 @@ enum MassMode { kCutoff = 0, kCross = 1 };
 // Returns the value's key; *n_c its count, *mass_c its group mass, *m_above the mass above it.
 template <class Tin>
 __device__ uint32_t radix_mass(const Row<Tin>& row, const CandList* list, int mode, float x0, float T, float mz,
-                               double target, Radix& s, uint32_t* n_c, u64* mass_c, u64* m_above) {
-  uint32_t prefix = 0;
-  u64 mprev = 0;
-  for (int lvl = 0; lvl < 4; ++lvl) {
-    const int shift = 24 - 8 * lvl;
+                               double target, Radix& s, uint32_t* n_c, u64* mass_c, u64* m_above,
+                               uint32_t prefix0 = 0, int bits0 = 0, u64 mprev0 = 0) {
+  // the descent starts below a known prefix of bits0 key bits (the elements above it hold mass
+  // mprev0), then takes digits of up to 8 bits
+  uint32_t prefix = prefix0;
+  u64 mprev = mprev0;
+  for (int done = bits0; done < 32;) {
+    const int width = 32 - done < 8 ? 32 - done : 8;
+    const int shift = 32 - done - width;
+    const uint32_t dmask = (1u << width) - 1u;
+    const bool all = done == 0;
     for (int i = threadIdx.x; i < 256; i += kThreads) {
       s.hcnt[i] = 0;
       s.hmass[i] = 0;
@@ -645,9 +651,9 @@ __device__ uint32_t radix_mass(const Row<Tin>& row, const CandList* list, int mo
     __syncthreads();
     auto one = [&](float x, bool valid) {
       const uint32_t key = key_of(x);
-      const bool m = valid && x >= x0 && (lvl == 0 || (key >> (shift + 8)) == prefix);
+      const bool m = valid && x >= x0 && (all || (key >> (shift + width)) == prefix);
       const u64 q = m ? mass_q(ptilde(x, T, mz)) : 0ull;
-      hist_mass(s.hcnt, s.hmass, (key >> shift) & 255u, q, m);
+      hist_mass(s.hcnt, s.hmass, (key >> shift) & dmask, q, m);
     };
     // (every lane calls `one` each round: its ballots and wave sums need the whole wave)
     if (list) {
@@ -710,11 +716,12 @@ __device__ uint32_t radix_mass(const Row<Tin>& row, const CandList* list, int mo
       }
     }
     __syncthreads();
-    prefix = (prefix << 8) | s.bk[0];
+    prefix = (prefix << width) | s.bk[0];
     mprev = s.bq[0];
     *n_c = s.bk[1];
     *mass_c = s.bq[1];
     __syncthreads();
+    done += width;
   }
   *m_above = mprev;
   return prefix;
@@ -820,8 +827,55 @@ __device__ __forceinline__ void resolve_idr(const SampleArgs& a, const Row<Tin>&
 }
 
 // ---- generic path -----------------------------------------------------------------------------
+// The generic path's chunk masses: chunk c holds the keys whose top 10 bits are 1023 - c (so
+// chunk 0 holds the largest values). Wave 0 picks the chunk a mass descent starts in and the
+// mass above it, with the comparisons radix_mass makes on its digits:
+//   kCutoff: the last chunk holding mass whose mass above is < target;
+//   kCross : the chunk with mass above <= target < mass above + its mass.
+// Lane l sums chunks 16l .. 16l + 15; the chunks of one lane are then searched across a 16-lane
+// row. Returns -1 when no chunk qualifies (the caller descends over the whole row instead).
+__device__ __forceinline__ int chunk_pick(const u64* cm, int mode, double target, u64* above_out) {
+  const int l = lane_id();
+  u64 sum = 0;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) sum += cm[16 * l + q];
+  const u64 incl = wave_incl_scan<u64>(sum);
+  const u64 base = incl - sum;
+  int L = -1;
+  if (mode == kCutoff) {
+    // the chunks with mass above < target are a prefix: the last lane starting below it when
+    // that lane holds mass, else the last lane before it holding mass
+    const u64 below = __ballot(static_cast<double>(base) < target);
+    if (below) {
+      const int lb = 63 - __clzll(static_cast<long long>(below));
+      const u64 held = __ballot(sum > 0 && l <= lb);
+      L = held ? 63 - __clzll(static_cast<long long>(held)) : -1;
+    }
+  } else {
+    const u64 hl = __ballot(sum > 0 && static_cast<double>(base) <= target && target < static_cast<double>(base + sum));
+    L = hl ? __ffsll(static_cast<long long>(hl)) - 1 : -1;
+  }
+  if (L < 0) return -1;
+  const u64 mq = cm[16 * L + (l & 15)];
+  const u64 run = readlane64(base, L) + row_incl_scan<u64>(mq) - mq;
+  u64 hm;
+  if (mode == kCutoff) {
+    hm = __ballot(mq > 0 && static_cast<double>(run) < target) & 0xFFFFull;
+    if (!hm) return -1;
+    const int q = 63 - __clzll(static_cast<long long>(hm));
+    *above_out = readlane64(run, q);
+    return 16 * L + q;
+  }
+  hm = __ballot(mq > 0 && static_cast<double>(run) <= target && target < static_cast<double>(run + mq)) & 0xFFFFull;
+  if (!hm) return -1;
+  const int q = __ffsll(static_cast<long long>(hm)) - 1;
+  *above_out = readlane64(run, q);
+  return 16 * L + q;
+}
+
 template <class Tin>
-__device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g) {
+__device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g,
+                                            FastSmem& f) {
   const int V = row.V;
   Search& s = g.srch;
   if (row.nexc > 0) build_bitmap(row, reinterpret_cast<uint32_t*>(&g) + kBitmapOffset);
@@ -934,12 +988,19 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     S0 = block_sum<u64>(S0, s.red64);
   } else {
   if (threadIdx.x == 0) g.rdx.ncand = 0;
+  // (chunk masses of the elements >= x0: they lead the descents when the list does not fit)
+  f.cmass[threadIdx.x] = 0;
+  static_assert(kThreads == 1024, "one chunk per thread");
   __syncthreads();
   {
     const float x0 = k.x0;
     for_each(row, [&](float x, int id) {
       const bool c = x >= x0;
-      if (c) S0 += mass_q(ptilde(x, T, mz));
+      if (c) {
+        const u64 q = mass_q(ptilde(x, T, mz));
+        S0 += q;
+        atomicAdd(&f.cmass[(0xFFFFFFFFu - key_of(x)) >> 22], q);
+      }
       // the candidates of this round of the wave: one counter update per wave
       const u64 bal = __ballot(listable && c);
       if (bal) {
@@ -962,7 +1023,25 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
     uint32_t nc;
     u64 massc, mabove;
-    const uint32_t ck = radix_mass(row, list, kCutoff, k.x0, T, mz, P, g.rdx, &nc, &massc, &mabove);
+    uint32_t ck;
+    if (list) {
+      ck = radix_mass(row, list, kCutoff, k.x0, T, mz, P, g.rdx, &nc, &massc, &mabove);
+    } else {
+      if (threadIdx.x < kWave) {
+        u64 ab = 0;
+        const int c = chunk_pick(f.cmass, kCutoff, P, &ab);
+        if (lane_id() == 0) {
+          g.rdx.bk[2] = static_cast<uint32_t>(c);
+          g.rdx.bq[2] = ab;
+        }
+      }
+      __syncthreads();
+      const int c = static_cast<int>(g.rdx.bk[2]);
+      const u64 ab = g.rdx.bq[2];
+      __syncthreads();
+      ck = c >= 0 ? radix_mass(row, nullptr, kCutoff, k.x0, T, mz, P, g.rdx, &nc, &massc, &mabove, 1023u - c, 10, ab)
+                  : radix_mass(row, nullptr, kCutoff, k.x0, T, mz, P, g.rdx, &nc, &massc, &mabove);
+    }
     k.has_cut = true;
     k.vc = val_of(ck);
     k.qc = nc ? massc / nc : 0ull;
@@ -991,8 +1070,29 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     } else {
       uint32_t nd;
       u64 massd, maboved;
-      const uint32_t dk = radix_mass(row, list, kCross, k.x0, T, mz, static_cast<double>(tdc), g.rdx, &nd, &massd,
-                                     &maboved);
+      uint32_t dk;
+      if (list) {
+        dk = radix_mass(row, list, kCross, k.x0, T, mz, static_cast<double>(tdc), g.rdx, &nd, &massd, &maboved);
+      } else {
+        // (the chunk masses hold the elements >= the pre-cutoff x0; the draw lands above the
+        // cutoff value here, where they are exact)
+        if (threadIdx.x < kWave) {
+          u64 ab = 0;
+          const int c = chunk_pick(f.cmass, kCross, static_cast<double>(tdc), &ab);
+          if (lane_id() == 0) {
+            g.rdx.bk[2] = static_cast<uint32_t>(c);
+            g.rdx.bq[2] = ab;
+          }
+        }
+        __syncthreads();
+        const int c = static_cast<int>(g.rdx.bk[2]);
+        const u64 ab = g.rdx.bq[2];
+        __syncthreads();
+        dk = c >= 0 ? radix_mass(row, nullptr, kCross, k.x0, T, mz, static_cast<double>(tdc), g.rdx, &nd, &massd,
+                                 &maboved, 1023u - c, 10, ab)
+                    : radix_mass(row, nullptr, kCross, k.x0, T, mz, static_cast<double>(tdc), g.rdx, &nd, &massd,
+                                 &maboved);
+      }
       vd = val_of(dk);
       const u64 qd = nd ? massd / nd : 0ull;
       j = qd ? (tdc - maboved) / qd : 0ull;
@@ -1060,11 +1160,6 @@ struct WalkResult {
   int ok;        // 0 if the chunk holds too many penalised values to resolve
 };
 
-__device__ __forceinline__ u64 readlane64(u64 x, int lane) {
-  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), lane);
-  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(x >> 32), lane);
-  return (static_cast<u64>(hi) << 32) | lo;
-}
 
 // Resolve a value inside chunk c, by the 64 lanes of one wave and no workgroup barrier (the
 // wave's LDS operations complete in order). `above` is the count or mass strictly above the
@@ -2071,7 +2166,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
     row.eid = a.ws.exc_id + p.h0;
     row.eval = a.ws.exc_val + p.h0;
   }
-  generic_row(a, row, p, g);
+  generic_row(a, row, p, g, f);
 }
 
 }  // namespace vs
