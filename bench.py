@@ -7,8 +7,8 @@ step's logits come from HBM. Per-launch durations come from HIP events recorded 
 the kernel runs on; the CPU baseline is the CPU oracle timed on a bounded sample of the same
 rows on this host.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
-Prints one JSON line.
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--decode]
+Prints one JSON line (``--decode``: the batched decode loop's line instead).
 
 `roofline.traffic` (HBM bytes per launch) comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE
 counter runs recorded in profiles/k_sample_bf16_peaked_flat_B256.md, each scaled by what the
@@ -92,6 +92,101 @@ def cpu_baseline(w, budget_s: float = 12.0):
     }
 
 
+def decode_loop(args) -> int:
+    """``--decode``: the continuous-batching decode loop at 64 live sequences, V=151936 bf16
+    (SyntheticLM logits, mixed per-request parameters with penalties). Prints one JSON line:
+    tokens/s of the whole loop and, beside it, the model step and the sampler call timed alone on
+    the same shapes."""
+    import numpy as np
+    import torch
+
+    from vinfer_amd.registry import BackendContext
+    from vinfer_amd.runtime import BatchDecoder
+    from vinfer_amd.sampler import SAMPLER
+    from vinfer_amd.sampling import SamplingParams
+    from vinfer_amd.workloads import SyntheticLM
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    V, B, L = 151936, 64, 4096
+    model = SyntheticLM(V, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    dec = BatchDecoder(model, hip, num_slots=B, max_seq_len=L, penalize_prompt=True)
+    rng = np.random.default_rng(1001)
+    ks = (0, 20, 50, 1000)
+    for i in range(B):
+        kw = dict(max_tokens=L - 64, ignore_eos=True, seed=int(rng.integers(0, 2**62)),
+                  repetition_penalty=1.05, presence_penalty=0.5, frequency_penalty=0.2)
+        if i % 4 == 0:
+            kw.update(temperature=0.0)
+        else:
+            kw.update(temperature=float(rng.uniform(0.3, 1.5)), top_k=ks[i % 4], top_p=float(rng.uniform(0.5, 1.0)))
+        dec.submit(rng.integers(0, V, size=32).tolist(), SamplingParams(**kw))
+    for _ in range(args.warmup):
+        dec.step()
+    torch.cuda.synchronize()
+    K = args.steps
+    t0 = time.perf_counter()
+    n_tok = 0
+    for _ in range(K):
+        n_tok += len(dec.step())
+    torch.cuda.synchronize()
+    loop_us = (time.perf_counter() - t0) / K * 1e6
+
+    # the two device parts alone, on the same shapes
+    slots = torch.arange(B, device=dev)
+    toks = torch.randint(0, V, (B,), device=dev)
+    pos = torch.full((B,), 100, device=dev)
+
+    def timed(fn, n=50):
+        for _ in range(5):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / n
+
+    model_us = timed(lambda: model.decode(slots, toks, pos))
+    seqs, logits = dec._pending
+    u = torch.rand(B, device=dev)
+    params = dec._params(seqs, dev)
+    ranges = torch.tensor([[s.slot * dec._hist_row, s.slot * dec._hist_row + s.hist_len] for s in seqs],
+                          dtype=torch.int32, device=dev)
+    sampler_us = timed(lambda: hip.sample_batch(logits, params, u, dec.hist, ranges))
+    out = {
+        "metric": "decode-loop tokens/s at 64 live sequences, V=151936 bf16",
+        "value": n_tok / (loop_us * K * 1e-6),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": loop_us / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode_loop",
+            "live_sequences": B,
+            "vocab": V,
+            "logits_dtype": "bf16",
+            "model": "SyntheticLM rank 64",
+            "params": "25% greedy, else T U[0.3,1.5], top-k {20,50,1000}, top-p U[0.5,1]; penalties 1.05/0.5/0.2",
+            "history": "prompt (32) + generated ids, per-slot ranges",
+        },
+        "us_per_step_loop": loop_us,
+        "us_model_step_alone": model_us,
+        "us_sampler_call_alone": sampler_us,
+        "us_host_and_rest": loop_us - model_us - sampler_us,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -99,6 +194,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-probe", action="store_true", help="run the counter-calibration copy and exit")
+    ap.add_argument("--decode", action="store_true", help="time the batched decode loop instead")
     args = ap.parse_args()
     if args.copy_probe:
         return copy_probe()
@@ -109,6 +205,8 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if args.decode:
+        return decode_loop(args)
 
     import numpy as np
     import torch

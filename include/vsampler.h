@@ -26,7 +26,10 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 1
+#define VSAMP_ABI_VERSION 2
+
+/* vsamp_args.flags bits. */
+#define VSAMP_HIST_RANGES 1u /* hist_offsets holds a [start, end) pair per row (see below) */
 
 enum vsamp_dtype { VSAMP_BF16 = 0, VSAMP_F32 = 1 };
 
@@ -64,10 +67,14 @@ typedef struct vsamp_args {
   const float* frequency_penalty;
 
   /* Token histories in CSR form: row r's ids are hist_ids[hist_offsets[r] .. hist_offsets[r+1]).
-   * Both NULL = empty histories. Ids outside [0, V) are ignored. */
+   * Both NULL = empty histories. Ids outside [0, V) are ignored.
+   * With VSAMP_HIST_RANGES in flags, hist_offsets holds 2B entries instead and row r's ids are
+   * hist_ids[hist_offsets[2r] .. hist_offsets[2r+1]): per-row ranges in any order, e.g. one
+   * fixed-size region per sequence slot of a decode batch. Ranges of different rows must not
+   * overlap (a row's workspace entries sit under its own range). */
   const int32_t* hist_ids;
   const int32_t* hist_offsets; /* B + 1 entries, non-decreasing, hist_offsets[0] = 0 */
-  int64_t hist_total;          /* hist_offsets[B], known to the caller (sizes the workspace) */
+  int64_t hist_total;          /* hist_offsets[B] (with ranges: >= every end); sizes the workspace */
 
   /* The draw: one uniform u in [0, 1) per row (required). */
   const float* uniforms;
@@ -84,7 +91,7 @@ typedef struct vsamp_args {
   void* workspace;
   size_t workspace_bytes;
 
-  uint32_t flags; /* must be 0 */
+  uint32_t flags; /* 0 or VSAMP_HIST_RANGES */
   uint32_t reserved1;
 } vsamp_args;
 

@@ -1,0 +1,322 @@
+"""The continuous-batching decode loop (``vinfer_amd.runtime``).
+
+The central property: batching never changes a request's tokens. Every test that runs several
+requests through ``BatchDecoder`` compares each request with a one-sequence loop that restates
+the engine's generate.py:118-144 (prefill, then per token: ``sample(logits, params, seed,
+position)``, stop checks, feed the token back) on the same model and sampler backend. The other
+tests port the engine's loop tests (tests/unit/runtime/test_generate.py) to the batched loop:
+stop ids and ``ignore_eos``, streamed text, stop strings, seeded reproducibility, the
+``max_seq_len`` rule, and the text stream's hold-back rules.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from vinfer_amd.registry import BackendContext
+from vinfer_amd.runtime import BatchDecoder, Step, TextStream, check_request
+from vinfer_amd.sampler import SAMPLER
+from vinfer_amd.sampling import SamplingParams, pack_params, uniform
+from vinfer_amd.workloads import SyntheticLM
+
+LETTERS = "abcdefghijklmnopqrstuvwxyz"
+PROMPT = [5, 17, 3, 88, 42, 9, 61, 70, 12]
+
+
+def decode(ids: list[int]) -> str:
+    return "".join(LETTERS[i % 26] for i in ids)
+
+
+def uniform_draw(sampler, logits, params, seed, position, history):
+    """One token by the uniform-driven draw: a one-row ``sample_batch`` with the uniform of
+    ``(seed, position)``. This is what the hip backend's ``sample`` does; the reference backend's
+    ``sample`` keeps the engine's exponential race instead (sampler.py:73-77)."""
+    dev = logits.device
+    u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)
+    hist = off = None
+    if params.penalized and history:
+        hist = torch.tensor(history, dtype=torch.int32, device=dev)
+        off = torch.tensor([0, len(history)], dtype=torch.int32, device=dev)
+    ids, _ = sampler.sample_batch(logits.reshape(1, -1), pack_params([params], dev), u, hist, off)
+    return int(ids[0])
+
+
+def one_at_a_time(model, sampler, prompt, params, eos=frozenset(), text=None, penalize_prompt=False):
+    """The engine's one-sequence loop (generate.py:118-144) over a ``DecodeModel``. On the GPU
+    it calls the hip backend's ``sample`` (the engine's per-token call); on the CPU, where the
+    reference backend's ``sample`` is the exponential race, ``uniform_draw``."""
+    stream = TextStream(text, params.stop) if text else None
+    stop_ids = set(params.stop_token_ids) | (set() if params.ignore_eos else set(eos))
+    dev = model.device
+    logits = model.prefill(0, torch.tensor(prompt, device=dev))
+    position = len(prompt)
+    generated: list[int] = []
+    steps = []
+    for n in range(1, params.max_tokens + 1):
+        history = (list(prompt) if penalize_prompt else []) + generated
+        if logits.is_cuda:
+            token = sampler.sample(logits, params, params.seed, position, history=history)
+        else:
+            token = uniform_draw(sampler, logits, params, params.seed, position, history)
+        generated.append(token)
+        if token in stop_ids:
+            steps.append(Step(token, stream.flush() if stream else "", "stop"))
+            return steps
+        delta, hit = stream.push(token) if stream else ("", False)
+        if hit:
+            steps.append(Step(token, delta, "stop"))
+            return steps
+        if n == params.max_tokens:
+            steps.append(Step(token, delta + (stream.flush() if stream else ""), "length"))
+            return steps
+        steps.append(Step(token, delta))
+        logits = model.decode(
+            torch.tensor([0], device=dev), torch.tensor([token], device=dev), torch.tensor([position], device=dev)
+        )[0]
+        position += 1
+    return steps
+
+
+def mixed_requests(n: int, vocab: int, seed: int = 0) -> list[tuple[list[int], SamplingParams]]:
+    """Prompts and parameters of every kind: greedy, top-k, top-p, min-p, penalties."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        prompt = rng.integers(0, vocab, size=int(rng.integers(1, 12))).tolist()
+        kind = i % 6
+        kw = dict(max_tokens=int(rng.integers(1, 20)), seed=int(rng.integers(0, 2**62)))
+        if kind == 0:
+            kw.update(temperature=0.0)
+        elif kind == 1:
+            kw.update(temperature=0.8, top_k=int(rng.choice([1, 5, 20])))
+        elif kind == 2:
+            kw.update(temperature=1.2, top_p=0.7)
+        elif kind == 3:
+            kw.update(min_p=0.1, top_p=0.95)
+        elif kind == 4:
+            kw.update(repetition_penalty=1.3, presence_penalty=0.5, frequency_penalty=0.4, temperature=0.7)
+        else:
+            kw.update(repetition_penalty=1.1, frequency_penalty=1.0, top_k=50, top_p=0.9)
+        out.append((prompt, SamplingParams(**kw)))
+    return out
+
+
+def run_batched(model, sampler, reqs, num_slots, max_seq_len=64, **kw):
+    dec = BatchDecoder(model, sampler, num_slots=num_slots, max_seq_len=max_seq_len, **kw)
+    rids = [dec.submit(p, sp) for p, sp in reqs]
+    done = dec.run()
+    assert dec._free == sorted(range(num_slots), reverse=True)  # every slot came back
+    return [done[r] for r in rids]
+
+
+@pytest.fixture(scope="module")
+def cpu_model():
+    return SyntheticLM(96, dim=16, scale=3.0, dtype=torch.float32)
+
+
+@pytest.fixture(scope="module")
+def ref_sampler():
+    return SAMPLER.resolve("reference", BackendContext(torch.device("cpu"), torch.float32))
+
+
+# ---- batching never changes a request's tokens ----------------------------------------------
+
+
+@pytest.mark.parametrize("num_slots", [1, 3, 16])
+@pytest.mark.parametrize("penalize_prompt", [False, True])
+def test_batched_tokens_equal_one_sequence_at_a_time(cpu_model, ref_sampler, num_slots, penalize_prompt):
+    reqs = mixed_requests(14, cpu_model.vocab_size)
+    got = run_batched(cpu_model, ref_sampler, reqs, num_slots, penalize_prompt=penalize_prompt)
+    for (prompt, sp), steps in zip(reqs, got):
+        want = one_at_a_time(cpu_model, ref_sampler, prompt, sp, penalize_prompt=penalize_prompt)
+        assert steps == want
+
+
+def test_penalties_see_the_request_s_own_history(cpu_model, ref_sampler):
+    # A strong frequency penalty on a greedy request forbids repeats while the history holds
+    # the token: the loop must hand each row its own, complete history.
+    sp = SamplingParams(max_tokens=20, temperature=0.0, frequency_penalty=100.0)
+    got = run_batched(cpu_model, ref_sampler, [(PROMPT, sp), ([1, 2], sp), ([7], sp)], num_slots=2)
+    for steps in got:
+        toks = [s.token_id for s in steps]
+        assert len(set(toks)) == len(toks)
+
+
+def test_unseeded_requests_draw_seeds_from_the_loop_seed(cpu_model, ref_sampler):
+    sp = SamplingParams(max_tokens=8, temperature=1.0)
+    runs = [run_batched(cpu_model, ref_sampler, [(PROMPT, sp)] * 3, num_slots=2, seed=11) for _ in range(2)]
+    assert runs[0] == runs[1]
+    other = run_batched(cpu_model, ref_sampler, [(PROMPT, sp)] * 3, num_slots=2, seed=12)
+    assert other != runs[0]
+
+
+def test_cancel_frees_the_slot_and_keeps_the_others(cpu_model, ref_sampler):
+    reqs = mixed_requests(4, cpu_model.vocab_size, seed=3)
+    reqs = [(p, SamplingParams(**{**sp.__dict__, "max_tokens": 15})) for p, sp in reqs]
+    dec = BatchDecoder(cpu_model, ref_sampler, num_slots=2, max_seq_len=64)
+    rids = [dec.submit(p, sp) for p, sp in reqs]
+    steps: dict[int, list[Step]] = {}
+    for rid, st in dec.step():
+        steps.setdefault(rid, []).append(st)
+    assert dec.cancel(rids[0]) and dec.cancel(rids[3])  # one running, one waiting
+    assert not dec.cancel(rids[3])
+    for rid, st in dec.run().items():
+        steps.setdefault(rid, []).extend(st)
+    assert rids[3] not in steps
+    for i in (1, 2):
+        assert steps[rids[i]] == one_at_a_time(cpu_model, ref_sampler, *reqs[i])
+
+
+# ---- the engine's loop tests, on the batched loop --------------------------------------------
+
+
+def test_greedy_output_is_the_argmax_chain(cpu_model, ref_sampler):
+    sp = SamplingParams(max_tokens=15, temperature=0)
+    (steps,) = run_batched(cpu_model, ref_sampler, [(PROMPT, sp)], num_slots=1)
+    tok, pos, want = PROMPT[-1], len(PROMPT) - 1, []
+    for _ in range(15):
+        row = cpu_model.decode(torch.tensor([0]), torch.tensor([tok]), torch.tensor([pos]))[0]
+        tok, pos = int(torch.argmax(row)), pos + 1
+        want.append(tok)
+    assert [s.token_id for s in steps] == want
+    assert steps[-1].finish_reason == "length" and all(s.finish_reason is None for s in steps[:-1])
+
+
+def test_eos_stops_unless_ignored(cpu_model, ref_sampler):
+    greedy = SamplingParams(max_tokens=10, temperature=0)
+    (steps,) = run_batched(cpu_model, ref_sampler, [(PROMPT, greedy)], num_slots=1)
+    tokens = [s.token_id for s in steps]
+    eos = {tokens[3]}
+    first = tokens.index(tokens[3])
+    (stopped,) = run_batched(cpu_model, ref_sampler, [(PROMPT, greedy)], num_slots=1, eos_token_ids=eos)
+    assert len(stopped) == first + 1 and stopped[-1].finish_reason == "stop"
+    ignored = SamplingParams(max_tokens=10, temperature=0, ignore_eos=True)
+    (kept,) = run_batched(cpu_model, ref_sampler, [(PROMPT, ignored)], num_slots=1, eos_token_ids=eos)
+    assert len(kept) == 10
+    stop_id = SamplingParams(max_tokens=10, temperature=0, stop_token_ids=(tokens[3],), ignore_eos=True)
+    (by_id,) = run_batched(cpu_model, ref_sampler, [(PROMPT, stop_id)], num_slots=1)
+    assert len(by_id) == first + 1 and by_id[-1].finish_reason == "stop"
+
+
+def test_streamed_text_is_the_decoded_output(cpu_model, ref_sampler):
+    reqs = [(PROMPT, SamplingParams(max_tokens=12, temperature=0)), ([3, 4], SamplingParams(max_tokens=9, seed=5))]
+    for (prompt, sp), steps in zip(reqs, run_batched(cpu_model, ref_sampler, reqs, num_slots=2, decode=decode)):
+        assert "".join(s.text for s in steps) == decode([s.token_id for s in steps])
+        assert steps == one_at_a_time(cpu_model, ref_sampler, prompt, sp, text=decode)
+
+
+def test_stop_string_ends_the_text_before_it(cpu_model, ref_sampler):
+    greedy = SamplingParams(max_tokens=12, temperature=0)
+    (steps,) = run_batched(cpu_model, ref_sampler, [(PROMPT, greedy)], num_slots=1)
+    full = decode([s.token_id for s in steps])
+    stop = full[5:7]
+    sp = SamplingParams(max_tokens=12, temperature=0, stop=(stop,))
+    (cut,) = run_batched(cpu_model, ref_sampler, [(PROMPT, sp)], num_slots=1, decode=decode)
+    assert "".join(s.text for s in cut) == full[: full.index(stop)]
+    assert cut[-1].finish_reason == "stop"
+
+
+def test_sampling_is_reproducible_with_a_seed(cpu_model, ref_sampler):
+    sp = SamplingParams(max_tokens=10, temperature=1.0, seed=3)
+    runs = [run_batched(cpu_model, ref_sampler, [(PROMPT, sp)], num_slots=1) for _ in range(2)]
+    assert runs[0] == runs[1]
+
+
+def test_prompt_plus_max_tokens_must_fit(cpu_model, ref_sampler):
+    # 9 prompt tokens + 4 generated: the last one is never fed back, so 12 positions suffice.
+    sp = SamplingParams(max_tokens=4, temperature=0, ignore_eos=True)
+    (steps,) = run_batched(cpu_model, ref_sampler, [(PROMPT, sp)], num_slots=1, max_seq_len=12)
+    assert len(steps) == 4
+    dec = BatchDecoder(cpu_model, ref_sampler, num_slots=1, max_seq_len=12)
+    with pytest.raises(ValueError, match="max_seq_len"):
+        dec.submit(PROMPT, SamplingParams(max_tokens=5))
+    with pytest.raises(ValueError, match="empty prompt"):
+        check_request(0, sp, 12)
+
+
+def test_history_rows_stay_inside_their_slot(cpu_model, ref_sampler):
+    # Every request runs to the last position its slot allows, with penalties (so its history
+    # grows to prompt + max_tokens ids): the neighbouring slots' rows must stay untouched.
+    sp = SamplingParams(max_tokens=4, temperature=0.9, repetition_penalty=1.2, ignore_eos=True, seed=1)
+    reqs = [(PROMPT[:2], sp), (PROMPT[2:4], sp), (PROMPT[4:6], sp)]
+    got = run_batched(cpu_model, ref_sampler, reqs, num_slots=3, max_seq_len=5, penalize_prompt=True)
+    for (prompt, p), steps in zip(reqs, got):
+        assert steps == one_at_a_time(cpu_model, ref_sampler, prompt, p, penalize_prompt=True)
+
+
+# ---- text stream (tests/unit/runtime/test_generate.py:104-129 behaviour) ---------------------
+
+
+def test_text_held_back_while_it_could_be_a_stop_string():
+    stream = TextStream(decode, ("cde",))
+    assert stream.push(0) == ("", False)
+    assert stream.push(1) == ("", False)
+    assert stream.push(2) == ("a", False)
+    assert stream.push(3) == ("b", False)
+    assert stream.push(4) == ("", True)
+
+
+def test_unfinished_utf8_is_held_back():
+    pieces = {0: "a", 1: "�", 2: "é"}
+
+    def partial(ids):
+        return "".join(pieces[i] for i in ids).replace("�é", "é")
+
+    stream = TextStream(partial, ())
+    assert stream.push(0) == ("a", False)
+    assert stream.push(1) == ("", False)
+    assert stream.push(2) == ("é", False)
+
+
+def test_flush_returns_what_was_held():
+    stream = TextStream(decode, ("zzz",))
+    assert [stream.push(t) for t in (0, 1, 2)] == [("", False), ("", False), ("a", False)]
+    assert stream.flush() == "bc"
+
+
+# ---- on the GPU: the hip backend, bf16 logits at V = 151936 ---------------------------------
+
+
+@pytest.mark.gpu
+def test_gpu_batched_tokens_equal_one_sequence_at_a_time():
+    dev = torch.device("cuda", 0)
+    model = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    reqs = mixed_requests(24, model.vocab_size, seed=7)
+    print("decode loop: 24 requests, 8 slots, V 151936 bf16", flush=True)
+    got = run_batched(model, hip, reqs, num_slots=8, max_seq_len=64, penalize_prompt=True)
+    for i, ((prompt, sp), steps) in enumerate(zip(reqs, got)):
+        want = one_at_a_time(model, hip, prompt, sp, penalize_prompt=True)
+        assert steps == want, f"request {i}"
+
+
+@pytest.mark.gpu
+def test_gpu_decode_loop_rows_match_the_oracle():
+    """Each token the loop draws is the oracle's token for the same logits row, history and
+    uniform (rows the tie classifier flags excepted)."""
+    from oracle.sampler_oracle import classify_ties, penalize, sample_row
+
+    dev = torch.device("cuda", 0)
+    model = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    reqs = mixed_requests(6, model.vocab_size, seed=9)
+    got = run_batched(model, hip, reqs, num_slots=4, max_seq_len=64)
+    checked = 0
+    for (prompt, sp), steps in zip(reqs, got):
+        tok, pos = prompt[-1], len(prompt) - 1
+        history: list[int] = []
+        for st in steps:
+            row = model.decode(*(torch.tensor([v], device=dev) for v in (0, tok, pos)))[0]
+            x = row.float().cpu().numpy()
+            if sp.penalized:
+                x, _ = penalize(x, np.asarray(history, np.int32), sp.repetition_penalty, sp.presence_penalty,
+                                sp.frequency_penalty)
+            r = sample_row(x, sp.temperature, sp.top_k, sp.top_p, sp.min_p, uniform(sp.seed, pos + 1))
+            if not classify_ties(r):
+                assert st.token_id == r.token
+                checked += 1
+            tok, pos = st.token_id, pos + 1
+            history.append(tok)
+    assert checked > 20

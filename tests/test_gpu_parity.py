@@ -146,6 +146,44 @@ def test_penalty_counts_and_values_are_exact(dtype):
             assert np.array_equal(xs[b], w.logits[b].float().numpy()), b
 
 
+def csr_as_ranges(hist_ids: torch.Tensor, hist_offsets: torch.Tensor, seed: int = 0):
+    """The same histories as per-row [start, end) ranges into a larger buffer: rows placed in a
+    shuffled order with gaps of junk ids between them."""
+    rng = np.random.default_rng(seed)
+    off = hist_offsets.tolist()
+    B = len(off) - 1
+    buf, ranges = [], [None] * B
+    for b in rng.permutation(B):
+        buf += rng.integers(0, 50, int(rng.integers(0, 5))).tolist()  # junk between rows
+        ranges[b] = (len(buf), len(buf) + off[b + 1] - off[b])
+        buf += hist_ids[off[b] : off[b + 1]].tolist()
+    buf += [7, 7, 7]
+    return torch.tensor(buf, dtype=torch.int32), torch.tensor(ranges, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_history_ranges_give_the_csr_results(dtype):
+    # 151936 (bf16: the fast path's presence bitmap) and 200000 (its hash table; fp32 and the
+    # penalty workspace throughout), with histories up to 5000 ids
+    for V, seed in ((151936, 21), (200000, 22)):
+        w = random_workload(seed, 24, V, dtype, hist_len=5000)
+        rid, rng_ = csr_as_ranges(w.hist_ids, w.hist_offsets, seed)
+        d = w.to(DEV)
+        s = hip(dtype)
+        print(f"ranges vs CSR V={V} {dtype}", flush=True)
+        a = s.sample_batch(d.logits, d.params, d.uniforms, d.hist_ids, d.hist_offsets, d.draft_ids)
+        b = s.sample_batch(d.logits, d.params, d.uniforms, rid.to(DEV), rng_.to(DEV), d.draft_ids)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+        pa = s.probs(d.logits, d.params, d.hist_ids, d.hist_offsets)
+        pb = s.probs(d.logits, d.params, rid.to(DEV), rng_.to(DEV))
+        assert torch.equal(pa, pb)
+        xa, ca = s.penalized_logits(d.logits, d.params, d.hist_ids, d.hist_offsets)
+        xb, cb = s.penalized_logits(d.logits, d.params, rid.to(DEV), rng_.to(DEV))
+        assert torch.equal(ca, cb) and torch.equal(xa.view(torch.int32), xb.view(torch.int32))
+        ties, bad = compare_ids(b[0].cpu(), oracle(w), b[1].cpu())
+        assert not bad, bad[:10]
+
+
 @pytest.mark.parametrize("name,B", [("mixed_bf16", 64), ("peaked_flat", 64), ("verify_bf16", 24), ("large_fp32", 12), ("single_fp32", 1)])
 def test_workload_rows_match_the_oracle(name, B):
     check(workloads.make(name, batch=B), max_tie_frac=0.1)

@@ -11,10 +11,11 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 VSAMP_BF16 = 0
 VSAMP_F32 = 1
+VSAMP_HIST_RANGES = 1
 
 STATUS = {0: "ok", 1: "VSAMP_E_ARG", 2: "VSAMP_E_DTYPE", 3: "VSAMP_E_HIP", 4: "VSAMP_E_WORKSPACE", 5: "VSAMP_E_DEVICE"}
 

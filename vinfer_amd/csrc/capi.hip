@@ -97,7 +97,8 @@ constexpr int64_t kMaxVocab = static_cast<int64_t>(vs::kMaxStripes) * vs::kThrea
 
 int validate(const vsamp_args* a, bool need_draw) {
   if (!a) return fail(VSAMP_E_ARG, "args is NULL");
-  if (a->flags != 0) return fail(VSAMP_E_ARG, "flags must be 0, got %u", a->flags);
+  if (a->flags & ~VSAMP_HIST_RANGES)
+    return fail(VSAMP_E_ARG, "flags must be 0 or VSAMP_HIST_RANGES, got %u", a->flags);
   if (a->dtype != VSAMP_BF16 && a->dtype != VSAMP_F32)
     return fail(VSAMP_E_DTYPE, "unsupported logits dtype %d (VSAMP_BF16=0, VSAMP_F32=1)", a->dtype);
   if (a->batch < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", a->batch);
@@ -155,6 +156,7 @@ vs::PenaltyArgs penalty_args(const vsamp_args* a, const vs::Workspace& ws) {
   p.freq = a->frequency_penalty;
   p.hist = a->hist_ids;
   p.off = a->hist_offsets;
+  p.hstep = (a->flags & VSAMP_HIST_RANGES) ? 2 : 1;
   p.ws = ws;
   p.dense_counts = nullptr;
   p.counts_stride = 0;

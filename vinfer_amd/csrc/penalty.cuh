@@ -32,6 +32,7 @@ struct PenaltyArgs {
   const float* freq;
   const int32_t* hist;
   const int32_t* off;
+  int hstep;  // entries of `off` per row: 1 (CSR) or 2 (a [start, end) pair per row)
   Workspace ws;
   int32_t* dense_counts;  // optional [B][counts_stride]
   int64_t counts_stride;
@@ -225,8 +226,8 @@ template <class Tin>
 __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, uint32_t* lds, uint32_t* red, ExcCache ec) {
   const int tid = threadIdx.x;
   const int V = a.V;
-  const int h0 = a.off ? a.off[r] : 0;
-  const int h1 = a.off ? a.off[r + 1] : 0;
+  const int h0 = a.off ? a.off[r * a.hstep] : 0;
+  const int h1 = a.off ? a.off[r * a.hstep + 1] : 0;
   const float rep = a.rep ? a.rep[r] : 1.0f;
   const float pres = a.pres ? a.pres[r] : 0.0f;
   const float freq = a.freq ? a.freq[r] : 0.0f;
@@ -390,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void k_penalized_out(PenaltyArgs a_, floa
   float* o = out + static_cast<int64_t>(r) * out_stride;
   for (int i = threadIdx.x; i < a.V; i += kThreads) o[i] = load_one<Tin>(row, i);
   __syncthreads();
-  const int h0 = a.off ? a.off[r] : 0;
+  const int h0 = a.off ? a.off[r * a.hstep] : 0;
   const uint32_t n = a.ws.n_exc[r];
   for (uint32_t e = threadIdx.x; e < n; e += kThreads) o[a.ws.exc_id[h0 + e]] = a.ws.exc_val[h0 + e];
 }

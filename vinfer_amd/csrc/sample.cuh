@@ -181,7 +181,7 @@ __device__ __forceinline__ uint32_t param_word(const SampleArgs& a, int r, int w
   const void* c = nullptr;
 #pragma unroll
   for (int k = 0; k < kParamWords; ++k) c = w == k ? cols[k] : c;
-  const int i = w == kParamWords - 1 ? r + 1 : r;
+  const int i = w >= kParamWords - 2 ? r * (PEN ? a.pen.hstep : 1) + (w - (kParamWords - 2)) : r;
   const uint32_t* q = c ? static_cast<const uint32_t*>(c) + i : &kParamDefaults[w];
   return ld_global(q);
 }

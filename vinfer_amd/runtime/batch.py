@@ -1,0 +1,272 @@
+"""Continuous-batching decode loop: every live sequence goes through one model step and one
+``sample_batch`` call per iteration.
+
+The engine decodes one sequence at a time (src/vinfer/runtime/generate.py:105-146, one request
+after another by scheduler/serial.py:1-5), so its sampler only ever sees one row. This loop keeps
+the engine's per-request behaviour and batches the rest:
+
+- requests are checked as generate.py:91-103 checks them (``check_request``), and a request
+  without a seed gets one from a ``random.Random(seed)`` of the loop (serial.py:36, :48-49);
+- the token at position ``n`` of a sequence is drawn with the uniform of ``(seed, n)``, the same
+  one the per-token ``sample`` uses, from that sequence's own logits and history, so batching
+  never changes a request's tokens;
+- a request ends, as in generate.py:130-142, on a stop id (the request's ``stop_token_ids``,
+  plus the end-of-sequence ids unless ``ignore_eos``; the stop token's own text is not output),
+  on a stop string (text ends before it), or after ``max_tokens`` tokens ("length"); each token
+  yields one ``Step``.
+
+Requests join whenever a slot is free (prefill, then their first token is sampled in the same
+iteration as everyone else's next token) and leave as soon as they finish, freeing their slot.
+
+Histories for the penalties live on the device, one row of ``max_seq_len + 1`` ids per slot,
+and are handed to the sampler as per-row ranges (no per-step packing): a sampled id is written
+into its row on the device right after the draw. A row's history is the request's generated
+tokens, preceded by its prompt when ``penalize_prompt`` is set.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import random
+from collections import deque
+from collections.abc import Callable, Iterable
+from dataclasses import dataclass, field
+from typing import Protocol
+
+import torch
+
+from vinfer_amd.runtime.text import TextStream
+from vinfer_amd.sampler.base import SamplerBackend
+from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params, uniform
+
+
+@dataclass
+class Step:
+    """One generated token of a request (generate.py:20-24)."""
+
+    token_id: int
+    text: str  # new text that is safe to show (empty while it could still be a stop string)
+    finish_reason: str | None = None  # "stop" | "length" | None
+
+
+def check_request(prompt_len: int, params: SamplingParams, max_seq_len: int) -> None:
+    """Raise ``ValueError`` if a request cannot run in ``max_seq_len`` positions (the rule of
+    generate.py:91-103: the last sampled token is never fed back, so a request needs
+    ``prompt_len + max_tokens - 1`` positions)."""
+    if prompt_len == 0:
+        raise ValueError("empty prompt")
+    needed = prompt_len + params.max_tokens - 1
+    if needed > max_seq_len:
+        raise ValueError(
+            f"prompt ({prompt_len}) + max_tokens ({params.max_tokens}) needs {needed} positions, "
+            f"more than max_seq_len ({max_seq_len})"
+        )
+
+
+class DecodeModel(Protocol):
+    """What the loop needs of a model: a prefill into a slot and a batched one-token step."""
+
+    device: torch.device
+    vocab_size: int
+
+    def prefill(self, slot: int, prompt_ids: torch.Tensor) -> torch.Tensor:
+        """Run ``prompt_ids`` (int64 ``[P]``) into ``slot``; the logits ``[V]`` of its last
+        position."""
+        ...
+
+    def decode(self, slots: torch.Tensor, tokens: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """Feed ``tokens[b]`` at ``positions[b]`` into ``slots[b]`` (int64 ``[B]`` each); the
+        logits ``[B, V]`` of those positions, row b for ``slots[b]``."""
+        ...
+
+
+@dataclass(eq=False)
+class _Seq:
+    rid: int
+    prompt: list[int]
+    params: SamplingParams  # seed always set
+    stop_ids: frozenset[int]
+    stream: TextStream | None
+    slot: int = -1
+    position: int = 0  # position of the next token to sample (= tokens in the sequence so far)
+    hist_len: int = 0  # ids in the slot's history row
+    generated: list[int] = field(default_factory=list)
+
+
+class BatchDecoder:
+    def __init__(
+        self,
+        model: DecodeModel,
+        sampler: SamplerBackend,
+        *,
+        num_slots: int,
+        max_seq_len: int,
+        eos_token_ids: Iterable[int] = (),
+        decode: Callable[[list[int]], str] | None = None,
+        seed: int = 0,
+        penalize_prompt: bool = False,
+    ) -> None:
+        if num_slots < 1 or max_seq_len < 1:
+            raise ValueError("num_slots and max_seq_len must be >= 1")
+        self.model = model
+        self.sampler = sampler
+        self.num_slots = num_slots
+        self.max_seq_len = max_seq_len
+        self.eos_token_ids = frozenset(eos_token_ids)
+        self.decode_text = decode
+        self.penalize_prompt = penalize_prompt
+        self._rng = random.Random(seed)
+        self._free = list(range(num_slots - 1, -1, -1))  # pop() hands out the lowest slot
+        self._waiting: deque[_Seq] = deque()
+        self._running: dict[int, _Seq] = {}
+        self._next_rid = 0
+        # Logits of the last model step, not yet sampled: (sequences, [n, V]).
+        self._pending: tuple[list[_Seq], torch.Tensor] | None = None
+        self._packed: dict[tuple[int, ...], PackedParams] = {}
+        # One history row per slot; the extra column takes the id drawn at the last position.
+        self._hist_row = max_seq_len + 1
+        self.hist = torch.zeros(num_slots * self._hist_row, dtype=torch.int32, device=model.device)
+
+    # ---- requests ------------------------------------------------------------------------------
+    def submit(self, prompt_ids: list[int], params: SamplingParams) -> int:
+        """Queue a request; returns its id. Raises ``ValueError`` if it can never run."""
+        check_request(len(prompt_ids), params, self.max_seq_len)
+        if params.seed is None:
+            params = dataclasses.replace(params, seed=self._rng.getrandbits(63))
+        stop_ids = frozenset(params.stop_token_ids) | (frozenset() if params.ignore_eos else self.eos_token_ids)
+        stream = TextStream(self.decode_text, params.stop) if self.decode_text else None
+        rid = self._next_rid
+        self._next_rid += 1
+        self._waiting.append(_Seq(rid, list(prompt_ids), params, stop_ids, stream))
+        return rid
+
+    def cancel(self, rid: int) -> bool:
+        """Drop a request (waiting or running); True if it was there."""
+        for s in self._waiting:
+            if s.rid == rid:
+                self._waiting.remove(s)
+                return True
+        s = self._running.pop(rid, None)
+        if s is None:
+            return False
+        if self._pending is not None and any(t is s for t in self._pending[0]):
+            seqs, logits = self._pending
+            keep = [i for i, t in enumerate(seqs) if t is not s]
+            self._pending = (
+                ([seqs[i] for i in keep], logits[torch.tensor(keep, device=logits.device)]) if keep else None
+            )
+        self._free.append(s.slot)
+        self._free.sort(reverse=True)
+        return True
+
+    @property
+    def busy(self) -> bool:
+        return bool(self._waiting or self._running)
+
+    @property
+    def num_running(self) -> int:
+        return len(self._running)
+
+    # ---- one iteration -----------------------------------------------------------------------
+    def step(self) -> list[tuple[int, Step]]:
+        """Admit what fits, draw one token for every running request, advance the model.
+        Returns ``(request id, Step)`` per request that produced a token."""
+        groups = []
+        if self._pending is not None:
+            groups.append(self._pending)
+            self._pending = None
+        admitted = self._admit()
+        if admitted is not None:
+            groups.append(admitted)
+        if not groups:
+            return []
+        drawn = [self._draw(seqs, logits) for seqs, logits in groups]
+        seqs = [s for g in groups for s in g[0]]
+        tokens = torch.cat(drawn).tolist()  # the iteration's one wait for the device
+        out: list[tuple[int, Step]] = []
+        going: list[_Seq] = []
+        for s, tok in zip(seqs, tokens):
+            step = self._advance(s, tok)
+            out.append((s.rid, step))
+            if step.finish_reason is None:
+                going.append(s)
+            else:
+                del self._running[s.rid]
+                self._free.append(s.slot)
+        self._free.sort(reverse=True)
+        if going:
+            dev = self.model.device
+            slots = torch.tensor([s.slot for s in going], dtype=torch.int64).to(dev)
+            toks = torch.tensor([s.generated[-1] for s in going], dtype=torch.int64).to(dev)
+            pos = torch.tensor([s.position - 1 for s in going], dtype=torch.int64).to(dev)
+            self._pending = (going, self.model.decode(slots, toks, pos))
+        return out
+
+    def run(self) -> dict[int, list[Step]]:
+        """Step until every queued request has finished; each request's steps in order."""
+        done: dict[int, list[Step]] = {}
+        while self.busy:
+            for rid, step in self.step():
+                done.setdefault(rid, []).append(step)
+        return done
+
+    # ---- internals ---------------------------------------------------------------------------
+    def _admit(self) -> tuple[list[_Seq], torch.Tensor] | None:
+        seqs, rows = [], []
+        dev = self.model.device
+        while self._waiting and self._free:
+            s = self._waiting.popleft()
+            s.slot = self._free.pop()
+            s.position = len(s.prompt)
+            prompt = torch.tensor(s.prompt, dtype=torch.int64)
+            s.hist_len = 0
+            if s.params.penalized and self.penalize_prompt:
+                base = s.slot * self._hist_row
+                self.hist[base : base + len(s.prompt)] = prompt.to(torch.int32).to(dev)
+                s.hist_len = len(s.prompt)
+            rows.append(self.model.prefill(s.slot, prompt.to(dev)).reshape(-1))
+            self._running[s.rid] = s
+            seqs.append(s)
+        return (seqs, torch.stack(rows)) if seqs else None
+
+    def _params(self, seqs: list[_Seq], dev: torch.device) -> PackedParams:
+        key = tuple(s.rid for s in seqs)
+        packed = self._packed.get(key)
+        if packed is None:
+            if len(self._packed) > 64:  # memberships change as requests come and go
+                self._packed.clear()
+            packed = self._packed[key] = pack_params([s.params for s in seqs], dev)
+        return packed
+
+    def _draw(self, seqs: list[_Seq], logits: torch.Tensor) -> torch.Tensor:
+        """Launch the sampler over one group; the drawn ids stay on the device."""
+        dev = logits.device
+        u = torch.tensor([uniform(s.params.seed, s.position) for s in seqs], dtype=torch.float32).to(dev)
+        params = self._params(seqs, dev)
+        if not any(s.params.penalized for s in seqs):
+            ids, _ = self.sampler.sample_batch(logits, params, u)
+            return ids
+        # Rows without penalties get an empty range (their slot's history is not kept).
+        ranges = torch.tensor(
+            [[s.slot * self._hist_row, s.slot * self._hist_row + s.hist_len * s.params.penalized] for s in seqs],
+            dtype=torch.int32,
+        ).to(dev)
+        ids, _ = self.sampler.sample_batch(logits, params, u, self.hist, ranges)
+        # The drawn id joins its row's history right behind the range just used.
+        self.hist.index_copy_(0, ranges[:, 1].long(), ids)
+        for s in seqs:
+            s.hist_len += s.params.penalized
+        return ids
+
+    def _advance(self, s: _Seq, tok: int) -> Step:
+        """The request-side logic of one token (generate.py:130-142)."""
+        s.generated.append(tok)
+        s.position += 1
+        if tok in s.stop_ids:  # the stop token's own text is not part of the output
+            return Step(tok, s.stream.flush() if s.stream else "", "stop")
+        text, hit = s.stream.push(tok) if s.stream else ("", False)
+        if hit:
+            return Step(tok, text, "stop")
+        if len(s.generated) == s.params.max_tokens:
+            return Step(tok, text + (s.stream.flush() if s.stream else ""), "length")
+        return Step(tok, text)

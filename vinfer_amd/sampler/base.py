@@ -42,7 +42,9 @@ class SamplerBackend(Protocol):
     ) -> tuple[torch.Tensor, torch.Tensor | None]:
         """One token per row of ``logits`` ``[B, V]``: ids int32 ``[B]`` and, when ``draft_ids``
         (int32 ``[B]``) is given, the final probability of each draft id (fp32 ``[B]``).
-        ``uniforms`` fp32 ``[B]`` in [0, 1); histories in CSR form (int32)."""
+        ``uniforms`` fp32 ``[B]`` in [0, 1). Histories (int32) are in CSR form (``hist_offsets``
+        ``[B + 1]``) or per-row ranges (``hist_offsets`` ``[B, 2]``: row b's ids are
+        ``hist_ids[start_b:end_b]``; ranges of different rows must not overlap)."""
         ...
 
     def probs(

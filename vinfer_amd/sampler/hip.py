@@ -86,8 +86,19 @@ class HipSampler:
         if (hist_ids is None) != (hist_offsets is None):
             raise ValueError("hist_ids and hist_offsets go together")
         hist_total = 0
+        flags = 0
         if hist_ids is not None:
-            hist_offsets = self._vec(hist_offsets, B + 1, torch.int32, dev, "hist_offsets")
+            if hist_offsets.dim() == 2:  # a [start, end) pair per row
+                if (
+                    hist_offsets.dtype != torch.int32
+                    or hist_offsets.device != dev
+                    or tuple(hist_offsets.shape) != (B, 2)
+                ):
+                    raise ValueError(f"hist_offsets as ranges must be a torch.int32 [{B}, 2] tensor on {dev}")
+                hist_offsets = hist_offsets.contiguous()
+                flags = _lib.VSAMP_HIST_RANGES
+            else:
+                hist_offsets = self._vec(hist_offsets, B + 1, torch.int32, dev, "hist_offsets")
             if hist_ids.dtype != torch.int32 or hist_ids.device != dev or hist_ids.dim() != 1:
                 raise ValueError(f"hist_ids must be an int32 1-D tensor on {dev}")
             hist_ids = hist_ids.contiguous()
@@ -103,6 +114,7 @@ class HipSampler:
         a.hist_ids = _ptr(hist_ids) if hist_total else None
         a.hist_offsets = _ptr(hist_offsets) if hist_total else None
         a.hist_total = hist_total
+        a.flags = flags if hist_total else 0
         if uniforms is not None:
             uniforms = self._vec(uniforms, B, torch.float32, dev, "uniforms")
             a.uniforms = _ptr(uniforms)

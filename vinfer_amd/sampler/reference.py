@@ -104,7 +104,10 @@ class ReferenceSampler:
         for b in range(B):
             x = logits[b].float()
             if hist_ids is not None:
-                h = hist_ids[int(hist_offsets[b]) : int(hist_offsets[b + 1])]
+                if hist_offsets.dim() == 2:  # per-row [start, end) ranges
+                    h = hist_ids[int(hist_offsets[b, 0]) : int(hist_offsets[b, 1])]
+                else:
+                    h = hist_ids[int(hist_offsets[b]) : int(hist_offsets[b + 1])]
             else:
                 h = torch.zeros(0, dtype=torch.int32, device=logits.device)
             row = {k: getattr(params, k)[b] for k in params.__dataclass_fields__}

@@ -149,3 +149,30 @@ def make(name: str, batch: int | None = None, vocab: int | None = None, seed: in
         draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
         return Workload(name, x, params, torch.from_numpy(rng.random(B, dtype=np.float32)), None, None, draft)
     raise ValueError(f"unknown workload {name!r}; known: {list(NAMES)}")
+
+
+class SyntheticLM:
+    """A stand-in model for the decode loop: the logits of a position are a random rank-``dim``
+    map of its token and position, ``(E[token] + P[position mod 64]) @ W``, in ``dtype`` (W scaled
+    so logits are about N(0, scale^2)). Slots hold no state: the logits depend on the last token
+    and its position only, so any order of steps over any set of slots gives the same rows."""
+
+    def __init__(self, vocab: int, *, dim: int = 64, scale: float = 3.0, dtype=torch.bfloat16,
+                 device="cpu", seed: int = 0) -> None:
+        g = torch.Generator().manual_seed(seed)
+        self.device = torch.device(device)
+        self.vocab_size = vocab
+        self.dtype = dtype
+        self.emb = torch.randn(vocab, dim, generator=g).to(dtype).to(self.device)
+        self.pos = torch.randn(64, dim, generator=g).to(dtype).to(self.device)
+        self.head = (torch.randn(dim, vocab, generator=g) * (scale / (2 * dim) ** 0.5)).to(dtype).to(self.device)
+
+    def decode(self, slots: torch.Tensor, tokens: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        h = self.emb[tokens] + self.pos[positions % 64]
+        return h @ self.head
+
+    def prefill(self, slot: int, prompt_ids: torch.Tensor) -> torch.Tensor:
+        n = int(prompt_ids.shape[0])
+        last = prompt_ids[n - 1 :]
+        return self.decode(torch.tensor([slot], device=self.device), last,
+                           torch.tensor([n - 1], device=self.device))[0]
