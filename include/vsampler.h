@@ -123,6 +123,12 @@ int vsamp_probs(const vsamp_args* args, float* out, int64_t out_stride, void* st
 int vsamp_penalized_logits(const vsamp_args* args, float* out, int32_t* counts,
                            int64_t out_stride, void* stream);
 
+/* Host function (no device work): the draw's uniform of (seeds[i], positions[i]) into out[i],
+ * i < n, all host memory. u = (splitmix64(position_seed(seed, position)) >> 40) * 2^-24, where
+ * position_seed is the engine's per-token seed, sampler.py:44-47 (BLAKE2b-8 of
+ * "<seed>:<position>", little-endian, top bit cleared); `uniforms` of vsamp_args takes these. */
+int vsamp_uniforms(const int64_t* seeds, const int64_t* positions, int32_t n, float* out);
+
 /* Description of the last failure on this thread ("" if none). */
 const char* vsamp_last_error(void);
 

@@ -112,3 +112,26 @@ def test_query_names_the_problem_without_a_gpu():
         pytest.skip("a GPU is visible")
     reason = _lib.query(0)
     assert reason and "device" in reason
+
+
+def test_host_uniforms_equal_the_python_derivation():
+    # vsamp_uniforms (BLAKE2b-8 + SplitMix64 in C, on the host) against the Python derivation
+    # over hashlib, whose position_seed the oracle tests pin to known values; signs, the int64
+    # extremes and long decimal texts included.
+    import numpy as np
+
+    from vinfer_amd.sampling import uniform
+
+    rng = np.random.default_rng(5)
+    seeds = [0, 7, 8, -1, -(1 << 63), (1 << 63) - 1, 1 << 62, 9] + rng.integers(
+        -(1 << 63), (1 << 63) - 1, 3000, dtype=np.int64
+    ).tolist()
+    positions = [0, 1, 2, 3, 10**12, (1 << 63) - 1, -5, 99] + rng.integers(0, 1 << 40, 3000).tolist()
+    got = _lib.position_uniforms(seeds, positions)
+    want = np.array([uniform(s, p) for s, p in zip(seeds, positions)], np.float32)
+    assert np.array_equal(got, want)
+    big = _lib.position_uniforms([1 << 70, 3], [4, 4])  # outside int64: the Python derivation
+    assert big.tolist() == [uniform(1 << 70, 4), uniform(3, 4)]
+    lib = _lib.load()
+    assert lib.vsamp_uniforms(None, None, -1, None) == 1
+    assert lib.vsamp_uniforms(None, None, 0, None) == 0

@@ -27,6 +27,7 @@ EXPORTS = (
     "vsamp_sample",
     "vsamp_probs",
     "vsamp_penalized_logits",
+    "vsamp_uniforms",
     "vsamp_last_error",
 )
 
@@ -102,6 +103,8 @@ def load() -> ctypes.CDLL:
             ctypes.c_void_p,
         ]
         lib.vsamp_penalized_logits.restype = ctypes.c_int
+        lib.vsamp_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
+        lib.vsamp_uniforms.restype = ctypes.c_int
         lib.vsamp_last_error.restype = ctypes.c_char_p
         version = lib.vsamp_abi_version()
         if version != ABI_VERSION:
@@ -122,3 +125,32 @@ def query(device_index: int) -> str | None:
     buf = ctypes.create_string_buffer(256)
     code = load().vsamp_query(device_index, buf, len(buf))
     return None if code == 0 else (buf.value.decode(errors="replace") or STATUS.get(code, str(code)))
+
+
+_INT64 = (-(1 << 63), 1 << 63)
+
+
+def position_uniforms(seeds, positions, out=None):
+    """The draw's uniforms of ``(seeds[i], positions[i])`` (``vsamp_uniforms``, on the host):
+    float32 numpy array, equal to ``vinfer_amd.sampling.uniform`` element for element. Seeds
+    outside int64 are not representable in the C call; such rows go through ``uniform``."""
+    import numpy as np
+
+    from vinfer_amd.sampling import uniform
+
+    n = len(seeds)
+    out = np.empty(n, np.float32) if out is None else out
+    if n == 0:
+        return out
+    try:
+        s = np.asarray(seeds, dtype=np.int64)
+    except OverflowError:
+        for i, (sd, p) in enumerate(zip(seeds, positions)):
+            out[i] = uniform(int(sd), int(p))
+        return out
+    p = np.ascontiguousarray(positions, dtype=np.int64)
+    s = np.ascontiguousarray(s)
+    if out.dtype != np.float32 or not out.flags["C_CONTIGUOUS"] or out.shape[0] < n:
+        raise ValueError("out must be a contiguous float32 array of at least n entries")
+    check(load().vsamp_uniforms(s.ctypes.data, p.ctypes.data, n, out.ctypes.data))
+    return out

@@ -11,6 +11,7 @@
 #include "common.cuh"
 #include "penalty.cuh"
 #include "sample.cuh"
+#include "uniform.h"
 
 namespace {
 
@@ -275,6 +276,14 @@ int vsamp_penalized_logits(const vsamp_args* a, float* out, int32_t* counts, int
                        out_stride);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_penalized_out");
+}
+
+int vsamp_uniforms(const int64_t* seeds, const int64_t* positions, int32_t n, float* out) {
+  g_err.clear();
+  if (n < 0) return fail(VSAMP_E_ARG, "n must be >= 0, got %d", n);
+  if (n > 0 && (!seeds || !positions || !out)) return fail(VSAMP_E_ARG, "seeds, positions and out must be set");
+  for (int32_t i = 0; i < n; ++i) out[i] = vs_host::position_uniform(seeds[i], positions[i]);
+  return VSAMP_OK;
 }
 
 const char* vsamp_last_error(void) { return g_err.c_str(); }

@@ -1,0 +1,111 @@
+// Host code: the draw's uniform of (seed, position), for many rows per call.
+//
+// position_seed(seed, position) is BLAKE2b with an 8-byte digest of the ASCII text
+// "<seed>:<position>", read little-endian, top bit cleared (src/vinfer/runtime/sampler.py:44-47).
+// BLAKE2b here follows RFC 7693 (unkeyed, one 128-byte block: the text is at most 41 bytes).
+// The uniform is then the top 24 bits of the SplitMix64 output function (Steele, Lea, Flood
+// 2014) of that seed, times 2^-24: a multiple of 2^-24 in [0, 1), exact in fp32.
+#pragma once
+
+#include <cstdint>
+#include <cstring>
+
+namespace vs_host {
+
+constexpr uint64_t kBlakeIV[8] = {0x6A09E667F3BCC908ull, 0xBB67AE8584CAA73Bull, 0x3C6EF372FE94F82Bull,
+                                  0xA54FF53A5F1D36F1ull, 0x510E527FADE682D1ull, 0x9B05688C2B3E6C1Full,
+                                  0x1F83D9ABFB41BD6Bull, 0x5BE0CD19137E2179ull};
+
+// Message word schedule of the ten distinct rounds (RFC 7693, section 2.7); round i uses row i % 10.
+constexpr uint8_t kSigma[10][16] = {
+    {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15}, {14, 10, 4, 8, 9, 15, 13, 6, 1, 12, 0, 2, 11, 7, 5, 3},
+    {11, 8, 12, 0, 5, 2, 15, 13, 10, 14, 3, 6, 7, 1, 9, 4}, {7, 9, 3, 1, 13, 12, 11, 14, 2, 6, 5, 10, 4, 0, 15, 8},
+    {9, 0, 5, 7, 2, 4, 10, 15, 14, 1, 11, 12, 6, 8, 3, 13}, {2, 12, 6, 10, 0, 11, 8, 3, 4, 13, 7, 5, 15, 14, 1, 9},
+    {12, 5, 1, 15, 14, 13, 4, 10, 0, 7, 6, 3, 9, 2, 8, 11}, {13, 11, 7, 14, 12, 1, 3, 9, 5, 0, 15, 4, 8, 6, 2, 10},
+    {6, 15, 14, 9, 11, 3, 0, 8, 12, 2, 13, 7, 1, 4, 10, 5}, {10, 2, 8, 4, 7, 6, 1, 5, 15, 11, 9, 14, 3, 12, 13, 0},
+};
+
+inline uint64_t rotr64(uint64_t x, int n) { return (x >> n) | (x << (64 - n)); }
+
+inline void blake_mix(uint64_t* v, int a, int b, int c, int d, uint64_t x, uint64_t y) {
+  v[a] = v[a] + v[b] + x;
+  v[d] = rotr64(v[d] ^ v[a], 32);
+  v[c] = v[c] + v[d];
+  v[b] = rotr64(v[b] ^ v[c], 24);
+  v[a] = v[a] + v[b] + y;
+  v[d] = rotr64(v[d] ^ v[a], 16);
+  v[c] = v[c] + v[d];
+  v[b] = rotr64(v[b] ^ v[c], 63);
+}
+
+// The first 8 bytes (little-endian) of the 8-byte BLAKE2b digest of text[0, n), n <= 128.
+inline uint64_t blake2b_8(const char* text, int n) {
+  uint64_t m[16] = {};
+  std::memcpy(m, text, static_cast<size_t>(n));  // little-endian words, zero padded
+  uint64_t h[8];
+  for (int i = 0; i < 8; ++i) h[i] = kBlakeIV[i];
+  h[0] ^= 0x01010000ull ^ 8ull;  // depth 1, fanout 1, no key, 8-byte digest
+  uint64_t v[16];
+  for (int i = 0; i < 8; ++i) {
+    v[i] = h[i];
+    v[i + 8] = kBlakeIV[i];
+  }
+  v[12] ^= static_cast<uint64_t>(n);  // bytes compressed (the high counter word stays 0)
+  v[14] = ~v[14];                     // the last block
+  for (int r = 0; r < 12; ++r) {
+    const uint8_t* s = kSigma[r % 10];
+    blake_mix(v, 0, 4, 8, 12, m[s[0]], m[s[1]]);
+    blake_mix(v, 1, 5, 9, 13, m[s[2]], m[s[3]]);
+    blake_mix(v, 2, 6, 10, 14, m[s[4]], m[s[5]]);
+    blake_mix(v, 3, 7, 11, 15, m[s[6]], m[s[7]]);
+    blake_mix(v, 0, 5, 10, 15, m[s[8]], m[s[9]]);
+    blake_mix(v, 1, 6, 11, 12, m[s[10]], m[s[11]]);
+    blake_mix(v, 2, 7, 8, 13, m[s[12]], m[s[13]]);
+    blake_mix(v, 3, 4, 9, 14, m[s[14]], m[s[15]]);
+  }
+  return h[0] ^ v[0] ^ v[8];
+}
+
+// Decimal text of x at p; returns the characters written (at most 20).
+inline int put_decimal(char* p, uint64_t x) {
+  char tmp[20];
+  int n = 0;
+  do {
+    tmp[n++] = static_cast<char>('0' + x % 10);
+    x /= 10;
+  } while (x);
+  for (int i = 0; i < n; ++i) p[i] = tmp[n - 1 - i];
+  return n;
+}
+
+inline uint64_t position_seed(int64_t seed, int64_t position) {
+  char text[48];
+  int n = 0;
+  uint64_t s = static_cast<uint64_t>(seed);
+  if (seed < 0) {
+    text[n++] = '-';
+    s = 0 - s;  // magnitude, also for INT64_MIN
+  }
+  n += put_decimal(text + n, s);
+  text[n++] = ':';
+  uint64_t p = static_cast<uint64_t>(position);
+  if (position < 0) {
+    text[n++] = '-';
+    p = 0 - p;
+  }
+  n += put_decimal(text + n, p);
+  return blake2b_8(text, n) & ((uint64_t(1) << 63) - 1);
+}
+
+inline uint64_t splitmix64(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+inline float position_uniform(int64_t seed, int64_t position) {
+  return static_cast<float>(splitmix64(position_seed(seed, position)) >> 40) * 0x1p-24f;
+}
+
+}  // namespace vs_host

@@ -33,11 +33,13 @@ from collections.abc import Callable, Iterable
 from dataclasses import dataclass, field
 from typing import Protocol
 
+import numpy as np
 import torch
 
+from vinfer_amd._lib import position_uniforms
 from vinfer_amd.runtime.text import TextStream
 from vinfer_amd.sampler.base import SamplerBackend
-from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params, uniform
+from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params
 
 
 @dataclass
@@ -78,6 +80,42 @@ class DecodeModel(Protocol):
         """Feed ``tokens[b]`` at ``positions[b]`` into ``slots[b]`` (int64 ``[B]`` each); the
         logits ``[B, V]`` of those positions, row b for ``slots[b]``."""
         ...
+
+
+class _Staging:
+    """Small per-step inputs (int32 words) gathered in one host buffer and sent to the device in
+    one copy. On a GPU the host buffer is pinned and the copy asynchronous: the host may refill
+    it only after a later synchronisation (the loop alternates two, and waits once per step)."""
+
+    def __init__(self, device: torch.device, words: int) -> None:
+        self.host = torch.empty(words, dtype=torch.int32, pin_memory=device.type == "cuda")
+        self.dev = torch.empty(words, dtype=torch.int32, device=device)
+        self.np = self.host.numpy()
+        self.n = 0
+
+    def reset(self) -> None:
+        self.n = 0
+
+    def reserve(self, n: int) -> int:
+        if self.n + n > self.np.shape[0]:
+            raise RuntimeError("staging buffer too small")
+        at, self.n = self.n, self.n + n
+        return at
+
+    def put(self, words: np.ndarray) -> int:
+        at = self.reserve(words.shape[0])
+        self.np[at : at + words.shape[0]] = words
+        return at
+
+    def host_view(self, at: int, n: int) -> np.ndarray:
+        return self.np[at : at + n]
+
+    def send(self) -> None:
+        if self.n:
+            self.dev[: self.n].copy_(self.host[: self.n], non_blocking=True)
+
+    def device(self, at: int, n: int) -> torch.Tensor:
+        return self.dev[at : at + n]
 
 
 @dataclass(eq=False)
@@ -126,6 +164,8 @@ class BatchDecoder:
         # One history row per slot; the extra column takes the id drawn at the last position.
         self._hist_row = max_seq_len + 1
         self.hist = torch.zeros(num_slots * self._hist_row, dtype=torch.int32, device=model.device)
+        # [0]: the sampler's inputs (uniforms, ranges: 3 words a row), [1]: the model's (3 a row)
+        self._stage = (_Staging(model.device, 6 * num_slots), _Staging(model.device, 3 * num_slots))
 
     # ---- requests ------------------------------------------------------------------------------
     def submit(self, prompt_ids: list[int], params: SamplingParams) -> int:
@@ -180,9 +220,14 @@ class BatchDecoder:
             groups.append(admitted)
         if not groups:
             return []
-        drawn = [self._draw(seqs, logits) for seqs, logits in groups]
+        # The sampler's per-row inputs of every group go to the device in one copy.
+        st = self._stage[0]
+        st.reset()
+        cols = [self._stage_draw(st, seqs) for seqs, _ in groups]
+        st.send()
+        drawn = [self._draw(seqs, logits, st, c) for (seqs, logits), c in zip(groups, cols)]
         seqs = [s for g in groups for s in g[0]]
-        tokens = torch.cat(drawn).tolist()  # the iteration's one wait for the device
+        tokens = torch.cat(drawn).tolist() if len(drawn) > 1 else drawn[0].tolist()  # the one wait
         out: list[tuple[int, Step]] = []
         going: list[_Seq] = []
         for s, tok in zip(seqs, tokens):
@@ -195,10 +240,13 @@ class BatchDecoder:
                 self._free.append(s.slot)
         self._free.sort(reverse=True)
         if going:
-            dev = self.model.device
-            slots = torch.tensor([s.slot for s in going], dtype=torch.int64).to(dev)
-            toks = torch.tensor([s.generated[-1] for s in going], dtype=torch.int64).to(dev)
-            pos = torch.tensor([s.position - 1 for s in going], dtype=torch.int64).to(dev)
+            st = self._stage[1]
+            st.reset()
+            n = len(going)
+            at = st.put(np.array([[s.slot for s in going], [s.generated[-1] for s in going],
+                                  [s.position - 1 for s in going]], dtype=np.int32).reshape(-1))
+            st.send()
+            slots, toks, pos = st.device(at, 3 * n).view(3, n).long()
             self._pending = (going, self.model.decode(slots, toks, pos))
         return out
 
@@ -238,19 +286,30 @@ class BatchDecoder:
             packed = self._packed[key] = pack_params([s.params for s in seqs], dev)
         return packed
 
-    def _draw(self, seqs: list[_Seq], logits: torch.Tensor) -> torch.Tensor:
-        """Launch the sampler over one group; the drawn ids stay on the device."""
-        dev = logits.device
-        u = torch.tensor([uniform(s.params.seed, s.position) for s in seqs], dtype=torch.float32).to(dev)
-        params = self._params(seqs, dev)
+    def _stage_draw(self, st: _Staging, seqs: list[_Seq]) -> tuple[int, int | None]:
+        """Stage one group's uniforms and (when a row has penalties) history ranges."""
+        n = len(seqs)
+        at_u = st.reserve(n)
+        position_uniforms([s.params.seed for s in seqs], [s.position for s in seqs],
+                          out=st.host_view(at_u, n).view(np.float32))
         if not any(s.params.penalized for s in seqs):
+            return at_u, None
+        # Rows without penalties get an empty range (their slot's history is not kept).
+        base = np.array([s.slot for s in seqs], dtype=np.int64) * self._hist_row
+        ln = np.array([s.hist_len if s.params.penalized else 0 for s in seqs], dtype=np.int64)
+        at_r = st.put(np.stack([base, base + ln], axis=1).astype(np.int32).reshape(-1))
+        return at_u, at_r
+
+    def _draw(self, seqs: list[_Seq], logits: torch.Tensor, st: _Staging, cols) -> torch.Tensor:
+        """Launch the sampler over one group; the drawn ids stay on the device."""
+        n = len(seqs)
+        at_u, at_r = cols
+        u = st.device(at_u, n).view(torch.float32)
+        params = self._params(seqs, logits.device)
+        if at_r is None:
             ids, _ = self.sampler.sample_batch(logits, params, u)
             return ids
-        # Rows without penalties get an empty range (their slot's history is not kept).
-        ranges = torch.tensor(
-            [[s.slot * self._hist_row, s.slot * self._hist_row + s.hist_len * s.params.penalized] for s in seqs],
-            dtype=torch.int32,
-        ).to(dev)
+        ranges = st.device(at_r, 2 * n).view(n, 2)
         ids, _ = self.sampler.sample_batch(logits, params, u, self.hist, ranges)
         # The drawn id joins its row's history right behind the range just used.
         self.hist.index_copy_(0, ranges[:, 1].long(), ids)
