@@ -7,8 +7,9 @@ step's logits come from HBM. Per-launch durations come from HIP events recorded 
 the kernel runs on; the CPU baseline is the CPU oracle timed on a bounded sample of the same
 rows on this host.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--decode]
-Prints one JSON line (``--decode``: the batched decode loop's line instead).
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--decode | --verify]
+Prints one JSON line (``--decode``: the batched decode loop's line instead; ``--verify``: the
+speculative-decoding verify's).
 
 `roofline.traffic` (HBM bytes per launch) comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE
 counter runs recorded in profiles/k_sample_bf16_peaked_flat_B256.md, each scaled by what the
@@ -187,6 +188,72 @@ def decode_loop(args) -> int:
     return 0
 
 
+def verify_bench(args) -> int:
+    """``--verify``: speculative-decoding verify of one draft per sequence at 192 sequences,
+    V=262144 bf16 (target logits ~ N(0, 2.5^2) at two positions, the draft a noisy copy of the
+    first, drafts drawn from the draft distribution; T U[0.5, 1.2], top-p 0.95). Prints one
+    JSON line: sequences/s, us per verify call, and the HBM roofline fraction over one read of
+    the target and draft logits."""
+    import numpy as np
+    import torch
+
+    from vinfer_amd.registry import BackendContext
+    from vinfer_amd.sampler import SAMPLER
+    from vinfer_amd.sampling import PackedParams
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, K, V = 192, 1, 262144
+    g = torch.Generator(device=dev).manual_seed(1005)
+    tgt = (torch.randn(B, K + 1, V, generator=g, device=dev) * 2.5).to(torch.bfloat16)
+    drf = (tgt[:, :K].float() + torch.randn(B, K, V, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    rng = np.random.default_rng(1005)
+    f32 = lambda a: torch.from_numpy(np.asarray(a, np.float32)).to(dev)  # noqa: E731
+    params = PackedParams(
+        temperature=f32(rng.uniform(0.5, 1.2, B)), top_k=torch.zeros(B, dtype=torch.int32, device=dev),
+        top_p=f32(np.full(B, 0.95)), min_p=f32(np.zeros(B)), repetition_penalty=f32(np.ones(B)),
+        presence_penalty=f32(np.zeros(B)), frequency_penalty=f32(np.zeros(B)))
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    drafts, _ = hip.sample_batch(drf.reshape(B * K, V), params.repeat_rows(K), f32(rng.random(B * K)))
+    drafts = drafts.reshape(B, K)
+    ua, ur, ub = f32(rng.random((B, K))), f32(rng.random((B, K))), f32(rng.random(B))
+    call = lambda: hip.verify(tgt, drf, drafts, params, ua, ur, ub)  # noqa: E731
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        tokens, counts = call()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    algo = (tgt.numel() + drf.numel()) * 2 + B * (K * 16 + 8)
+    achieved = algo / (us * 1e-6) / 1e9
+    out = {
+        "metric": "verified sequences/s + us/call at B=192, K=1, V=262144 bf16; % HBM roofline",
+        "value": B / (us * 1e-6),
+        "unit": "sequences/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": us / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": "verify_k1", "batch": B, "num_draft": K, "vocab": V, "logits_dtype": "bf16",
+                   "temperature": "U[0.5,1.2]", "top_p": 0.95, "draft": "target + N(0, 0.5^2)"},
+        "us_per_call": us,
+        "mean_tokens_emitted": float(counts.float().mean()),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "algorithmic_bytes_per_call": algo},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -195,6 +262,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-probe", action="store_true", help="run the counter-calibration copy and exit")
     ap.add_argument("--decode", action="store_true", help="time the batched decode loop instead")
+    ap.add_argument("--verify", action="store_true", help="time the speculative-decoding verify instead")
     args = ap.parse_args()
     if args.copy_probe:
         return copy_probe()
@@ -207,6 +275,8 @@ def main() -> int:
         return 2
     if args.decode:
         return decode_loop(args)
+    if args.verify:
+        return verify_bench(args)
 
     import numpy as np
     import torch

@@ -123,6 +123,42 @@ int vsamp_probs(const vsamp_args* args, float* out, int64_t out_stride, void* st
 int vsamp_penalized_logits(const vsamp_args* args, float* out, int32_t* counts,
                            int64_t out_stride, void* stream);
 
+/*
+ * Speculative-decoding verify for B sequences with K drafted tokens each (an MTP head or a draft
+ * model proposed them). Draft j of sequence b is accepted when u_accept[b, j] * q < p, p and q
+ * being the target's and the draft's final probabilities of that token (every filter applied,
+ * as vsamp_probs computes them); at the first rejection the emitted token is drawn with
+ * u_residual[b, j] from max(0, p - q) over ascending ids (in the kernels' fixed point: token masses
+ * P = rint(p~ * 2^42), kept mass S, weights (P_t * S_d >> s) - (P_d * S_t >> s)); when all
+ * K are accepted the target's draw at position K (its uniform: target.uniforms of that row) is
+ * the bonus token. Emitted tokens are then distributed exactly as the target's distribution.
+ *
+ * target: B * (K + 1) rows, row b * (K + 1) + j = the target's logits at draft position j
+ * (j = K: the position after the last draft), with per-row parameters as in vsamp_sample.
+ * draft: B * K rows, row b * K + j = the draft distribution that proposed draft j.
+ * Both: the same vocab and dtype; no penalties (hist_ids NULL); draft_ids, out_ids and
+ * out_draft_prob NULL (the call uses its workspace); target.uniforms required, draft.uniforms
+ * optional. Replaces nothing in the engine, which skips its checkpoint's MTP head
+ * (src/vinfer/models/loader.py:27); the C5 verify workload (draft-id probability) feeds it.
+ */
+typedef struct vsamp_verify_args {
+  vsamp_args target;
+  vsamp_args draft;
+  int32_t batch;     /* B */
+  int32_t num_draft; /* K, 1 <= K <= 64 */
+  const int32_t* draft_tokens; /* [B, K] */
+  const float* u_accept;       /* [B, K] in [0, 1) */
+  const float* u_residual;     /* [B, K] in [0, 1) */
+  int32_t* out_tokens;         /* [B, K + 1]: the emitted tokens, then -1 */
+  int32_t* out_count;          /* [B]: tokens emitted, 1 .. K + 1 (accepted drafts + 1) */
+  void* workspace;             /* vsamp_verify_workspace_bytes(B, K) bytes, 256-byte aligned */
+  size_t workspace_bytes;
+} vsamp_verify_args;
+
+size_t vsamp_verify_workspace_bytes(int32_t batch, int32_t num_draft);
+
+int vsamp_verify(const vsamp_verify_args* args, void* stream);
+
 /* Host function (no device work): the draw's uniform of (seeds[i], positions[i]) into out[i],
  * i < n, all host memory. u = (splitmix64(position_seed(seed, position)) >> 40) * 2^-24, where
  * position_seed is the engine's per-token seed, sampler.py:44-47 (BLAKE2b-8 of

@@ -27,6 +27,11 @@ What it restates, row by row, in numpy (fp32 where the engine computes in fp32, 
    prefix ``C_j > u * S``; the last kept token with positive mass if rounding leaves none.
    Draft probability ``p~_d / S`` (0 if ``d`` was dropped).
 
+10. Speculative-decoding verify (not in the engine, which skips its checkpoint's MTP head,
+   src/vinfer/models/loader.py:27): ``verify_row`` restates speculative sampling (Leviathan,
+   Kalman, Matias 2023; Chen et al. 2023) over rows of steps 1-9; its own docstring states the
+   fixed-point residual and the tie rules.
+
 ``classify_ties`` flags rows whose result two correct implementations may legitimately disagree
 on; the device kernels' masses are fixed-point with quantum ``2**-42`` (``p~ <= 1``), so a
 decision is fragile when it sits within ``(n + 4) * 2**-42`` of its threshold.
@@ -226,3 +231,80 @@ def sample_batch(
             sample_row(x, temperature[b], int(top_k[b]), top_p[b], min_p[b], u[b], d, want_probs)
         )
     return out
+
+
+# ---- speculative-decoding verify ----------------------------------------------------------------
+POINT_MASS = 2**42  # mass of a point-mass row's token (and its kept mass)
+
+
+@dataclass
+class VerifyResult:
+    tokens: list[int]  # the emitted tokens: accepted drafts, then the residual or bonus token
+    ties: list[str] = field(default_factory=list)
+
+
+def token_masses(res: RowResult, V: int) -> tuple[list[int], int, int]:
+    """Fixed-point masses of a row's tokens, ``rint(p~ * 2^42)`` (0 for dropped tokens), their
+    sum S and the number of kept tokens; a point-mass row has 2^42 at its token."""
+    if res.kind != "sampled":
+        P = [0] * V
+        P[res.token] = POINT_MASS
+        return P, POINT_MASS, 1
+    P = np.rint(res.info["pt"] * 2.0**42).astype(np.int64).tolist()
+    return P, int(sum(P)), int(res.info["n_kept"])
+
+
+def verify_row(target: list[RowResult], draft: list[RowResult], drafts, u_acc, u_res, V: int) -> VerifyResult:
+    """Speculative sampling for one sequence (Leviathan, Kalman, Matias 2023; Chen et al. 2023),
+    in the device kernels' fixed point, exact integer arithmetic.
+
+    ``target`` holds K + 1 rows (row K drawn with the bonus uniform), ``draft`` K rows. With P,
+    Q the token masses (``token_masses``) and S_t, S_d their sums, draft j is accepted when
+    ``m * Q_d * S_t < P_d * S_d * 2^24`` (m = floor(u_acc[j] * 2^24)), i.e. ``u < p / q``. At
+    the first rejection the token is the first id (ascending) whose inclusive prefix of
+    ``w_i = max(0, (P_i * S_d >> s) - (Q_i * S_t >> s))`` (s = floor(log2(max(S_t, S_d)))) exceeds
+    ``floor(m * R / 2^24)``, m from u_res[j] and R the sum; R = 0 takes the target's own draw
+    there. With every draft accepted, the target's draw at K is added.
+
+    Ties: a row whose own result is fragile, or a decision within what the masses can move
+    between two exp implementations (each mass by one unit, so each S by its kept count)."""
+    K = len(drafts)
+    res = VerifyResult([])
+    for j in range(K):
+        if classify_ties(target[j]) or classify_ties(draft[j]):
+            res.ties.append(f"row {j}")
+        d = int(drafts[j])
+        P, St, nt = token_masses(target[j], V)
+        Q, Sd, nd = token_masses(draft[j], V)
+        if not 0 <= d < V:
+            accept = False
+        else:
+            m = int(F32(u_acc[j]) * F32(2.0**24))
+            lhs, rhs = m * Q[d] * St, (P[d] * Sd) << 24
+            eps = m * (St + Q[d] * nt) + ((Sd + P[d] * nd) << 24)
+            if lhs != rhs and abs(lhs - rhs) <= eps:
+                res.ties.append("accept")
+            accept = lhs < rhs
+        if accept:
+            res.tokens.append(d)
+            continue
+        s = max(St, Sd).bit_length() - 1
+        w = [max(0, ((p * Sd) >> s) - ((q * St) >> s)) for p, q in zip(P, Q)]
+        R = sum(w)
+        if R == 0:
+            res.tokens.append(target[j].token)
+            return res
+        m = int(F32(u_res[j]) * F32(2.0**24))
+        tg = min((m * R) >> 24, R - 1)
+        C = np.cumsum(np.array(w, dtype=np.int64))
+        tok = int(np.searchsorted(C, tg, side="right"))
+        err = ((V * (Sd + St) + St * nd + Sd * nt) >> s) + V
+        lo = int(C[tok - 1]) if tok > 0 else 0
+        if tg - lo <= 2 * err or int(C[tok]) - 1 - tg <= 2 * err:
+            res.ties.append("residual")
+        res.tokens.append(tok)
+        return res
+    if classify_ties(target[K]):
+        res.ties.append("bonus")
+    res.tokens.append(target[K].token)
+    return res

@@ -135,3 +135,51 @@ def test_host_uniforms_equal_the_python_derivation():
     lib = _lib.load()
     assert lib.vsamp_uniforms(None, None, -1, None) == 1
     assert lib.vsamp_uniforms(None, None, 0, None) == 0
+
+
+def test_verify_arguments_are_checked_before_any_launch():
+    lib = _lib.load()
+    v = _lib.VsampVerifyArgs()
+    v.target = _args(batch=6, out_ids=None)
+    v.draft = _args(batch=3, uniforms=None, out_ids=None)
+    v.batch, v.num_draft = 3, 1
+    v.draft_tokens = v.u_accept = v.u_residual = v.out_tokens = v.out_count = 0x6000
+    cases = [
+        ({"num_draft": 0}, "num_draft"),
+        ({"batch": 2}, "target.batch"),
+        ({"draft_tokens": None}, "draft_tokens"),
+    ]
+    for kw, msg in cases:
+        w = _lib.VsampVerifyArgs.from_buffer_copy(v)
+        for k, val in kw.items():
+            setattr(w, k, val)
+        assert lib.vsamp_verify(ctypes.byref(w), None) == 1
+        assert msg in lib.vsamp_last_error().decode()
+    w = _lib.VsampVerifyArgs.from_buffer_copy(v)
+    w.target.out_ids = 0x3000  # outputs of the inner calls belong to the call
+    assert lib.vsamp_verify(ctypes.byref(w), None) == 1 and b"leave them NULL" in lib.vsamp_last_error()
+    w = _lib.VsampVerifyArgs.from_buffer_copy(v)
+    w.target.out_ids = None
+    w.target.hist_ids, w.target.hist_offsets, w.target.hist_total = 0x7000, 0x7100, 10
+    w.target.repetition_penalty = 0x7200
+    assert lib.vsamp_verify(ctypes.byref(w), None) == 1 and b"penalties" in lib.vsamp_last_error()
+    assert lib.vsamp_verify_workspace_bytes(3, 1) > 0 and lib.vsamp_verify_workspace_bytes(3, 0) == 0
+
+
+def test_verify_struct_matches_the_binding(tmp_path):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    fields = [f for f, _ in _lib.VsampVerifyArgs._fields_]
+    src = tmp_path / "vlayout.c"
+    lines = [f'printf("%zu\\n", offsetof(vsamp_verify_args, {f}));' for f in fields]
+    src.write_text(
+        "#include <stdio.h>\n#include <stddef.h>\n#include \"vsampler.h\"\nint main(void){"
+        + "".join(lines)
+        + 'printf("%zu\\n", sizeof(vsamp_verify_args));return 0;}\n'
+    )
+    exe = tmp_path / "vlayout"
+    subprocess.run([gcc, f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [getattr(_lib.VsampVerifyArgs, f).offset for f in fields] + [ctypes.sizeof(_lib.VsampVerifyArgs)]
+    assert got == want

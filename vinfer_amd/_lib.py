@@ -28,6 +28,8 @@ EXPORTS = (
     "vsamp_probs",
     "vsamp_penalized_logits",
     "vsamp_uniforms",
+    "vsamp_verify",
+    "vsamp_verify_workspace_bytes",
     "vsamp_last_error",
 )
 
@@ -60,6 +62,24 @@ class VsampArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("flags", ctypes.c_uint32),
         ("reserved1", ctypes.c_uint32),
+    ]
+
+
+class VsampVerifyArgs(ctypes.Structure):
+    """``vsamp_verify_args`` field for field."""
+
+    _fields_ = [
+        ("target", VsampArgs),
+        ("draft", VsampArgs),
+        ("batch", ctypes.c_int32),
+        ("num_draft", ctypes.c_int32),
+        ("draft_tokens", ctypes.c_void_p),
+        ("u_accept", ctypes.c_void_p),
+        ("u_residual", ctypes.c_void_p),
+        ("out_tokens", ctypes.c_void_p),
+        ("out_count", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -103,6 +123,10 @@ def load() -> ctypes.CDLL:
             ctypes.c_void_p,
         ]
         lib.vsamp_penalized_logits.restype = ctypes.c_int
+        lib.vsamp_verify.argtypes = [ctypes.POINTER(VsampVerifyArgs), ctypes.c_void_p]
+        lib.vsamp_verify.restype = ctypes.c_int
+        lib.vsamp_verify_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32]
+        lib.vsamp_verify_workspace_bytes.restype = ctypes.c_size_t
         lib.vsamp_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
         lib.vsamp_uniforms.restype = ctypes.c_int
         lib.vsamp_last_error.restype = ctypes.c_char_p

@@ -12,6 +12,7 @@
 #include "penalty.cuh"
 #include "sample.cuh"
 #include "uniform.h"
+#include "verify.cuh"
 
 namespace {
 
@@ -172,7 +173,8 @@ int launch_penalties(const vs::PenaltyArgs& p, int B, hipStream_t st) {
 }
 
 template <class Tin>
-int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStream_t st) {
+int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStream_t st,
+               vs::RowState* state = nullptr) {
   const bool pen = wants_penalties(a);
   vs::SampleArgs s;
   std::memset(&s, 0, sizeof s);
@@ -197,6 +199,7 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
   s.out_dprob = a->out_draft_prob;
   s.out_probs = probs;
   s.probs_stride = probs_stride;
+  s.out_state = state;
   // One launch per step: the penalty phase runs at the start of the same kernel.
   if (pen)
     hipLaunchKernelGGL((vs::k_sample<Tin, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
@@ -204,6 +207,32 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
     hipLaunchKernelGGL((vs::k_sample<Tin, false>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_sample");
+}
+
+struct VerifyLayout {
+  size_t tids, dids, ts, ds, jr, done, sums, total;
+};
+
+VerifyLayout verify_layout(int64_t B, int64_t K) {
+  VerifyLayout L;
+  const size_t nt = static_cast<size_t>(B * (K + 1)), nd = static_cast<size_t>(B * K);
+  size_t o = 0;
+  L.tids = o;
+  o = align_up(o + 4 * nt);
+  L.dids = o;
+  o = align_up(o + 4 * nd);
+  L.ts = o;
+  o = align_up(o + sizeof(vs::RowState) * nt);
+  L.ds = o;
+  o = align_up(o + sizeof(vs::RowState) * nd);
+  L.jr = o;
+  o = align_up(o + 4 * static_cast<size_t>(B));
+  L.done = o;
+  o = align_up(o + 4 * static_cast<size_t>(B));
+  L.sums = o;
+  o = align_up(o + 8 * static_cast<size_t>(B) * vs::kMaxStripes);
+  L.total = o;
+  return L;
 }
 
 }  // namespace
@@ -276,6 +305,83 @@ int vsamp_penalized_logits(const vsamp_args* a, float* out, int32_t* counts, int
                        out_stride);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_penalized_out");
+}
+
+size_t vsamp_verify_workspace_bytes(int32_t batch, int32_t num_draft) {
+  if (batch < 0 || num_draft < 1) return 0;
+  return verify_layout(batch, num_draft).total;
+}
+
+int vsamp_verify(const vsamp_verify_args* v, void* stream) {
+  g_err.clear();
+  if (!v) return fail(VSAMP_E_ARG, "args is NULL");
+  const int B = v->batch, K = v->num_draft;
+  if (B < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", B);
+  if (K < 1 || K > 64) return fail(VSAMP_E_ARG, "num_draft must be in [1, 64], got %d", K);
+  vsamp_args t = v->target, d = v->draft;
+  if (t.batch != B * (K + 1))
+    return fail(VSAMP_E_ARG, "target.batch must be batch * (num_draft + 1) = %d, got %d", B * (K + 1), t.batch);
+  if (d.batch != B * K)
+    return fail(VSAMP_E_ARG, "draft.batch must be batch * num_draft = %d, got %d", B * K, d.batch);
+  if (t.vocab != d.vocab) return fail(VSAMP_E_ARG, "target and draft vocab differ (%d, %d)", t.vocab, d.vocab);
+  if (t.dtype != d.dtype) return fail(VSAMP_E_DTYPE, "target and draft logits dtypes differ");
+  if (t.draft_ids || t.out_ids || t.out_draft_prob || d.draft_ids || d.out_ids || d.out_draft_prob)
+    return fail(VSAMP_E_ARG, "draft_ids and outputs of target and draft are set by the call: leave them NULL");
+  if (wants_penalties(&t) || wants_penalties(&d))
+    return fail(VSAMP_E_ARG, "verify does not apply penalties (histories must be NULL)");
+  if (B > 0 && (!v->draft_tokens || !v->u_accept || !v->u_residual || !v->out_tokens || !v->out_count))
+    return fail(VSAMP_E_ARG, "draft_tokens, u_accept, u_residual, out_tokens and out_count must be set");
+  if (!d.uniforms) d.uniforms = v->u_residual;  // (the draft rows' own draws are not used)
+  const VerifyLayout L = verify_layout(B, K);
+  if (v->workspace_bytes < L.total || (L.total && !v->workspace))
+    return fail(VSAMP_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", v->workspace_bytes, L.total);
+  if (reinterpret_cast<uintptr_t>(v->workspace) & 255u)
+    return fail(VSAMP_E_WORKSPACE, "workspace must be 256-byte aligned");
+  char* w = static_cast<char*>(v->workspace);
+  int32_t* tids = reinterpret_cast<int32_t*>(w + L.tids);
+  int32_t* dids = reinterpret_cast<int32_t*>(w + L.dids);
+  vs::RowState* ts = reinterpret_cast<vs::RowState*>(w + L.ts);
+  vs::RowState* ds = reinterpret_cast<vs::RowState*>(w + L.ds);
+  t.out_ids = tids;
+  d.out_ids = dids;  // (the draft rows' own draws are not used)
+  if (int rc = validate(&t, true)) return rc;
+  if (int rc = validate(&d, true)) return rc;
+  if (B == 0) return VSAMP_OK;
+  if (int rc = check_current_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool bf = t.dtype == VSAMP_BF16;
+  if (int rc = bf ? run_sample<uint16_t>(&t, nullptr, 0, st, ts) : run_sample<float>(&t, nullptr, 0, st, ts)) return rc;
+  if (int rc = bf ? run_sample<uint16_t>(&d, nullptr, 0, st, ds) : run_sample<float>(&d, nullptr, 0, st, ds)) return rc;
+  vs::VerifyArgs a;
+  a.tgt = t.logits;
+  a.tstride = t.row_stride;
+  a.drf = d.logits;
+  a.dstride = d.row_stride;
+  a.V = t.vocab;
+  a.K = K;
+  a.drafts = v->draft_tokens;
+  a.u_acc = v->u_accept;
+  a.u_res = v->u_residual;
+  a.tids = tids;
+  a.ts = ts;
+  a.ds = ds;
+  a.out_tokens = v->out_tokens;
+  a.out_count = v->out_count;
+  a.jr = reinterpret_cast<int32_t*>(w + L.jr);
+  a.done = reinterpret_cast<uint32_t*>(w + L.done);
+  a.sums = reinterpret_cast<vs::u64*>(w + L.sums);
+  const int nstripes = ((t.vocab + vs::kBlk - 1) / vs::kBlk + vs::kThreads - 1) / vs::kThreads;
+  a.slices = nstripes < 8 ? nstripes : 8;
+  const dim3 ga((B + 255) / 256), gr(a.slices, B);
+  if (bf) {
+    hipLaunchKernelGGL(vs::k_verify_accept<uint16_t>, ga, dim3(256), 0, st, a, B);
+    hipLaunchKernelGGL(vs::k_verify_residual<uint16_t>, gr, dim3(vs::kThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(vs::k_verify_accept<float>, ga, dim3(256), 0, st, a, B);
+    hipLaunchKernelGGL(vs::k_verify_residual<float>, gr, dim3(vs::kThreads), 0, st, a);
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_verify");
 }
 
 int vsamp_uniforms(const int64_t* seeds, const int64_t* positions, int32_t n, float* out) {

@@ -32,6 +32,15 @@
 
 namespace vs {
 
+// A row's kept set and normalisation as the sampling kernel found them: with it a later kernel
+// recomputes any token's final probability, bit for bit as probs mode writes it.
+struct RowState {
+  float mz, T, x0, vc;           // max scaled logit, temperature, cutoff value, cutoff group value
+  int32_t partial, idr, point;   // the cutoff group split at id idr; a point mass at `point`
+  int32_t pad;
+  u64 S;                         // kept mass (fixed point, 2^42)
+};
+
 struct SampleArgs {
   const void* logits;
   int64_t stride;
@@ -46,6 +55,7 @@ struct SampleArgs {
   float* out_dprob;
   float* out_probs;  // probs mode when non-null
   int64_t probs_stride;
+  RowState* out_state;  // optional: each row's RowState
   Workspace ws;
   int has_exc;  // the workspace holds this batch's exceptions
   const int32_t* off;
@@ -781,6 +791,19 @@ __device__ __forceinline__ void finish(const SampleArgs& a, const Row<Tin>& row,
                        const Kept& k, int draw, float* vslot) {
   const int tid = threadIdx.x;
   const int r = blockIdx.x;
+  if (a.out_state && tid == 0) {
+    RowState st;
+    st.mz = mz;
+    st.T = p.T;
+    st.x0 = k.x0;
+    st.vc = k.vc;
+    st.partial = k.partial;
+    st.idr = k.idr;
+    st.point = k.point;
+    st.pad = 0;
+    st.S = k.S;
+    a.out_state[r] = st;
+  }
   if (a.out_probs) {
     float* o = a.out_probs + static_cast<int64_t>(r) * a.probs_stride;
     if (k.point >= 0) {
@@ -818,7 +841,7 @@ template <class Tin>
 __device__ __forceinline__ void resolve_idr(const SampleArgs& a, const Row<Tin>& row, const RowParams& p, Kept& k,
                             Search& s) {
   if (!k.partial) return;
-  bool need = a.out_probs != nullptr;
+  bool need = a.out_probs != nullptr || a.out_state != nullptr;
   if (!need && p.draft >= 0 && p.draft < row.V && a.out_dprob) need = value_of(row, p.draft, &s.vslot) == k.vc;
   if (need) {
     const float vc = k.vc;
@@ -2114,6 +2137,7 @@ __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
   a.out_ids = as_global(a.out_ids);
   a.out_dprob = as_global(a.out_dprob);
   a.out_probs = as_global(a.out_probs);
+  a.out_state = as_global(a.out_state);
   a.ws = globalized(a.ws);
   a.off = as_global(a.off);
   a.pen = globalized(a.pen);

@@ -58,6 +58,29 @@ class SamplerBackend(Protocol):
         sampler.py:50-65, plus penalties and min-p)."""
         ...
 
+    def verify(
+        self,
+        target_logits: torch.Tensor,
+        draft_logits: torch.Tensor,
+        draft_tokens: torch.Tensor,
+        params: PackedParams,
+        u_accept: torch.Tensor,
+        u_residual: torch.Tensor,
+        u_bonus: torch.Tensor,
+        draft_params: PackedParams | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Speculative-decoding verify of ``K`` drafted tokens per sequence: draft ``j`` is
+        accepted when ``u_accept[b, j] * q < p`` (``p``, ``q``: the target's and the draft's
+        final probabilities of it); at the first rejection the token is drawn with
+        ``u_residual[b, j]`` from ``max(0, p - q)`` over ascending ids; with every draft
+        accepted, the target's draw at position ``K`` (uniform ``u_bonus[b]``) is added.
+        ``target_logits`` ``[B, K + 1, V]``, ``draft_logits`` ``[B, K, V]`` (same dtype),
+        ``draft_tokens`` int32 ``[B, K]``, uniforms fp32; ``params`` (one row per sequence)
+        apply to the target rows, ``draft_params`` (default: the same) to the draft rows;
+        penalties are not applied. Returns ``tokens`` int32 ``[B, K + 1]`` (emitted tokens,
+        then -1) and ``counts`` int32 ``[B]`` (1 .. K + 1)."""
+        ...
+
     def penalized_logits(
         self,
         logits: torch.Tensor,

@@ -192,6 +192,48 @@ class HipSampler:
         del keep
         return out, counts
 
+    def verify(self, target_logits, draft_logits, draft_tokens, params, u_accept, u_residual, u_bonus,
+               draft_params=None):
+        if target_logits.dim() != 3 or draft_logits.dim() != 3:
+            raise ValueError("target_logits must be [B, K + 1, V] and draft_logits [B, K, V]")
+        B, K1, V = target_logits.shape
+        K = K1 - 1
+        if K < 1 or tuple(draft_logits.shape) != (B, K, V):
+            raise ValueError(f"draft_logits must be [{B}, {K}, {V}] for target_logits {tuple(target_logits.shape)}")
+        if draft_logits.dtype != target_logits.dtype:
+            raise ValueError("target and draft logits must have one dtype")
+        dev = target_logits.device
+        tl = target_logits.reshape(B * K1, V)
+        dl = draft_logits.reshape(B * K, V)
+        dparams = params if draft_params is None else draft_params
+        if params.batch != B or dparams.batch != B:
+            raise ValueError(f"params must describe the {B} sequences")
+        drafts = draft_tokens.to(torch.int32).contiguous()
+        ua = u_accept.to(torch.float32).contiguous()
+        ur = u_residual.to(torch.float32).contiguous()
+        for name, t, shape in (("draft_tokens", drafts, (B, K)), ("u_accept", ua, (B, K)), ("u_residual", ur, (B, K))):
+            if tuple(t.shape) != shape or t.device != dev:
+                raise ValueError(f"{name} must be [{B}, {K}] on {dev}")
+        tu = torch.zeros(B, K1, dtype=torch.float32, device=dev)
+        tu[:, K] = self._vec(u_bonus.to(torch.float32), B, torch.float32, dev, "u_bonus")
+        tu = tu.reshape(-1)
+        ta, tkeep = self._args(tl, params.repeat_rows(K1), None, None, tu)
+        da, dkeep = self._args(dl, dparams.repeat_rows(K), None, None, None)
+        v = _lib.VsampVerifyArgs()
+        v.target, v.draft = ta, da
+        v.batch, v.num_draft = B, K
+        v.draft_tokens, v.u_accept, v.u_residual = drafts.data_ptr(), ua.data_ptr(), ur.data_ptr()
+        tokens = torch.empty(B, K1, dtype=torch.int32, device=dev)
+        counts = torch.empty(B, dtype=torch.int32, device=dev)
+        v.out_tokens, v.out_count = tokens.data_ptr(), counts.data_ptr()
+        need = int(self._lib.vsamp_verify_workspace_bytes(B, K))
+        ws = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+        v.workspace = (ws.data_ptr() + 255) & ~255
+        v.workspace_bytes = need
+        _lib.check(self._lib.vsamp_verify(ctypes.byref(v), self._stream(dev)))
+        del tkeep, dkeep
+        return tokens, counts
+
     def sample(
         self,
         logits: torch.Tensor,

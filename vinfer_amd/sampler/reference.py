@@ -56,6 +56,13 @@ def _penalize(x: torch.Tensor, hist: torch.Tensor, rep, pres, freq):
 
 def _row(x: torch.Tensor, T, k: int, tp, mp):
     """Final fp64 probabilities of one penalised fp32 row (``T`` etc. are 0-dim fp32)."""
+    pt = _ptilde(x, T, k, tp, mp)
+    return pt / pt.sum()
+
+
+def _ptilde(x: torch.Tensor, T, k: int, tp, mp):
+    """``exp(z - max z)`` (fp64) over the tokens every filter keeps, 0 elsewhere; a one-hot
+    1.0 for greedy and degenerate rows."""
     V = x.shape[0]
     if not bool(T > 0):
         out = torch.zeros(V, dtype=torch.float64, device=x.device)
@@ -91,7 +98,7 @@ def _row(x: torch.Tensor, T, k: int, tp, mp):
         before = torch.cumsum(sp, 0) - sp
         drop = order[(before >= float(tp) * pt.sum()) & (sp > 0)]
         pt[drop] = 0.0
-    return pt / pt.sum()
+    return pt
 
 
 @SAMPLER.register("reference")
@@ -143,6 +150,63 @@ class ReferenceSampler:
         out = torch.tensor(ids, dtype=torch.int32, device=dev)
         dp = torch.tensor(dps, dtype=torch.float32, device=dev) if draft_ids is not None else None
         return out, dp
+
+    def verify(self, target_logits, draft_logits, draft_tokens, params, u_accept, u_residual, u_bonus,
+               draft_params=None):
+        """Speculative sampling (see the protocol) in exact integers: token masses
+        ``rint(p~ * 2^42)`` and their sums S; accept when ``m * Q_d * S_t < P_d * S_d * 2^24``
+        (``m = floor(u * 2^24)``); the residual ``max(0, (P_i * S_d >> s) - (Q_i * S_t >> s))`` with
+        ``s = floor(log2(max(S_t, S_d)))`` over ascending ids."""
+        B, K1, V = target_logits.shape
+        K = K1 - 1
+        dparams = params if draft_params is None else draft_params
+        dev = target_logits.device
+        tokens = torch.full((B, K1), -1, dtype=torch.int32)
+        counts = torch.zeros(B, dtype=torch.int32)
+
+        def masses(x, prm, b):
+            r = {k: getattr(prm, k)[b] for k in prm.__dataclass_fields__}
+            pt = _ptilde(x.float(), r["temperature"], int(r["top_k"]), r["top_p"], r["min_p"])
+            P = torch.round(pt.cpu() * 2.0**42).long().tolist()
+            return P, sum(P)
+
+        def m24(u):
+            return int(torch.tensor(float(u), dtype=torch.float32) * 2.0**24)
+
+        def own_draw(b, j, u):
+            row = {k: getattr(params, k)[b : b + 1] for k in params.__dataclass_fields__}
+            ids, _ = self.sample_batch(target_logits[b, j : j + 1], type(params)(**row),
+                                       torch.full((1,), float(u), dtype=torch.float32, device=dev))
+            return int(ids[0])
+
+        for b in range(B):
+            out = []
+            for j in range(K):
+                P, St = masses(target_logits[b, j], params, b)
+                Q, Sd = masses(draft_logits[b, j], dparams, b)
+                d = int(draft_tokens[b, j])
+                if 0 <= d < V and m24(u_accept[b, j]) * Q[d] * St < (P[d] * Sd) << 24:
+                    out.append(d)
+                    continue
+                sh = max(St, Sd).bit_length() - 1
+                w = [max(0, ((p * Sd) >> sh) - ((q * St) >> sh)) for p, q in zip(P, Q)]
+                R = sum(w)
+                if R == 0:  # the target's own draw at this position (its uniform is 0)
+                    out.append(own_draw(b, j, 0.0))
+                else:
+                    tg = min((m24(u_residual[b, j]) * R) >> 24, R - 1)
+                    c = 0
+                    for i, wi in enumerate(w):
+                        c += wi
+                        if c > tg:
+                            out.append(i)
+                            break
+                break
+            else:
+                out.append(own_draw(b, K, u_bonus[b]))
+            tokens[b, : len(out)] = torch.tensor(out, dtype=torch.int32)
+            counts[b] = len(out)
+        return tokens.to(dev), counts.to(dev)
 
     def sample(
         self,
