@@ -320,3 +320,30 @@ def test_gpu_decode_loop_rows_match_the_oracle():
             tok, pos = st.token_id, pos + 1
             history.append(tok)
     assert checked > 20
+
+
+def test_the_model_hears_when_a_slot_is_released(cpu_model, ref_sampler):
+    class Tracking:
+        def __init__(self, inner):
+            self.inner, self.device, self.live = inner, inner.device, set()
+
+        def prefill(self, slot, prompt):
+            assert slot not in self.live
+            self.live.add(slot)
+            return self.inner.prefill(slot, prompt)
+
+        def decode(self, slots, tokens, positions):
+            assert set(slots.tolist()) <= self.live
+            return self.inner.decode(slots, tokens, positions)
+
+        def release(self, slot):
+            self.live.remove(slot)
+
+    m = Tracking(cpu_model)
+    reqs = mixed_requests(9, cpu_model.vocab_size, seed=4)
+    dec = BatchDecoder(m, ref_sampler, num_slots=3, max_seq_len=64)
+    rids = [dec.submit(p, sp) for p, sp in reqs]
+    dec.step()
+    dec.cancel(rids[1])
+    dec.run()
+    assert m.live == set()

@@ -66,10 +66,11 @@ def check_request(prompt_len: int, params: SamplingParams, max_seq_len: int) -> 
 
 
 class DecodeModel(Protocol):
-    """What the loop needs of a model: a prefill into a slot and a batched one-token step."""
+    """What the loop needs of a model: a prefill into a slot and a batched one-token step. A
+    model may also define ``release(slot)``, called when a slot's request ends (where a state
+    pool would free it, generate.py:146)."""
 
     device: torch.device
-    vocab_size: int
 
     def prefill(self, slot: int, prompt_ids: torch.Tensor) -> torch.Tensor:
         """Run ``prompt_ids`` (int64 ``[P]``) into ``slot``; the logits ``[V]`` of its last
@@ -195,7 +196,7 @@ class BatchDecoder:
             self._pending = (
                 ([seqs[i] for i in keep], logits[torch.tensor(keep, device=logits.device)]) if keep else None
             )
-        self._free.append(s.slot)
+        self._retire(s, running=False)
         self._free.sort(reverse=True)
         return True
 
@@ -236,8 +237,7 @@ class BatchDecoder:
             if step.finish_reason is None:
                 going.append(s)
             else:
-                del self._running[s.rid]
-                self._free.append(s.slot)
+                self._retire(s)
         self._free.sort(reverse=True)
         if going:
             st = self._stage[1]
@@ -259,6 +259,14 @@ class BatchDecoder:
         return done
 
     # ---- internals ---------------------------------------------------------------------------
+    def _retire(self, s: _Seq, running: bool = True) -> None:
+        if running:
+            del self._running[s.rid]
+        self._free.append(s.slot)
+        release = getattr(self.model, "release", None)
+        if release is not None:
+            release(s.slot)
+
     def _admit(self) -> tuple[list[_Seq], torch.Tensor] | None:
         seqs, rows = [], []
         dev = self.model.device
