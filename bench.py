@@ -7,9 +7,9 @@ step's logits come from HBM. Per-launch durations come from HIP events recorded 
 the kernel runs on; the CPU baseline is the CPU oracle timed on a bounded sample of the same
 rows on this host.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--decode | --verify]
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--decode | --verify | --logprobs]
 Prints one JSON line (``--decode``: the batched decode loop's line instead; ``--verify``: the
-speculative-decoding verify's).
+speculative-decoding verify's; ``--logprobs``: the raw log-probabilities').
 
 `roofline.traffic` (HBM bytes per launch) comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE
 counter runs recorded in profiles/k_sample_bf16_peaked_flat_B256.md, each scaled by what the
@@ -254,6 +254,58 @@ def verify_bench(args) -> int:
     return 0
 
 
+def logprobs_bench(args) -> int:
+    """``--logprobs``: raw log-probabilities of the sampled token and the top 20 per row over the
+    headline logits (256 x 151936 bf16, four rotated input sets). Prints one JSON line: rows/s,
+    us per launch and the HBM roofline fraction over one read of the logits."""
+    import torch
+
+    from vinfer_amd.registry import BackendContext
+    from vinfer_amd.sampler import SAMPLER
+    from vinfer_amd.workloads import make
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    w = make("peaked_flat")
+    x = w.logits.to(dev)
+    sets = [x] + [torch.roll(x, shifts=7919 * i, dims=1).contiguous() for i in range(1, N_SETS)]
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    tokens = torch.randint(0, w.vocab, (w.batch,), dtype=torch.int32, device=dev)
+    for i in range(args.warmup):
+        hip.logprobs(sets[i % N_SETS], tokens, 20)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(args.steps):
+        hip.logprobs(sets[i % N_SETS], tokens, 20)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    algo = x.numel() * 2 + w.batch * (4 + 4 + 20 * 8)
+    achieved = algo / (us * 1e-6) / 1e9
+    out = {
+        "metric": "logprob rows/s + us/launch at B=256, V=151936 bf16, top 20; % HBM roofline",
+        "value": w.batch / (us * 1e-6),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": us / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": "logprobs_peaked_flat", "batch": w.batch, "vocab": w.vocab, "logits_dtype": "bf16",
+                   "n_top": 20, "input_sets": N_SETS},
+        "us_per_launch": us,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": algo},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -263,6 +315,7 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true", help="run the counter-calibration copy and exit")
     ap.add_argument("--decode", action="store_true", help="time the batched decode loop instead")
     ap.add_argument("--verify", action="store_true", help="time the speculative-decoding verify instead")
+    ap.add_argument("--logprobs", action="store_true", help="time the raw log-probabilities instead")
     args = ap.parse_args()
     if args.copy_probe:
         return copy_probe()
@@ -277,6 +330,8 @@ def main() -> int:
         return decode_loop(args)
     if args.verify:
         return verify_bench(args)
+    if args.logprobs:
+        return logprobs_bench(args)
 
     import numpy as np
     import torch

@@ -159,6 +159,16 @@ size_t vsamp_verify_workspace_bytes(int32_t batch, int32_t num_draft);
 
 int vsamp_verify(const vsamp_verify_args* args, void* stream);
 
+/* Log-probabilities of the raw logits (the log-softmax of the model's output, before penalties,
+ * temperature and filters, as OpenAI-style `logprobs` / `top_logprobs` report them): for each
+ * row, out_token_logprob[r] = logprob of tokens[r] (NaN outside [0, V)), and the row's n_top
+ * largest logits (descending, ties by ascending id) as out_top_ids / out_top_logprobs
+ * [B, n_top] (-1 / -inf past V). Only logits, dtype, batch, vocab and row_stride of `args` are
+ * read. A row whose max logit is not finite reports NaN. n_top in [0, 32]. The engine's API
+ * layer rejects these fields today (server/protocol.py:131-132). */
+int vsamp_logprobs(const vsamp_args* args, const int32_t* tokens, int32_t n_top, float* out_token_logprob,
+                   int32_t* out_top_ids, float* out_top_logprobs, void* stream);
+
 /* Host function (no device work): the draw's uniform of (seeds[i], positions[i]) into out[i],
  * i < n, all host memory. u = (splitmix64(position_seed(seed, position)) >> 40) * 2^-24, where
  * position_seed is the engine's per-token seed, sampler.py:44-47 (BLAKE2b-8 of

@@ -32,6 +32,10 @@ What it restates, row by row, in numpy (fp32 where the engine computes in fp32, 
    Kalman, Matias 2023; Chen et al. 2023) over rows of steps 1-9; its own docstring states the
    fixed-point residual and the tie rules.
 
+11. Log-probabilities (``logprobs_row``, not in the engine, whose API layer rejects the
+   ``logprobs`` / ``top_logprobs`` fields, server/protocol.py:131-132): the log-softmax of the
+   raw logits in fp64 and the top n by descending logit, ties by ascending id.
+
 ``classify_ties`` flags rows whose result two correct implementations may legitimately disagree
 on; the device kernels' masses are fixed-point with quantum ``2**-42`` (``p~ <= 1``), so a
 decision is fragile when it sits within ``(n + 4) * 2**-42`` of its threshold.
@@ -308,3 +312,24 @@ def verify_row(target: list[RowResult], draft: list[RowResult], drafts, u_acc, u
         res.ties.append("bonus")
     res.tokens.append(target[K].token)
     return res
+
+
+# ---- log-probabilities of the raw logits -----------------------------------------------------
+def logprobs_row(x: np.ndarray, token: int | None, n_top: int) -> tuple[float | None, list[int], np.ndarray]:
+    """The log-softmax of one raw fp32 row in fp64 (``x - M - log(sum exp(x - M))``, M the max;
+    NaN throughout when M is not finite): the logprob of ``token`` (NaN outside the row) and the
+    row's ``n_top`` largest logits, descending, ties by ascending id (NaN counts as largest);
+    entries past the row are id -1, logprob -inf."""
+    x = np.asarray(x, dtype=F32).astype(np.float64)
+    V = x.size
+    m = np.max(x) if not np.isnan(x).any() else np.nan
+    if np.isfinite(m):
+        lp = x - m - math.log(math.fsum(np.exp(x - m)))
+    else:
+        lp = np.full(V, np.nan)
+    tok = None if token is None else (float(lp[token]) if 0 <= token < V else float("nan"))
+    key = np.where(np.isnan(x), -np.inf, -x)
+    order = np.lexsort((np.arange(V), key))[: min(n_top, V)]
+    ids = order.tolist() + [-1] * (n_top - order.size)
+    vals = np.concatenate([lp[order], np.full(n_top - order.size, -np.inf)])
+    return tok, ids, vals

@@ -28,6 +28,7 @@ EXPORTS = (
     "vsamp_probs",
     "vsamp_penalized_logits",
     "vsamp_uniforms",
+    "vsamp_logprobs",
     "vsamp_verify",
     "vsamp_verify_workspace_bytes",
     "vsamp_last_error",
@@ -127,6 +128,16 @@ def load() -> ctypes.CDLL:
         lib.vsamp_verify.restype = ctypes.c_int
         lib.vsamp_verify_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32]
         lib.vsamp_verify_workspace_bytes.restype = ctypes.c_size_t
+        lib.vsamp_logprobs.argtypes = [
+            ctypes.POINTER(VsampArgs),
+            ctypes.c_void_p,
+            ctypes.c_int32,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+        ]
+        lib.vsamp_logprobs.restype = ctypes.c_int
         lib.vsamp_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
         lib.vsamp_uniforms.restype = ctypes.c_int
         lib.vsamp_last_error.restype = ctypes.c_char_p

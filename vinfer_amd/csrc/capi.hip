@@ -13,6 +13,7 @@
 #include "sample.cuh"
 #include "uniform.h"
 #include "verify.cuh"
+#include "logprobs.cuh"
 
 namespace {
 
@@ -382,6 +383,44 @@ int vsamp_verify(const vsamp_verify_args* v, void* stream) {
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_verify");
+}
+
+int vsamp_logprobs(const vsamp_args* a, const int32_t* tokens, int32_t n_top, float* out_token_logprob,
+                   int32_t* out_top_ids, float* out_top_logprobs, void* stream) {
+  g_err.clear();
+  if (!a) return fail(VSAMP_E_ARG, "args is NULL");
+  if (a->dtype != VSAMP_BF16 && a->dtype != VSAMP_F32)
+    return fail(VSAMP_E_DTYPE, "unsupported logits dtype %d (VSAMP_BF16=0, VSAMP_F32=1)", a->dtype);
+  if (a->batch < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", a->batch);
+  if (a->vocab < 1 || a->vocab > kMaxVocab)
+    return fail(VSAMP_E_ARG, "vocab must be in [1, %lld], got %d", static_cast<long long>(kMaxVocab), a->vocab);
+  if (a->row_stride < a->vocab)
+    return fail(VSAMP_E_ARG, "row_stride (%lld) must be >= vocab (%d)", static_cast<long long>(a->row_stride),
+                a->vocab);
+  if (n_top < 0 || n_top > vs::kMaxTop) return fail(VSAMP_E_ARG, "n_top must be in [0, %d], got %d", vs::kMaxTop, n_top);
+  if ((tokens == nullptr) != (out_token_logprob == nullptr))
+    return fail(VSAMP_E_ARG, "tokens and out_token_logprob must both be set or both NULL");
+  if (n_top > 0 && (!out_top_ids || !out_top_logprobs))
+    return fail(VSAMP_E_ARG, "out_top_ids and out_top_logprobs must be set when n_top > 0");
+  if (a->batch == 0) return VSAMP_OK;
+  if (!a->logits) return fail(VSAMP_E_ARG, "logits is NULL");
+  if (int rc = check_current_device()) return rc;
+  vs::LogprobArgs l;
+  l.logits = a->logits;
+  l.stride = a->row_stride;
+  l.V = a->vocab;
+  l.tokens = tokens;
+  l.n_top = n_top;
+  l.out_token = out_token_logprob;
+  l.out_top_ids = out_top_ids;
+  l.out_top = out_top_logprobs;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->dtype == VSAMP_BF16)
+    hipLaunchKernelGGL(vs::k_logprobs<uint16_t>, dim3(a->batch), dim3(vs::kThreads), 0, st, l);
+  else
+    hipLaunchKernelGGL(vs::k_logprobs<float>, dim3(a->batch), dim3(vs::kThreads), 0, st, l);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_logprobs");
 }
 
 int vsamp_uniforms(const int64_t* seeds, const int64_t* positions, int32_t n, float* out) {

@@ -176,6 +176,10 @@ __device__ __forceinline__ u64 mov(u64 x) {
   return (static_cast<u64>(hi) << 32) | lo;
 }
 template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double mov(double x) {
+  return __longlong_as_double(static_cast<long long>(mov<CTRL, ROW_MASK>(static_cast<u64>(__double_as_longlong(x)))));
+}
+template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ int mov(int x) {
   return static_cast<int>(mov<CTRL, ROW_MASK>(static_cast<uint32_t>(x)));
 }
@@ -187,6 +191,9 @@ __device__ __forceinline__ u64 last(u64 x) {
   const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), 63);
   const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(x >> 32), 63);
   return (static_cast<u64>(hi) << 32) | lo;
+}
+__device__ __forceinline__ double last(double x) {
+  return __longlong_as_double(static_cast<long long>(last(static_cast<u64>(__double_as_longlong(x)))));
 }
 
 // Reduction with an associative, commutative op: every 16-lane row ends with its row total in

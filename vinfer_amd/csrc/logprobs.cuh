@@ -1,0 +1,215 @@
+// Log-probabilities of the raw logits: for each row, lp_i = x_i - M - log(sum_j exp(x_j - M))
+// with M the row max (the log-softmax of the model's output, before penalties, temperature and
+// filters), reported for one given token per row and for the row's n largest logits (ties by
+// ascending id). The sum adds fp32 exponentials in fp64; a row whose max is not finite reports
+// NaN throughout.
+//
+// One workgroup per row: a pass for the max and a histogram of the keys' top 13 bits, which
+// gives the bin of the n-th largest key; a pass that sums the exponentials and copies every
+// element of that bin and the bins above to LDS (at most kCandCap); the n-th largest key by a
+// radix descent over that list, and the top n from it. A row whose top bins hold more than
+// kCandCap elements (massive ties) takes the n-th key over the row and its first members in
+// id order by two more passes.
+#pragma once
+
+#include "sample.cuh"
+
+namespace vs {
+
+constexpr int kMaxTop = 32;  // most top logprobs per row
+
+struct LogprobArgs {
+  const void* logits;  // row r at logits + r * stride
+  int64_t stride;
+  int V;
+  const int32_t* tokens;  // [B] or null: the token whose logprob is reported
+  int n_top;              // 0 .. kMaxTop
+  float* out_token;       // [B] or null
+  int32_t* out_top_ids;   // [B * n_top]
+  float* out_top;         // [B * n_top]
+};
+
+template <class Tin>
+__global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
+  constexpr int kBins = 8192;  // by the top 13 bits of the ordered key
+  __shared__ uint32_t h13[kBins];  // (then the candidate list: kCandCap 8-byte entries)
+  __shared__ Radix rdx;
+  __shared__ Search srch;
+  __shared__ Cand top[kMaxTop];
+  __shared__ uint32_t sh[8];
+  static_assert(sizeof(Cand) * kCandCap <= sizeof(uint32_t) * kBins, "the candidate list fits over the bins");
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  Row<Tin> row;
+  row.p = static_cast<const Tin*>(a.logits) + static_cast<int64_t>(r) * a.stride;
+  row.V = a.V;
+  row.nblk = (a.V + kBlk - 1) / kBlk;
+  row.nstripes = (row.nblk + kThreads - 1) / kThreads;
+  row.vec = (reinterpret_cast<uintptr_t>(row.p) & 15u) == 0;
+  row.bm = nullptr;
+  row.eid = nullptr;
+  row.eval = nullptr;
+  row.nexc = 0;
+  const int n = a.n_top;
+  for (int i = tid; i < kBins; i += kThreads) h13[i] = 0;
+  if (tid < 8) sh[tid] = 0;
+  __syncthreads();
+  // 1. the max key and the bins
+  uint32_t mk = 0;
+  for_each(row, [&](float x, int) {
+    const uint32_t k = key_of(x);
+    mk = k > mk ? k : mk;
+    if (n > 0) atomicAdd(&h13[k >> 19], 1u);
+  });
+  mk = static_cast<uint32_t>(block_max_u64(mk, srch.red64));
+  const float M = val_of(mk);
+  const bool finite = mk < key_of(INFINITY) && mk > key_of(-INFINITY);
+  // the bin of the n-th largest key (thread t sums bins 8191 - 8t .. 8184 - 8t, descending)
+  uint32_t bin = 0;
+  if (n > 0) {
+    uint32_t c8[8], s8 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      c8[i] = h13[kBins - 1 - 8 * tid - i];
+      s8 += c8[i];
+    }
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan<uint32_t>(s8, rdx.hcnt, &tot);
+    const uint32_t nn = static_cast<uint32_t>(n) < tot ? static_cast<uint32_t>(n) : tot;
+    if (nn > 0 && ex < nn && nn <= ex + s8) {
+      uint32_t above = ex;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (above < nn && nn <= above + c8[i]) sh[0] = static_cast<uint32_t>(kBins - 1 - 8 * tid - i);
+        above += c8[i];
+      }
+    }
+    __syncthreads();
+    bin = sh[0];
+  }
+  // 2. the sum of exponentials; the elements of the top bins to LDS
+  Cand* cand = reinterpret_cast<Cand*>(h13);
+  double s = 0.0;
+  for_each(row, [&](float x, int id) {
+    s += static_cast<double>(__expf(x - M));
+    if (n > 0) {
+      const bool c = (key_of(x) >> 19) >= bin;
+      const u64 bal = __ballot(c);  // (one counter update per wave round)
+      if (bal) {
+        const int leader = __ffsll(static_cast<long long>(bal)) - 1;
+        uint32_t at = 0;
+        if (lane_id() == leader) at = atomicAdd(&sh[1], static_cast<uint32_t>(__popcll(bal)));
+        at = __builtin_amdgcn_readlane(at, leader) + static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
+        if (c && at < static_cast<uint32_t>(kCandCap)) cand[at] = Cand{x, id};
+      }
+    }
+  });
+  s = block_sum<double>(s, reinterpret_cast<double*>(srch.red64));
+  const double lse = static_cast<double>(M) + log(s);
+  auto lp = [&](float x) -> float { return finite ? static_cast<float>(static_cast<double>(x) - lse) : NAN; };
+  if (tid == 0 && a.out_token && a.tokens) {
+    const int t = a.tokens[r];
+    a.out_token[r] = t >= 0 && t < a.V ? lp(load_one<Tin>(row.p, t)) : NAN;
+  }
+  if (n <= 0) return;
+  // 3. the n-th largest key (with multiplicity), from the list when it holds the top bins
+  __syncthreads();
+  const uint32_t nc = sh[1];
+  const uint32_t nn = static_cast<uint32_t>(n) < static_cast<uint32_t>(a.V) ? static_cast<uint32_t>(n)
+                                                                            : static_cast<uint32_t>(a.V);
+  const bool listed = nc <= static_cast<uint32_t>(kCandCap);
+  const CandList cl{cand, static_cast<int>(listed ? nc : 0)};
+  const uint32_t kk = listed ? radix_kth(row, &cl, nn, rdx) : radix_kth(row, nullptr, nn, rdx);
+  // 4. the elements above it (fewer than nn), then the first of those equal to it by id
+  if (tid == 0) sh[2] = 0;
+  __syncthreads();
+  if (listed) {
+    for (int i = tid; i < static_cast<int>(nc); i += kThreads) {
+      const Cand c = cand[i];
+      if (key_of(c.x) > kk) {
+        const uint32_t at = atomicAdd(&sh[2], 1u);
+        if (at < static_cast<uint32_t>(kMaxTop)) top[at] = c;
+      }
+    }
+  } else {
+    for_each(row, [&](float x, int id) {
+      if (key_of(x) > kk) {
+        const uint32_t at = atomicAdd(&sh[2], 1u);
+        if (at < static_cast<uint32_t>(kMaxTop)) top[at] = Cand{x, id};
+      }
+    });
+  }
+  __syncthreads();
+  const uint32_t na = sh[2];
+  const uint32_t need = nn - na;
+  if (listed) {
+    // a tied entry's place: the tied entries with a smaller id
+    for (int i = tid; i < static_cast<int>(nc); i += kThreads) {
+      const Cand c = cand[i];
+      if (key_of(c.x) != kk) continue;
+      uint32_t rank = 0;
+      for (int j = 0; j < static_cast<int>(nc); ++j) rank += key_of(cand[j].x) == kk && cand[j].id < c.id;
+      if (rank < need) top[na + rank] = c;
+    }
+  } else {
+    // the ties' per-stripe counts, then their places stripe by stripe (ascending id)
+    const int wv = tid / kWave;
+    for (int j = 0; j < row.nstripes; ++j) {
+      const int b = j * kThreads + tid;
+      uint32_t c = 0;
+      if (b < row.nblk) {
+        float v[kBlk];
+        const uint32_t valid = row.load(b, v);
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i) c += (valid >> i & 1u) && key_of(v[i]) == kk;
+      }
+      c = wave_sum<uint32_t>(c);
+      if (lane_id() == 0) srch.cell[wv][j] = c;
+    }
+    __syncthreads();
+    uint32_t done = 0;
+    for (int j = 0; j < row.nstripes && done < need; ++j) {
+      uint32_t cj = 0;
+      for (int w = 0; w < kWaves; ++w) cj += static_cast<uint32_t>(srch.cell[w][j]);
+      if (cj == 0) continue;  // (uniform)
+      const int b = j * kThreads + tid;
+      float v[kBlk];
+      const uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
+      uint32_t c = 0;
+#pragma unroll
+      for (int i = 0; i < kBlk; ++i) c += (valid >> i & 1u) && key_of(v[i]) == kk;
+      uint32_t tot;
+      uint32_t at = done + block_excl_scan<uint32_t>(c, rdx.hcnt, &tot);
+#pragma unroll
+      for (int i = 0; i < kBlk; ++i) {
+        if ((valid >> i & 1u) && key_of(v[i]) == kk) {
+          if (at < need) top[na + at] = Cand{v[i], b * kBlk + i};
+          ++at;
+        }
+      }
+      done += tot;
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  // 5. order: descending value, ascending id (the ties are last, already in id order)
+  if (tid < static_cast<int>(nn)) {
+    const Cand c = top[tid];
+    uint32_t rank = tid;
+    if (tid < static_cast<int>(na)) {
+      rank = 0;
+      for (int j = 0; j < static_cast<int>(na); ++j) {
+        const Cand o = top[j];
+        rank += key_of(o.x) > key_of(c.x) || (key_of(o.x) == key_of(c.x) && o.id < c.id);
+      }
+    }
+    a.out_top_ids[static_cast<int64_t>(r) * n + rank] = c.id;
+    a.out_top[static_cast<int64_t>(r) * n + rank] = lp(c.x);
+  }
+  for (int i = static_cast<int>(nn) + tid; i < n; i += kThreads) {  // n > V: the rest are empty
+    a.out_top_ids[static_cast<int64_t>(r) * n + i] = -1;
+    a.out_top[static_cast<int64_t>(r) * n + i] = -INFINITY;
+  }
+}
+
+}  // namespace vs

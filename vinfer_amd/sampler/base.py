@@ -81,6 +81,17 @@ class SamplerBackend(Protocol):
         then -1) and ``counts`` int32 ``[B]`` (1 .. K + 1)."""
         ...
 
+    def logprobs(
+        self, logits: torch.Tensor, tokens: torch.Tensor | None = None, n_top: int = 0
+    ) -> tuple[torch.Tensor | None, torch.Tensor, torch.Tensor]:
+        """Log-probabilities of the raw logits ``[B, V]`` (log-softmax before penalties,
+        temperature and filters: what ``logprobs`` / ``top_logprobs`` report): of ``tokens``
+        (int32 ``[B]``, NaN outside the vocabulary) and of each row's ``n_top`` (0 .. 32)
+        largest logits, descending with ties by ascending id. Returns ``(token_logprobs fp32
+        [B] or None, top_ids int32 [B, n_top], top_logprobs fp32 [B, n_top])``; a row whose max
+        logit is not finite reports NaN."""
+        ...
+
     def penalized_logits(
         self,
         logits: torch.Tensor,

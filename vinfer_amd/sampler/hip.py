@@ -192,6 +192,28 @@ class HipSampler:
         del keep
         return out, counts
 
+    def logprobs(self, logits, tokens=None, n_top=0):
+        dev = self._device(logits)
+        B, V = logits.shape
+        if not 0 <= n_top <= 32:
+            raise ValueError(f"n_top must be in [0, 32], got {n_top}")
+        a = _lib.VsampArgs()
+        a.logits = logits.data_ptr()
+        a.dtype = _DTYPES[logits.dtype]
+        a.batch, a.vocab = B, V
+        a.row_stride = logits.stride(0) if B > 1 else V
+        tok = self._vec(tokens.to(torch.int32) if tokens is not None else None, B, torch.int32, dev, "tokens")
+        out_tok = torch.empty(B, dtype=torch.float32, device=dev) if tok is not None else None
+        ids = torch.empty(B, n_top, dtype=torch.int32, device=dev)
+        lps = torch.empty(B, n_top, dtype=torch.float32, device=dev)
+        _lib.check(
+            self._lib.vsamp_logprobs(
+                ctypes.byref(a), _ptr(tok), n_top, _ptr(out_tok),
+                ids.data_ptr() if n_top else None, lps.data_ptr() if n_top else None, self._stream(dev)
+            )
+        )
+        return out_tok, ids, lps
+
     def verify(self, target_logits, draft_logits, draft_tokens, params, u_accept, u_residual, u_bonus,
                draft_params=None):
         if target_logits.dim() != 3 or draft_logits.dim() != 3:

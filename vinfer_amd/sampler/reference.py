@@ -151,6 +151,33 @@ class ReferenceSampler:
         dp = torch.tensor(dps, dtype=torch.float32, device=dev) if draft_ids is not None else None
         return out, dp
 
+    def logprobs(self, logits, tokens=None, n_top=0):
+        """Log-softmax of the raw fp32 logits in fp64; top ``n_top`` by descending logit, ties by
+        ascending id."""
+        if not 0 <= n_top <= 32:
+            raise ValueError(f"n_top must be in [0, 32], got {n_top}")
+        B, V = logits.shape
+        x = logits.double()
+        m = x.max(dim=1, keepdim=True).values
+        finite = torch.isfinite(m)
+        lp = x - m - torch.log(torch.exp(x - m).sum(dim=1, keepdim=True))
+        lp = torch.where(finite, lp, torch.full_like(lp, float("nan")))
+        out_tok = None
+        if tokens is not None:
+            t = tokens.long()
+            ok = (t >= 0) & (t < V)
+            out_tok = torch.where(ok, lp.gather(1, t.clamp(0, V - 1).view(-1, 1)).view(-1),
+                                  torch.full((B,), float("nan"), dtype=torch.float64, device=x.device)).float()
+        k = min(n_top, V)
+        # descending value, ascending id: a stable sort of the negated values (NaN first, as largest)
+        key = torch.where(torch.isnan(x), torch.full_like(x, -float("inf")), -x)
+        order = torch.sort(key, dim=1, stable=True).indices[:, :k]
+        ids = torch.full((B, n_top), -1, dtype=torch.int32, device=x.device)
+        lps = torch.full((B, n_top), -float("inf"), dtype=torch.float32, device=x.device)
+        ids[:, :k] = order.int()
+        lps[:, :k] = lp.gather(1, order).float()
+        return out_tok, ids, lps
+
     def verify(self, target_logits, draft_logits, draft_tokens, params, u_accept, u_residual, u_bonus,
                draft_params=None):
         """Speculative sampling (see the protocol) in exact integers: token masses
