@@ -177,6 +177,7 @@ template <class Tin>
 int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStream_t st,
                vs::RowState* state = nullptr) {
   const bool pen = wants_penalties(a);
+  if (state && pen) return fail(VSAMP_E_ARG, "row states are written without penalties only");
   vs::SampleArgs s;
   std::memset(&s, 0, sizeof s);
   if (pen) {
@@ -202,7 +203,9 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
   s.probs_stride = probs_stride;
   s.out_state = state;
   // One launch per step: the penalty phase runs at the start of the same kernel.
-  if (pen)
+  if (state)  // (the verify's launches, which apply no penalties)
+    hipLaunchKernelGGL((vs::k_sample<Tin, false, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
+  else if (pen)
     hipLaunchKernelGGL((vs::k_sample<Tin, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
   else
     hipLaunchKernelGGL((vs::k_sample<Tin, false>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);

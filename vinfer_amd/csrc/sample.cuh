@@ -784,14 +784,14 @@ __device__ __forceinline__ bool degenerate(const Row<Tin>& row, const RowParams&
   return false;
 }
 
-// Writes the row's outputs: probabilities (probs mode) or the sampled id and draft probability.
-// `draw` is the drawn token (ignored for point rows).
-template <class Tin>
+// Writes the row's outputs: probabilities (probs mode) or the sampled id and draft probability,
+// and with STATE the row's RowState. `draw` is the drawn token (ignored for point rows).
+template <bool STATE, class Tin>
 __device__ __forceinline__ void finish(const SampleArgs& a, const Row<Tin>& row, const RowParams& p, float mz,
                        const Kept& k, int draw, float* vslot) {
   const int tid = threadIdx.x;
   const int r = blockIdx.x;
-  if (a.out_state && tid == 0) {
+  if (STATE && tid == 0) {
     RowState st;
     st.mz = mz;
     st.T = p.T;
@@ -837,11 +837,11 @@ __device__ __forceinline__ void finish(const SampleArgs& a, const Row<Tin>& row,
 
 // With the cutoff group partial, the id of its r-th member (what kept() needs): only probs mode
 // and a draft token inside that group ask for it.
-template <class Tin>
+template <bool STATE, class Tin>
 __device__ __forceinline__ void resolve_idr(const SampleArgs& a, const Row<Tin>& row, const RowParams& p, Kept& k,
                             Search& s) {
   if (!k.partial) return;
-  bool need = a.out_probs != nullptr || a.out_state != nullptr;
+  bool need = STATE || a.out_probs != nullptr;
   if (!need && p.draft >= 0 && p.draft < row.V && a.out_dprob) need = value_of(row, p.draft, &s.vslot) == k.vc;
   if (need) {
     const float vc = k.vc;
@@ -896,7 +896,7 @@ __device__ __forceinline__ int chunk_pick(const u64* cm, int mode, double target
   return 16 * L + q;
 }
 
-template <class Tin>
+template <bool STATE, class Tin>
 __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g,
                                             FastSmem& f) {
   const int V = row.V;
@@ -927,7 +927,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
   const float mz = xmax / T;
   Kept k;
   if (degenerate(row, p, mkey, imax, mz, s, k)) {
-    finish(a, row, p, mz, k, 0, &s.vslot);
+    finish<STATE>(a, row, p, mz, k, 0, &s.vslot);
     return;
   }
   const uint32_t lo_key = key_of(-INFINITY);
@@ -1079,7 +1079,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     if (!k.partial) k.x0 = k.vc;
     k.S = mabove + static_cast<u64>(rr) * k.qc;
   }
-  resolve_idr(a, row, p, k, s);
+  resolve_idr<STATE>(a, row, p, k, s);
   int draw = 0;
   if (!a.out_probs) {
     // the draw: descending value, ascending id within a value
@@ -1154,7 +1154,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     }
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, s);
   }
-  finish(a, row, p, mz, k, draw, &s.vslot);
+  finish<STATE>(a, row, p, mz, k, draw, &s.vslot);
 }
 
 // ---- bf16 fast path: a 16-bit key histogram -----------------------------------------------------
@@ -1547,7 +1547,7 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
 // Loads here sit outside divergent branches (a lane past the end rereads a valid block whose
 // data it ignores): a load inside one needs a copy at the join, and that copy waits for every
 // load in flight.
-template <bool PEN>
+template <bool PEN, bool STATE>
 __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row, const RowParams& p, uint32_t* hist,
                                          FastSmem& f, Search& srch, uint32_t pw) {
   const int tid = threadIdx.x;
@@ -1917,7 +1917,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     if (f.plan.nnan) k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
     else if (!(T > 0.0f)) k.point = find_first(row, [&](float x, int) -> u64 { return x == xmax; }, 0ull, srch);
     else if (!degenerate(row, p, mkey, 0, mz, srch, k)) k.point = 0;
-    finish(a, row, p, mz, k, 0, &srch.vslot);
+    finish<STATE>(a, row, p, mz, k, 0, &srch.vslot);
     return true;
   }
   // ---- 5. [all] per-chunk masses of elements >= x0 ---------------------------------------
@@ -2115,14 +2115,14 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
       row.bm = reinterpret_cast<const uint8_t*>(bmw);
     }
   }
-  resolve_idr(a, row, p, k, srch);
+  resolve_idr<STATE>(a, row, p, k, srch);
   int draw = 0;
   if (!a.out_probs) {
     draw = cells_fit ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb, first)
                      : -1;
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
   }
-  finish(a, row, p, mz, k, draw, &srch.vslot);
+  finish<STATE>(a, row, p, mz, k, draw, &srch.vslot);
   return true;
 }
 
@@ -2144,7 +2144,8 @@ __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
   return a;
 }
 
-template <class Tin, bool PEN>
+// STATE: also write each row's RowState (the speculative verify's launches; never with PEN).
+template <class Tin, bool PEN, bool STATE = false>
 __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   const SampleArgs a = globalized(a_);
   // 128 KB: the key histogram (or the generic path's penalty counts), then the id-search /
@@ -2173,7 +2174,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   row.eval = f.eval;
   GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
   if constexpr (sizeof(Tin) == 2) {
-    if (fast_row<PEN>(a, row, f.prm, big, f, g.srch, pw)) return;
+    if (fast_row<PEN, STATE>(a, row, f.prm, big, f, g.srch, pw)) return;
     lds_barrier();  // (every thread is done with the fast path's LDS; f.prm is set)
   } else {
     if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
@@ -2190,7 +2191,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
     row.eid = a.ws.exc_id + p.h0;
     row.eval = a.ws.exc_val + p.h0;
   }
-  generic_row(a, row, p, g, f);
+  generic_row<STATE>(a, row, p, g, f);
 }
 
 }  // namespace vs
