@@ -134,11 +134,12 @@ int vsamp_penalized_logits(const vsamp_args* args, float* out, int32_t* counts,
  * the bonus token. Emitted tokens are then distributed exactly as the target's distribution.
  *
  * target: B * (K + 1) rows, row b * (K + 1) + j = the target's logits at draft position j
- * (j = K: the position after the last draft), with per-row parameters as in vsamp_sample.
- * draft: B * K rows, row b * K + j = the draft distribution that proposed draft j.
+ * (j = K: the position after the last draft). draft: B * K rows, row b * K + j = the draft
+ * distribution that proposed draft j. In both, the parameter arrays and uniforms hold ONE entry
+ * per sequence (B), which applies to all of its rows; target.uniforms[b] draws the bonus token
+ * (and the replacement when a residual is empty), draft.uniforms is optional and unused.
  * Both: the same vocab and dtype; no penalties (hist_ids NULL); draft_ids, out_ids and
- * out_draft_prob NULL (the call uses its workspace); target.uniforms required, draft.uniforms
- * optional. Replaces nothing in the engine, which skips its checkpoint's MTP head
+ * out_draft_prob NULL (the call uses its workspace). Replaces nothing in the engine, which skips its checkpoint's MTP head
  * (src/vinfer/models/loader.py:27); the C5 verify workload (draft-id probability) feeds it.
  */
 typedef struct vsamp_verify_args {

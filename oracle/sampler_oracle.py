@@ -262,7 +262,7 @@ def verify_row(target: list[RowResult], draft: list[RowResult], drafts, u_acc, u
     """Speculative sampling for one sequence (Leviathan, Kalman, Matias 2023; Chen et al. 2023),
     in the device kernels' fixed point, exact integer arithmetic.
 
-    ``target`` holds K + 1 rows (row K drawn with the bonus uniform), ``draft`` K rows. With P,
+    ``target`` holds K + 1 rows (each drawn with the sequence's bonus uniform), ``draft`` K rows. With P,
     Q the token masses (``token_masses``) and S_t, S_d their sums, draft j is accepted when
     ``m * Q_d * S_t < P_d * S_d * 2^24`` (m = floor(u_acc[j] * 2^24)), i.e. ``u < p / q``. At
     the first rejection the token is the first id (ascending) whose inclusive prefix of

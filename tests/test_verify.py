@@ -102,9 +102,8 @@ def test_reference_backend_matches_the_oracle():
                                 torch.from_numpy(ua), torch.from_numpy(ur), torch.from_numpy(ub))
     for b in range(B):
         r = params.row(b)
-        t = [sample_row(xt[b, j], r["temperature"], r["top_k"], r["top_p"], r["min_p"],
-                        float(ub[b]) if j == K else 0.0, int(drafts[b, j]) if j < K else None, want_probs=True)
-             for j in range(K + 1)]
+        t = [sample_row(xt[b, j], r["temperature"], r["top_k"], r["top_p"], r["min_p"], float(ub[b]),
+                        int(drafts[b, j]) if j < K else None, want_probs=True) for j in range(K + 1)]
         d = [sample_row(xq[b, j], r["temperature"], r["top_k"], r["top_p"], r["min_p"], 0.0, int(drafts[b, j]),
                         want_probs=True) for j in range(K)]
         want = verify_row(t, d, drafts[b], ua[b], ur[b], V)
@@ -147,9 +146,8 @@ def oracle_verify(xt, xq, drafts, params, ua, ur, ub):
     out = []
     for b in range(B):
         r = params.row(b)
-        t = [sample_row(xt[b, j], r["temperature"], r["top_k"], r["top_p"], r["min_p"],
-                        float(ub[b]) if j == K else 0.0, int(drafts[b, j]) if j < K else None, want_probs=True)
-             for j in range(K + 1)]
+        t = [sample_row(xt[b, j], r["temperature"], r["top_k"], r["top_p"], r["min_p"], float(ub[b]),
+                        int(drafts[b, j]) if j < K else None, want_probs=True) for j in range(K + 1)]
         d = [sample_row(xq[b, j], r["temperature"], r["top_k"], r["top_p"], r["min_p"], 0.0, int(drafts[b, j]),
                         want_probs=True) for j in range(K)]
         out.append(verify_row(t, d, drafts[b], ua[b], ur[b], V))

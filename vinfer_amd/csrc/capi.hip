@@ -175,7 +175,7 @@ int launch_penalties(const vs::PenaltyArgs& p, int B, hipStream_t st) {
 
 template <class Tin>
 int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStream_t st,
-               vs::RowState* state = nullptr) {
+               vs::RowState* state = nullptr, int param_div = 1) {
   const bool pen = wants_penalties(a);
   if (state && pen) return fail(VSAMP_E_ARG, "row states are written without penalties only");
   vs::SampleArgs s;
@@ -202,6 +202,7 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
   s.out_probs = probs;
   s.probs_stride = probs_stride;
   s.out_state = state;
+  s.param_div = param_div;
   // One launch per step: the penalty phase runs at the start of the same kernel.
   if (state)  // (the verify's launches, which apply no penalties)
     hipLaunchKernelGGL((vs::k_sample<Tin, false, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
@@ -354,8 +355,11 @@ int vsamp_verify(const vsamp_verify_args* v, void* stream) {
   if (int rc = check_current_device()) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bf = t.dtype == VSAMP_BF16;
-  if (int rc = bf ? run_sample<uint16_t>(&t, nullptr, 0, st, ts) : run_sample<float>(&t, nullptr, 0, st, ts)) return rc;
-  if (int rc = bf ? run_sample<uint16_t>(&d, nullptr, 0, st, ds) : run_sample<float>(&d, nullptr, 0, st, ds)) return rc;
+  // parameters and uniforms: one entry per sequence for all of its rows
+  if (int rc = bf ? run_sample<uint16_t>(&t, nullptr, 0, st, ts, K + 1) : run_sample<float>(&t, nullptr, 0, st, ts, K + 1))
+    return rc;
+  if (int rc = bf ? run_sample<uint16_t>(&d, nullptr, 0, st, ds, K) : run_sample<float>(&d, nullptr, 0, st, ds, K))
+    return rc;
   vs::VerifyArgs a;
   a.tgt = t.logits;
   a.tstride = t.row_stride;
@@ -375,7 +379,7 @@ int vsamp_verify(const vsamp_verify_args* v, void* stream) {
   a.done = reinterpret_cast<uint32_t*>(w + L.done);
   a.sums = reinterpret_cast<vs::u64*>(w + L.sums);
   const int nstripes = ((t.vocab + vs::kBlk - 1) / vs::kBlk + vs::kThreads - 1) / vs::kThreads;
-  a.slices = nstripes < 8 ? nstripes : 8;
+  a.slices = nstripes < 2 ? nstripes : 2;  // (measured: more slices add more fixed cost than they save)
   const dim3 ga((B + 255) / 256), gr(a.slices, B);
   if (bf) {
     hipLaunchKernelGGL(vs::k_verify_accept<uint16_t>, ga, dim3(256), 0, st, a, B);

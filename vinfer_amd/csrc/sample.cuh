@@ -56,6 +56,7 @@ struct SampleArgs {
   float* out_probs;  // probs mode when non-null
   int64_t probs_stride;
   RowState* out_state;  // optional: each row's RowState
+  int param_div;        // (row-state launches) rows per parameter entry: row r reads entry r / param_div
   Workspace ws;
   int has_exc;  // the workspace holds this batch's exceptions
   const int32_t* off;
@@ -183,8 +184,9 @@ __device__ const uint32_t kParamDefaults[16] = {0x3F800000u, 0x3F800000u, 0u, 0u
 // instead would index the argument struct, which then has to live in scratch memory.
 // Word w of row r's parameters, one load per lane: the lane picks its column's address (or the
 // default's) first, so nothing waits for the load until the word is used.
-template <bool PEN>
-__device__ __forceinline__ uint32_t param_word(const SampleArgs& a, int r, int w) {
+template <bool PEN, bool STATE = false>
+__device__ __forceinline__ uint32_t param_word(const SampleArgs& a, int r0, int w) {
+  const int r = STATE ? r0 / a.param_div : r0;
   const void* cols[kParamWords] = {a.temp, a.topp, a.minp, a.u, a.topk, a.draft,
                                    PEN ? a.pen.rep : nullptr, PEN ? a.pen.pres : nullptr,
                                    PEN ? a.pen.freq : nullptr, PEN ? a.off : nullptr, PEN ? a.off : nullptr};
@@ -2159,7 +2161,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   exp_table_init();  // (published by the first barrier of either path)
   // the row's parameters: thread w < kParamWords loads word w, the others word 0 (every thread
   // loads: a load on one branch only would make later waits wait for every load in flight)
-  const uint32_t pw = param_word<PEN>(a, r, tid < kParamWords ? tid : 0);
+  const uint32_t pw = param_word<PEN, STATE>(a, r, tid < kParamWords ? tid : 0);
   __builtin_amdgcn_sched_barrier(0);  // (issued before the row's first loads)
 
   Row<Tin> row;

@@ -67,10 +67,11 @@ class HipSampler:
             raise ValueError(f"{name} must be a {dtype} [{n}] tensor on {dev}")
         return t.contiguous()
 
-    def _args(self, logits, params, hist_ids, hist_offsets, uniforms=None, draft_ids=None):
+    def _args(self, logits, params, hist_ids, hist_offsets, uniforms=None, draft_ids=None, param_rows=None):
         dev = self._device(logits)
         B, V = logits.shape
-        if params.batch != B:
+        P = B if param_rows is None else param_rows  # parameter entries (verify: one per sequence)
+        if params.batch != P:
             raise ValueError(f"params describe {params.batch} rows, logits have {B}")
         cols = {}
         for name in (
@@ -81,8 +82,8 @@ class HipSampler:
             "presence_penalty",
             "frequency_penalty",
         ):
-            cols[name] = self._vec(getattr(params, name), B, torch.float32, dev, name)
-        cols["top_k"] = self._vec(params.top_k, B, torch.int32, dev, "top_k")
+            cols[name] = self._vec(getattr(params, name), P, torch.float32, dev, name)
+        cols["top_k"] = self._vec(params.top_k, P, torch.int32, dev, "top_k")
         if (hist_ids is None) != (hist_offsets is None):
             raise ValueError("hist_ids and hist_offsets go together")
         hist_total = 0
@@ -116,7 +117,7 @@ class HipSampler:
         a.hist_total = hist_total
         a.flags = flags if hist_total else 0
         if uniforms is not None:
-            uniforms = self._vec(uniforms, B, torch.float32, dev, "uniforms")
+            uniforms = self._vec(uniforms, P, torch.float32, dev, "uniforms")
             a.uniforms = _ptr(uniforms)
         if draft_ids is not None:
             draft_ids = self._vec(draft_ids, B, torch.int32, dev, "draft_ids")
@@ -236,11 +237,9 @@ class HipSampler:
         for name, t, shape in (("draft_tokens", drafts, (B, K)), ("u_accept", ua, (B, K)), ("u_residual", ur, (B, K))):
             if tuple(t.shape) != shape or t.device != dev:
                 raise ValueError(f"{name} must be [{B}, {K}] on {dev}")
-        tu = torch.zeros(B, K1, dtype=torch.float32, device=dev)
-        tu[:, K] = self._vec(u_bonus.to(torch.float32), B, torch.float32, dev, "u_bonus")
-        tu = tu.reshape(-1)
-        ta, tkeep = self._args(tl, params.repeat_rows(K1), None, None, tu)
-        da, dkeep = self._args(dl, dparams.repeat_rows(K), None, None, None)
+        ub = self._vec(u_bonus.to(torch.float32), B, torch.float32, dev, "u_bonus")
+        ta, tkeep = self._args(tl, params, None, None, ub, param_rows=B)
+        da, dkeep = self._args(dl, dparams, None, None, None, param_rows=B)
         v = _lib.VsampVerifyArgs()
         v.target, v.draft = ta, da
         v.batch, v.num_draft = B, K

@@ -218,8 +218,8 @@ class ReferenceSampler:
                 sh = max(St, Sd).bit_length() - 1
                 w = [max(0, ((p * Sd) >> sh) - ((q * St) >> sh)) for p, q in zip(P, Q)]
                 R = sum(w)
-                if R == 0:  # the target's own draw at this position (its uniform is 0)
-                    out.append(own_draw(b, j, 0.0))
+                if R == 0:  # the target's own draw at this position (the sequence's bonus uniform)
+                    out.append(own_draw(b, j, u_bonus[b]))
                 else:
                     tg = min((m24(u_residual[b, j]) * R) >> 24, R - 1)
                     c = 0
