@@ -347,3 +347,40 @@ def test_the_model_hears_when_a_slot_is_released(cpu_model, ref_sampler):
     dec.cancel(rids[1])
     dec.run()
     assert m.live == set()
+
+
+def logprob_steps_match_the_oracle(model, sampler, atol):
+    from oracle.sampler_oracle import logprobs_row
+
+    sp = SamplingParams(max_tokens=6, temperature=0.9, top_p=0.9, seed=5, logprobs=True, top_logprobs=3)
+    plain = SamplingParams(max_tokens=6, temperature=0.9, seed=6)
+    got = run_batched(model, sampler, [(PROMPT, sp), ([4, 2], plain)], num_slots=2)
+    assert all(st.logprob is None and st.top_logprobs is None for st in got[1])
+    tok, pos = PROMPT[-1], len(PROMPT) - 1
+    dev = model.device
+    for st in got[0]:
+        row = model.decode(*(torch.tensor([v], device=dev) for v in (0, tok, pos)))[0]
+        wt, wids, wv = logprobs_row(row.float().cpu().numpy(), st.token_id, 3)
+        assert abs(st.logprob - wt) <= atol + 2.0**-22 * abs(wt)  # (fp32 outputs)
+        assert [i for i, _ in st.top_logprobs] == wids
+        assert all(abs(v - w) <= atol + 2.0**-22 * abs(w) for (_, v), w in zip(st.top_logprobs, wv))
+        tok, pos = st.token_id, pos + 1
+
+
+def test_requested_logprobs_come_with_each_step(cpu_model, ref_sampler):
+    logprob_steps_match_the_oracle(cpu_model, ref_sampler, 1e-6)
+
+
+def test_logprob_fields_are_validated():
+    with pytest.raises(ValueError, match="top_logprobs"):
+        SamplingParams(top_logprobs=21, logprobs=True)
+    with pytest.raises(ValueError, match="needs logprobs"):
+        SamplingParams(top_logprobs=2)
+
+
+@pytest.mark.gpu
+def test_gpu_requested_logprobs_come_with_each_step():
+    dev = torch.device("cuda", 0)
+    model = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    logprob_steps_match_the_oracle(model, hip, 2e-5)

@@ -49,6 +49,10 @@ class Step:
     token_id: int
     text: str  # new text that is safe to show (empty while it could still be a stop string)
     finish_reason: str | None = None  # "stop" | "length" | None
+    # with SamplingParams.logprobs: the token's log-probability under the raw logits, and the
+    # top_logprobs most likely (token id, log-probability) pairs
+    logprob: float | None = None
+    top_logprobs: list[tuple[int, float]] | None = None
 
 
 def check_request(prompt_len: int, params: SamplingParams, max_seq_len: int) -> None:
@@ -162,6 +166,7 @@ class BatchDecoder:
         # Logits of the last model step, not yet sampled: (sequences, [n, V]).
         self._pending: tuple[list[_Seq], torch.Tensor] | None = None
         self._packed: dict[tuple[int, ...], PackedParams] = {}
+        self._lp: list = []  # this step's log-probability launches
         # One history row per slot; the extra column takes the id drawn at the last position.
         self._hist_row = max_seq_len + 1
         self.hist = torch.zeros(num_slots * self._hist_row, dtype=torch.int32, device=model.device)
@@ -226,13 +231,18 @@ class BatchDecoder:
         st.reset()
         cols = [self._stage_draw(st, seqs) for seqs, _ in groups]
         st.send()
+        self._lp = []
         drawn = [self._draw(seqs, logits, st, c) for (seqs, logits), c in zip(groups, cols)]
         seqs = [s for g in groups for s in g[0]]
         tokens = torch.cat(drawn).tolist() if len(drawn) > 1 else drawn[0].tolist()  # the one wait
+        lp_of = self._host_logprobs()
         out: list[tuple[int, Step]] = []
         going: list[_Seq] = []
         for s, tok in zip(seqs, tokens):
             step = self._advance(s, tok)
+            if s.params.logprobs:
+                step.logprob, top = lp_of[id(s)]
+                step.top_logprobs = top[: s.params.top_logprobs] if s.params.top_logprobs else None
             out.append((s.rid, step))
             if step.finish_reason is None:
                 going.append(s)
@@ -309,21 +319,36 @@ class BatchDecoder:
         return at_u, at_r
 
     def _draw(self, seqs: list[_Seq], logits: torch.Tensor, st: _Staging, cols) -> torch.Tensor:
-        """Launch the sampler over one group; the drawn ids stay on the device."""
+        """Launch the sampler over one group; the drawn ids stay on the device. With a row that
+        asks for log-probabilities, their launch follows (results kept for ``_advance``)."""
         n = len(seqs)
         at_u, at_r = cols
         u = st.device(at_u, n).view(torch.float32)
         params = self._params(seqs, logits.device)
         if at_r is None:
             ids, _ = self.sampler.sample_batch(logits, params, u)
-            return ids
-        ranges = st.device(at_r, 2 * n).view(n, 2)
-        ids, _ = self.sampler.sample_batch(logits, params, u, self.hist, ranges)
-        # The drawn id joins its row's history right behind the range just used.
-        self.hist.index_copy_(0, ranges[:, 1].long(), ids)
-        for s in seqs:
-            s.hist_len += s.params.penalized
+        else:
+            ranges = st.device(at_r, 2 * n).view(n, 2)
+            ids, _ = self.sampler.sample_batch(logits, params, u, self.hist, ranges)
+            # The drawn id joins its row's history right behind the range just used.
+            self.hist.index_copy_(0, ranges[:, 1].long(), ids)
+            for s in seqs:
+                s.hist_len += s.params.penalized
+        if any(s.params.logprobs for s in seqs):
+            n_top = max(s.params.top_logprobs for s in seqs)
+            tok_lp, top_ids, top_lp = self.sampler.logprobs(logits, ids, n_top)
+            self._lp.append((seqs, tok_lp, top_ids, top_lp))
         return ids
+
+    def _host_logprobs(self) -> dict[int, tuple[float, list[tuple[int, float]]]]:
+        """The step's log-probabilities on the host, by sequence (after the step's wait)."""
+        out = {}
+        for seqs, tok_lp, top_ids, top_lp in self._lp:
+            tl, ti, tv = tok_lp.tolist(), top_ids.tolist(), top_lp.tolist()
+            for i, s in enumerate(seqs):
+                if s.params.logprobs:
+                    out[id(s)] = (tl[i], list(zip(ti[i], tv[i])))
+        return out
 
     def _advance(self, s: _Seq, tok: int) -> Step:
         """The request-side logic of one token (generate.py:130-142)."""

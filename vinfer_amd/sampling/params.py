@@ -1,10 +1,11 @@
 """Per-request sampling parameters, per-position seeds and the per-step uniform.
 
 ``SamplingParams`` keeps every field, default and validation rule of the engine's class
-(src/vinfer/runtime/sampler.py:18-41) and adds four fields the engine's API layer names but does
-not implement (server/protocol.py:133-135, :142): ``repetition_penalty``, ``presence_penalty``,
-``frequency_penalty`` and ``min_p``. Each is added with its "off" value as default, so existing
-callers construct the same objects and get the same behaviour.
+(src/vinfer/runtime/sampler.py:18-41) and adds six fields the engine's API layer names but does
+not implement (server/protocol.py:131-135, :142): ``repetition_penalty``, ``presence_penalty``,
+``frequency_penalty`` and ``min_p`` change the draw; ``logprobs`` and ``top_logprobs`` only ask
+the decode loop to report log-probabilities. Each is added with its "off" value as default, so
+existing callers construct the same objects and get the same behaviour.
 
 ``position_seed`` is the engine's 63-bit seed of ``(seed, position)`` (sampler.py:44-47).
 ``uniform`` turns it into the one uniform ``u`` in [0, 1) that the inverse-CDF draw consumes:
@@ -37,6 +38,9 @@ class SamplingParams:
     presence_penalty: float = 0.0  # 0 = off; subtracted once from every token in the history
     frequency_penalty: float = 0.0  # 0 = off; subtracted once per occurrence in the history
     min_p: float = 0.0  # 0 = off; drop tokens with p < min_p * max p
+    # Reported, not sampled (names and off-values as the API layer lists them, protocol.py:131-132):
+    logprobs: bool = False  # the drawn token's log-probability under the raw logits
+    top_logprobs: int = 0  # and the n most likely tokens' (0 .. 20; needs logprobs)
 
     def __post_init__(self) -> None:
         # The first four checks and messages are sampler.py:29-37.
@@ -55,6 +59,10 @@ class SamplingParams:
                 raise ValueError(f"{name} must be finite, got {getattr(self, name)}")
         if not 0 <= self.min_p <= 1:
             raise ValueError(f"min_p must be in [0, 1], got {self.min_p}")
+        if not 0 <= self.top_logprobs <= 20:
+            raise ValueError(f"top_logprobs must be in [0, 20], got {self.top_logprobs}")
+        if self.top_logprobs and not self.logprobs:
+            raise ValueError("top_logprobs needs logprobs")
 
     @property
     def greedy(self) -> bool:
