@@ -102,7 +102,7 @@ def decode_loop(args) -> int:
     import torch
 
     from vinfer_amd.registry import BackendContext
-    from vinfer_amd.runtime import BatchDecoder
+    from vinfer_amd.runtime import BatchDecoder, SpeculativeDecoder
     from vinfer_amd.sampler import SAMPLER
     from vinfer_amd.sampling import SamplingParams
     from vinfer_amd.workloads import SyntheticLM
@@ -112,12 +112,22 @@ def decode_loop(args) -> int:
     V, B, L = 151936, 64, 4096
     model = SyntheticLM(V, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
     hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
-    dec = BatchDecoder(model, hip, num_slots=B, max_seq_len=L, penalize_prompt=True)
+    K = args.num_draft
+    if K:
+        # the draft: the target's map with its head perturbed (a cheap, mostly agreeing proposer)
+        draft = SyntheticLM(V, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+        g = torch.Generator(device=dev).manual_seed(7)
+        draft.head = (draft.head.float() + torch.randn(draft.head.shape, generator=g, device=dev)
+                      * draft.head.float().std() * 0.5).to(torch.bfloat16)
+        dec = SpeculativeDecoder(model, hip, draft_model=draft, num_draft=K, num_slots=B, max_seq_len=L)
+    else:
+        dec = BatchDecoder(model, hip, num_slots=B, max_seq_len=L, penalize_prompt=True)
     rng = np.random.default_rng(1001)
     ks = (0, 20, 50, 1000)
     for i in range(B):
-        kw = dict(max_tokens=L - 64, ignore_eos=True, seed=int(rng.integers(0, 2**62)),
-                  repetition_penalty=1.05, presence_penalty=0.5, frequency_penalty=0.2)
+        kw = dict(max_tokens=L - 64, ignore_eos=True, seed=int(rng.integers(0, 2**62)))
+        if not K:
+            kw.update(repetition_penalty=1.05, presence_penalty=0.5, frequency_penalty=0.2)
         if i % 4 == 0:
             kw.update(temperature=0.0)
         else:
@@ -151,14 +161,19 @@ def decode_loop(args) -> int:
         return a.elapsed_time(b) * 1e3 / n
 
     model_us = timed(lambda: model.decode(slots, toks, pos))
-    seqs, logits = dec._pending
+    logits = model.decode(slots, toks, pos)
     u = torch.rand(B, device=dev)
+    seqs = list(dec._running.values())
     params = dec._params(seqs, dev)
-    ranges = torch.tensor([[s.slot * dec._hist_row, s.slot * dec._hist_row + s.hist_len] for s in seqs],
-                          dtype=torch.int32, device=dev)
-    sampler_us = timed(lambda: hip.sample_batch(logits, params, u, dec.hist, ranges))
+    if K:
+        sampler_us = timed(lambda: hip.sample_batch(logits, params, u))
+    else:
+        ranges = torch.tensor([[s.slot * dec._hist_row, s.slot * dec._hist_row + s.hist_len] for s in seqs],
+                              dtype=torch.int32, device=dev)
+        sampler_us = timed(lambda: hip.sample_batch(logits, params, u, dec.hist, ranges))
     out = {
-        "metric": "decode-loop tokens/s at 64 live sequences, V=151936 bf16",
+        "metric": "decode-loop tokens/s at 64 live sequences, V=151936 bf16"
+        + (f", speculative K={K}" if K else ""),
         "value": n_tok / (loop_us * K * 1e-6),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -176,9 +191,13 @@ def decode_loop(args) -> int:
             "vocab": V,
             "logits_dtype": "bf16",
             "model": "SyntheticLM rank 64",
-            "params": "25% greedy, else T U[0.3,1.5], top-k {20,50,1000}, top-p U[0.5,1]; penalties 1.05/0.5/0.2",
-            "history": "prompt (32) + generated ids, per-slot ranges",
+            "params": "25% greedy, else T U[0.3,1.5], top-k {20,50,1000}, top-p U[0.5,1]"
+            + ("" if K else "; penalties 1.05/0.5/0.2"),
+            "history": "prompt (32) + generated ids, per-slot ranges" if not K else "none (no penalties)",
+            "num_draft": K,
+            "draft": "target head + N(0, (0.5 sd)^2)" if K else None,
         },
+        "tokens_per_iteration": n_tok / args.steps,
         "us_per_step_loop": loop_us,
         "us_model_step_alone": model_us,
         "us_sampler_call_alone": sampler_us,
@@ -314,6 +333,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-probe", action="store_true", help="run the counter-calibration copy and exit")
     ap.add_argument("--decode", action="store_true", help="time the batched decode loop instead")
+    ap.add_argument("--num-draft", type=int, default=0, help="with --decode: speculative decoding, K drafts")
     ap.add_argument("--verify", action="store_true", help="time the speculative-decoding verify instead")
     ap.add_argument("--logprobs", action="store_true", help="time the raw log-probabilities instead")
     args = ap.parse_args()

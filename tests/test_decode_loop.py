@@ -384,3 +384,78 @@ def test_gpu_requested_logprobs_come_with_each_step():
     model = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
     hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
     logprob_steps_match_the_oracle(model, hip, 2e-5)
+
+
+# ---- speculative decoding ----------------------------------------------------------------------
+
+
+def run_speculative(model, draft, sampler, reqs, num_slots, K, max_seq_len=80, **kw):
+    from vinfer_amd.runtime import SpeculativeDecoder
+
+    dec = SpeculativeDecoder(model, sampler, draft_model=draft, num_draft=K, num_slots=num_slots,
+                             max_seq_len=max_seq_len, **kw)
+    rids = [dec.submit(p, sp) for p, sp in reqs]
+    done = dec.run()
+    assert dec._free == sorted(range(num_slots), reverse=True)
+    return [done[r] for r in rids]
+
+
+def greedy_requests(n, vocab, seed=0, **kw):
+    rng = np.random.default_rng(seed)
+    return [(rng.integers(0, vocab, int(rng.integers(1, 8))).tolist(),
+             SamplingParams(max_tokens=int(rng.integers(1, 25)), temperature=0.0, **kw)) for _ in range(n)]
+
+
+@pytest.mark.parametrize("K", [1, 3])
+def test_speculative_greedy_equals_the_plain_loop(cpu_model, ref_sampler, K):
+    # whatever the draft proposes, a greedy target keeps its own argmax chain
+    draft = SyntheticLM(96, dim=16, scale=3.0, dtype=torch.float32, seed=1)
+    reqs = greedy_requests(7, 96)
+    want = run_batched(cpu_model, ref_sampler, reqs, num_slots=3)
+    got = run_speculative(cpu_model, draft, ref_sampler, reqs, num_slots=3, K=K)
+    assert got == want
+
+
+def test_speculative_stops_inside_a_block(cpu_model, ref_sampler):
+    draft = SyntheticLM(96, dim=16, scale=3.0, dtype=torch.float32, seed=2)
+    (plain,) = run_batched(cpu_model, ref_sampler, [(PROMPT, SamplingParams(max_tokens=12, temperature=0))], 1)
+    stop = plain[4].token_id
+    sp = SamplingParams(max_tokens=12, temperature=0, stop_token_ids=(stop,))
+    (want,) = run_batched(cpu_model, ref_sampler, [(PROMPT, sp)], 1)
+    (got,) = run_speculative(cpu_model, draft, ref_sampler, [(PROMPT, sp)], 1, K=3)
+    assert got == want and got[-1].finish_reason == "stop"
+
+
+def test_a_perfect_draft_is_always_accepted(cpu_model, ref_sampler):
+    from vinfer_amd.runtime import SpeculativeDecoder
+
+    sp = SamplingParams(max_tokens=13, temperature=1.0, top_p=0.9, seed=3)
+    dec = SpeculativeDecoder(cpu_model, ref_sampler, draft_model=cpu_model, num_draft=3, num_slots=1, max_seq_len=40)
+    dec.submit(PROMPT, sp)
+    sizes = []
+    while dec.busy:
+        sizes.append(len(dec.step()))
+    assert sizes == [1, 4, 4, 4]  # the first token from the prefill, then K + 1 per iteration
+    with pytest.raises(ValueError, match="penalties"):
+        dec.submit(PROMPT, SamplingParams(repetition_penalty=1.2))
+
+
+def test_speculative_sampling_is_seeded(cpu_model, ref_sampler):
+    draft = SyntheticLM(96, dim=16, scale=3.0, dtype=torch.float32, seed=1)
+    reqs = [(PROMPT, SamplingParams(max_tokens=15, temperature=0.9, seed=s)) for s in (1, 2, 3)]
+    a = run_speculative(cpu_model, draft, ref_sampler, reqs, 2, K=2)
+    b = run_speculative(cpu_model, draft, ref_sampler, reqs, 3, K=2)
+    assert a == b and all(len(x) == 15 for x in a)
+
+
+@pytest.mark.gpu
+def test_gpu_speculative_greedy_equals_the_plain_loop():
+    dev = torch.device("cuda", 0)
+    model = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+    draft = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev, seed=1)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    reqs = greedy_requests(10, 151936, seed=4)
+    print("speculative greedy: 10 requests, K=2, V 151936 bf16", flush=True)
+    want = run_batched(model, hip, reqs, num_slots=4)
+    got = run_speculative(model, draft, hip, reqs, num_slots=4, K=2)
+    assert got == want

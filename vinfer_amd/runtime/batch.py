@@ -362,3 +362,125 @@ class BatchDecoder:
         if len(s.generated) == s.params.max_tokens:
             return Step(tok, text + (s.stream.flush() if s.stream else ""), "length")
         return Step(tok, text)
+
+
+class SpeculativeDecoder(BatchDecoder):
+    """The batched loop with speculative decoding: a draft model proposes ``num_draft`` tokens
+    per sequence, the target scores them in one step, and ``verify`` keeps each draft with
+    probability min(1, p / q), replacing the first rejected one from the residual, or adds the
+    target's bonus token when all are kept -- so a sequence advances 1 .. K + 1 tokens per
+    iteration and its tokens are distributed exactly as the target's sampling (the MTP flow of
+    the engine's reference deployments, vllm/configs/tuned-mtp.sh:13, whose head the engine's
+    loader skips, models/loader.py:27).
+
+    A sequence's first token is drawn from its prefill as in ``BatchDecoder``. After that, the
+    token at position n is decided with uniforms of ``(seed, -(4n + c))``, c = 1 (the draft's
+    draw), 2 (acceptance), 3 (residual), 4 (bonus): independent streams of the same per-request
+    seed. Greedy requests therefore get exactly the tokens the plain loop gives them, whatever
+    the draft proposes. Penalties and log-probabilities are not available here (``verify``
+    applies no penalties).
+
+    The target may define ``extend(slots, tokens [B, T], positions [B]) -> logits [B, T, V]``
+    (T tokens per slot from ``positions[b]``); without it the loop calls ``decode`` on the
+    flattened tokens, which is right for a model without per-slot state only. The draft model
+    is a ``DecodeModel``; a rejected draft leaves positions that the next iteration overwrites.
+    """
+
+    def __init__(self, model: DecodeModel, sampler: SamplerBackend, *, draft_model: DecodeModel, num_draft: int,
+                 **kw) -> None:
+        if num_draft < 1:
+            raise ValueError("num_draft must be >= 1")
+        super().__init__(model, sampler, **kw)
+        self.draft_model = draft_model
+        self.num_draft = num_draft
+        self._ready: list[_Seq] = []  # sequences with a first token, waiting for an iteration
+
+    def submit(self, prompt_ids: list[int], params: SamplingParams) -> int:
+        if params.penalized:
+            raise ValueError("speculative decoding applies no penalties")
+        if params.logprobs:
+            raise ValueError("speculative decoding reports no log-probabilities")
+        # positions up to prompt + max_tokens - 1 + num_draft are scored (the last block's drafts)
+        check_request(len(prompt_ids), dataclasses.replace(params, max_tokens=params.max_tokens + self.num_draft),
+                      self.max_seq_len)
+        return super().submit(prompt_ids, params)
+
+    def step(self) -> list[tuple[int, Step]]:
+        out: list[tuple[int, Step]] = []
+        spec = [s for s in self._ready if s.rid in self._running]
+        self._ready = []
+        if spec:
+            out += self._speculate(spec)
+        admitted = self._admit()
+        if admitted is not None:
+            seqs, logits = admitted
+            for s in seqs:
+                self.draft_model.prefill(s.slot, torch.tensor(s.prompt, dtype=torch.int64, device=self.draft_model.device))
+            st = self._stage[0]
+            st.reset()
+            cols = self._stage_draw(st, seqs)
+            st.send()
+            self._lp = []
+            tokens = self._draw(seqs, logits, st, cols).tolist()
+            for s, tok in zip(seqs, tokens):
+                step = self._advance(s, tok)
+                out.append((s.rid, step))
+                if step.finish_reason is None:
+                    self._ready.append(s)
+                else:
+                    self._retire(s)
+        self._free.sort(reverse=True)
+        return out
+
+    def _uniforms(self, seqs: list[_Seq], offsets: range, c: int, dev: torch.device) -> torch.Tensor:
+        """[len(seqs), len(offsets)] uniforms of stream c at positions s.position + offset."""
+        seeds = [s.params.seed for s in seqs for _ in offsets]
+        pos = [-(4 * (s.position + o) + c) for s in seqs for o in offsets]
+        u = position_uniforms(seeds, pos)
+        return torch.from_numpy(u).view(len(seqs), len(offsets)).to(dev)
+
+    def _speculate(self, seqs: list[_Seq]) -> list[tuple[int, Step]]:
+        K = self.num_draft
+        n = len(seqs)
+        dev = self.model.device
+        params = self._params(seqs, dev)
+        slots = torch.tensor([s.slot for s in seqs], dtype=torch.int64, device=dev)
+        last = torch.tensor([s.generated[-1] for s in seqs], dtype=torch.int64, device=dev)
+        pos0 = torch.tensor([s.position - 1 for s in seqs], dtype=torch.int64, device=dev)  # the last token's
+        u_draft = self._uniforms(seqs, range(K), 1, dev)
+        # the draft proposes K tokens
+        x = last
+        draft_rows, drafts = [], []
+        for j in range(K):
+            logits = self.draft_model.decode(slots, x, pos0 + j)
+            ids, _ = self.sampler.sample_batch(logits, params, u_draft[:, j].contiguous())
+            draft_rows.append(logits)
+            drafts.append(ids)
+            x = ids.long()
+        drafts_t = torch.stack(drafts, dim=1)  # [n, K]
+        # the target scores the last token and the K drafts
+        toks = torch.cat([last.view(n, 1), drafts_t.long()], dim=1)  # [n, K + 1]
+        extend = getattr(self.model, "extend", None)
+        if extend is not None:
+            target = extend(slots, toks, pos0)
+        else:
+            steps = torch.arange(K + 1, device=dev)
+            target = self.model.decode(slots.repeat_interleave(K + 1), toks.reshape(-1),
+                                       (pos0.view(n, 1) + steps).reshape(-1)).view(n, K + 1, -1)
+        tokens, counts = self.sampler.verify(
+            target, torch.stack(draft_rows, dim=1), drafts_t, params,
+            self._uniforms(seqs, range(K), 2, dev), self._uniforms(seqs, range(K), 3, dev),
+            self._uniforms(seqs, range(K, K + 1), 4, dev).view(n),
+        )
+        tokens, counts = tokens.tolist(), counts.tolist()  # the iteration's wait
+        out: list[tuple[int, Step]] = []
+        for s, row, c in zip(seqs, tokens, counts):
+            for tok in row[:c]:
+                step = self._advance(s, tok)
+                out.append((s.rid, step))
+                if step.finish_reason is not None:
+                    self._retire(s)
+                    break
+            else:
+                self._ready.append(s)
+        return out
