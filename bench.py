@@ -249,6 +249,25 @@ def verify_bench(args) -> int:
     us = e0.elapsed_time(e1) * 1e3 / args.steps
     algo = (tgt.numel() + drf.numel()) * 2 + B * (K * 16 + 8)
     achieved = algo / (us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        # the oracle's verify on the same sequences, cycling, for a bounded time
+        from oracle.sampler_oracle import sample_row, verify_row  # the checker, timed here as the baseline
+
+        xt, xd = tgt.float().cpu().numpy(), drf.float().cpu().numpy()
+        T, d = params.temperature.cpu().numpy(), drafts.cpu().numpy()
+        a_, r_, b_ = ua.cpu().numpy(), ur.cpu().numpy(), ub.cpu().numpy()
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0:
+            b = done % B
+            t = [sample_row(xt[b, j], T[b], 0, 0.95, 0.0, float(b_[b]), int(d[b, j]) if j < K else None,
+                            want_probs=True) for j in range(K + 1)]
+            q = [sample_row(xd[b, j], T[b], 0, 0.95, 0.0, 0.0, int(d[b, j]), want_probs=True) for j in range(K)]
+            verify_row(t, q, d[b], a_[b], r_[b], V)
+            done += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": done / dt, "unit": "sequences/s", "cores": 1, "kind": "port",
+               "sample": f"{done} sequences of the same batch (cycling), numpy fp64 oracle on one thread; {dt:.1f} s"}
     out = {
         "metric": "verified sequences/s + us/call at B=192, K=1, V=262144 bf16; % HBM roofline",
         "value": B / (us * 1e-6),
@@ -269,6 +288,8 @@ def verify_bench(args) -> int:
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "algorithmic_bytes_per_call": algo},
     }
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
     return 0
 
@@ -302,6 +323,18 @@ def logprobs_bench(args) -> int:
     us = e0.elapsed_time(e1) * 1e3 / args.steps
     algo = x.numel() * 2 + w.batch * (4 + 4 + 20 * 8)
     achieved = algo / (us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        from oracle.sampler_oracle import logprobs_row  # the checker, timed here as the baseline
+
+        xs, tk = w.logits.float().numpy(), tokens.cpu().numpy()
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0:
+            logprobs_row(xs[done % w.batch], int(tk[done % w.batch]), 20)
+            done += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": done / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": f"{done} rows of the same logits (cycling), numpy fp64 oracle on one thread; {dt:.1f} s"}
     out = {
         "metric": "logprob rows/s + us/launch at B=256, V=151936 bf16, top 20; % HBM roofline",
         "value": w.batch / (us * 1e-6),
@@ -321,6 +354,8 @@ def logprobs_bench(args) -> int:
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": algo},
     }
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
     return 0
 
