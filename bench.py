@@ -233,20 +233,25 @@ def verify_bench(args) -> int:
         top_p=f32(np.full(B, 0.95)), min_p=f32(np.zeros(B)), repetition_penalty=f32(np.ones(B)),
         presence_penalty=f32(np.zeros(B)), frequency_penalty=f32(np.zeros(B)))
     hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
-    drafts, _ = hip.sample_batch(drf.reshape(B * K, V), params.repeat_rows(K), f32(rng.random(B * K)))
-    drafts = drafts.reshape(B, K)
+    # the drafts, drawn as a drafter would, keeping their rows' states for the verify
+    drafts, states = hip.sample_states(drf.reshape(B * K, V), params.repeat_rows(K), f32(rng.random(B * K)))
+    drafts, states = drafts.reshape(B, K), states.reshape(B, K, -1)
     ua, ur, ub = f32(rng.random((B, K))), f32(rng.random((B, K))), f32(rng.random(B))
-    call = lambda: hip.verify(tgt, drf, drafts, params, ua, ur, ub)  # noqa: E731
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        tokens, counts = call()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / args.steps
+
+    def timed(call):
+        for _ in range(args.warmup):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            res = call()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / args.steps, res
+
+    us, (tokens, counts) = timed(lambda: hip.verify(tgt, drf, drafts, params, ua, ur, ub, draft_states=states))
+    us_recompute, _ = timed(lambda: hip.verify(tgt, drf, drafts, params, ua, ur, ub))
     algo = (tgt.numel() + drf.numel()) * 2 + B * (K * 16 + 8)
     achieved = algo / (us * 1e-6) / 1e9
     cpu = None
@@ -284,6 +289,8 @@ def verify_bench(args) -> int:
         "config": {"workload": "verify_k1", "batch": B, "num_draft": K, "vocab": V, "logits_dtype": "bf16",
                    "temperature": "U[0.5,1.2]", "top_p": 0.95, "draft": "target + N(0, 0.5^2)"},
         "us_per_call": us,
+        "draft_states": "saved when the drafts were drawn (vsamp_sample_states)",
+        "us_per_call_recomputing_draft_states": us_recompute,
         "mean_tokens_emitted": float(counts.float().mean()),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "algorithmic_bytes_per_call": algo},

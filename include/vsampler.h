@@ -26,7 +26,10 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 2
+#define VSAMP_ABI_VERSION 3
+
+/* Bytes of one row's sampling state (vsamp_sample_states), an opaque record. */
+#define VSAMP_ROW_STATE_BYTES 40
 
 /* vsamp_args.flags bits. */
 #define VSAMP_HIST_RANGES 1u /* hist_offsets holds a [start, end) pair per row (see below) */
@@ -154,9 +157,18 @@ typedef struct vsamp_verify_args {
   int32_t* out_count;          /* [B]: tokens emitted, 1 .. K + 1 (accepted drafts + 1) */
   void* workspace;             /* vsamp_verify_workspace_bytes(B, K) bytes, 256-byte aligned */
   size_t workspace_bytes;
+  /* Optional: the draft rows' states [B * K] (row b * K + j), as vsamp_sample_states wrote them
+   * when the drafts were drawn, with the same parameters; then the draft rows are not sampled
+   * again (their logits are still read where a residual is drawn). NULL: computed here. */
+  const void* draft_states;
 } vsamp_verify_args;
 
 size_t vsamp_verify_workspace_bytes(int32_t batch, int32_t num_draft);
+
+/* vsamp_sample, and each row's sampling state (VSAMP_ROW_STATE_BYTES per row, out_states +
+ * r * VSAMP_ROW_STATE_BYTES, 8-byte aligned) for a later vsamp_verify of those rows as drafts.
+ * No penalties. */
+int vsamp_sample_states(const vsamp_args* args, void* out_states, void* stream);
 
 int vsamp_verify(const vsamp_verify_args* args, void* stream);
 

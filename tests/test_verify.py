@@ -202,3 +202,30 @@ def test_gpu_verify_on_tied_rows_with_split_cutoff_groups(dtype):
            (int(counts[b]) != len(w.tokens) or tokens[b, : len(w.tokens)].tolist() != w.tokens)]
     assert not bad, [(b, tokens[b].tolist(), want[b].tokens) for b in bad]
     assert sum(bool(w.ties) for w in want) <= B // 4
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_gpu_saved_draft_states_give_the_same_verify(dtype):
+    # the drafts drawn with sample_states, then verify with those states: the same tokens as a
+    # verify that samples the draft rows itself
+    dev = torch.device("cuda", 0)
+    B, K, V = 24, 3, 151936
+    xt, xq, _, params, ua, ur, ub = verify_case(55, B, K, V, dtype)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, dtype))
+    to = lambda a, t=None: torch.from_numpy(np.ascontiguousarray(a)).to(dev) if t is None else torch.from_numpy(a).to(t).to(dev)  # noqa: E731
+    tq = to(xq, dtype)
+    p = params.to(dev)
+    u = torch.rand(B, K, device=dev)
+    drafts, states = [], []
+    for j in range(K):
+        ids, st = hip.sample_states(tq[:, j].contiguous(), p, u[:, j].contiguous())
+        ids2, _ = hip.sample_batch(tq[:, j].contiguous(), p, u[:, j].contiguous())
+        assert torch.equal(ids, ids2)
+        drafts.append(ids)
+        states.append(st)
+    drafts = torch.stack(drafts, dim=1)
+    print(f"saved draft states B={B} K={K} V={V} {dtype}", flush=True)
+    a = hip.verify(to(xt, dtype), tq, drafts, p, to(ua), to(ur), to(ub))
+    b = hip.verify(to(xt, dtype), tq, drafts, p, to(ua), to(ur), to(ub), draft_states=torch.stack(states, dim=1))
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])

@@ -11,7 +11,8 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
+ROW_STATE_BYTES = 40
 
 VSAMP_BF16 = 0
 VSAMP_F32 = 1
@@ -29,6 +30,7 @@ EXPORTS = (
     "vsamp_penalized_logits",
     "vsamp_uniforms",
     "vsamp_logprobs",
+    "vsamp_sample_states",
     "vsamp_verify",
     "vsamp_verify_workspace_bytes",
     "vsamp_last_error",
@@ -81,6 +83,7 @@ class VsampVerifyArgs(ctypes.Structure):
         ("out_count", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("draft_states", ctypes.c_void_p),
     ]
 
 
@@ -124,6 +127,8 @@ def load() -> ctypes.CDLL:
             ctypes.c_void_p,
         ]
         lib.vsamp_penalized_logits.restype = ctypes.c_int
+        lib.vsamp_sample_states.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p, ctypes.c_void_p]
+        lib.vsamp_sample_states.restype = ctypes.c_int
         lib.vsamp_verify.argtypes = [ctypes.POINTER(VsampVerifyArgs), ctypes.c_void_p]
         lib.vsamp_verify.restype = ctypes.c_int
         lib.vsamp_verify_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32]

@@ -358,8 +358,12 @@ int vsamp_verify(const vsamp_verify_args* v, void* stream) {
   // parameters and uniforms: one entry per sequence for all of its rows
   if (int rc = bf ? run_sample<uint16_t>(&t, nullptr, 0, st, ts, K + 1) : run_sample<float>(&t, nullptr, 0, st, ts, K + 1))
     return rc;
-  if (int rc = bf ? run_sample<uint16_t>(&d, nullptr, 0, st, ds, K) : run_sample<float>(&d, nullptr, 0, st, ds, K))
+  if (v->draft_states) {
+    if (reinterpret_cast<uintptr_t>(v->draft_states) & 7u) return fail(VSAMP_E_ARG, "draft_states must be 8-byte aligned");
+    ds = static_cast<vs::RowState*>(const_cast<void*>(v->draft_states));
+  } else if (int rc = bf ? run_sample<uint16_t>(&d, nullptr, 0, st, ds, K) : run_sample<float>(&d, nullptr, 0, st, ds, K)) {
     return rc;
+  }
   vs::VerifyArgs a;
   a.tgt = t.logits;
   a.tstride = t.row_stride;
@@ -428,6 +432,19 @@ int vsamp_logprobs(const vsamp_args* a, const int32_t* tokens, int32_t n_top, fl
     hipLaunchKernelGGL(vs::k_logprobs<float>, dim3(a->batch), dim3(vs::kThreads), 0, st, l);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_logprobs");
+}
+
+int vsamp_sample_states(const vsamp_args* a, void* out_states, void* stream) {
+  g_err.clear();
+  if (int rc = validate(a, true)) return rc;
+  if (a->batch == 0) return VSAMP_OK;
+  if (!out_states || (reinterpret_cast<uintptr_t>(out_states) & 7u))
+    return fail(VSAMP_E_ARG, "out_states must be set and 8-byte aligned");
+  if (wants_penalties(a)) return fail(VSAMP_E_ARG, "row states are written without penalties only");
+  if (int rc = check_current_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  vs::RowState* s = static_cast<vs::RowState*>(out_states);
+  return a->dtype == VSAMP_BF16 ? run_sample<uint16_t>(a, nullptr, 0, st, s) : run_sample<float>(a, nullptr, 0, st, s);
 }
 
 int vsamp_uniforms(const int64_t* seeds, const int64_t* positions, int32_t n, float* out) {

@@ -40,6 +40,7 @@ struct RowState {
   int32_t pad;
   u64 S;                         // kept mass (fixed point, 2^42)
 };
+static_assert(sizeof(RowState) == 40, "VSAMP_ROW_STATE_BYTES");
 
 struct SampleArgs {
   const void* logits;

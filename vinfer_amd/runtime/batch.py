@@ -450,10 +450,15 @@ class SpeculativeDecoder(BatchDecoder):
         u_draft = self._uniforms(seqs, range(K), 1, dev)
         # the draft proposes K tokens
         x = last
-        draft_rows, drafts = [], []
+        draft_rows, drafts, states = [], [], []
+        with_states = hasattr(self.sampler, "sample_states")  # (the draft rows' states, for verify)
         for j in range(K):
             logits = self.draft_model.decode(slots, x, pos0 + j)
-            ids, _ = self.sampler.sample_batch(logits, params, u_draft[:, j].contiguous())
+            if with_states:
+                ids, st = self.sampler.sample_states(logits, params, u_draft[:, j].contiguous())
+                states.append(st)
+            else:
+                ids, _ = self.sampler.sample_batch(logits, params, u_draft[:, j].contiguous())
             draft_rows.append(logits)
             drafts.append(ids)
             x = ids.long()
@@ -471,6 +476,7 @@ class SpeculativeDecoder(BatchDecoder):
             target, torch.stack(draft_rows, dim=1), drafts_t, params,
             self._uniforms(seqs, range(K), 2, dev), self._uniforms(seqs, range(K), 3, dev),
             self._uniforms(seqs, range(K, K + 1), 4, dev).view(n),
+            draft_states=torch.stack(states, dim=1) if with_states else None,
         )
         tokens, counts = tokens.tolist(), counts.tolist()  # the iteration's wait
         out: list[tuple[int, Step]] = []

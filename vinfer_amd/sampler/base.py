@@ -68,6 +68,7 @@ class SamplerBackend(Protocol):
         u_residual: torch.Tensor,
         u_bonus: torch.Tensor,
         draft_params: PackedParams | None = None,
+        draft_states: torch.Tensor | None = None,
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """Speculative-decoding verify of ``K`` drafted tokens per sequence: draft ``j`` is
         accepted when ``u_accept[b, j] * q < p`` (``p``, ``q``: the target's and the draft's
@@ -77,8 +78,11 @@ class SamplerBackend(Protocol):
         ``target_logits`` ``[B, K + 1, V]``, ``draft_logits`` ``[B, K, V]`` (same dtype),
         ``draft_tokens`` int32 ``[B, K]``, uniforms fp32; ``params`` (one row per sequence)
         apply to the target rows, ``draft_params`` (default: the same) to the draft rows;
-        penalties are not applied. Returns ``tokens`` int32 ``[B, K + 1]`` (emitted tokens,
-        then -1) and ``counts`` int32 ``[B]`` (1 .. K + 1)."""
+        penalties are not applied. A backend with ``sample_states`` (an optional method: the
+        draws plus each row's opaque sampling state) takes the drafts' saved states as
+        ``draft_states`` ``[B, K, ...]`` instead of sampling the draft rows again. Returns
+        ``tokens`` int32 ``[B, K + 1]`` (emitted tokens, then -1) and ``counts`` int32 ``[B]``
+        (1 .. K + 1)."""
         ...
 
     def logprobs(

@@ -215,8 +215,21 @@ class HipSampler:
         )
         return out_tok, ids, lps
 
+    def sample_states(self, logits, params, uniforms):
+        """``sample_batch`` without histories, plus each row's sampling state (uint8 ``[B, 40]``,
+        opaque) for a later ``verify`` of these rows as drafts (``draft_states``)."""
+        a, keep = self._args(logits, params, None, None, uniforms)
+        dev = logits.device
+        B = logits.shape[0]
+        ids = torch.empty(B, dtype=torch.int32, device=dev)
+        states = torch.empty(B, _lib.ROW_STATE_BYTES // 8, dtype=torch.int64, device=dev)  # (8-byte aligned)
+        a.out_ids = ids.data_ptr()
+        _lib.check(self._lib.vsamp_sample_states(ctypes.byref(a), states.data_ptr(), self._stream(dev)))
+        del keep
+        return ids, states.view(torch.uint8).view(B, _lib.ROW_STATE_BYTES)
+
     def verify(self, target_logits, draft_logits, draft_tokens, params, u_accept, u_residual, u_bonus,
-               draft_params=None):
+               draft_params=None, draft_states=None):
         if target_logits.dim() != 3 or draft_logits.dim() != 3:
             raise ValueError("target_logits must be [B, K + 1, V] and draft_logits [B, K, V]")
         B, K1, V = target_logits.shape
@@ -247,6 +260,12 @@ class HipSampler:
         tokens = torch.empty(B, K1, dtype=torch.int32, device=dev)
         counts = torch.empty(B, dtype=torch.int32, device=dev)
         v.out_tokens, v.out_count = tokens.data_ptr(), counts.data_ptr()
+        if draft_states is not None:
+            ds = draft_states.reshape(B * K, _lib.ROW_STATE_BYTES)
+            if ds.dtype != torch.uint8 or ds.device != dev or ds.data_ptr() % 8:
+                raise ValueError("draft_states must be the uint8 [B, K, 40] states sample_states returned")
+            ds = ds.contiguous()
+            v.draft_states = ds.data_ptr()
         need = int(self._lib.vsamp_verify_workspace_bytes(B, K))
         ws = torch.empty(need + 256, dtype=torch.uint8, device=dev)
         v.workspace = (ws.data_ptr() + 255) & ~255

@@ -179,11 +179,12 @@ class ReferenceSampler:
         return out_tok, ids, lps
 
     def verify(self, target_logits, draft_logits, draft_tokens, params, u_accept, u_residual, u_bonus,
-               draft_params=None):
+               draft_params=None, draft_states=None):
         """Speculative sampling (see the protocol) in exact integers: token masses
         ``rint(p~ * 2^42)`` and their sums S; accept when ``m * Q_d * S_t < P_d * S_d * 2^24``
         (``m = floor(u * 2^24)``); the residual ``max(0, (P_i * S_d >> s) - (Q_i * S_t >> s))`` with
-        ``s = floor(log2(max(S_t, S_d)))`` over ascending ids."""
+        ``s = floor(log2(max(S_t, S_d)))`` over ascending ids. ``draft_states`` (the hip backend's
+        saved draft states) are not needed here: the draft rows are always recomputed."""
         B, K1, V = target_logits.shape
         K = K1 - 1
         dparams = params if draft_params is None else draft_params
