@@ -112,3 +112,22 @@ def test_gpu_logprobs_match_the_oracle(dtype, V, n_top):
             assert math.isnan(tl[b])
         else:
             assert abs(tl[b] - wt) <= 2e-6 + 1e-6 * abs(wt), (b, tl[b], wt)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_gpu_logprobs_on_unaligned_strided_rows(dtype):
+    # rows that start one element past a 16-byte boundary, with a row stride above V
+    dev = torch.device("cuda", 0)
+    B, V = 6, 5000
+    x, tokens = lp_case(9, B, V + 3, dtype)
+    view = x.to(dev)[:, 1 : V + 1]
+    print(f"logprobs unaligned rows B={B} V={V} {dtype}", flush=True)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, dtype))
+    tl, ids, lps = hip.logprobs(view, tokens.clamp(-1, V).to(dev), 7)
+    xs = x[:, 1 : V + 1].float().numpy()
+    for b in range(B):
+        wt, wids, wv = logprobs_row(xs[b], int(tokens.clamp(-1, V)[b]), 7)
+        assert ids[b].tolist() == wids
+        fin = np.isfinite(wv)
+        np.testing.assert_allclose(lps[b].cpu().numpy()[fin], wv[fin], rtol=1e-6, atol=2e-6)

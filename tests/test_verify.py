@@ -156,7 +156,7 @@ def oracle_verify(xt, xq, drafts, params, ua, ur, ub):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
-@pytest.mark.parametrize("K,V,B", [(1, 1000, 48), (3, 1000, 48), (1, 151936, 12), (2, 151936, 8)])
+@pytest.mark.parametrize("K,V,B", [(1, 1000, 48), (3, 1000, 48), (1, 151936, 12), (2, 151936, 8), (2, 4099, 24)])
 def test_gpu_verify_matches_the_oracle(dtype, K, V, B):
     dev = torch.device("cuda", 0)
     xt, xq, drafts, params, ua, ur, ub = verify_case(100 + K + V % 97, B, K, V, dtype)
