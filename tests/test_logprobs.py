@@ -1,8 +1,8 @@
 """Log-probabilities of the raw logits (``logprobs`` / ``top_logprobs``): the oracle's
 ``logprobs_row``, the reference backend and the hip kernel (``vsamp_logprobs``).
 
-The oracle is pinned by the closed form on the engine's test fixture (test_sampler.py:10: the
-softmax of Appendix B, so its logs), by scipy's ``log_softmax`` on random rows, by brute-force
+The oracle is pinned by the closed form on the engine's test fixture (test_sampler.py:10: its
+softmax at T = 1 in fp64, so its logs), by scipy's ``log_softmax`` on random rows, by brute-force
 ordering of the top n (descending value, ties by ascending id) on rows with many ties, and by
 the non-finite cases. Device results: top ids exact, logprobs within 2e-6 + 1e-6 |lp| (fp32
 output of an fp64 log of a sum of fp32 exponentials)."""
@@ -20,7 +20,7 @@ from vinfer_amd.registry import BackendContext
 from vinfer_amd.sampler import SAMPLER
 
 LOGITS = np.array([2.0, 1.0, 0.5, 0.0, -1.0, -3.0], np.float32)
-SOFTMAX_T1 = [0.560893, 0.206341, 0.125152, 0.075909, 0.027925, 0.003779]  # Appendix B
+SOFTMAX_T1 = [0.560893, 0.206341, 0.125152, 0.075909, 0.027925, 0.003779]  # softmax(LOGITS), closed form
 
 
 def test_closed_form_on_the_fixture():
