@@ -7,7 +7,8 @@ step's logits come from HBM. Per-launch durations come from HIP events recorded 
 the kernel runs on; the CPU baseline is the CPU oracle timed on a bounded sample of the same
 rows on this host.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--decode | --verify | --logprobs]
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+                       [--decode [--num-draft K] | --verify | --logprobs | --workloads]
 Prints one JSON line (``--decode``: the batched decode loop's line instead; ``--verify``: the
 speculative-decoding verify's; ``--logprobs``: the raw log-probabilities').
 
@@ -367,6 +368,70 @@ def logprobs_bench(args) -> int:
     return 0
 
 
+def workloads_bench(args) -> int:
+    """``--workloads``: every named sampler workload (the five survey shapes), one JSON line
+    each: the launch time (back-to-back launches between HIP events on the launch stream, after
+    warmup; inputs rotated over four copies when they fit in 8 GB), the HBM roofline fraction of
+    its algorithmic bytes, and the CPU oracle on a bounded sample of its rows."""
+    import numpy as np
+    import torch
+
+    from oracle.sampler_oracle import sample_batch  # the checker, timed here as the baseline
+    from vinfer_amd.registry import BackendContext
+    from vinfer_amd.sampler import SAMPLER
+    from vinfer_amd.workloads import NAMES, make
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    for name in NAMES:
+        w = make(name)
+        d = w.to(dev)
+        s = SAMPLER.resolve("hip", BackendContext(dev, w.logits.dtype))
+        nbytes = d.logits.numel() * d.logits.element_size()
+        sets = [d.logits] + ([torch.roll(d.logits, shifts=7919 * i, dims=1).contiguous() for i in range(1, N_SETS)]
+                             if nbytes * N_SETS <= 8 << 30 else [])
+        steps = [s.prepare_batch(x, d.params, d.uniforms, d.hist_ids, d.hist_offsets, d.draft_ids) for x in sets]
+        stream = torch.cuda.current_stream(dev)
+        for i in range(args.warmup):
+            steps[i % len(steps)].launch(stream.cuda_stream)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        K = max(1, args.steps // 4)
+        e0.record(stream)
+        for i in range(K):
+            steps[i % len(steps)].launch(stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / K
+        algo = w.algorithmic_bytes()
+        out = {"workload": name, "batch": w.batch, "vocab": w.vocab, "logits_dtype": str(w.logits.dtype).split(".")[-1],
+               "us_per_launch": us, "rows_per_s": w.batch / (us * 1e-6), "launches": K,
+               "input_sets": len(steps), "algorithmic_bytes": algo,
+               "roofline_frac": algo / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+        if not args.no_cpu:
+            f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+            p = w.params
+            cols = [f(getattr(p, k)) for k in ("temperature", "top_k", "top_p", "min_p", "repetition_penalty",
+                                                "presence_penalty", "frequency_penalty")]
+            hist = w.hist_ids.numpy() if w.hist_ids is not None else np.zeros(0, np.int32)
+            off = w.hist_offsets.numpy() if w.hist_offsets is not None else np.zeros(w.batch + 1, np.int32)
+            x, u = f(w.logits), f(w.uniforms)
+            dr = w.draft_ids.numpy() if w.draft_ids is not None else None
+            rows, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 3.0:
+                r = rows % w.batch
+                sample_batch(x[r : r + 1], *[c[r : r + 1] for c in cols], hist, off[r : r + 2], u[r : r + 1],
+                             None if dr is None else dr[r : r + 1])
+                rows += 1
+            dt = time.perf_counter() - t0
+            out["cpu_baseline"] = {"value": rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+                                   "sample": f"{rows} rows of the workload (cycling), numpy fp64 oracle; {dt:.1f} s"}
+        print(json.dumps(out), flush=True)
+        del steps, sets, d
+        torch.cuda.empty_cache()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -378,6 +443,7 @@ def main() -> int:
     ap.add_argument("--num-draft", type=int, default=0, help="with --decode: speculative decoding, K drafts")
     ap.add_argument("--verify", action="store_true", help="time the speculative-decoding verify instead")
     ap.add_argument("--logprobs", action="store_true", help="time the raw log-probabilities instead")
+    ap.add_argument("--workloads", action="store_true", help="time every named workload (one line each)")
     args = ap.parse_args()
     if args.copy_probe:
         return copy_probe()
@@ -394,6 +460,8 @@ def main() -> int:
         return verify_bench(args)
     if args.logprobs:
         return logprobs_bench(args)
+    if args.workloads:
+        return workloads_bench(args)
 
     import numpy as np
     import torch
