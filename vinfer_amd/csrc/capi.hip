@@ -36,6 +36,8 @@ int hip_fail(hipError_t e, const char* what) {
 
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_dev_ok[kMaxDevices];  // 0 unknown, 1 gfx950, 2 not
+std::atomic<int> g_dev_cus[kMaxDevices];  // compute units of a checked device
+constexpr int kMaxResidualSlices = 2;      // workgroups per rejected row of a verify call (measured: 1, 4 slower)
 
 int check_device(int dev, char* why, size_t n) {
   int count = 0;
@@ -56,7 +58,10 @@ int check_device(int dev, char* why, size_t n) {
     return VSAMP_E_HIP;
   }
   const bool ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-  if (dev < kMaxDevices) g_dev_ok[dev].store(ok ? 1 : 2);
+  if (dev < kMaxDevices) {
+    g_dev_cus[dev].store(prop.multiProcessorCount);
+    g_dev_ok[dev].store(ok ? 1 : 2);
+  }
   if (!ok) {
     if (why && n) snprintf(why, n, "needs a gfx950 (MI355X) GPU, device %d is %s", dev, prop.gcnArchName);
     return VSAMP_E_DEVICE;
@@ -72,6 +77,13 @@ int check_current_device() {
   int rc = check_device(dev, why, sizeof why);
   if (rc) return fail(rc, "%s", why);
   return VSAMP_OK;
+}
+
+// Compute units of the current device (checked by check_current_device first).
+int current_cus() {
+  int dev = 0;
+  const int n = hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices ? g_dev_cus[dev].load() : 0;
+  return n > 0 ? n : 256;
 }
 
 size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -215,7 +227,7 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
 }
 
 struct VerifyLayout {
-  size_t tids, dids, ts, ds, jr, done, sums, total;
+  size_t tids, dids, ts, ds, jr, done, sums, rej, nrej, total;
 };
 
 VerifyLayout verify_layout(int64_t B, int64_t K) {
@@ -236,6 +248,10 @@ VerifyLayout verify_layout(int64_t B, int64_t K) {
   o = align_up(o + 4 * static_cast<size_t>(B));
   L.sums = o;
   o = align_up(o + 8 * static_cast<size_t>(B) * vs::kMaxStripes);
+  L.rej = o;
+  o = align_up(o + 4 * static_cast<size_t>(B));
+  L.nrej = o;
+  o = align_up(o + 4);
   L.total = o;
   return L;
 }
@@ -382,14 +398,19 @@ int vsamp_verify(const vsamp_verify_args* v, void* stream) {
   a.jr = reinterpret_cast<int32_t*>(w + L.jr);
   a.done = reinterpret_cast<uint32_t*>(w + L.done);
   a.sums = reinterpret_cast<vs::u64*>(w + L.sums);
+  a.rej = reinterpret_cast<int32_t*>(w + L.rej);
+  a.nrej = reinterpret_cast<int32_t*>(w + L.nrej);
   const int nstripes = ((t.vocab + vs::kBlk - 1) / vs::kBlk + vs::kThreads - 1) / vs::kThreads;
-  a.slices = nstripes < 2 ? nstripes : 2;  // (measured: more slices add more fixed cost than they save)
-  const dim3 ga((B + 255) / 256), gr(a.slices, B);
+  a.max_slices = 1;
+  while (2 * a.max_slices <= nstripes && 2 * a.max_slices <= kMaxResidualSlices) a.max_slices *= 2;
+  // at most one workgroup per CU: items beyond the rejected rows' exit without holding a CU
+  const int64_t items = B * a.max_slices;
+  const dim3 gr(static_cast<unsigned>(items < current_cus() ? items : current_cus()));
   if (bf) {
-    hipLaunchKernelGGL(vs::k_verify_accept<uint16_t>, ga, dim3(256), 0, st, a, B);
+    hipLaunchKernelGGL(vs::k_verify_accept<uint16_t>, dim3(1), dim3(vs::kThreads), 0, st, a, B);
     hipLaunchKernelGGL(vs::k_verify_residual<uint16_t>, gr, dim3(vs::kThreads), 0, st, a);
   } else {
-    hipLaunchKernelGGL(vs::k_verify_accept<float>, ga, dim3(256), 0, st, a, B);
+    hipLaunchKernelGGL(vs::k_verify_accept<float>, dim3(1), dim3(vs::kThreads), 0, st, a, B);
     hipLaunchKernelGGL(vs::k_verify_residual<float>, gr, dim3(vs::kThreads), 0, st, a);
   }
   const hipError_t e = hipGetLastError();

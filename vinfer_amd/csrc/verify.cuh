@@ -49,7 +49,9 @@ struct VerifyArgs {
   int32_t* jr;            // [B] the first rejected position (K: none)
   uint32_t* done;         // [B] slices of the row's residual finished
   u64* sums;              // [B * kMaxStripes] per-stripe residual sums
-  int slices;             // workgroups per rejected row
+  int32_t* rej;           // [B] the rejected sequences, ascending
+  int32_t* nrej;          // [1] how many
+  int max_slices;         // most workgroups per rejected row (a power of two)
 };
 
 using u128 = unsigned __int128;
@@ -81,82 +83,141 @@ __device__ __forceinline__ float bf16_of_key(uint32_t key) {
 
 constexpr int kTab = 8192;  // tabulated keys per row (bf16)
 
-// One row's side of the residual: the term (mass * other_S) >> shift of each token.
+// Block b of a 16-byte-aligned row whose block is wholly inside it, as loaded (one
+// unconditional vector load, so that several in flight are waited for together: Row::load's
+// per-lane range test puts each load behind a branch), and its values.
+template <class Tin>
+struct WholeBlock;
+template <>
+struct WholeBlock<uint16_t> {
+  uint4 d;
+  __device__ __forceinline__ void load(const uint16_t* p, int b) { d = *reinterpret_cast<const uint4*>(p + b * kBlk); }
+  __device__ __forceinline__ void values(float v[kBlk]) const {
+    const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+};
+template <>
+struct WholeBlock<float> {
+  float4 d0, d1;
+  __device__ __forceinline__ void load(const float* p, int b) {
+    d0 = *reinterpret_cast<const float4*>(p + b * kBlk);
+    d1 = *reinterpret_cast<const float4*>(p + b * kBlk + 4);
+  }
+  __device__ __forceinline__ void values(float v[kBlk]) const {
+    v[0] = d0.x; v[1] = d0.y; v[2] = d0.z; v[3] = d0.w;
+    v[4] = d1.x; v[5] = d1.y; v[6] = d1.z; v[7] = d1.w;
+  }
+};
+
+// One row's side of the residual: the term (mass * other_S) >> shift of each token. Both forms
+// are free of branches (a point row has lo = +inf and its token in pid; other rows pid = -1),
+// so that the per-token code stays one straight run.
 struct ResidualSide {
   RowState st;
   u64 other_S;
   int shift;
-  float lo;               // kept tokens have x >= lo (x0, or the split group's value)
-  uint32_t klo, tlo, thi;  // keys >= klo are kept (x >= x0); keys in [tlo, thi] are tabulated
+  float lo;                // kept tokens have x >= lo (x0, or the split group's value); point row: +inf
+  float vcx;               // the split group's value (partial rows), else NaN
+  int pid;                 // a point row's token, else -1
+  uint32_t tlo, thi;       // tabulated keys: [tlo, thi] at tab[1 + k - tlo] (tab[0] = 0)
   const u64* tab;
   u64 point_term;  // a point row's token
 
-  __device__ __forceinline__ u64 direct(float x, int id) const {
-    return static_cast<u64>((static_cast<u128>(token_mass(x, id, st)) * other_S) >> shift);
+  __device__ __forceinline__ bool kept(float x, int id) const {
+    return (x >= lo) & !((x == vcx) & (id > st.idr));
   }
-  // bf16, every kept key of the row tabulated: the term of key k (value x)
+  // a kept token of value x (not a point row)
+  __device__ __forceinline__ u64 kept_term(float x) const {
+    return static_cast<u64>((static_cast<u128>(mass_q(ptilde(x, st.T, st.mz))) * other_S) >> shift);
+  }
+  __device__ __forceinline__ u64 direct(float x, int id) const {
+    return kept(x, id) ? kept_term(x) : (id == pid ? point_term : 0ull);
+  }
+  // bf16 row (not a point row) whose kept keys are all tabulated: the term of key k, value x
+  // (every key >= tlo is a value >= lo, every key below maps to entry 0)
   __device__ __forceinline__ u64 term(float x, uint32_t k, int id) const {
-    if (st.point >= 0) return id == st.point ? point_term : 0;
-    if (!(x >= lo) || (st.partial && x == st.vc && id > st.idr)) return 0;
-    return tab[k - tlo];
+    const int i = static_cast<int>(k) - static_cast<int>(tlo) + 1;
+    const u64 t = tab[i > 0 ? i : 0];
+    return (x == vcx) & (id > st.idr) ? 0ull : t;
   }
 };
 
-// One thread per sequence: the acceptance chain. Writes the accepted drafts and, when all are
-// accepted, the bonus token; leaves the first rejected position in jr and clears the row's
-// slice counter for k_verify_residual.
+// One workgroup, a thread per sequence: the acceptance chain. Writes the accepted drafts and,
+// when all are accepted, the bonus token; leaves the first rejected position in jr, clears the
+// row's slice counter and lists the rejected sequences (ascending) for k_verify_residual.
 template <class Tin>
-__global__ __launch_bounds__(256) void k_verify_accept(VerifyArgs a, int B) {
+__global__ __launch_bounds__(kThreads) void k_verify_accept(VerifyArgs a, int B) {
+  __shared__ uint32_t red[kWaves];
   exp_table_init();
   __syncthreads();
-  const int b = blockIdx.x * 256 + threadIdx.x;
-  if (b >= B) return;
   const int K = a.K;
   const Tin* tgt = static_cast<const Tin*>(a.tgt);
   const Tin* drf = static_cast<const Tin*>(a.drf);
-  int j = 0;
-  for (; j < K; ++j) {
-    const int d = a.drafts[b * K + j];
-    if (d < 0 || d >= a.V) break;  // a token outside the vocabulary is never accepted
-    const RowState st = a.ts[b * (K + 1) + j];
-    const RowState sd = a.ds[b * K + j];
-    const float xt = load_one<Tin>(tgt + static_cast<int64_t>(b * (K + 1) + j) * a.tstride, d);
-    const float xd = load_one<Tin>(drf + static_cast<int64_t>(b * K + j) * a.dstride, d);
-    const u64 P = token_mass(xt, d, st), Q = token_mass(xd, d, sd);
-    const u128 lhs = static_cast<u128>(u24(a.u_acc[b * K + j])) * Q * kept_mass(st);  // < 2^127
-    const u128 rhs = (static_cast<u128>(P) * kept_mass(sd)) << 24;
-    if (!(lhs < rhs)) break;
+  uint32_t listed = 0;
+  for (int b0 = 0; b0 < B; b0 += kThreads) {
+    const int b = b0 + static_cast<int>(threadIdx.x);
+    int j = K;
+    if (b < B) {
+      for (j = 0; j < K; ++j) {
+        const int d = a.drafts[b * K + j];
+        if (d < 0 || d >= a.V) break;  // a token outside the vocabulary is never accepted
+        const RowState st = a.ts[b * (K + 1) + j];
+        const RowState sd = a.ds[b * K + j];
+        const float xt = load_one<Tin>(tgt + static_cast<int64_t>(b * (K + 1) + j) * a.tstride, d);
+        const float xd = load_one<Tin>(drf + static_cast<int64_t>(b * K + j) * a.dstride, d);
+        const u64 P = token_mass(xt, d, st), Q = token_mass(xd, d, sd);
+        const u128 lhs = static_cast<u128>(u24(a.u_acc[b * K + j])) * Q * kept_mass(st);  // < 2^127
+        const u128 rhs = (static_cast<u128>(P) * kept_mass(sd)) << 24;
+        if (!(lhs < rhs)) break;
+      }
+      int32_t* out = a.out_tokens + static_cast<int64_t>(b) * (K + 1);
+      for (int i = 0; i <= K; ++i) out[i] = i < j ? a.drafts[b * K + i] : -1;
+      if (j == K) {
+        out[K] = a.tids[b * (K + 1) + K];
+        a.out_count[b] = K + 1;
+      }
+      a.jr[b] = j;
+      a.done[b] = 0;
+    }
+    const uint32_t r = j < K ? 1u : 0u;
+    uint32_t tot;
+    const uint32_t at = listed + block_excl_scan<uint32_t>(r, red, &tot);
+    if (r) a.rej[at] = b;
+    listed += tot;
   }
-  int32_t* out = a.out_tokens + static_cast<int64_t>(b) * (K + 1);
-  for (int i = 0; i <= K; ++i) out[i] = i < j ? a.drafts[b * K + i] : -1;
-  if (j == K) {
-    out[K] = a.tids[b * (K + 1) + K];
-    a.out_count[b] = K + 1;
-  }
-  a.jr[b] = j;
-  a.done[b] = 0;
+  if (threadIdx.x == 0) *a.nrej = static_cast<int32_t>(listed);
 }
 
-// The residual draw of each rejected row, spread over a.slices workgroups per row (grid
-// (slices, B)): each sums the residual over its share of the row's stripes; the last one to
-// finish finds the stripe that holds floor(m * R / 2^24) and the token inside it.
+// Workgroups per rejected row: the largest power of two with every (row, slice) item on its own
+// workgroup of the grid, at most max_slices.
+__device__ __forceinline__ int residual_slices(int nrej, int grid, int max_slices) {
+  int s = 1;
+  while (2 * s <= max_slices && static_cast<int64_t>(2 * s) * nrej <= grid) s *= 2;
+  return s;
+}
+
+// One (row, slice) item of the residual draw of rejected sequence b: the slice sums the residual
+// over its share of the row's stripes; the last slice of the row to finish finds the stripe that
+// holds floor(m * R / 2^24) and the token inside it.
 template <class Tin>
-__global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
+__device__ __forceinline__ void residual_item(const VerifyArgs& a, int b, int slice, int slices) {
   constexpr bool kBf16 = sizeof(Tin) == 2;
   __shared__ u64 cell[kWaves][kMaxStripes];
   __shared__ u64 red[kWaves];
   __shared__ u64 tab[2][kBf16 ? kTab : 1];
   __shared__ u64 sq[4];
   __shared__ int si[4];
-  const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int wv = tid / kWave;
   const int K = a.K;
   const int jr = a.jr[b];
-  if (jr >= K) return;  // (uniform) every draft accepted
   const Tin* tgt = static_cast<const Tin*>(a.tgt);
   const Tin* drf = static_cast<const Tin*>(a.drf);
-  exp_table_init();
   int32_t* out = a.out_tokens + static_cast<int64_t>(b) * (K + 1);
   // The rejected position's residual, over the target and draft rows at position jr.
   Row<Tin> rt, rd;
@@ -172,8 +233,8 @@ __global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
   rt.eval = rd.eval = nullptr;
   rt.nexc = rd.nexc = 0;
   // this workgroup's stripes
-  const int per = (rt.nstripes + a.slices - 1) / a.slices;
-  const int j_begin = blockIdx.x * per;
+  const int per = (rt.nstripes + slices - 1) / slices;
+  const int j_begin = slice * per;
   const int j_end = min(rt.nstripes, j_begin + per);
   ResidualSide side[2];
   bool tabled = kBf16;
@@ -183,12 +244,13 @@ __global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
   const int shift = 63 - __clzll(static_cast<long long>(St > Sd ? St : Sd));
   side[0].other_S = Sd;
   side[1].other_S = St;
-  __syncthreads();  // (publishes the exp table)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     ResidualSide& sd = side[h];
     sd.shift = shift;
-    sd.lo = sd.st.partial && sd.st.vc > sd.st.x0 ? sd.st.vc : sd.st.x0;
+    sd.lo = sd.st.point >= 0 ? INFINITY : sd.st.partial && sd.st.vc > sd.st.x0 ? sd.st.vc : sd.st.x0;
+    sd.vcx = sd.st.point < 0 && sd.st.partial ? sd.st.vc : NAN;
+    sd.pid = sd.st.point >= 0 ? sd.st.point : -1;
     sd.point_term = static_cast<u64>((static_cast<u128>(kPointMass) * sd.other_S) >> shift);
     sd.tab = tab[h];
     sd.tlo = 1;
@@ -205,26 +267,34 @@ __global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
           else hi = mid - 1;
         }
         sd.thi = lo;
-        sd.klo = sd.lo == -INFINITY ? 0x007Fu : bf16_key(__float_as_uint(sd.lo) >> 16);
-        sd.tlo = sd.klo;
-        if (sd.thi >= sd.tlo && sd.thi - sd.tlo < static_cast<uint32_t>(kTab)) {
+        // the smallest key whose value is >= lo (lo need not be a bf16 value)
+        uint32_t klo = 0x007Fu;
+        if (sd.lo != -INFINITY) {
+          klo = bf16_key(__float_as_uint(sd.lo) >> 16);
+          if (bf16_of_key(klo) < sd.lo) ++klo;
+        }
+        sd.tlo = klo;
+        if (sd.thi >= sd.tlo && sd.thi - sd.tlo < static_cast<uint32_t>(kTab - 1)) {
+          if (tid == 0) tab[h][0] = 0;
           for (uint32_t k = sd.tlo + tid; k <= sd.thi; k += kThreads)
-            tab[h][k - sd.tlo] = sd.direct(bf16_of_key(k), -1);  // (id -1: a kept member of a split group)
+            tab[h][1 + k - sd.tlo] = sd.kept_term(bf16_of_key(k));  // (x >= lo: kept, but for a split group's ids)
         } else {
           tabled = false;  // (uniform) the kept keys do not fit: every term computed directly
         }
+      } else {
+        tabled = false;  // (uniform) a point row: its one term computed directly
       }
     }
   }
   __syncthreads();
   // The residual is 0 wherever the target drops the token (P = 0).
-  const RowState& tst = side[0].st;
   const float tlo = side[0].lo;
+  const int tpid = side[0].pid;
   auto kept_lanes = [&](const float (&vt)[kBlk], uint32_t valid, int blk) {
     uint32_t kept = 0;
 #pragma unroll
     for (int i = 0; i < kBlk; ++i) {
-      const bool k = tst.point >= 0 ? blk * kBlk + i == tst.point : vt[i] >= tlo;
+      const bool k = vt[i] >= tlo || blk * kBlk + i == tpid;
       kept |= ((valid >> i) & 1u) && k ? 1u << i : 0u;
     }
     return kept;
@@ -253,24 +323,39 @@ __global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
     // 1. this slice's per-stripe sums; four stripes' loads of both rows in flight (the draft
     // block is read whether or not a target value in it is kept: a load behind a branch would
     // be waited for alone)
+    auto stripe_sum = [&](int j, const float (&vt)[kBlk], const float (&vd)[kBlk], uint32_t valid) {
+      const int blk = j * kThreads + tid;
+      u64 w[kBlk];
+      weights(vt, vd, kept_lanes(vt, valid, blk), blk, w, tab_mode);
+      u64 s = 0;
+#pragma unroll
+      for (int i = 0; i < kBlk; ++i) s += w[i];
+      s = wave_sum<u64>(s);
+      if (lane_id() == 0) cell[wv][j - j_begin] = s;
+    };
     for (int j0 = j_begin; j0 < j_end; j0 += 4) {
-      float vt[4][kBlk], vd[4][kBlk];
-      uint32_t valid[4];
+      if (rt.vec && rd.vec && j0 + 4 <= j_end && (j0 + 4) * kThreads * kBlk <= a.V) {
+        // (uniform) four stripes wholly inside both rows
+        WholeBlock<Tin> qt[4], qd[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int blk = (j0 + k) * kThreads + tid;
-        valid[k] = j0 + k < j_end && blk < rt.nblk ? rt.load(blk, vt[k]) & rd.load(blk, vd[k]) : 0u;
-      }
+        for (int k = 0; k < 4; ++k) {
+          qt[k].load(rt.p, (j0 + k) * kThreads + tid);
+          qd[k].load(rd.p, (j0 + k) * kThreads + tid);
+        }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int blk = (j0 + k) * kThreads + tid;
-        u64 w[kBlk];
-        weights(vt[k], vd[k], kept_lanes(vt[k], valid[k], blk), blk, w, tab_mode);
-        u64 s = 0;
-#pragma unroll
-        for (int i = 0; i < kBlk; ++i) s += w[i];
-        s = wave_sum<u64>(s);
-        if (lane_id() == 0 && j0 + k < j_end) cell[wv][j0 + k - j_begin] = s;
+        for (int k = 0; k < 4; ++k) {
+          float vt[kBlk], vd[kBlk];
+          qt[k].values(vt);
+          qd[k].values(vd);
+          stripe_sum(j0 + k, vt, vd, 0xFFu);
+        }
+      } else {
+        for (int j = j0; j < j_end && j < j0 + 4; ++j) {
+          const int blk = j * kThreads + tid;
+          float vt[kBlk], vd[kBlk];
+          const uint32_t valid = blk < rt.nblk ? rt.load(blk, vt) & rd.load(blk, vd) : 0u;
+          stripe_sum(j, vt, vd, valid);
+        }
       }
     }
     __syncthreads();
@@ -283,7 +368,7 @@ __global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
     __syncthreads();
     if (tid == 0) si[2] = static_cast<int>(atomicAdd(&a.done[b], 1u));
     __syncthreads();
-    if (si[2] != a.slices - 1) return;  // (uniform) another slice finishes the row
+    if (si[2] != slices - 1) return;  // (uniform) another slice finishes the row
     __threadfence();
     // 2. (last slice) stripe totals; the stripe where the running sum passes floor(m * R / 2^24)
     if (wv == 0) {
@@ -319,7 +404,15 @@ __global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
     // 3. per-thread sums inside stripe js; the thread whose block holds the target
     u64 w[kBlk] = {};
     const int blk = js * kThreads + tid;
-    if (blk < rt.nblk) {
+    if (rt.vec && rd.vec && (js + 1) * kThreads * kBlk <= a.V) {  // (uniform) a whole stripe
+      WholeBlock<Tin> qt, qd;
+      qt.load(rt.p, blk);
+      qd.load(rd.p, blk);
+      float vt[kBlk], vd[kBlk];
+      qt.values(vt);
+      qd.values(vd);
+      weights(vt, vd, kept_lanes(vt, 0xFFu, blk), blk, w, tab_mode);
+    } else if (blk < rt.nblk) {
       float vt[kBlk], vd[kBlk];
       const uint32_t valid = rt.load(blk, vt) & rd.load(blk, vd);
       weights(vt, vd, kept_lanes(vt, valid, blk), blk, w, tab_mode);
@@ -346,6 +439,19 @@ __global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
     residual(std::integral_constant<bool, kBf16>{});
   else
     residual(std::false_type{});
+}
+
+// The residual draws of the rejected rows: a grid of at most one workgroup per CU walks the
+// (row, slice) items, row-major over the list of rejected sequences.
+template <class Tin>
+__global__ __launch_bounds__(kThreads) void k_verify_residual(VerifyArgs a) {
+  exp_table_init();
+  const int nrej = *a.nrej;
+  const int slices = residual_slices(nrej, static_cast<int>(gridDim.x), a.max_slices);
+  for (int item = blockIdx.x; item < nrej * slices; item += gridDim.x) {
+    __syncthreads();  // (publishes the exp table; the previous item's LDS is free)
+    residual_item<Tin>(a, a.rej[item / slices], item % slices, slices);
+  }
 }
 
 }  // namespace vs
