@@ -229,3 +229,36 @@ def test_gpu_saved_draft_states_give_the_same_verify(dtype):
     a = hip.verify(to(xt, dtype), tq, drafts, p, to(ua), to(ur), to(ub))
     b = hip.verify(to(xt, dtype), tq, drafts, p, to(ua), to(ur), to(ub), draft_states=torch.stack(states, dim=1))
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_gpu_verify_with_a_point_row_on_one_side(dtype):
+    # a +inf logit makes a row a point mass at that id: even rows put it in the draft row (at the
+    # drafted id) against a sampled target row, odd rows in the target row against a sampled draft
+    dev = torch.device("cuda", 0)
+    B, K, V = 16, 1, 151936
+    xt, xq, drafts, _, ua, ur, ub = verify_case(91, B, K, V, dtype)
+    kinds = [dict(temperature=1.0, top_p=0.9), dict(temperature=0.8, top_k=50), dict(temperature=1.2, min_p=0.05)]
+    params = pack_params([SamplingParams(**kinds[b % 3]) for b in range(B)])
+    rng = np.random.default_rng(5)
+    for b in range(B):
+        i = int(rng.integers(0, V))
+        if b % 2 == 0:
+            xq[b, 0, i] = np.inf
+            drafts[b, 0] = i
+        else:
+            xt[b, 0, i] = np.inf
+    print(f"verify point rows B={B} K={K} V={V} {dtype}", flush=True)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, dtype))
+    to = lambda a, t=None: torch.from_numpy(np.ascontiguousarray(a)).to(dev) if t is None else torch.from_numpy(a).to(t).to(dev)  # noqa: E731
+    tokens, counts = hip.verify(to(xt, dtype), to(xq, dtype), to(drafts), params.to(dev), to(ua), to(ur), to(ub))
+    want = oracle_verify(xt, xq, drafts, params, ua, ur, ub)
+    tokens, counts = tokens.cpu(), counts.cpu()
+    rejected = 0
+    for b, w in enumerate(want):
+        assert not w.ties
+        rejected += len(w.tokens) == 1 and w.tokens[0] != int(drafts[b, 0])
+        assert int(counts[b]) == len(w.tokens), (b, counts[b], w.tokens)
+        assert tokens[b, : len(w.tokens)].tolist() == w.tokens, (b, tokens[b].tolist(), w.tokens)
+    assert rejected >= B // 2  # both kinds reach the residual draw
