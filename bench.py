@@ -137,13 +137,13 @@ def decode_loop(args) -> int:
     for _ in range(args.warmup):
         dec.step()
     torch.cuda.synchronize()
-    K = args.steps
+    steps = args.steps
     t0 = time.perf_counter()
     n_tok = 0
-    for _ in range(K):
+    for _ in range(steps):
         n_tok += len(dec.step())
     torch.cuda.synchronize()
-    loop_us = (time.perf_counter() - t0) / K * 1e6
+    loop_us = (time.perf_counter() - t0) / steps * 1e6
 
     # the two device parts alone, on the same shapes
     slots = torch.arange(B, device=dev)
@@ -175,10 +175,10 @@ def decode_loop(args) -> int:
     out = {
         "metric": "decode-loop tokens/s at 64 live sequences, V=151936 bf16"
         + (f", speculative K={K}" if K else ""),
-        "value": n_tok / (loop_us * K * 1e-6),
+        "value": n_tok / (loop_us * steps * 1e-6),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": K,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": loop_us / 1e3,
         "higher_is_better": True,
