@@ -369,7 +369,7 @@ def logprobs_bench(args) -> int:
 
 
 def workloads_bench(args) -> int:
-    """``--workloads``: every named sampler workload (the five survey shapes), one JSON line
+    """``--workloads``: every named sampler workload (``vinfer_amd.workloads.NAMES``), one JSON line
     each: the launch time (back-to-back launches between HIP events on the launch stream, after
     warmup; inputs rotated over four copies when they fit in 8 GB), the HBM roofline fraction of
     its algorithmic bytes, and the CPU oracle on a bounded sample of its rows."""
