@@ -56,7 +56,7 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
   __syncthreads();
   // 1. the max key and the bins
   uint32_t mk = 0;
-  for_each(row, [&](float x, int) {
+  for_each_ahead(row, [&](float x, int) {
     const uint32_t k = key_of(x);
     mk = k > mk ? k : mk;
     if (n > 0) atomicAdd(&h13[k >> 19], 1u);
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
   // 2. the sum of exponentials; the elements of the top bins to LDS
   Cand* cand = reinterpret_cast<Cand*>(h13);
   double s = 0.0;
-  for_each(row, [&](float x, int id) {
+  for_each_ahead(row, [&](float x, int id) {
     s += static_cast<double>(__expf(x - M));
     if (n > 0) {
       const bool c = (key_of(x) >> 19) >= bin;

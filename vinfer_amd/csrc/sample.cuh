@@ -262,6 +262,37 @@ static_assert(offsetof(FastSmem, eid) == offsetof(FastSmem, eval) + sizeof(float
               "ccnt .. eid must be contiguous");
 static_assert(kExcCap <= 2 * kThreads, "two ranks per thread");
 
+// Block b of a 16-byte-aligned row whose block is wholly inside it, as loaded (one
+// unconditional vector load, so that several in flight are waited for together: Row::load's
+// per-lane range test puts each load behind a branch), and its values.
+template <class Tin>
+struct WholeBlock;
+template <>
+struct WholeBlock<uint16_t> {
+  uint4 d;
+  __device__ __forceinline__ void load(const uint16_t* p, int b) { d = *reinterpret_cast<const uint4*>(p + b * kBlk); }
+  __device__ __forceinline__ void values(float v[kBlk]) const {
+    const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+};
+template <>
+struct WholeBlock<float> {
+  float4 d0, d1;
+  __device__ __forceinline__ void load(const float* p, int b) {
+    d0 = *reinterpret_cast<const float4*>(p + b * kBlk);
+    d1 = *reinterpret_cast<const float4*>(p + b * kBlk + 4);
+  }
+  __device__ __forceinline__ void values(float v[kBlk]) const {
+    v[0] = d0.x; v[1] = d0.y; v[2] = d0.z; v[3] = d0.w;
+    v[4] = d1.x; v[5] = d1.y; v[6] = d1.z; v[7] = d1.w;
+  }
+};
+
 template <class Tin>
 struct Row {
   const Tin* p;
@@ -328,9 +359,45 @@ __device__ __forceinline__ uint32_t Row<float>::load(int b, float v[kBlk]) const
 }
 
 // Visit every element of the row once: bulk lanes through `f(x, id)` in the calling thread's
-// blocks, exceptions spread over the workgroup.
+// blocks, exceptions spread over the workgroup. The groups of kDepth stripes wholly inside an
+// aligned row have their loads (and lane masks) issued together, ahead of the work on them.
 template <class Tin, class F>
-__device__ __forceinline__ void for_each(const Row<Tin>& row, F f) {
+__device__ __forceinline__ void for_each_ahead(const Row<Tin>& row, F f) {
+  constexpr int kDepth = 4;
+  const int whole = row.vec ? row.V / kBlk / kThreads : 0;  // (uniform) such stripes
+  int j = 0;
+  for (; j + kDepth <= whole; j += kDepth) {
+    WholeBlock<Tin> q[kDepth];
+    uint32_t masked[kDepth];
+#pragma clang loop unroll(full)
+    for (int k = 0; k < kDepth; ++k) {
+      const int b = (j + k) * kThreads + threadIdx.x;
+      q[k].load(row.p, b);
+      masked[k] = row.bm ? row.bm[b] : 0u;
+    }
+#pragma clang loop unroll(full)
+    for (int k = 0; k < kDepth; ++k) {
+      const int b = (j + k) * kThreads + threadIdx.x;
+      float v[kBlk];
+      q[k].values(v);
+#pragma unroll
+      for (int i = 0; i < kBlk; ++i)
+        if (!(masked[k] & (1u << i))) f(v[i], b * kBlk + i);
+    }
+  }
+  for (int b = j * kThreads + threadIdx.x; b < row.nblk; b += kThreads) {
+    float v[kBlk];
+    const uint32_t valid = row.load(b, v);
+#pragma unroll
+    for (int i = 0; i < kBlk; ++i)
+      if (valid & (1u << i)) f(v[i], b * kBlk + i);
+  }
+  for (int e = threadIdx.x; e < row.nexc; e += kThreads) f(row.eval[e], row.eid[e]);
+}
+
+// The same visit, one block at a time.
+template <class Tin, class F>
+__device__ __forceinline__ void for_each_plain(const Row<Tin>& row, F f) {
   for (int b = threadIdx.x; b < row.nblk; b += kThreads) {
     float v[kBlk];
     const uint32_t valid = row.load(b, v);
@@ -339,6 +406,17 @@ __device__ __forceinline__ void for_each(const Row<Tin>& row, F f) {
       if (valid & (1u << i)) f(v[i], b * kBlk + i);
   }
   for (int e = threadIdx.x; e < row.nexc; e += kThreads) f(row.eval[e], row.eid[e]);
+}
+
+// The sampling kernels' visit: loads ahead for fp32 rows; bf16 rows, which reach it only off the
+// fast path, one block at a time (the loads-ahead code there measured 0.5 us slower on the fast
+// path's own launches, through the kernel's code size).
+template <class Tin, class F>
+__device__ __forceinline__ void for_each(const Row<Tin>& row, F f) {
+  if constexpr (sizeof(Tin) == 4)
+    for_each_ahead(row, f);
+  else
+    for_each_plain(row, f);
 }
 
 // The penalised logit of token d (bulk or exception); all threads call, all get the value.

@@ -83,37 +83,6 @@ __device__ __forceinline__ float bf16_of_key(uint32_t key) {
 
 constexpr int kTab = 8192;  // tabulated keys per row (bf16)
 
-// Block b of a 16-byte-aligned row whose block is wholly inside it, as loaded (one
-// unconditional vector load, so that several in flight are waited for together: Row::load's
-// per-lane range test puts each load behind a branch), and its values.
-template <class Tin>
-struct WholeBlock;
-template <>
-struct WholeBlock<uint16_t> {
-  uint4 d;
-  __device__ __forceinline__ void load(const uint16_t* p, int b) { d = *reinterpret_cast<const uint4*>(p + b * kBlk); }
-  __device__ __forceinline__ void values(float v[kBlk]) const {
-    const uint32_t w[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(w[i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-    }
-  }
-};
-template <>
-struct WholeBlock<float> {
-  float4 d0, d1;
-  __device__ __forceinline__ void load(const float* p, int b) {
-    d0 = *reinterpret_cast<const float4*>(p + b * kBlk);
-    d1 = *reinterpret_cast<const float4*>(p + b * kBlk + 4);
-  }
-  __device__ __forceinline__ void values(float v[kBlk]) const {
-    v[0] = d0.x; v[1] = d0.y; v[2] = d0.z; v[3] = d0.w;
-    v[4] = d1.x; v[5] = d1.y; v[6] = d1.z; v[7] = d1.w;
-  }
-};
-
 // One row's side of the residual: the term (mass * other_S) >> shift of each token. Both forms
 // are free of branches (a point row has lo = +inf and its token in pid; other rows pid = -1),
 // so that the per-token code stays one straight run.
