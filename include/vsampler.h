@@ -13,8 +13,10 @@
  *    Nothing synchronises the host.
  *  - Return 0 on success, a VSAMP_E_* code otherwise; vsamp_last_error() then describes the
  *    failure (thread-local, valid until the next call on the same thread).
- *  - No global mutable state: calls on different streams may run concurrently as long as they
- *    use different workspaces.
+ *  - Calls on different streams may run concurrently as long as they use different
+ *    workspaces. The only global state is a per-device cache of the device check (gfx950 or
+ *    not, compute units), filled on first use and never changed after, and the thread-local
+ *    error message.
  */
 #ifndef VSAMPLER_H
 #define VSAMPLER_H

@@ -144,3 +144,21 @@ def test_reference_sample_keeps_the_engine_call():
     assert toks == [s.sample(logits, SamplingParams(top_k=2), 7, p) for p in range(30)]
     assert set(toks) <= {0, 1}
     assert HipSampler is SAMPLER._entries["hip"].factory
+
+
+def test_sample_with_penalties_needs_the_history():
+    # The engine's per-token call passes no history (generate.py:129): with a penalty on, that
+    # is an error in both backends, never a silent sample without the penalty.
+    s = ReferenceSampler(_ctx(CPU))
+    logits = torch.tensor([2.0, 1.0, 0.5, 0.0, -1.0, -3.0])
+    pen = SamplingParams(repetition_penalty=1.3)
+    with pytest.raises(ValueError, match="history"):
+        s.sample(logits, pen, 7, 0)
+    assert s.sample(logits, pen, 7, 0, history=[]) == s.sample(logits, SamplingParams(), 7, 0)
+    assert s.sample(logits, SamplingParams(), 7, 0) in range(6)  # no penalty: no history needed
+    # a strong penalty on the top token moves the greedy choice
+    greedy = SamplingParams(temperature=0, frequency_penalty=10.0)
+    assert s.sample(logits, greedy, 7, 0, history=[0]) == 1
+    hip = HipSampler.__new__(HipSampler)  # (no library needed: the check comes first)
+    with pytest.raises(ValueError, match="history"):
+        hip.sample(logits, pen, 7, 0)

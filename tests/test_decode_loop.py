@@ -5,8 +5,9 @@ requests through ``BatchDecoder`` compares each request with a one-sequence loop
 the engine's generate.py:118-144 (prefill, then per token: ``sample(logits, params, seed,
 position)``, stop checks, feed the token back) on the same model and sampler backend. The other
 tests port the engine's loop tests (tests/unit/runtime/test_generate.py) to the batched loop:
-stop ids and ``ignore_eos``, streamed text, stop strings, seeded reproducibility, the
-``max_seq_len`` rule, and the text stream's hold-back rules.
+stop ids and ``ignore_eos``, streamed text, stop strings, seeded reproducibility and the
+``max_seq_len`` rule. Text and stop strings come from a caller-supplied stream; here a plain
+test-local one (``WholeTextStream``) stands in for the engine's.
 """
 
 from __future__ import annotations
@@ -16,7 +17,7 @@ import pytest
 import torch
 
 from vinfer_amd.registry import BackendContext
-from vinfer_amd.runtime import BatchDecoder, Step, TextStream, check_request
+from vinfer_amd.runtime import BatchDecoder, Step, check_request
 from vinfer_amd.sampler import SAMPLER
 from vinfer_amd.sampling import SamplingParams, pack_params, uniform
 from vinfer_amd.workloads import SyntheticLM
@@ -29,25 +30,37 @@ def decode(ids: list[int]) -> str:
     return "".join(LETTERS[i % 26] for i in ids)
 
 
-def uniform_draw(sampler, logits, params, seed, position, history):
-    """One token by the uniform-driven draw: a one-row ``sample_batch`` with the uniform of
-    ``(seed, position)``. This is what the hip backend's ``sample`` does; the reference backend's
-    ``sample`` keeps the engine's exponential race instead (sampler.py:73-77)."""
-    dev = logits.device
-    u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)
-    hist = off = None
-    if params.penalized and history:
-        hist = torch.tensor(history, dtype=torch.int32, device=dev)
-        off = torch.tensor([0, len(history)], dtype=torch.int32, device=dev)
-    ids, _ = sampler.sample_batch(logits.reshape(1, -1), pack_params([params], dev), u, hist, off)
-    return int(ids[0])
+class WholeTextStream:
+    """A test-local text stream: decodes every token so far on each push, reports the first stop
+    string (the text ends before it), and holds back the longest stop string's length minus one
+    characters until the request ends."""
+
+    def __init__(self, decode_fn, stops):
+        self.decode_fn, self.stops, self.ids, self.sent = decode_fn, tuple(stops), [], 0
+        self.hold = max((len(x) for x in self.stops), default=1) - 1
+
+    def push(self, token):
+        self.ids.append(token)
+        text = self.decode_fn(self.ids)
+        hits = [i for i in (text.find(x) for x in self.stops) if i >= 0]
+        end = min(hits) if hits else max(self.sent, len(text) - self.hold)
+        piece, self.sent = text[self.sent : end], max(self.sent, end)
+        return piece, bool(hits)
+
+    def flush(self):
+        text = self.decode_fn(self.ids)
+        piece, self.sent = text[self.sent :], len(text)
+        return piece
+
+
+def streams(decode_fn):
+    return lambda stops: WholeTextStream(decode_fn, stops)
 
 
 def one_at_a_time(model, sampler, prompt, params, eos=frozenset(), text=None, penalize_prompt=False):
-    """The engine's one-sequence loop (generate.py:118-144) over a ``DecodeModel``. On the GPU
-    it calls the hip backend's ``sample`` (the engine's per-token call); on the CPU, where the
-    reference backend's ``sample`` is the exponential race, ``uniform_draw``."""
-    stream = TextStream(text, params.stop) if text else None
+    """The engine's one-sequence loop (generate.py:118-144) over a ``DecodeModel``, calling the
+    backend's per-token ``sample`` (the engine's call, generate.py:129)."""
+    stream = WholeTextStream(text, params.stop) if text else None
     stop_ids = set(params.stop_token_ids) | (set() if params.ignore_eos else set(eos))
     dev = model.device
     logits = model.prefill(0, torch.tensor(prompt, device=dev))
@@ -56,10 +69,7 @@ def one_at_a_time(model, sampler, prompt, params, eos=frozenset(), text=None, pe
     steps = []
     for n in range(1, params.max_tokens + 1):
         history = (list(prompt) if penalize_prompt else []) + generated
-        if logits.is_cuda:
-            token = sampler.sample(logits, params, params.seed, position, history=history)
-        else:
-            token = uniform_draw(sampler, logits, params, params.seed, position, history)
+        token = sampler.sample(logits, params, params.seed, position, history=history)
         generated.append(token)
         if token in stop_ids:
             steps.append(Step(token, stream.flush() if stream else "", "stop"))
@@ -202,7 +212,7 @@ def test_eos_stops_unless_ignored(cpu_model, ref_sampler):
 
 def test_streamed_text_is_the_decoded_output(cpu_model, ref_sampler):
     reqs = [(PROMPT, SamplingParams(max_tokens=12, temperature=0)), ([3, 4], SamplingParams(max_tokens=9, seed=5))]
-    for (prompt, sp), steps in zip(reqs, run_batched(cpu_model, ref_sampler, reqs, num_slots=2, decode=decode)):
+    for (prompt, sp), steps in zip(reqs, run_batched(cpu_model, ref_sampler, reqs, num_slots=2, text_stream=streams(decode))):
         assert "".join(s.text for s in steps) == decode([s.token_id for s in steps])
         assert steps == one_at_a_time(cpu_model, ref_sampler, prompt, sp, text=decode)
 
@@ -213,7 +223,7 @@ def test_stop_string_ends_the_text_before_it(cpu_model, ref_sampler):
     full = decode([s.token_id for s in steps])
     stop = full[5:7]
     sp = SamplingParams(max_tokens=12, temperature=0, stop=(stop,))
-    (cut,) = run_batched(cpu_model, ref_sampler, [(PROMPT, sp)], num_slots=1, decode=decode)
+    (cut,) = run_batched(cpu_model, ref_sampler, [(PROMPT, sp)], num_slots=1, text_stream=streams(decode))
     assert "".join(s.text for s in cut) == full[: full.index(stop)]
     assert cut[-1].finish_reason == "stop"
 
@@ -244,36 +254,6 @@ def test_history_rows_stay_inside_their_slot(cpu_model, ref_sampler):
     got = run_batched(cpu_model, ref_sampler, reqs, num_slots=3, max_seq_len=5, penalize_prompt=True)
     for (prompt, p), steps in zip(reqs, got):
         assert steps == one_at_a_time(cpu_model, ref_sampler, prompt, p, penalize_prompt=True)
-
-
-# ---- text stream (tests/unit/runtime/test_generate.py:104-129 behaviour) ---------------------
-
-
-def test_text_held_back_while_it_could_be_a_stop_string():
-    stream = TextStream(decode, ("cde",))
-    assert stream.push(0) == ("", False)
-    assert stream.push(1) == ("", False)
-    assert stream.push(2) == ("a", False)
-    assert stream.push(3) == ("b", False)
-    assert stream.push(4) == ("", True)
-
-
-def test_unfinished_utf8_is_held_back():
-    pieces = {0: "a", 1: "�", 2: "é"}
-
-    def partial(ids):
-        return "".join(pieces[i] for i in ids).replace("�é", "é")
-
-    stream = TextStream(partial, ())
-    assert stream.push(0) == ("a", False)
-    assert stream.push(1) == ("", False)
-    assert stream.push(2) == ("é", False)
-
-
-def test_flush_returns_what_was_held():
-    stream = TextStream(decode, ("zzz",))
-    assert [stream.push(t) for t in (0, 1, 2)] == [("", False), ("", False), ("a", False)]
-    assert stream.flush() == "bc"
 
 
 # ---- on the GPU: the hip backend, bf16 logits at V = 151936 ---------------------------------

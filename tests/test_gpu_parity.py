@@ -189,9 +189,87 @@ def test_workload_rows_match_the_oracle(name, B):
     check(workloads.make(name, batch=B), max_tie_frac=0.1)
 
 
+def fp32_rule_ties(w: Workload, rows) -> int:
+    """Rows of ``w`` on which the engine's own fp32 rule is ambiguous (oracle/fp32_rule.py)."""
+    from oracle.fp32_rule import fp32_rule
+
+    p, n = w.params, 0
+    for b in rows:
+        x = w.logits[b].float().numpy()
+        if w.hist_ids is not None:
+            h = w.hist_ids[int(w.hist_offsets[b]) : int(w.hist_offsets[b + 1])].numpy()
+            x, _ = penalize(x, h, float(p.repetition_penalty[b]), float(p.presence_penalty[b]),
+                            float(p.frequency_penalty[b]))
+        n += bool(fp32_rule(x, float(p.temperature[b]), int(p.top_k[b]), float(p.top_p[b]),
+                            float(p.min_p[b]), float(w.uniforms[b])).ties)
+    return n
+
+
 def test_headline_shape_full_batch():
-    ties = check(workloads.make("peaked_flat"), max_tie_frac=0.1)
-    print("ties", ties)
+    w = workloads.make("peaked_flat")
+    ties = check(w, max_tie_frac=0.1)
+    print(f"headline B=256: oracle ties {ties}, fp32-rule ties {fp32_rule_ties(w, range(w.batch))}", flush=True)
+
+
+def check_subset(w: Workload, n: int, seed: int):
+    """One launch over the whole batch; a seeded subset of ``n`` rows against the oracle."""
+    print(f"case {w.name} full B={w.batch} V={w.vocab}, {n} rows checked", flush=True)
+    ids, dp = run(w)
+    rows = np.sort(np.random.default_rng(seed).choice(w.batch, n, replace=False))
+    sub = Workload(w.name, w.logits[rows], w.params.select(torch.from_numpy(rows)), w.uniforms[rows],
+                   *_sub_hist(w, rows), None if w.draft_ids is None else w.draft_ids[rows])
+    res = oracle(sub)
+    ties, bad = compare_ids(ids[rows], res, None if dp is None else dp[rows])
+    assert not bad, bad[:10]
+    assert ties <= max(1, 0.1 * n), ties
+    return rows, ties
+
+
+def _sub_hist(w: Workload, rows):
+    if w.hist_ids is None:
+        return None, None
+    hs = [w.hist_ids[int(w.hist_offsets[b]) : int(w.hist_offsets[b + 1])].tolist() for b in rows]
+    return pack_history(hs)
+
+
+def test_large_fp32_full_launch():
+    # 1024 x 151936 fp32 rows, histories up to 32768 ids, one launch: a 1024-workgroup grid and
+    # the full-size history workspace; 64 rows checked, and the exact counts of the 8 longest
+    # histories
+    w = workloads.make("large_fp32")
+    check_subset(w, 64, seed=11)
+    lens = (w.hist_offsets[1:] - w.hist_offsets[:-1]).numpy()
+    longest = np.argsort(-lens, kind="stable")[:8]
+    d = w.to(DEV)
+    _, counts = hip(torch.float32).penalized_logits(d.logits, d.params, d.hist_ids, d.hist_offsets)
+    got = counts[torch.from_numpy(longest).to(DEV)].cpu().numpy()
+    for i, b in enumerate(longest):
+        h = w.hist_ids[int(w.hist_offsets[b]) : int(w.hist_offsets[b + 1])].numpy()
+        assert lens[b] > 30000
+        assert (got[i] == np.bincount(h, minlength=w.vocab)).all(), int(b)
+
+
+def test_verify_bf16_full_launch():
+    # 192 x 262144 bf16 rows with draft probabilities, one launch; 64 rows checked
+    check_subset(workloads.make("verify_bf16"), 64, seed=12)
+
+
+def test_gpu_torch_division_by_a_scalar():
+    # The engine runs sample() on the model's device: what torch's GPU kernel computes for
+    # logits.float() / T (sampler.py:52), over every bf16 value, against IEEE division and a
+    # reciprocal multiply. The kernels divide, as torch's CPU kernel does.
+    x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    xn = x.float().numpy()
+    same = lambda a, b: (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))  # noqa: E731
+    for T in (0.3, 0.5, 0.7, 0.8, 1.0, 1.2, 1.5):
+        got = (x.to(DEV).float() / T).cpu().numpy()
+        with np.errstate(all="ignore"):
+            div = xn / np.float32(T)
+            rec = (xn * (np.float32(1.0) / np.float32(T))).astype(np.float32)
+        n_div, n_rec = int((~same(got, div)).sum()), int((~same(got, rec)).sum())
+        print(f"T={T}: torch GPU differs from division on {n_div}, from the reciprocal multiply on {n_rec}",
+              flush=True)
+        assert n_div == 0 or n_rec == 0
 
 
 def test_single_row_many_steps():

@@ -16,9 +16,6 @@ PKG = Path(__file__).resolve().parents[1]
 ROOT = PKG.parent
 LIB = PKG / "libvsampler.so"
 SOURCES = [PKG / "csrc" / "capi.hip"]
-DEPS = [PKG / "csrc" / n for n in ("common.cuh", "penalty.cuh", "sample.cuh")] + [
-    ROOT / "include" / "vsampler.h"
-]
 
 # -ffp-contract=off: the penalty arithmetic rounds every operation on its own.
 # -fhip-fp32-correctly-rounded-divide-sqrt: x / T is IEEE division, as on the CPU.

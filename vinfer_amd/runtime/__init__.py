@@ -1,6 +1,5 @@
-"""Callers of the sampler: the continuous-batching decode loop and its text stream."""
+"""Callers of the sampler: the continuous-batching decode loop."""
 
-from vinfer_amd.runtime.batch import BatchDecoder, DecodeModel, SpeculativeDecoder, Step, check_request
-from vinfer_amd.runtime.text import TextStream
+from vinfer_amd.runtime.batch import BatchDecoder, DecodeModel, SpeculativeDecoder, Step, TextStream, check_request
 
 __all__ = ["BatchDecoder", "DecodeModel", "SpeculativeDecoder", "Step", "TextStream", "check_request"]

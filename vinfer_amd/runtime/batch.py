@@ -12,8 +12,12 @@ the engine's per-request behaviour and batches the rest:
   never changes a request's tokens;
 - a request ends, as in generate.py:130-142, on a stop id (the request's ``stop_token_ids``,
   plus the end-of-sequence ids unless ``ignore_eos``; the stop token's own text is not output),
-  on a stop string (text ends before it), or after ``max_tokens`` tokens ("length"); each token
-  yields one ``Step``.
+  on a stop string, or after ``max_tokens`` tokens ("length"); each token yields one ``Step``.
+
+Detokenization and stop strings are the caller's: ``text_stream(stop_strings)`` makes one
+``TextStream`` per request (the engine passes its own, generate.py:27-88), whose ``push`` and
+``flush`` give each step's text and report a stop string; without it steps carry no text and
+stop strings are not checked.
 
 Requests join whenever a slot is free (prefill, then their first token is sampled in the same
 iteration as everyone else's next token) and leave as soon as they finish, freeing their slot.
@@ -37,9 +41,18 @@ import numpy as np
 import torch
 
 from vinfer_amd._lib import position_uniforms
-from vinfer_amd.runtime.text import TextStream
 from vinfer_amd.sampler.base import SamplerBackend
 from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params
+
+
+class TextStream(Protocol):
+    """One request's streamed text, supplied by the caller (the engine's ``_TextStream``,
+    generate.py:27-88): ``push(token)`` returns ``(text that is safe to show, stop string
+    hit)``; ``flush()`` returns what was held back, once the request ends."""
+
+    def push(self, token: int) -> tuple[str, bool]: ...
+
+    def flush(self) -> str: ...
 
 
 @dataclass
@@ -145,7 +158,7 @@ class BatchDecoder:
         num_slots: int,
         max_seq_len: int,
         eos_token_ids: Iterable[int] = (),
-        decode: Callable[[list[int]], str] | None = None,
+        text_stream: Callable[[tuple[str, ...]], TextStream] | None = None,
         seed: int = 0,
         penalize_prompt: bool = False,
     ) -> None:
@@ -156,7 +169,7 @@ class BatchDecoder:
         self.num_slots = num_slots
         self.max_seq_len = max_seq_len
         self.eos_token_ids = frozenset(eos_token_ids)
-        self.decode_text = decode
+        self.text_stream = text_stream
         self.penalize_prompt = penalize_prompt
         self._rng = random.Random(seed)
         self._free = list(range(num_slots - 1, -1, -1))  # pop() hands out the lowest slot
@@ -180,7 +193,7 @@ class BatchDecoder:
         if params.seed is None:
             params = dataclasses.replace(params, seed=self._rng.getrandbits(63))
         stop_ids = frozenset(params.stop_token_ids) | (frozenset() if params.ignore_eos else self.eos_token_ids)
-        stream = TextStream(self.decode_text, params.stop) if self.decode_text else None
+        stream = self.text_stream(params.stop) if self.text_stream else None
         rid = self._next_rid
         self._next_rid += 1
         self._waiting.append(_Seq(rid, list(prompt_ids), params, stop_ids, stream))

@@ -28,7 +28,9 @@ class SamplerBackend(Protocol):
         history: Sequence[int] | torch.Tensor | None = None,
     ) -> int:
         """One token id from ``logits`` (``[V]``) for the token at ``position``. ``history`` is
-        the request's token ids so far; it matters only when a penalty is on."""
+        the request's token ids so far (empty for the first token): it is required when a
+        penalty is on (``ValueError`` if it is ``None``), since the penalties are computed from
+        it, and ignored otherwise."""
         ...
 
     def sample_batch(
@@ -105,6 +107,17 @@ class SamplerBackend(Protocol):
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """Penalised fp32 logits ``[B, V]`` and the history count of every id (int32 ``[B, V]``)."""
         ...
+
+
+def require_history(params: SamplingParams, history) -> None:
+    """``ValueError`` when ``params`` turns a penalty on and no history was passed: the engine's
+    per-token call (src/vinfer/runtime/generate.py:129) passes none, and silently sampling
+    without the penalties would be a fallback (kernels/registry.py:5-7 rules those out)."""
+    if params.penalized and history is None:
+        raise ValueError(
+            "repetition/presence/frequency penalties need the request's token history: "
+            "pass history= (the token ids so far, empty for the first token)"
+        )
 
 
 SAMPLER: BackendRegistry[SamplerBackend] = BackendRegistry("sampler")

@@ -19,7 +19,7 @@ import torch
 
 from vinfer_amd import _lib
 from vinfer_amd.registry import BackendContext
-from vinfer_amd.sampler.base import SAMPLER
+from vinfer_amd.sampler.base import SAMPLER, require_history
 from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params, uniform
 
 _DTYPES = {torch.bfloat16: _lib.VSAMP_BF16, torch.float32: _lib.VSAMP_F32}
@@ -282,11 +282,12 @@ class HipSampler:
         position: int,
         history: Sequence[int] | torch.Tensor | None = None,
     ) -> int:
+        require_history(params, history)
         dev = logits.device
         packed = pack_params([params], dev)
         u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)
         hist_ids = hist_offsets = None
-        if history is not None and params.penalized and len(history) > 0:
+        if params.penalized and len(history) > 0:
             hist_ids = torch.as_tensor(history, dtype=torch.int32).to(dev)
             hist_offsets = torch.tensor([0, hist_ids.shape[0]], dtype=torch.int32, device=dev)
         ids, _ = self.sample_batch(logits.reshape(1, -1), packed, u, hist_ids, hist_offsets)

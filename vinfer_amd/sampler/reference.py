@@ -1,15 +1,13 @@
 """The ``reference`` sampler backend: slow, readable torch code on any device.
 
-``sample`` is the engine's own sampler (src/vinfer/runtime/sampler.py:50-77): temperature,
-top-k, top-p and the exponential race ``argmax(p / E)`` with ``E`` drawn from a
-``torch.Generator`` seeded by ``position_seed(seed, position)``. It is what the engine runs
-with ``sampler_backend=reference``, the default. When a penalty or min-p is on it uses the
-batched path below instead, since the engine's sampler has neither.
-
-``sample_batch`` and ``probs`` restate the batched semantics the ``hip`` backend implements,
-row by row in torch: penalties, fp32 division by the temperature, top-k, fp64 softmax, min-p,
-top-p with ties broken by ascending id, and the inverse-CDF draw from the caller's uniform over
-the kept tokens in that same order (descending probability, ties by ascending id).
+It restates, row by row in torch, the batched semantics the ``hip`` backend implements:
+penalties, fp32 division by the temperature, top-k, fp64 softmax, min-p, top-p with ties broken
+by ascending id, and the inverse-CDF draw from the caller's uniform over the kept tokens in that
+same order (descending probability, ties by ascending id). ``sample`` is the engine's per-token
+call (src/vinfer/runtime/sampler.py:68) through that same draw, with the uniform of
+``(seed, position)``; it does not reproduce the engine's exponential race (sampler.py:73-77),
+whose tokens depend on the torch version and device. In the engine, the ``reference`` name
+stays bound to the engine's own ``sample``.
 """
 
 from __future__ import annotations
@@ -19,24 +17,8 @@ from collections.abc import Sequence
 import torch
 
 from vinfer_amd.registry import BackendContext
-from vinfer_amd.sampler.base import SAMPLER
-from vinfer_amd.sampling import SamplingParams, pack_params, position_seed, uniform
-
-
-def filtered_probs(logits: torch.Tensor, params: SamplingParams) -> torch.Tensor:
-    """Probabilities after temperature, top-k and top-p, fp32 (sampler.py:50-65)."""
-    logits = logits.float() / params.temperature
-    if params.top_k and params.top_k < logits.shape[-1]:
-        kth = torch.topk(logits, params.top_k, dim=-1).values[..., -1:]
-        logits = logits.masked_fill(logits < kth, float("-inf"))
-    probs = torch.softmax(logits, dim=-1)
-    if params.top_p < 1:
-        sorted_probs, order = torch.sort(probs, dim=-1, descending=True)
-        before = sorted_probs.cumsum(-1) - sorted_probs
-        sorted_probs = sorted_probs.masked_fill(before >= params.top_p, 0.0)
-        probs = torch.zeros_like(probs).scatter(-1, order, sorted_probs)
-        probs = probs / probs.sum(-1, keepdim=True)
-    return probs
+from vinfer_amd.sampler.base import SAMPLER, require_history
+from vinfer_amd.sampling import SamplingParams, pack_params, uniform
 
 
 def _penalize(x: torch.Tensor, hist: torch.Tensor, rep, pres, freq):
@@ -244,23 +226,15 @@ class ReferenceSampler:
         position: int,
         history: Sequence[int] | torch.Tensor | None = None,
     ) -> int:
-        if params.penalized or params.min_p > 0:
-            dev = logits.device
-            hist = None
-            if history is not None and len(history) > 0:
-                hist = torch.as_tensor(history, dtype=torch.int32, device=dev)
-            off = None if hist is None else torch.tensor([0, hist.numel()], dtype=torch.int32, device=dev)
-            u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)
-            ids, _ = self.sample_batch(logits.reshape(1, -1), pack_params([params], dev), u, hist, off)
-            return int(ids[0])
-        # sampler.py:68-77
-        if params.greedy:
-            return int(torch.argmax(logits))
-        probs = filtered_probs(logits, params)
-        gen = torch.Generator(device=probs.device).manual_seed(position_seed(seed, position))
-        noise = torch.empty_like(probs).exponential_(generator=gen)
-        noise.clamp_min_(torch.finfo(noise.dtype).tiny)
-        return int(torch.argmax(probs / noise))
+        require_history(params, history)
+        dev = logits.device
+        hist = off = None
+        if params.penalized and len(history) > 0:
+            hist = torch.as_tensor(history, dtype=torch.int32).to(dev)
+            off = torch.tensor([0, hist.numel()], dtype=torch.int32, device=dev)
+        u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)
+        ids, _ = self.sample_batch(logits.reshape(1, -1), pack_params([params], dev), u, hist, off)
+        return int(ids[0])
 
 
-__all__ = ["ReferenceSampler", "filtered_probs"]
+__all__ = ["ReferenceSampler"]

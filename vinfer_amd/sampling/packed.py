@@ -60,6 +60,10 @@ class PackedParams:
         """Each row ``n`` times in a row (``B * n`` rows: row ``b * n + j`` is row ``b``)."""
         return PackedParams(**{k: getattr(self, k).repeat_interleave(n) for k in self.__dataclass_fields__})
 
+    def select(self, rows: torch.Tensor) -> PackedParams:
+        """The rows ``rows`` (an index tensor), in that order."""
+        return PackedParams(**{k: getattr(self, k)[rows] for k in self.__dataclass_fields__})
+
     def row(self, i: int) -> dict[str, float | int]:
         """Row ``i`` as plain Python numbers (fp32 values widened exactly to float)."""
         out: dict[str, float | int] = {k: float(getattr(self, k)[i]) for k in F32_FIELDS}
