@@ -117,6 +117,16 @@ size_t vsamp_workspace_bytes(int32_t batch, int32_t vocab, int64_t hist_total);
  * (sampler.py:68-77) for B rows at once. */
 int vsamp_sample(const vsamp_args* args, void* stream);
 
+/* vsamp_sample without a caller workspace and without any allocation: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the engine. The library's own workspace, a static 16 MiB
+ * per GPU (held until the process ends), takes the place of `workspace`, which must be NULL with
+ * workspace_bytes 0. Sizes whose vsamp_workspace_bytes() exceeds 16 MiB (histories beyond ~1.39 M
+ * ids in all) fail with VSAMP_E_WORKSPACE. All calls on one GPU share that workspace: calls that
+ * overlap on one GPU (different streams or threads) race. Results are identical to
+ * vsamp_sample's. */
+int vsamp_sample_noalloc(const vsamp_args* args, void* stream);
+
 /* The final per-token probabilities [B, V] fp32 that vsamp_sample draws from (0 for dropped
  * tokens); row r at out + r * out_stride. Replaces `filtered_probs` (sampler.py:50-65), with the
  * extensions applied. `uniforms` and the outputs in `args` are not used. */

@@ -26,6 +26,7 @@ EXPORTS = (
     "vsamp_query",
     "vsamp_workspace_bytes",
     "vsamp_sample",
+    "vsamp_sample_noalloc",
     "vsamp_probs",
     "vsamp_penalized_logits",
     "vsamp_uniforms",
@@ -117,6 +118,8 @@ def load() -> ctypes.CDLL:
         lib.vsamp_workspace_bytes.restype = ctypes.c_size_t
         lib.vsamp_sample.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p]
         lib.vsamp_sample.restype = ctypes.c_int
+        lib.vsamp_sample_noalloc.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p]
+        lib.vsamp_sample_noalloc.restype = ctypes.c_int
         lib.vsamp_probs.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
         lib.vsamp_probs.restype = ctypes.c_int
         lib.vsamp_penalized_logits.argtypes = [

@@ -110,6 +110,33 @@ Layout layout(int64_t B, int64_t V, int64_t H) {
 
 constexpr int64_t kMaxVocab = static_cast<int64_t>(vs::kMaxStripes) * vs::kThreads * vs::kBlk;
 
+// ---- the library's own workspace, for callers that cannot allocate (vsamp_sample_noalloc) ----
+// 16 MiB per GPU, held from the library's first use on that GPU until the process ends: the
+// workspace of histories up to ~1.39 M ids in all (4 B per row + 12 B per history id). Every
+// call on one GPU shares it, so calls that overlap on one GPU (different streams, or threads)
+// race. The kernels write every word of it they read within the launch, so nothing has to be
+// cleared between calls.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::atomic<void*> g_scratch[kMaxDevices];  // the array's address on each device
+
+// `scratch`'s device address on the current device (the name itself is a host-side stand-in:
+// never passed to a kernel), looked up once per device.
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(VSAMP_E_DEVICE, "device %d out of range", dev);
+  void* p = g_scratch[dev].load();
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch[dev].store(p);
+  }
+  *out = p;
+  return VSAMP_OK;
+}
+
 int validate(const vsamp_args* a, bool need_draw) {
   if (!a) return fail(VSAMP_E_ARG, "args is NULL");
   if (a->flags & ~VSAMP_HIST_RANGES)
@@ -280,6 +307,28 @@ int vsamp_sample(const vsamp_args* a, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   return a->dtype == VSAMP_BF16 ? run_sample<uint16_t>(a, nullptr, 0, st)
                                 : run_sample<float>(a, nullptr, 0, st);
+}
+
+int vsamp_sample_noalloc(const vsamp_args* a, void* stream) {
+  g_err.clear();
+  if (int rc = validate(a, true)) return rc;
+  if (a->workspace || a->workspace_bytes)
+    return fail(VSAMP_E_ARG, "vsamp_sample_noalloc uses the library's own workspace: leave workspace NULL");
+  if (a->batch == 0) return VSAMP_OK;
+  if (int rc = check_current_device()) return rc;
+  const size_t need = layout(a->batch, a->vocab, a->hist_total).total;
+  if (wants_penalties(a) && need > kScratchBytes)
+    return fail(VSAMP_E_WORKSPACE,
+                "vsamp_sample_noalloc: batch %d with %lld history ids needs %zu workspace bytes, more than its "
+                "%zu; use vsamp_sample with a caller workspace",
+                a->batch, static_cast<long long>(a->hist_total), need, kScratchBytes);
+  vsamp_args c = *a;
+  if (wants_penalties(a)) {
+    if (int rc = scratch_of_current_device(&c.workspace)) return rc;
+    c.workspace_bytes = kScratchBytes;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return c.dtype == VSAMP_BF16 ? run_sample<uint16_t>(&c, nullptr, 0, st) : run_sample<float>(&c, nullptr, 0, st);
 }
 
 int vsamp_probs(const vsamp_args* a, float* out, int64_t out_stride, void* stream) {
