@@ -420,6 +420,46 @@ def test_a_perfect_draft_is_always_accepted(cpu_model, ref_sampler):
         dec.submit(PROMPT, SamplingParams(repetition_penalty=1.2))
 
 
+class RecordingDraft:
+    """A draft model that checks, on every decode, that each earlier position of the slot holds
+    the sequence's own token: the position's token was fed since the slot's prefill, and later
+    feeds replaced the rejected drafts."""
+
+    def __init__(self, model, sequences):
+        self.model, self.device, self.seqs = model, model.device, sequences
+        self.fed: dict[int, dict[int, int]] = {}
+        self.slot_rid: dict[int, int] = {}
+        self.calls = 0
+
+    def prefill(self, slot, prompt_ids):
+        self.fed[slot] = dict(enumerate(prompt_ids.tolist()))
+        return self.model.prefill(slot, prompt_ids)
+
+    def decode(self, slots, tokens, positions):
+        for sl, t, p in zip(slots.tolist(), tokens.tolist(), positions.tolist()):
+            fed = self.fed[sl]
+            missing = [q for q in range(p) if q not in fed]
+            assert not missing, f"slot {sl}: position {p} decoded, positions {missing} never fed"
+            fed[p] = t
+            for q in [q for q in fed if q > p]:  # positions past p are stale now
+                del fed[q]
+        self.calls += 1
+        return self.model.decode(slots, tokens, positions)
+
+
+def test_the_draft_model_is_fed_every_position(cpu_model, ref_sampler):
+    # A perfect draft keeps every block (K drafts + the bonus): its last draft must still reach
+    # the draft model, at its position, before the next block's drafts.
+    reqs = [(PROMPT, SamplingParams(max_tokens=14, temperature=1.0, seed=4)),
+            ([3, 9], SamplingParams(max_tokens=11, temperature=0.7, top_p=0.9, seed=5))]
+    draft = RecordingDraft(cpu_model, reqs)
+    got = run_speculative(cpu_model, draft, ref_sampler, reqs, num_slots=2, K=3)
+    assert [len(g) for g in got] == [14, 11] and draft.calls > 0
+    # a draft that disagrees (rejections leave positions to overwrite)
+    other = RecordingDraft(SyntheticLM(96, dim=16, scale=3.0, dtype=torch.float32, seed=2), reqs)
+    run_speculative(cpu_model, other, ref_sampler, reqs, num_slots=2, K=2)
+
+
 def test_speculative_sampling_is_seeded(cpu_model, ref_sampler):
     draft = SyntheticLM(96, dim=16, scale=3.0, dtype=torch.float32, seed=1)
     reqs = [(PROMPT, SamplingParams(max_tokens=15, temperature=0.9, seed=s)) for s in (1, 2, 3)]

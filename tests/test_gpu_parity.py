@@ -255,9 +255,10 @@ def test_verify_bf16_full_launch():
 
 
 def test_gpu_torch_division_by_a_scalar():
-    # The engine runs sample() on the model's device: what torch's GPU kernel computes for
-    # logits.float() / T (sampler.py:52), over every bf16 value, against IEEE division and a
-    # reciprocal multiply. The kernels divide, as torch's CPU kernel does.
+    # The engine runs sample() on the model's device: torch's GPU kernel computes
+    # logits.float() / T (sampler.py:52) as x * fl32(1 / T), a reciprocal multiply, over every
+    # bf16 value; its CPU kernel divides. The kernels divide (the CPU rule); the values where
+    # the two differ are counted in tests/test_fp32_rule.py (RECIPROCAL_DIFFERS).
     x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
     xn = x.float().numpy()
     same = lambda a, b: (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))  # noqa: E731
@@ -269,7 +270,7 @@ def test_gpu_torch_division_by_a_scalar():
         n_div, n_rec = int((~same(got, div)).sum()), int((~same(got, rec)).sum())
         print(f"T={T}: torch GPU differs from division on {n_div}, from the reciprocal multiply on {n_rec}",
               flush=True)
-        assert n_div == 0 or n_rec == 0
+        assert n_rec == 0
 
 
 def test_single_row_many_steps():

@@ -262,3 +262,41 @@ def test_gpu_verify_with_a_point_row_on_one_side(dtype):
         assert int(counts[b]) == len(w.tokens), (b, counts[b], w.tokens)
         assert tokens[b, : len(w.tokens)].tolist() == w.tokens, (b, tokens[b].tolist(), w.tokens)
     assert rejected >= B // 2  # both kinds reach the residual draw
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_gpu_verify_residual_over_signed_zeros(dtype):
+    # The target keeps only its max, 0, held by 32 tokens of +0.0 and 32 of -0.0 (min-p 1): one
+    # value. Each draft proposes a token the target drops, so the residual is drawn over the 64
+    # zeros, uniformly: -0.0 tokens must carry the same weight as +0.0 ones.
+    dev = torch.device("cuda", 0)
+    B, K, V = 48, 1, 4096
+    rng = np.random.default_rng(31)
+    xt = -rng.uniform(1.0, 5.0, (B, K + 1, V)).astype(np.float32)
+    xq = rng.normal(0, 1, (B, K, V)).astype(np.float32)
+    drafts = np.zeros((B, K), np.int32)
+    neg = []
+    for b in range(B):
+        z = rng.choice(V, 65, replace=False)
+        xt[b, :, z[:32]] = 0.0
+        xt[b, :, z[32:64]] = -0.0
+        neg.append(set(z[32:64].tolist()))
+        drafts[b, 0] = z[64]  # a token the target drops
+        xq[b, 0, z[64]] = 30.0  # the draft keeps only it
+    xt = torch.from_numpy(xt).to(dtype).float().numpy()
+    xq = torch.from_numpy(xq).to(dtype).float().numpy()
+    params = pack_params([SamplingParams(temperature=1.0, min_p=1.0) for _ in range(B)])
+    ua, ur, ub = rng.random((B, K), np.float32), rng.random((B, K), np.float32), rng.random(B, dtype=np.float32)
+    print(f"verify signed zeros B={B} V={V} {dtype}", flush=True)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, dtype))
+    to = lambda a, t=None: torch.from_numpy(np.ascontiguousarray(a)).to(dev) if t is None else torch.from_numpy(a).to(t).to(dev)  # noqa: E731
+    tokens, counts = hip.verify(to(xt, dtype), to(xq, dtype), to(drafts), params.to(dev), to(ua), to(ur), to(ub))
+    tokens, counts = tokens.cpu(), counts.cpu()
+    want = oracle_verify(xt, xq, drafts, params, ua, ur, ub)
+    on_neg = 0
+    for b, w in enumerate(want):
+        assert not w.ties
+        assert int(counts[b]) == 1 and tokens[b, 0].item() == w.tokens[0], (b, tokens[b].tolist(), w.tokens)
+        on_neg += w.tokens[0] in neg[b]
+    assert 10 <= on_neg <= 38  # about half the draws land on a -0.0 token

@@ -76,6 +76,9 @@ __device__ __forceinline__ u64 u24(float u) {
 
 // Order-preserving 16-bit key of a bf16 value (its bits), and the value of a key.
 __device__ __forceinline__ uint32_t bf16_key(uint32_t bits) { return (bits & 0x8000u) ? (~bits & 0xFFFFu) : (bits | 0x8000u); }
+// The key of a token's bf16 value for the residual's table: -0.0 takes +0.0's key (they are one
+// value, and the kept set's bound `lo` is +0.0 when it is zero).
+__device__ __forceinline__ uint32_t bf16_key_z(uint32_t bits) { return bf16_key(bits == 0x8000u ? 0u : bits); }
 __device__ __forceinline__ float bf16_of_key(uint32_t key) {
   const uint32_t bits = (key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu);
   return __uint_as_float(bits << 16);
@@ -277,8 +280,8 @@ __device__ __forceinline__ void residual_item(const VerifyArgs& a, int b, int sl
         const int id = blk * kBlk + i;
         u64 pt, qd;
         if constexpr (decltype(tab_mode)::value) {
-          pt = side[0].term(vt[i], bf16_key(__float_as_uint(vt[i]) >> 16), id);
-          qd = side[1].term(vd[i], bf16_key(__float_as_uint(vd[i]) >> 16), id);
+          pt = side[0].term(vt[i], bf16_key_z(__float_as_uint(vt[i]) >> 16), id);
+          qd = side[1].term(vd[i], bf16_key_z(__float_as_uint(vd[i]) >> 16), id);
         } else {
           pt = side[0].direct(vt[i], id);
           qd = side[1].direct(vd[i], id);

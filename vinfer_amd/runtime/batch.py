@@ -147,6 +147,8 @@ class _Seq:
     position: int = 0  # position of the next token to sample (= tokens in the sequence so far)
     hist_len: int = 0  # ids in the slot's history row
     generated: list[int] = field(default_factory=list)
+    # (speculative loop) a token the draft model has not been fed yet: (token, position)
+    draft_gap: tuple[int, int] | None = None
 
 
 class BatchDecoder:
@@ -396,7 +398,11 @@ class SpeculativeDecoder(BatchDecoder):
     The target may define ``extend(slots, tokens [B, T], positions [B]) -> logits [B, T, V]``
     (T tokens per slot from ``positions[b]``); without it the loop calls ``decode`` on the
     flattened tokens, which is right for a model without per-slot state only. The draft model
-    is a ``DecodeModel``; a rejected draft leaves positions that the next iteration overwrites.
+    is a ``DecodeModel`` fed every token of the sequence at its position: a rejected draft leaves
+    positions that the next iteration overwrites, and after a block with every draft accepted the
+    last draft (which the draft model proposed but was never fed) is fed at the start of the next
+    iteration, before the new drafts, so a draft with per-slot state never attends to a stale
+    position.
     """
 
     def __init__(self, model: DecodeModel, sampler: SamplerBackend, *, draft_model: DecodeModel, num_draft: int,
@@ -461,6 +467,14 @@ class SpeculativeDecoder(BatchDecoder):
         last = torch.tensor([s.generated[-1] for s in seqs], dtype=torch.int64, device=dev)
         pos0 = torch.tensor([s.position - 1 for s in seqs], dtype=torch.int64, device=dev)  # the last token's
         u_draft = self._uniforms(seqs, range(K), 1, dev)
+        # the last draft of a fully accepted block reaches the draft model first (logits unused)
+        gap = [s for s in seqs if s.draft_gap is not None]
+        if gap:
+            self.draft_model.decode(*(torch.tensor(v, dtype=torch.int64, device=self.draft_model.device) for v in
+                                      ([s.slot for s in gap], [s.draft_gap[0] for s in gap],
+                                       [s.draft_gap[1] for s in gap])))
+            for s in gap:
+                s.draft_gap = None
         # the draft proposes K tokens
         x = last
         draft_rows, drafts, states = [], [], []
@@ -494,6 +508,8 @@ class SpeculativeDecoder(BatchDecoder):
         tokens, counts = tokens.tolist(), counts.tolist()  # the iteration's wait
         out: list[tuple[int, Step]] = []
         for s, row, c in zip(seqs, tokens, counts):
+            if c == K + 1:  # every draft kept: the draft model has not seen the last one
+                s.draft_gap = (row[K - 1], s.position + K - 1)
             for tok in row[:c]:
                 step = self._advance(s, tok)
                 out.append((s.rid, step))
