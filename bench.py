@@ -62,36 +62,102 @@ def copy_probe() -> int:
     return 0
 
 
-def cpu_baseline(w, budget_s: float = 12.0):
-    """The CPU oracle on rows of the same workload, 8 at a time and cycling through the batch,
-    until ``budget_s`` of CPU work."""
-    from oracle.sampler_oracle import sample_batch  # the checker, timed here as the baseline
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+
+def cpu_baseline(w, budget_s: float = 5.0):
+    """The CPU reference sampler on rows of the same workload, one row per call as the engine's
+    ``sample`` runs (sampler.py:68-77), cycling through the batch: torch's CPU kernels on the
+    engine's fp32 rule plus the extensions (oracle/fp32_rule.py:torch_cpu_sample), for
+    ``budget_s`` with torch's default thread count on this host's share and again with one
+    thread; beside it, the fp64 numpy oracle on one thread."""
+    import torch
+
+    from oracle.fp32_rule import torch_cpu_sample  # the checker's CPU restatement, timed as the baseline
+    from oracle.sampler_oracle import sample_batch
+
     p = w.params
+    rows_args = []
+    for b in range(w.batch):
+        h = w.hist_ids[int(w.hist_offsets[b]) : int(w.hist_offsets[b + 1])]
+        rows_args.append((w.logits[b], h, float(p.temperature[b]), int(p.top_k[b]), float(p.top_p[b]),
+                          float(p.min_p[b]), float(p.repetition_penalty[b]), float(p.presence_penalty[b]),
+                          float(p.frequency_penalty[b]), float(w.uniforms[b])))
+
+    def timed(threads):
+        torch.set_num_threads(threads)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s:
+            torch_cpu_sample(*rows_args[n % w.batch])
+            n += 1
+        return n, time.perf_counter() - t0
+
+    default_threads = torch.get_num_threads()
+    n_all, dt_all = timed(default_threads)
+    n_one, dt_one = timed(1)
+    torch.set_num_threads(default_threads)
+
+    # the numpy fp64 oracle, one thread, 8 rows per call
+    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
     logits = f(w.logits)
     cols = [f(getattr(p, k)) for k in ("temperature", "top_k", "top_p", "min_p")]
     pens = [f(getattr(p, k)) for k in ("repetition_penalty", "presence_penalty", "frequency_penalty")]
     hist, off, u = w.hist_ids.numpy(), w.hist_offsets.numpy(), f(w.uniforms)
-    B, step = w.batch, 8
     rows, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < budget_s:
-        r0 = rows % B
-        sl = slice(r0, r0 + step)
-        sample_batch(
-            logits[sl], *[c[sl] for c in cols], *[c[sl] for c in pens],
-            hist, off[r0 : r0 + step + 1], u[sl],
-        )
-        rows += step
-    dt = time.perf_counter() - t0
+        r0 = rows % w.batch
+        sl = slice(r0, r0 + 8)
+        sample_batch(logits[sl], *[c[sl] for c in cols], *[c[sl] for c in pens], hist, off[r0 : r0 + 9], u[sl])
+        rows += 8
+    dt_np = time.perf_counter() - t0
     return {
-        "value": rows / dt,
+        "value": n_all / dt_all,
         "unit": "rows/s",
-        "cores": 1,
+        "cores": default_threads,
         "kind": "port",
-        "sample": f"{rows} rows of the same workload, 8 per call, cycling through its {B} rows (half peaked, "
-        f"half flat) with penalties, min-p and top-p; numpy fp64 oracle on one thread; {dt:.1f} s",
+        "sample": f"{n_all} rows of the same workload (cycling through its {w.batch} rows, half peaked, half flat), "
+        f"one row per call: torch CPU fp32 sampler (penalties, softmax, min-p, sorted top-p, inverse-CDF draw) "
+        f"on {default_threads} threads, {dt_all:.1f} s",
+        "single_thread": {"value": n_one / dt_one, "unit": "rows/s", "rows": n_one, "seconds": round(dt_one, 2)},
+        "numpy_oracle_fp64_one_thread": {"value": rows / dt_np, "unit": "rows/s", "rows": rows,
+                                         "seconds": round(dt_np, 2)},
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "torch": torch.__version__,
     }
+
+
+def tie_counts(w, ids) -> dict:
+    """Tie rows of the batch under both classifiers, and the kernel's ids against the oracle off
+    the oracle's ties (the launch's own parity check)."""
+    import numpy as np
+
+    from oracle.fp32_rule import fp32_rule
+    from oracle.sampler_oracle import classify_ties, penalize, sample_row
+
+    p = w.params
+    n_or = n_fp = bad = 0
+    ids = ids.tolist()
+    for b in range(w.batch):
+        h = w.hist_ids[int(w.hist_offsets[b]) : int(w.hist_offsets[b + 1])].numpy()
+        x, _ = penalize(w.logits[b].float().numpy(), h, float(p.repetition_penalty[b]), float(p.presence_penalty[b]),
+                        float(p.frequency_penalty[b]))
+        args = (float(p.temperature[b]), int(p.top_k[b]), float(p.top_p[b]), float(p.min_p[b]), float(w.uniforms[b]))
+        r = sample_row(x, *args)
+        tie = bool(classify_ties(r))
+        n_or += tie
+        n_fp += bool(fp32_rule(np.asarray(x), *args).ties)
+        bad += (not tie) and ids[b] != r.token
+    return {"rows": w.batch, "oracle_fixed_point": n_or, "engine_fp32_rule": n_fp,
+            "kernel_differs_off_oracle_ties": bad}
 
 
 def decode_loop(args) -> int:
@@ -519,6 +585,29 @@ def main() -> int:
     torch.cuda.synchronize()
     cached_us = e0.elapsed_time(e1) * 1e3 / 50
 
+    # the two regimes of the headline alone (every row peaked, every row flat), same method
+    regimes = {}
+    for regime in ("peaked", "flat"):
+        wr = make("peaked_flat", regime=regime)
+        dr = wr.to(dev)
+        rs = [dr.logits] + [torch.roll(dr.logits, shifts=7919 * i, dims=1).contiguous() for i in range(1, N_SETS)]
+        rsteps = [s.prepare_batch(x, dr.params, dr.uniforms, dr.hist_ids, dr.hist_offsets) for x in rs]
+        for i in range(10):
+            rsteps[i % N_SETS].launch(stream.cuda_stream)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(50):
+            rsteps[i % N_SETS].launch(stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        regimes[regime] = e0.elapsed_time(e1) * 1e3 / 50
+        del rsteps, rs, dr
+    # the ids of the headline inputs (input set 0), for the parity check beside the CPU leg
+    steps[0].launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    ids0 = steps[0].ids.cpu()
+
     B = w.batch
     us_step = total_us / K
     algo = w.algorithmic_bytes()
@@ -554,6 +643,8 @@ def main() -> int:
         "us_per_step": us_step,
         "us_per_launch_event_bracketed_p10_p50_p90": [float(np.percentile(per, q)) for q in (10, 50, 90)],
         "us_per_step_cache_resident": cached_us,
+        "us_per_step_peaked_rows_only": regimes["peaked"],
+        "us_per_step_flat_rows_only": regimes["flat"],
         "wall_s": wall,
         "roofline": {
             "bound": "hbm",
@@ -571,6 +662,7 @@ def main() -> int:
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w)
+        out["ties"] = tie_counts(w, ids0)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -127,3 +127,39 @@ def fp32_rule(x: np.ndarray, temperature: float, top_k: int, top_p: float, min_p
     if int(grp.sum()) > 1 and torch.unique(z[grp]).numel() > 1:
         ties.append("merged_draw")
     return Fp32Row("sampled", kept, kept_sort, tok, ties)
+
+
+def torch_cpu_sample(row: torch.Tensor, hist: torch.Tensor, temperature: float, top_k: int, top_p: float,
+                     min_p: float, rep: float, pres: float, freq: float, u: float) -> int:
+    """One row through the engine's fp32 rule with torch's CPU kernels, the way the engine's
+    sampler would run on a CPU (sampler.py:50-77, with the extensions: penalties from the
+    history, min-p, and the inverse-CDF draw on ``u`` over the kept tokens in descending
+    probability). The CPU baseline's unit of work; no tie classification."""
+    x = row.float()
+    V = x.numel()
+    if hist.numel() and (rep != 1.0 or pres != 0.0 or freq != 0.0):
+        h = hist[(hist >= 0) & (hist < V)].long()
+        counts = torch.bincount(h, minlength=V)
+        sel = counts > 0
+        xs = x[sel]
+        xs = torch.where(xs > 0, xs / rep, xs * rep)
+        xs = xs - freq * counts[sel].float()
+        x = x.clone()
+        x[sel] = xs - pres
+    if not temperature > 0:
+        return int(torch.argmax(x))
+    z = x / temperature
+    if 0 < top_k < V:
+        kth = torch.topk(z, top_k).values[-1]
+        z = torch.where(z >= kth, z, torch.tensor(-float("inf")))
+    p = torch.softmax(z, dim=0)
+    if min_p > 0:
+        p = torch.where(p >= p.max() * min_p, p, torch.zeros(()))
+    sp, order = torch.sort(p, descending=True)
+    C = torch.cumsum(sp, 0)
+    if top_p < 1:
+        before = C - sp
+        n = max(int((before < top_p * C[-1]).sum()), 1)
+        sp, order, C = sp[:n], order[:n], C[:n]
+    j = int(torch.searchsorted(C, torch.tensor([u * float(C[-1])]), right=True)[0])
+    return int(order[min(j, order.numel() - 1)])

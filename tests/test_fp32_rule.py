@@ -122,3 +122,24 @@ def test_a_planted_mistake_is_not_hidden_by_the_tie_classes():
 
     n = compare("mixed_bf16", 24, rule=no_temperature)
     assert len(n["unexplained"]) > 0
+
+
+@pytest.mark.parametrize("name,batch", [("mixed_bf16", 16), ("large_fp32", 8), ("peaked_flat", 8)])
+def test_the_cpu_baseline_sampler_draws_the_oracle_s_tokens(name, batch):
+    # bench.py's CPU baseline (torch_cpu_sample) computes the same thing as the oracle wherever
+    # neither classifier flags the row
+    from oracle.fp32_rule import torch_cpu_sample
+
+    w = make(name, batch=batch)
+    p = w.params
+    checked = 0
+    for b, x, args in rows_of(name, batch):
+        h = w.hist_ids[int(w.hist_offsets[b]) : int(w.hist_offsets[b + 1])]
+        tok = torch_cpu_sample(w.logits[b], h, args[0], args[1], args[2], args[3], float(p.repetition_penalty[b]),
+                               float(p.presence_penalty[b]), float(p.frequency_penalty[b]), args[4])
+        r = sample_row(x, *args)
+        if fp32_rule(x, *args).ties or classify_ties(r):
+            continue
+        assert tok == r.token, (name, b)
+        checked += 1
+    assert checked >= batch // 2

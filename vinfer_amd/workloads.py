@@ -99,8 +99,11 @@ def _csr(hists: list[np.ndarray]) -> tuple[torch.Tensor, torch.Tensor]:
     return torch.from_numpy(ids), torch.from_numpy(off.astype(np.int32))
 
 
-def make(name: str, batch: int | None = None, vocab: int | None = None, seed: int | None = None) -> Workload:
-    """The named workload; ``batch``/``vocab`` shrink it for tests (same generator)."""
+def make(name: str, batch: int | None = None, vocab: int | None = None, seed: int | None = None,
+         regime: str | None = None) -> Workload:
+    """The named workload; ``batch``/``vocab`` shrink it for tests (same generator).
+    ``peaked_flat`` with ``regime`` "peaked" or "flat" makes every row of that regime instead
+    of alternating them (the other inputs are generated the same way)."""
     rng = np.random.default_rng(SEEDS[name] if seed is None else seed)
     g = torch.Generator().manual_seed(SEEDS[name] if seed is None else seed)
     rep, pres, freq = PENALTIES
@@ -125,10 +128,15 @@ def make(name: str, batch: int | None = None, vocab: int | None = None, seed: in
     if name == "peaked_flat":
         B, V = batch or 256, vocab or 151936
         x = torch.randn(B, V, generator=g)
-        x[1::2] *= 0.1
+        flat = [b % 2 == 1 for b in range(B)] if regime is None else [regime == "flat"] * B
+        if regime not in (None, "flat", "peaked"):
+            raise ValueError(f"regime must be 'peaked' or 'flat', got {regime!r}")
         peak = rng.integers(0, V, B)
-        for b in range(0, B, 2):
-            x[b, int(peak[b])] += 15.0
+        for b in range(B):
+            if flat[b]:
+                x[b] *= 0.1
+            else:
+                x[b, int(peak[b])] += 15.0
         x = x.to(torch.bfloat16)
         params = _params(B, 1.0, 0, 0.95, 0.05, rep, pres, freq)
         perm = rng.permutation(V)
