@@ -449,31 +449,44 @@ def workloads_bench(args) -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    for name in NAMES:
-        w = make(name)
+    for name in NAMES + ("single_bf16",):
+        if name == "single_bf16":  # the per-token row in the model's dtype
+            w = make("single_fp32")
+            w.logits = w.logits.to(torch.bfloat16)
+            w.name = name
+        else:
+            w = make(name)
         d = w.to(dev)
         s = SAMPLER.resolve("hip", BackendContext(dev, w.logits.dtype))
         nbytes = d.logits.numel() * d.logits.element_size()
         sets = [d.logits] + ([torch.roll(d.logits, shifts=7919 * i, dims=1).contiguous() for i in range(1, N_SETS)]
                              if nbytes * N_SETS <= 8 << 30 else [])
-        steps = [s.prepare_batch(x, d.params, d.uniforms, d.hist_ids, d.hist_offsets, d.draft_ids) for x in sets]
         stream = torch.cuda.current_stream(dev)
-        for i in range(args.warmup):
-            steps[i % len(steps)].launch(stream.cuda_stream)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         K = max(1, args.steps // 4)
-        e0.record(stream)
-        for i in range(K):
-            steps[i % len(steps)].launch(stream.cuda_stream)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / K
+
+        def timed(split_rows: bool) -> float:
+            s.split_rows = split_rows
+            steps = [s.prepare_batch(x, d.params, d.uniforms, d.hist_ids, d.hist_offsets, d.draft_ids) for x in sets]
+            s.split_rows = False
+            for i in range(args.warmup):
+                steps[i % len(steps)].launch(stream.cuda_stream)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(K):
+                steps[i % len(steps)].launch(stream.cuda_stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / K
+
+        us = timed(False)
         algo = w.algorithmic_bytes()
         out = {"workload": name, "batch": w.batch, "vocab": w.vocab, "logits_dtype": str(w.logits.dtype).split(".")[-1],
                "us_per_launch": us, "rows_per_s": w.batch / (us * 1e-6), "launches": K,
-               "input_sets": len(steps), "algorithmic_bytes": algo,
+               "input_sets": len(sets), "algorithmic_bytes": algo,
                "roofline_frac": algo / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+        if args.split_rows and w.logits.dtype == torch.bfloat16 and w.batch <= 128:
+            out["us_per_launch_split_rows"] = timed(True)  # (VSAMP_SPLIT_ROWS: identical ids)
         if not args.no_cpu:
             f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
             p = w.params
@@ -493,8 +506,26 @@ def workloads_bench(args) -> int:
             out["cpu_baseline"] = {"value": rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
                                    "sample": f"{rows} rows of the workload (cycling), numpy fp64 oracle; {dt:.1f} s"}
         print(json.dumps(out), flush=True)
-        del steps, sets, d
+        del sets, d
         torch.cuda.empty_cache()
+    # the engine's per-token call, unchanged (generate.py:129): sample(logits[V], params, seed,
+    # position) -> int, host work and the id's copy back included
+    from vinfer_amd.sampling import SamplingParams
+
+    for dtype in (torch.bfloat16, torch.float32):
+        s = SAMPLER.resolve("hip", BackendContext(dev, dtype))
+        w = make("single_fp32")
+        row = w.logits[0].to(dtype).to(dev)
+        sp = SamplingParams(temperature=0.7, top_k=20, top_p=0.8)
+        for i in range(20):
+            s.sample(row, sp, 7, i)
+        torch.cuda.synchronize()
+        n, t0 = 200, time.perf_counter()
+        for i in range(n):
+            s.sample(row, sp, 7, i)
+        us = (time.perf_counter() - t0) / n * 1e6
+        print(json.dumps({"call": "sample(logits[V], params, seed, position)", "vocab": w.vocab,
+                          "logits_dtype": str(dtype).split(".")[-1], "us_per_call_host_inclusive": us}), flush=True)
     return 0
 
 
@@ -510,6 +541,8 @@ def main() -> int:
     ap.add_argument("--verify", action="store_true", help="time the speculative-decoding verify instead")
     ap.add_argument("--logprobs", action="store_true", help="time the raw log-probabilities instead")
     ap.add_argument("--workloads", action="store_true", help="time every named workload (one line each)")
+    ap.add_argument("--split-rows", action="store_true",
+                    help="with --workloads: also time small bf16 batches with split rows (VSAMP_SPLIT_ROWS)")
     args = ap.parse_args()
     if args.copy_probe:
         return copy_probe()

@@ -28,13 +28,19 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 3
+#define VSAMP_ABI_VERSION 4
 
 /* Bytes of one row's sampling state (vsamp_sample_states), an opaque record. */
 #define VSAMP_ROW_STATE_BYTES 40
 
 /* vsamp_args.flags bits. */
 #define VSAMP_HIST_RANGES 1u /* hist_offsets holds a [start, end) pair per row (see below) */
+/* Split rows: vsamp_sample spreads each bf16 row of a batch of at most 128 rows (V >= 32768,
+ * 16-byte aligned rows) over several workgroups, when the workspace holds
+ * vsamp_split_workspace_bytes(); other calls run one workgroup per row. The results are
+ * identical either way. On MI355X it is slower than whole rows at every batch measured (the
+ * slices' merge needs device-scope fences), so it is off unless asked for. */
+#define VSAMP_SPLIT_ROWS 2u
 
 enum vsamp_dtype { VSAMP_BF16 = 0, VSAMP_F32 = 1 };
 
@@ -96,7 +102,7 @@ typedef struct vsamp_args {
   void* workspace;
   size_t workspace_bytes;
 
-  uint32_t flags; /* 0 or VSAMP_HIST_RANGES */
+  uint32_t flags; /* VSAMP_HIST_RANGES and / or VSAMP_SPLIT_ROWS, or 0 */
   uint32_t reserved1;
 } vsamp_args;
 
@@ -110,6 +116,11 @@ int vsamp_query(int device, char* why, size_t n);
 
 /* Workspace bytes vsamp_sample / vsamp_probs / vsamp_penalized_logits need. */
 size_t vsamp_workspace_bytes(int32_t batch, int32_t vocab, int64_t hist_total);
+
+/* Workspace bytes of a vsamp_sample call with VSAMP_SPLIT_ROWS (the slice records and the rows'
+ * arrival words after the above; equal to it when the batch does not split). The arrival words
+ * need no clearing: each launch tags them. No counterpart in the engine. */
+size_t vsamp_split_workspace_bytes(int32_t batch, int32_t vocab, int64_t hist_total);
 
 /* Sample one token per row: penalties, temperature, top-k, softmax, min-p, top-p, then the
  * inverse-CDF draw with u over the kept tokens taken in descending probability (equal

@@ -471,3 +471,54 @@ def test_errors_are_raised_not_swallowed():
     with pytest.raises(ValueError):
         s.sample_batch(x.half(), p, torch.zeros(4, device=DEV))
     assert math.isfinite(float(s.probs(x, p).sum()))
+
+
+def _launch(a, lib):
+    import ctypes
+
+    _lib.check(lib.vsamp_sample(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)))
+
+
+@pytest.mark.parametrize("pen", [False, True], ids=["plain", "penalties"])
+@pytest.mark.parametrize("B,V,pad", [(1, 151936, 0), (1, 32768, 0), (3, 151939, 5), (17, 65536, 0),
+                                     (64, 151936, 0), (128, 40000, 8), (8, 262144, 0)])
+def test_split_rows_equal_whole_rows(B, V, pad, pen):
+    # Small bf16 batches split each row over several workgroups of one launch when the workspace
+    # holds the slice records (the row's last slice to arrive finishes it); with a workspace too
+    # small for them the same call runs one workgroup per row. Both must draw the same ids (and
+    # probabilities of the draft ids), bit for bit; and both match the oracle. Three launches in a
+    # row on the same workspace: the arrival words left by one launch must not confuse the next.
+    w = random_workload(B * 1000 + V + pen, B, V, torch.bfloat16, penalties=pen, hist_len=300 if pen else 0)
+    w.params.top_k[::3] = 0  # (more rows through the top-p / min-p path)
+    s = hip(torch.bfloat16)
+    x = torch.zeros(B, V + pad, dtype=torch.bfloat16, device=DEV)
+    x[:, :V] = w.logits.to(DEV)
+    x = x[:, :V]  # row stride V + pad: a ragged vocabulary on 16-byte aligned rows
+    d = w.to(DEV)
+    print(f"split vs whole B={B} V={V} stride={V + pad} penalties={pen}", flush=True)
+    hi, ho = (d.hist_ids, d.hist_offsets) if pen else (None, None)
+    s.split_rows = True
+    try:
+        a, keep = s._args(x, d.params, hi, ho, d.uniforms, d.draft_ids)
+    finally:
+        s.split_rows = False
+    assert a.flags & _lib.VSAMP_SPLIT_ROWS
+    need = a.workspace_bytes
+    assert need > 0  # (the slice records)
+    lib = _lib.load()
+    outs = []
+    for ws in (True, True, False, True):
+        ids = torch.full((B,), -1, dtype=torch.int32, device=DEV)
+        dp = torch.full((B,), -1.0, dtype=torch.float32, device=DEV)
+        a.out_ids, a.out_draft_prob = ids.data_ptr(), dp.data_ptr()
+        # (one byte short of the records: the whole-row path, with the penalty part intact)
+        a.workspace_bytes = need if ws else need - 1
+        _launch(a, lib)
+        torch.cuda.synchronize()
+        outs.append((ids.cpu(), dp.cpu()))
+    del keep
+    i1, p1 = outs[0]
+    for i2, p2 in outs[1:]:
+        assert torch.equal(i1, i2) and torch.equal(p1.view(torch.int32), p2.view(torch.int32))
+    ties, bad = compare_ids(i1, oracle(w), p1)
+    assert not bad, bad[:10]

@@ -11,12 +11,13 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 ROW_STATE_BYTES = 40
 
 VSAMP_BF16 = 0
 VSAMP_F32 = 1
 VSAMP_HIST_RANGES = 1
+VSAMP_SPLIT_ROWS = 2
 
 STATUS = {0: "ok", 1: "VSAMP_E_ARG", 2: "VSAMP_E_DTYPE", 3: "VSAMP_E_HIP", 4: "VSAMP_E_WORKSPACE", 5: "VSAMP_E_DEVICE"}
 
@@ -25,6 +26,7 @@ EXPORTS = (
     "vsamp_abi_version",
     "vsamp_query",
     "vsamp_workspace_bytes",
+    "vsamp_split_workspace_bytes",
     "vsamp_sample",
     "vsamp_sample_noalloc",
     "vsamp_probs",
@@ -116,6 +118,8 @@ def load() -> ctypes.CDLL:
         lib.vsamp_query.restype = ctypes.c_int
         lib.vsamp_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int64]
         lib.vsamp_workspace_bytes.restype = ctypes.c_size_t
+        lib.vsamp_split_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int64]
+        lib.vsamp_split_workspace_bytes.restype = ctypes.c_size_t
         lib.vsamp_sample.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p]
         lib.vsamp_sample.restype = ctypes.c_int
         lib.vsamp_sample_noalloc.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p]

@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -11,6 +12,7 @@
 #include "common.cuh"
 #include "penalty.cuh"
 #include "sample.cuh"
+#include "split.cuh"
 #include "uniform.h"
 #include "verify.cuh"
 #include "logprobs.cuh"
@@ -110,12 +112,45 @@ Layout layout(int64_t B, int64_t V, int64_t H) {
 
 constexpr int64_t kMaxVocab = static_cast<int64_t>(vs::kMaxStripes) * vs::kThreads * vs::kBlk;
 
+// ---- split rows -------------------------------------------------------------------------------
+// A batch of at most kSplitMaxBatch bf16 rows of at least kSplitMinVocab spreads each row over G
+// workgroups of the one launch (k_sample in split mode): G = 256 / B clamped to [2, 16], so the
+// launch has about 256 workgroups (one per CU) while a row's last slice merges at most 15 other
+// slice records. The records, then one arrival word per row, follow the penalty part of the
+// workspace.
+constexpr int kSplitMaxBatch = 128;
+constexpr int kSplitMinVocab = 32768;
+constexpr int kSplitTarget = 256;
+constexpr int kSplitMaxSlices = 16;
+static_assert(kSplitMaxSlices <= vs::kMaxSlices, "slices per row");
+
+int split_slices(int64_t B, int64_t V) {
+  if (B < 1 || B > kSplitMaxBatch || V < kSplitMinVocab) return 1;
+  const int64_t g = kSplitTarget / B;
+  return static_cast<int>(g < 2 ? 2 : (g > kSplitMaxSlices ? kSplitMaxSlices : g));
+}
+
+// Byte offset of the slice records in the workspace (after the penalty part), and the workspace's
+// size with the records and arrival words.
+size_t split_records(int64_t B, int64_t V, int64_t H) { return align_up(layout(B, V, H).total); }
+size_t split_total(int64_t B, int64_t V, int64_t H) {
+  const int G = split_slices(B, V);
+  if (G < 2) return layout(B, V, H).total;
+  return split_records(B, V, H) + static_cast<size_t>(B) * G * vs::kSliceRecord + 8 * static_cast<size_t>(B);
+}
+
+// Every launch's tag for the arrival words: distinct across the launches of this process, and
+// starting from a value a workspace's earlier contents are unlikely to hold.
+std::atomic<uint64_t> g_epoch{(static_cast<uint64_t>(std::chrono::steady_clock::now().time_since_epoch().count()) *
+                               0x9E3779B97F4A7C15ull) >> 16};
+uint64_t next_epoch() { return g_epoch.fetch_add(1, std::memory_order_relaxed) & 0xFFFFFFFFFFFFull; }
+
 // ---- the library's own workspace, for callers that cannot allocate (vsamp_sample_noalloc) ----
 // 16 MiB per GPU, held from the library's first use on that GPU until the process ends: the
 // workspace of histories up to ~1.39 M ids in all (4 B per row + 12 B per history id). Every
 // call on one GPU shares it, so calls that overlap on one GPU (different streams, or threads)
-// race. The kernels write every word of it they read within the launch, so nothing has to be
-// cleared between calls.
+// race. The kernels write every word of it they read within the launch (the split rows' arrival
+// words are tagged with the launch), so nothing has to be cleared between calls.
 constexpr size_t kScratchBytes = size_t(16) << 20;
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 std::atomic<void*> g_scratch[kMaxDevices];  // the array's address on each device
@@ -139,8 +174,9 @@ int scratch_of_current_device(void** out) {
 
 int validate(const vsamp_args* a, bool need_draw) {
   if (!a) return fail(VSAMP_E_ARG, "args is NULL");
-  if (a->flags & ~VSAMP_HIST_RANGES)
-    return fail(VSAMP_E_ARG, "flags must be 0 or VSAMP_HIST_RANGES, got %u", a->flags);
+  if (a->flags & ~(VSAMP_HIST_RANGES | VSAMP_SPLIT_ROWS))
+    return fail(VSAMP_E_ARG, "flags must be a combination of VSAMP_HIST_RANGES and VSAMP_SPLIT_ROWS, got %u",
+                a->flags);
   if (a->dtype != VSAMP_BF16 && a->dtype != VSAMP_F32)
     return fail(VSAMP_E_DTYPE, "unsupported logits dtype %d (VSAMP_BF16=0, VSAMP_F32=1)", a->dtype);
   if (a->batch < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", a->batch);
@@ -242,6 +278,25 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
   s.probs_stride = probs_stride;
   s.out_state = state;
   s.param_div = param_div;
+  s.nrows = a->batch;
+  // Small batches of bf16 rows, when asked for: split rows if the workspace holds the records.
+  const int G = (a->flags & VSAMP_SPLIT_ROWS) ? split_slices(a->batch, a->vocab) : 1;
+  if (sizeof(Tin) == 2 && !state && !probs && G >= 2 && a->workspace &&
+      !(reinterpret_cast<uintptr_t>(a->workspace) & 255u) &&
+      a->workspace_bytes >= split_total(a->batch, a->vocab, a->hist_total) &&
+      !(reinterpret_cast<uintptr_t>(a->logits) & 15u) && a->row_stride % vs::kBlk == 0) {
+    uint8_t* rec = static_cast<uint8_t*>(a->workspace) + split_records(a->batch, a->vocab, a->hist_total);
+    s.slices = rec;
+    s.arrive = reinterpret_cast<vs::u64*>(rec + static_cast<size_t>(a->batch) * G * vs::kSliceRecord);
+    s.epoch = next_epoch();
+    s.G = G;
+    if (pen)
+      hipLaunchKernelGGL((vs::k_sample<Tin, true, false, true>), dim3(a->batch * G), dim3(vs::kThreads), 0, st, s);
+    else
+      hipLaunchKernelGGL((vs::k_sample<Tin, false, false, true>), dim3(a->batch * G), dim3(vs::kThreads), 0, st, s);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_sample (split rows)");
+  }
   // One launch per step: the penalty phase runs at the start of the same kernel.
   if (state)  // (the verify's launches, which apply no penalties)
     hipLaunchKernelGGL((vs::k_sample<Tin, false, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
@@ -299,6 +354,11 @@ size_t vsamp_workspace_bytes(int32_t batch, int32_t vocab, int64_t hist_total) {
   return layout(batch, vocab, hist_total).total;
 }
 
+size_t vsamp_split_workspace_bytes(int32_t batch, int32_t vocab, int64_t hist_total) {
+  if (batch < 0 || vocab < 1 || hist_total < 0) return 0;
+  return split_total(batch, vocab, hist_total);
+}
+
 int vsamp_sample(const vsamp_args* a, void* stream) {
   g_err.clear();
   if (int rc = validate(a, true)) return rc;
@@ -322,11 +382,9 @@ int vsamp_sample_noalloc(const vsamp_args* a, void* stream) {
                 "vsamp_sample_noalloc: batch %d with %lld history ids needs %zu workspace bytes, more than its "
                 "%zu; use vsamp_sample with a caller workspace",
                 a->batch, static_cast<long long>(a->hist_total), need, kScratchBytes);
-  vsamp_args c = *a;
-  if (wants_penalties(a)) {
-    if (int rc = scratch_of_current_device(&c.workspace)) return rc;
-    c.workspace_bytes = kScratchBytes;
-  }
+  vsamp_args c = *a;  // (the slice records of split rows too, when they fit)
+  if (int rc = scratch_of_current_device(&c.workspace)) return rc;
+  c.workspace_bytes = kScratchBytes;
   hipStream_t st = static_cast<hipStream_t>(stream);
   return c.dtype == VSAMP_BF16 ? run_sample<uint16_t>(&c, nullptr, 0, st) : run_sample<float>(&c, nullptr, 0, st);
 }

@@ -28,6 +28,18 @@ __device__ __forceinline__ T* as_global(T* p) {
   return (T*)((__attribute__((address_space(1))) T*)p);
 }
 
+// A load through an explicitly global pointer (never a flat load).
+template <class T>
+__device__ __forceinline__ T ld_global(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+// The same for 16 bytes (through a vector type: uint4's copy constructor takes no address space).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_global_u4(const uint4* p) {
+  const u32x4_t v = ld_global(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // ---- ordered keys ---------------------------------------------------------------------------
 // A 32-bit key whose unsigned order is the numeric order of fp32 values, with -0.0 folded onto
 // +0.0 (they compare equal) and every NaN mapped above +inf.

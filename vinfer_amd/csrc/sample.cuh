@@ -29,6 +29,7 @@
 
 #include "common.cuh"
 #include "penalty.cuh"
+#include "split.cuh"
 
 namespace vs {
 
@@ -62,7 +63,18 @@ struct SampleArgs {
   int has_exc;  // the workspace holds this batch's exceptions
   const int32_t* off;
   PenaltyArgs pen;  // the penalty phase's inputs (used when the kernel runs it)
+  // split rows (G > 1): workgroup b takes slice b / nrows of row b % nrows
+  uint8_t* slices;  // the rows' slice records, G per row
+  u64* arrive;      // per row: (epoch << 16 | slices arrived)
+  u64 epoch;        // this launch's tag (48 bits), distinct from every earlier launch's
+  int G;            // slices per row (0: one workgroup per row)
+  int nrows;        // B
 };
+
+// The row of this workgroup.
+__device__ __forceinline__ int row_index(const SampleArgs& a) {
+  return a.G > 1 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(a.nrows)) : static_cast<int>(blockIdx.x);
+}
 
 // Scratch of the id-order search.
 struct Search {
@@ -160,14 +172,8 @@ struct __align__(16) FastSmem {
   FastPlan plan;
 };
 
-// A load through an explicitly global pointer (never a flat load).
-template <class T>
-__device__ __forceinline__ T ld_global(const T* p) {
-  return *(const __attribute__((address_space(1))) T*)p;
-}
 
 // 16-byte block b of a bf16 row.
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __align__(16) uint16_t g_unused_block[kBlk];  // (read, never written)
 
 __device__ __forceinline__ uint4 ld_block(const uint16_t* base, int b) {
@@ -869,9 +875,8 @@ __device__ __forceinline__ bool degenerate(const Row<Tin>& row, const RowParams&
 // and with STATE the row's RowState. `draw` is the drawn token (ignored for point rows).
 template <bool STATE, class Tin>
 __device__ __forceinline__ void finish(const SampleArgs& a, const Row<Tin>& row, const RowParams& p, float mz,
-                       const Kept& k, int draw, float* vslot) {
+                       const Kept& k, int draw, float* vslot, int r) {
   const int tid = threadIdx.x;
-  const int r = blockIdx.x;
   if (STATE && tid == 0) {
     RowState st;
     st.mz = mz;
@@ -979,7 +984,7 @@ __device__ __forceinline__ int chunk_pick(const u64* cm, int mode, double target
 
 template <bool STATE, class Tin>
 __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g,
-                                            FastSmem& f) {
+                                            FastSmem& f, int r) {
   const int V = row.V;
   Search& s = g.srch;
   if (row.nexc > 0) build_bitmap(row, reinterpret_cast<uint32_t*>(&g) + kBitmapOffset);
@@ -1008,7 +1013,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
   const float mz = xmax / T;
   Kept k;
   if (degenerate(row, p, mkey, imax, mz, s, k)) {
-    finish<STATE>(a, row, p, mz, k, 0, &s.vslot);
+    finish<STATE>(a, row, p, mz, k, 0, &s.vslot, r);
     return;
   }
   const uint32_t lo_key = key_of(-INFINITY);
@@ -1235,7 +1240,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     }
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, s);
   }
-  finish<STATE>(a, row, p, mz, k, draw, &s.vslot);
+  finish<STATE>(a, row, p, mz, k, draw, &s.vslot, r);
 }
 
 // ---- bf16 fast path: a 16-bit key histogram -----------------------------------------------------
@@ -1612,6 +1617,93 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
   return f.si[6];  // (nothing writes f.si[6] again in this launch)
 }
 
+// (merge mode) The id of the j-th (0-based, ascending id) token whose penalised value is v, or
+// -1. Each slice's count of members comes from its record (the bulk count of v's key; of both
+// zero keys when v is 0), minus its penalised ids whose original value is v, plus its penalised
+// ids whose new value is v; the slice holding the j-th member is then searched alone, as a row
+// of its own. `scratch` is LDS past the position bitmap (kMaxSlices + 2 kExcCap + 4 words);
+// needs row.bm built when the row has penalised ids.
+__device__ __forceinline__ int split_find(const SampleArgs& a, const Row<uint16_t>& row, FastSmem& f, int ne,
+                                          float v, u64 j, Search& srch, uint32_t* scratch, const uint8_t* recs) {
+  const int tid = threadIdx.x;
+  const int G = a.G;
+  uint32_t* cnt = scratch;
+  int32_t* xid = reinterpret_cast<int32_t*>(scratch + kMaxSlices);
+  float* xval = reinterpret_cast<float*>(scratch + kMaxSlices + kExcCap);
+  uint32_t* misc = scratch + kMaxSlices + 2 * kExcCap;  // listed ids, the slice, the index in it
+  const uint32_t vb = __float_as_uint(v);
+  const bool bf = (vb & 0xFFFFu) == 0u;  // bulk tokens can hold v
+  const int nfull = row.V / kBlk;
+  if (tid < G) {
+    uint32_t c = 0;
+    if (bf) {
+      const uint32_t k1 = ok16(vb >> 16);
+      const uint32_t k2 = v == 0.0f ? ok16((vb >> 16) ^ 0x8000u) : k1;
+      const uint8_t* rec = recs + static_cast<size_t>(tid) * kSliceRecord;
+      for (int t = 0; t < (k2 != k1 ? 2 : 1); ++t) {
+        const uint32_t key = t ? k2 : k1;
+        const uint32_t ch = (65535u - key) >> 6;
+        const uint32_t e = ld_global(reinterpret_cast<const uint16_t*>(rec + kSliceEmap) + ch);
+        if (e != kNoEntry) {
+          const uint32_t w0 = 32768u - 32u * ch - 32u;  // the chunk's first histogram word
+          const uint32_t word = ld_global(reinterpret_cast<const uint32_t*>(rec + kSliceData) + 32u * e + ((key >> 1) - w0));
+          c += (word >> ((key & 1u) << 4)) & 0xFFFFu;
+        }
+      }
+    }
+    cnt[tid] = c;
+  }
+  if (tid == 0) misc[0] = 0;
+  lds_barrier();
+  auto slice_of = [&](int id) {  // the last g with slice_begin(g) <= id's block
+    const int64_t b = id / kBlk;
+    const int g = static_cast<int>(((b + 1) * G + nfull - 1) / nfull) - 1;
+    return g < G - 1 ? g : G - 1;
+  };
+  for (int e = tid; e < ne; e += kThreads) {
+    const int id = f.eid[e];
+    const int g = slice_of(id);
+    if (bf && bf16_to_f32(ld_global(row.p + id)) == v) atomicSub(&cnt[g], 1u);
+    if (f.eval[e] == v) atomicAdd(&cnt[g], 1u);
+  }
+  lds_barrier();
+  if (tid < kWave) {
+    const u64 c = tid < G ? cnt[tid] : 0u;
+    const u64 inc = wave_incl_scan<u64>(c);
+    const bool hit = c > 0 && inc - c <= j && j < inc;
+    const u64 hm = __ballot(hit);
+    if (tid == 0) misc[1] = hm ? static_cast<uint32_t>(__ffsll(static_cast<long long>(hm)) - 1) : 0xFFFFFFFFu;
+    if (hit) misc[2] = static_cast<uint32_t>(j - (inc - c));
+  }
+  lds_barrier();
+  const uint32_t gs = misc[1];
+  if (gs == 0xFFFFFFFFu) return -1;  // (uniform)
+  const u64 jj = misc[2];
+  const int b0 = slice_begin(nfull, G, static_cast<int>(gs));
+  const int s0 = b0 * kBlk;
+  const int s1 = static_cast<int>(gs) == G - 1 ? row.V : slice_begin(nfull, G, static_cast<int>(gs) + 1) * kBlk;
+  for (int e = tid; e < ne; e += kThreads) {
+    const int id = f.eid[e];
+    if (id >= s0 && id < s1) {
+      const uint32_t i = atomicAdd(&misc[0], 1u);
+      xid[i] = id - s0;
+      xval[i] = f.eval[e];
+    }
+  }
+  lds_barrier();
+  Row<uint16_t> sr = row;
+  sr.p = row.p + s0;
+  sr.V = s1 - s0;
+  sr.nblk = (sr.V + kBlk - 1) / kBlk;
+  sr.nstripes = (sr.nblk + kThreads - 1) / kThreads;
+  sr.bm = row.bm ? row.bm + b0 : nullptr;
+  sr.eid = xid;
+  sr.eval = xval;
+  sr.nexc = static_cast<int>(misc[0]);
+  const int res = find_first(sr, [&](float x, int) -> u64 { return x == v ? 1ull : 0ull; }, jj, srch);
+  return res < 0 ? -1 : res + s0;
+}
+
 // The bf16 fast path (every temperature: T <= 0 is greedy). Returns false (before writing any
 // output) when the row needs the generic path: a history longer than kFastMaxL or with more
 // than kExcCap distinct ids, a key count past 65535, or a chunk with more than kMaxL penalised
@@ -1628,9 +1720,13 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
 // Loads here sit outside divergent branches (a lane past the end rereads a valid block whose
 // data it ignores): a load inside one needs a copy at the join, and that copy waits for every
 // load in flight.
-template <bool PEN, bool STATE>
+// SPLIT: the workgroup takes one slice of the row (split.cuh): it builds the slice's histogram
+// and record and returns true unless it is the row's last slice to arrive, which adds the other
+// slices' records to its histogram and finishes the row; the drawn member is found by
+// split_find. `r` is the row.
+template <bool PEN, bool STATE, bool SPLIT = false>
 __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row, const RowParams& p, uint32_t* hist,
-                                         FastSmem& f, Search& srch, uint32_t pw) {
+                                         FastSmem& f, Search& srch, uint32_t pw, int r) {
   const int tid = threadIdx.x;
   const int V = row.V;
   // ---- 1. histogram of every key, then the penalised tokens' original keys taken out ----------
@@ -1644,11 +1740,14 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   // only would make the first wait for the parameters wait for every load in flight.)
   constexpr int D = 4;
   uint4 d[D];
-  {
+  if constexpr (!SPLIT) {
     const uint16_t* src = nfull > 0 ? base : g_unused_block;
 #pragma unroll
     for (int k = 0; k < D; ++k) d[k] = ld_block(src, min(tid + k * kThreads, max(nfull - 1, 0)));
   }
+  // (split rows) this workgroup's slice of the row and the row's slice records
+  uint8_t* recs = SPLIT ? a.slices + static_cast<size_t>(r) * a.G * kSliceRecord : nullptr;
+  const int gown = SPLIT ? static_cast<int>(blockIdx.x) / a.nrows : 0;
   if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
   uint32_t* htab = fast_htab(f);
   for (int i = tid; i < kChunk / 4; i += kThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0, 0, 0, 0);
@@ -1684,6 +1783,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
 #pragma unroll
     for (int k = 0; k < kFastHistPer; ++k) hid[k] = static_cast<uint32_t>(ld_global(h + min(tid + k * kThreads, hl)));
   }
+
   // mx2: the largest key this thread has seen, per 16-bit half (the member search skips the
   // threads whose largest key is below the value it looks for)
   ushort2_t mx2 = ushort2_t{0, 0};
@@ -1703,9 +1803,14 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   // in flight.)
   uint32_t sl[4] = {kEmpty, kEmpty, kEmpty, kEmpty};
   uint32_t e0 = 0, nexc = 0;
-  const int rounds = (nfull + D * kThreads - 1) / (D * kThreads);  // (uniform)
+  const int rounds = SPLIT ? 1 : (nfull + D * kThreads - 1) / (D * kThreads);  // (uniform)
   uint4 kb[kKeepRounds * D];  // this thread's first blocks, kept for the member search
   auto round = [&](int it) {
+    if constexpr (SPLIT) {
+      // (the row's last slice) the other slices' records into the histogram
+      slice_merge(recs, a.G, gown, hist, f.lkey);
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < D; ++k) {
       const int b = tid + (it * D + k) * kThreads;
@@ -1719,6 +1824,13 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
       d[k] = ld_block(base, min(b + D * kThreads, nfull - 1));
     }
   };
+  if constexpr (SPLIT) {
+    // this slice's keys, its record, and its arrival: only the row's last slice goes on
+    slice_hist(base, V, a.G, gown, hist);
+    lds_barrier();
+    slice_record(hist, recs + static_cast<size_t>(gown) * kSliceRecord, f.red32);
+    if (!slice_arrive(a.arrive + r, a.epoch, a.G, &f.si[7])) return true;  // (uniform)
+  }
   if (rounds > 0) round(0);
   // The presence path's four steps follow rounds 0 .. 3, each while the next round's blocks
   // arrive: the bits and their prefix; ranks and counts; the ids in rank order; each thread's two
@@ -1813,7 +1925,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   for (int it = 5; it < rounds; ++it) round(it);
   // the rest: a ragged tail, or every element of an unaligned row
   uint32_t mxk = mx2.x > mx2.y ? mx2.x : mx2.y;
-  for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
+  for (int i = nfull * kBlk + tid; !SPLIT && i < V; i += kThreads) {  // (split rows: the last slice's)
     const uint32_t ko = ok16(base[i]);
     atomicAdd(&hist[ko >> 1], 1u << ((ko & 1u) << 4));
     mxk = ko > mxk ? ko : mxk;
@@ -1996,9 +2108,13 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     if (ne > 0) build_bitmap(row, hist + kBitmapOffset);
     // point rows: the first NaN, the first max (greedy), the first +inf z, or index 0 (all -inf)
     if (f.plan.nnan) k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
-    else if (!(T > 0.0f)) k.point = find_first(row, [&](float x, int) -> u64 { return x == xmax; }, 0ull, srch);
+    else if (!(T > 0.0f)) {
+      int pt = -1;
+      if constexpr (SPLIT) pt = split_find(a, row, f, ne, xmax, 0ull, srch, hist + kMatchOffset, recs);
+      k.point = pt >= 0 ? pt : find_first(row, [&](float x, int) -> u64 { return x == xmax; }, 0ull, srch);
+    }
     else if (!degenerate(row, p, mkey, 0, mz, srch, k)) k.point = 0;
-    finish<STATE>(a, row, p, mz, k, 0, &srch.vslot);
+    finish<STATE>(a, row, p, mz, k, 0, &srch.vslot, r);
     return true;
   }
   // ---- 5. [all] per-chunk masses of elements >= x0 ---------------------------------------
@@ -2039,7 +2155,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   }
   lds_barrier();
   uint4 first[4];
-  member_prefetch(row, first);
+  if constexpr (!SPLIT) member_prefetch(row, first);
   // ---- 6/7. [wave 0] the total, the top-p cutoff, the draw ---------------------------------
   if (tid < kWave) {
     const int l = tid;
@@ -2178,7 +2294,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   const u64 j = f.plan.j;
   // the histogram is dead: the id searches below use its memory. One pass zeroes the position
   // bitmap of the penalised ids and the member search's cells.
-  const bool cells_fit = !a.out_probs && cells_per(row) * kThreads <= 4 * kMatchWords;
+  const bool cells_fit = !SPLIT && !a.out_probs && cells_per(row) * kThreads <= 4 * kMatchWords;
   {
     uint32_t* bmw = hist + kBitmapOffset;
     const int nbw = ne > 0 ? (row.nblk + 3) / 4 : 0;
@@ -2199,11 +2315,13 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   resolve_idr<STATE>(a, row, p, k, srch);
   int draw = 0;
   if (!a.out_probs) {
-    draw = cells_fit ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb, first)
-                     : -1;
+    if constexpr (SPLIT) draw = split_find(a, row, f, ne, vd, j, srch, hist + kMatchOffset, recs);
+    else
+      draw = cells_fit ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb, first)
+                       : -1;
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
   }
-  finish<STATE>(a, row, p, mz, k, draw, &srch.vslot);
+  finish<STATE>(a, row, p, mz, k, draw, &srch.vslot, r);
   return true;
 }
 
@@ -2222,11 +2340,14 @@ __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
   a.ws = globalized(a.ws);
   a.off = as_global(a.off);
   a.pen = globalized(a.pen);
+  a.slices = as_global(a.slices);
+  a.arrive = as_global(a.arrive);
   return a;
 }
 
 // STATE: also write each row's RowState (the speculative verify's launches; never with PEN).
-template <class Tin, bool PEN, bool STATE = false>
+// SPLIT: a bf16 split-row launch (grid B * G).
+template <class Tin, bool PEN, bool STATE = false, bool SPLIT = false>
 __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   const SampleArgs a = globalized(a_);
   // 128 KB: the key histogram (or the generic path's penalty counts), then the id-search /
@@ -2235,7 +2356,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   __shared__ FastSmem f;
   static_assert(sizeof(GenericSmem) <= sizeof(uint32_t) * kBitmapOffset, "scratch must fit below the bitmap");
   static_assert(kMatchOffset + kMatchWords <= kChunk, "count cells must fit");
-  const int r = blockIdx.x;
+  const int r = SPLIT ? row_index(a) : static_cast<int>(blockIdx.x);
   const int tid = threadIdx.x;
   exp_table_init();  // (published by the first barrier of either path)
   // the row's parameters: thread w < kParamWords loads word w, the others word 0 (every thread
@@ -2255,7 +2376,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   row.eval = f.eval;
   GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
   if constexpr (sizeof(Tin) == 2) {
-    if (fast_row<PEN, STATE>(a, row, f.prm, big, f, g.srch, pw)) return;
+    if (fast_row<PEN, STATE, SPLIT>(a, row, f.prm, big, f, g.srch, pw, r)) return;
     lds_barrier();  // (every thread is done with the fast path's LDS; f.prm is set)
   } else {
     if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
@@ -2272,7 +2393,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
     row.eid = a.ws.exc_id + p.h0;
     row.eval = a.ws.exc_val + p.h0;
   }
-  generic_row<STATE>(a, row, p, g, f);
+  generic_row<STATE>(a, row, p, g, f, r);
 }
 
 }  // namespace vs

@@ -48,6 +48,9 @@ class HipSampler:
         self.ctx = ctx
         self._lib = _lib.load()
         self._workspace = torch.empty(0, dtype=torch.uint8)
+        # Split small bf16 batches' rows over several workgroups (VSAMP_SPLIT_ROWS): identical
+        # results, slower than whole rows on MI355X at every batch measured, so off by default.
+        self.split_rows = False
 
     # ---- argument checks ---------------------------------------------------------------------
     def _device(self, logits: torch.Tensor) -> torch.device:
@@ -115,14 +118,16 @@ class HipSampler:
         a.hist_ids = _ptr(hist_ids) if hist_total else None
         a.hist_offsets = _ptr(hist_offsets) if hist_total else None
         a.hist_total = hist_total
-        a.flags = flags if hist_total else 0
+        a.flags = (flags if hist_total else 0) | (_lib.VSAMP_SPLIT_ROWS if self.split_rows else 0)
         if uniforms is not None:
             uniforms = self._vec(uniforms, P, torch.float32, dev, "uniforms")
             a.uniforms = _ptr(uniforms)
         if draft_ids is not None:
             draft_ids = self._vec(draft_ids, B, torch.int32, dev, "draft_ids")
             a.draft_ids = _ptr(draft_ids)
-        need = int(self._lib.vsamp_workspace_bytes(B, V, hist_total)) if hist_total else 0
+        # (histories' penalty lists and, with split rows, the slices' records)
+        ws_bytes = self._lib.vsamp_split_workspace_bytes if self.split_rows else self._lib.vsamp_workspace_bytes
+        need = int(ws_bytes(B, V, hist_total))
         if need:
             if self._workspace.device != dev or self._workspace.numel() < need + 256:
                 self._workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
