@@ -1452,40 +1452,32 @@ __device__ __forceinline__ uint32_t wave_bisect(uint32_t lo, uint32_t hi, uint32
 // The id of the j-th (0-based, ascending id) token whose penalised value is vd: bulk positions
 // holding vd that are not penalised, and penalised ids whose new value is vd.
 // One pass writes, per 8-id block, the mask of its members into a byte cell (`cells`: cell b
-// is block b, kThreads * cells_per(row) bytes of LDS): unpenalised lanes whose bf16 value is vd
-// (penalised lanes masked out by the position bitmap), then penalised ids whose new value is
-// vd. Per-thread popcounts of consecutive cells and a scan find the block; its mask, the lane.
-// Thread t reads the blocks it read in the histogram pass (t + m * kThreads, and the tail
-// elements t + n * kThreads): the first kKeep from `keep` (registers), the rest from memory,
-// last to first (the end of the row, read last, is the part most likely still in L2); `first`
-// holds the first four of those, requested by the caller before the draw was known (see
-// member_prefetch). `mxk` is
-// the largest key the thread saw in that pass: a thread whose largest key is below vd's holds
-// no member and reads nothing. Needs row.bm built when the row has penalised ids.
+// is block b, kThreads * cells_per(row) bytes of LDS, zeroed by the caller): unpenalised lanes
+// whose bf16 value is vd (penalised lanes masked out by the position bitmap), then penalised ids
+// whose new value is vd. Per-thread popcounts of consecutive cells and a scan find the block;
+// its mask, the lane.
+// Thread t holds the low bytes of the blocks it read in the histogram pass (t + m * kThreads,
+// m < kLowBlocks: `low`, two words per block). A block whose low bytes hold none of vd's cannot
+// hold a member; the others (the members' blocks and about 1/256 of the rest per distinct value
+// of the row) are read again and matched in full, up to kProbe per thread at a time. Blocks
+// m >= kLowBlocks (V > 155,648) are read again whole. `mxk` is the largest key the thread saw in
+// the pass: a thread whose largest key is below vd's holds no member and reads nothing. Needs
+// row.bm built when the row has penalised ids.
 __device__ __forceinline__ int cells_per(const Row<uint16_t>& row) { return (row.nstripes + 3) & ~3; }
 
-// Histogram rounds (of 4 blocks per thread) whose blocks stay in registers for the member search.
-constexpr int kKeepRounds = 2;
-constexpr int kKeep = 4 * kKeepRounds;
+// Blocks per thread whose low bytes the histogram pass keeps in registers (2 words per block).
+constexpr int kLowBlocks = 19;
+constexpr int kProbe = 6;  // candidate blocks a thread reads at a time
 
-// The member search's first four reads (this thread's last four blocks beyond the kept ones,
-// clamped into the row), requested before the draw is known so that they arrive during the
-// cutoff and draw walks. Every thread requests them (no branch), used or not.
-__device__ __forceinline__ void member_prefetch(const Row<uint16_t>& row, uint4 (&first)[4]) {
-  const int tid = threadIdx.x;
-  const int nfull = row.vec ? row.V / kBlk : 0;
-  const int nm = tid < nfull ? (nfull - 1 - tid) / kThreads + 1 : 0;
-  const uint16_t* src = nfull > 0 ? row.p : g_unused_block;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    first[k] = ld_block(src, min(tid + max(nm - 1 - k, kKeep) * kThreads, max(nfull - 1, 0)));
-    __builtin_amdgcn_sched_barrier(0);  // (issued in slot order, the order they are used in)
-  }
-}
+// The low bytes of a block's eight bf16 values, elements 0-3 and 4-7 (v_perm_b32 picks bytes
+// 0 and 2 of each word).
+__device__ __forceinline__ uint32_t low4(uint32_t lo, uint32_t hi) { return __builtin_amdgcn_perm(hi, lo, 0x06040200u); }
+// Bit 7 of byte i set when byte i of w is zero (and possibly for a byte above a zero byte): not
+// 0 exactly when one of the four bytes of w is zero.
+__device__ __forceinline__ uint32_t zero_bytes(uint32_t w) { return (w - 0x01010101u) & ~w & 0x80808080u; }
 
 __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, float vd, u64 j,
-                                            uint8_t* cells, uint32_t mxk, const uint4 (&keep)[kKeep],
-                                            const uint4 (&first)[4]) {
+                                            uint8_t* cells, uint32_t mxk, const uint32_t (&low)[2 * kLowBlocks]) {
   const int tid = threadIdx.x;
   const uint32_t vb = __float_as_uint(vd);
   const bool bf = (vb & 0xFFFFu) == 0u;  // vd is a bf16 value: bulk tokens can hold it
@@ -1521,35 +1513,55 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     const int nfull = row.vec ? V / kBlk : 0;
     const uint32_t ka = ok16(t16), kb = ok16(t16b);
     const bool cand = mxk >= (ka < kb ? ka : kb);
-    // this thread's blocks tid + m * kThreads, m < nm; m >= kKeep from memory with a rolling
-    // prefetch (slot k: m = m0 - k), m < kKeep from `keep`
-    const int nm = tid < nfull ? (nfull - 1 - tid) / kThreads + 1 : 0;
-    if (cand && nm > kKeep) {
-      constexpr int D = 4;
-      static_assert(D == 4, "the first four blocks come in `first`");
-      uint4 d[D];
+    // this thread's blocks tid + m * kThreads, m < nm
+    const int nm = cand && tid < nfull ? (nfull - 1 - tid) / kThreads + 1 : 0;
+    // (the low bytes of +0.0 and -0.0 are both 0: one pattern serves both)
+    const uint32_t pat8 = (t16 & 0xFFu) * 0x01010101u;
+    uint32_t todo = 0;  // bit m: block m's low bytes hold vd's (branch-free: 8 VALU per block)
+    if (nm > 0) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) d[k] = first[k];
-      for (int m0 = nm - 1; m0 >= kKeep; m0 -= D) {
+      for (int m = 0; m < kLowBlocks; ++m) {
+        const uint32_t h = zero_bytes(low[2 * m] ^ pat8) | zero_bytes(low[2 * m + 1] ^ pat8);
+        todo |= min(h, 1u) << m;
+      }
+      todo &= nm >= 32 ? 0xFFFFFFFFu : (1u << nm) - 1u;
+    }
+    // Up to kProbe candidate blocks per round, all requested before any is matched; a wave takes
+    // as many slots as its lane with the most candidates (a lane without one rereads its first
+    // block, unused).
+    auto mark = [&](int b, uint4 w) {
+      uint32_t mask = match8(w);
+      if (row.bm) mask &= ~static_cast<uint32_t>(row.bm[b]);
+      if (mask) cells[b] = static_cast<uint8_t>(mask);  // (block b belongs to this thread alone)
+    };
+    auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+    for (int round = 0; round < 4; ++round) {  // (19 blocks: at most 4 rounds of 6)
+      const int slots = static_cast<int>(dpp::reduce(static_cast<uint32_t>(__popc(todo)), umax));  // (uniform)
+      if (slots == 0) break;
+      int mb[kProbe];
+      uint4 w[kProbe];
 #pragma unroll
-        for (int k = 0; k < D; ++k) {
-          const int m = m0 - k;
-          const int b = tid + (m < kKeep ? kKeep : m) * kThreads;
-          uint32_t mask = match8(d[k]);
-          d[k] = ld_block(base, tid + max(m - D, kKeep) * kThreads);
-          if (row.bm) mask &= ~static_cast<uint32_t>(row.bm[b]);
-          // block b is written by the one thread reading it
-          if (m >= kKeep) cells[b] = static_cast<uint8_t>(mask);
+      for (int c = 0; c < kProbe; ++c) {
+        if (c < slots) {
+          mb[c] = todo ? __ffs(todo) - 1 : -1;
+          todo &= todo - 1u;
+          w[c] = ld_block(base, mb[c] >= 0 ? tid + mb[c] * kThreads : min(tid, max(nfull - 1, 0)));
         }
       }
-    }
-    if (cand) {
 #pragma unroll
-      for (int m = 0; m < kKeep; ++m) {
-        const int b = tid + m * kThreads;
-        uint32_t mask = match8(keep[m]);
-        if (row.bm && m < nm) mask &= ~static_cast<uint32_t>(row.bm[b]);
-        if (m < nm) cells[b] = static_cast<uint8_t>(mask);
+      for (int c = 0; c < kProbe; ++c)
+        if (c < slots && mb[c] >= 0) mark(tid + mb[c] * kThreads, w[c]);
+    }
+    // blocks past the kept ones (V > 155,648), read again whole, four at a time
+    if (__ballot(nm > kLowBlocks)) {  // (uniform)
+      constexpr int D = 4;
+      for (int m0 = kLowBlocks; __ballot(m0 < nm); m0 += D) {  // (uniform over the wave)
+        uint4 q[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) q[k] = ld_block(base, min(tid + (m0 + k) * kThreads, max(nfull - 1, 0)));
+#pragma unroll
+        for (int k = 0; k < D; ++k)
+          if (m0 + k < nm) mark(tid + (m0 + k) * kThreads, q[k]);
       }
     }
     lds_barrier();  // (the byte stores above land before the word atomics below)
@@ -1804,7 +1816,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   uint32_t sl[4] = {kEmpty, kEmpty, kEmpty, kEmpty};
   uint32_t e0 = 0, nexc = 0;
   const int rounds = SPLIT ? 1 : (nfull + D * kThreads - 1) / (D * kThreads);  // (uniform)
-  uint4 kb[kKeepRounds * D];  // this thread's first blocks, kept for the member search
+  uint32_t low[2 * kLowBlocks];  // the low bytes of this thread's blocks, for the member search
   auto round = [&](int it) {
     if constexpr (SPLIT) {
       // (the row's last slice) the other slices' records into the histogram
@@ -1820,7 +1832,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
         add2(d[k].z);
         add2(d[k].w);
       }
-      if (it < kKeepRounds) kb[it * D + k] = d[k];
+      if (it * D + k < kLowBlocks) {  // (a constant test at every peeled round, false in the loop)
+        low[2 * (it * D + k)] = low4(d[k].x, d[k].y);
+        low[2 * (it * D + k) + 1] = low4(d[k].z, d[k].w);
+      }
       d[k] = ld_block(base, min(b + D * kThreads, nfull - 1));
     }
   };
@@ -1918,7 +1933,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   uint32_t og[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) og[k] = ld_global(base + (sl[k] != kEmpty ? sl[k] >> 13 : 0u));
-  static_assert(kKeepRounds <= 4, "the rounds whose blocks are kept are among the peeled ones");
+  static_assert(kLowBlocks <= 5 * D, "the blocks whose low bytes are kept are read in the peeled rounds");
   // (round 4 is peeled too: the first use of its blocks then waits for them alone, not for the
   // original values just requested, as a wait at a loop's head would)
   if (rounds > 4) round(4);
@@ -2154,8 +2169,6 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     }
   }
   lds_barrier();
-  uint4 first[4];
-  if constexpr (!SPLIT) member_prefetch(row, first);
   // ---- 6/7. [wave 0] the total, the top-p cutoff, the draw ---------------------------------
   if (tid < kWave) {
     const int l = tid;
@@ -2297,10 +2310,12 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   const bool cells_fit = !SPLIT && !a.out_probs && cells_per(row) * kThreads <= 4 * kMatchWords;
   {
     uint32_t* bmw = hist + kBitmapOffset;
-    const int nbw = ne > 0 ? (row.nblk + 3) / 4 : 0;
-    const int ncw = cells_fit ? cells_per(row) * kThreads / 4 : 0;
-    for (int i = tid; i < nbw; i += kThreads) bmw[i] = 0;
-    for (int i = tid; i < ncw; i += kThreads) hist[kMatchOffset + i] = 0;
+    // (16-byte stores: both regions start 16-byte aligned, and the bitmap's last quad stays in
+    // its region)
+    const int nbq = ne > 0 ? (row.nblk + 15) / 16 : 0;
+    const int ncq = cells_fit ? cells_per(row) * kThreads / 16 : 0;
+    for (int i = tid; i < nbq; i += kThreads) reinterpret_cast<uint4*>(bmw)[i] = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < ncq; i += kThreads) reinterpret_cast<uint4*>(hist + kMatchOffset)[i] = make_uint4(0, 0, 0, 0);
     if (tid == 0) f.si[6] = -1;
     lds_barrier();
     if (ne > 0) {
@@ -2317,7 +2332,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   if (!a.out_probs) {
     if constexpr (SPLIT) draw = split_find(a, row, f, ne, vd, j, srch, hist + kMatchOffset, recs);
     else
-      draw = cells_fit ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, kb, first)
+      draw = cells_fit ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, low)
                        : -1;
     if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
   }

@@ -115,7 +115,7 @@ struct ResidualSide {
   __device__ __forceinline__ u64 term(float x, uint32_t k, int id) const {
     const int i = static_cast<int>(k) - static_cast<int>(tlo) + 1;
     const u64 t = tab[i > 0 ? i : 0];
-    return (x == vcx) & (id > st.idr) ? 0ull : t;
+    return ((x == vcx) & (id > st.idr)) ? 0ull : t;
   }
 };
 
