@@ -205,6 +205,38 @@ int vsamp_verify(const vsamp_verify_args* args, void* stream);
 int vsamp_logprobs(const vsamp_args* args, const int32_t* tokens, int32_t n_top, float* out_token_logprob,
                    int32_t* out_top_ids, float* out_top_logprobs, void* stream);
 
+/* The LM head fused with the log-softmax's statistics. */
+#define VSAMP_LM_TILE 128 /* logits per statistics tile */
+typedef struct vsamp_lm_head_args {
+  const void* hidden; /* [batch, dim] bf16, rows 16-byte aligned */
+  int64_t hidden_stride;
+  const void* weight; /* [vocab, dim] bf16 (the LM head's weight), rows 16-byte aligned */
+  int64_t weight_stride;
+  void* logits; /* [batch, vocab] bf16, out */
+  int64_t logits_stride;
+  float* tile_max; /* [batch, ceil(vocab / VSAMP_LM_TILE)] each, out: per 128 logits of a row, */
+  float* tile_sum; /* their max and the sum of exp(x - max) */
+  int32_t batch;
+  int32_t dim; /* a multiple of 64 */
+  int32_t vocab;
+  int32_t reserved;
+} vsamp_lm_head_args;
+
+/* logits = hidden @ weight^T with bf16 operands, fp32 accumulation and the result rounded to
+ * bf16 (what `F.linear(hidden, W)` returns for bf16 tensors; replaces the engine's LM head call,
+ * models/qwen/model.py:230-233), plus the per-tile statistics vsamp_logprobs_tiles takes. One
+ * hand-written MFMA kernel; the logits then feed vsamp_sample as any bf16 logits do. */
+int vsamp_lm_head(const vsamp_lm_head_args* args, void* stream);
+
+/* vsamp_logprobs over bf16 logits that vsamp_lm_head wrote, with its tile statistics: the
+ * normaliser comes from the statistics and the top n from the few tiles whose max can hold
+ * them, instead of two passes over every row. Same outputs as vsamp_logprobs (within fp32
+ * rounding of the normaliser). No counterpart in the engine (its API layer rejects logprobs,
+ * server/protocol.py:131-132). */
+int vsamp_logprobs_tiles(const vsamp_args* args, const float* tile_max, const float* tile_sum, const int32_t* tokens,
+                         int32_t n_top, float* out_token_logprob, int32_t* out_top_ids, float* out_top_logprobs,
+                         void* stream);
+
 /* Host function (no device work): the draw's uniform of (seeds[i], positions[i]) into out[i],
  * i < n, all host memory. u = (splitmix64(position_seed(seed, position)) >> 40) * 2^-24, where
  * position_seed is the engine's per-token seed, sampler.py:44-47 (BLAKE2b-8 of

@@ -183,3 +183,34 @@ def test_verify_struct_matches_the_binding(tmp_path):
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [getattr(_lib.VsampVerifyArgs, f).offset for f in fields] + [ctypes.sizeof(_lib.VsampVerifyArgs)]
     assert got == want
+
+
+def test_lm_head_struct_matches_the_binding(tmp_path):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    fields = [f for f, _ in _lib.VsampLmHeadArgs._fields_]
+    src = tmp_path / "llayout.c"
+    lines = [f'printf("%zu\\n", offsetof(vsamp_lm_head_args, {f}));' for f in fields]
+    src.write_text(
+        "#include <stdio.h>\n#include <stddef.h>\n#include \"vsampler.h\"\nint main(void){"
+        + "".join(lines)
+        + 'printf("%zu\\n", sizeof(vsamp_lm_head_args));printf("%d\\n", VSAMP_LM_TILE);return 0;}\n'
+    )
+    exe = tmp_path / "llayout"
+    subprocess.run([gcc, f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [getattr(_lib.VsampLmHeadArgs, f).offset for f in fields] + [ctypes.sizeof(_lib.VsampLmHeadArgs), _lib.LM_TILE]
+    assert got == want
+
+
+def test_lm_head_arguments_are_checked_before_any_launch():
+    lib = _lib.load()
+    a = _lib.VsampLmHeadArgs()
+    a.batch, a.dim, a.vocab = 2, 100, 10
+    a.hidden_stride, a.weight_stride, a.logits_stride = 100, 100, 10
+    assert lib.vsamp_lm_head(ctypes.byref(a), None) == 1 and b"multiple of 64" in lib.vsamp_last_error()
+    a.dim = a.hidden_stride = a.weight_stride = 128
+    assert lib.vsamp_lm_head(ctypes.byref(a), None) == 1 and b"must be set" in lib.vsamp_last_error()
+    a.batch = 0
+    assert lib.vsamp_lm_head(ctypes.byref(a), None) == 0  # (an empty batch is a no-op)

@@ -33,6 +33,8 @@ EXPORTS = (
     "vsamp_penalized_logits",
     "vsamp_uniforms",
     "vsamp_logprobs",
+    "vsamp_logprobs_tiles",
+    "vsamp_lm_head",
     "vsamp_sample_states",
     "vsamp_verify",
     "vsamp_verify_workspace_bytes",
@@ -68,6 +70,28 @@ class VsampArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("flags", ctypes.c_uint32),
         ("reserved1", ctypes.c_uint32),
+    ]
+
+
+LM_TILE = 128  # VSAMP_LM_TILE: logits per statistics tile
+
+
+class VsampLmHeadArgs(ctypes.Structure):
+    """``vsamp_lm_head_args`` field for field."""
+
+    _fields_ = [
+        ("hidden", ctypes.c_void_p),
+        ("hidden_stride", ctypes.c_int64),
+        ("weight", ctypes.c_void_p),
+        ("weight_stride", ctypes.c_int64),
+        ("logits", ctypes.c_void_p),
+        ("logits_stride", ctypes.c_int64),
+        ("tile_max", ctypes.c_void_p),
+        ("tile_sum", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -150,6 +174,17 @@ def load() -> ctypes.CDLL:
             ctypes.c_void_p,
         ]
         lib.vsamp_logprobs.restype = ctypes.c_int
+        lib.vsamp_logprobs_tiles.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p, ctypes.c_void_p] + [
+            ctypes.c_void_p,
+            ctypes.c_int32,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+        ]
+        lib.vsamp_logprobs_tiles.restype = ctypes.c_int
+        lib.vsamp_lm_head.argtypes = [ctypes.POINTER(VsampLmHeadArgs), ctypes.c_void_p]
+        lib.vsamp_lm_head.restype = ctypes.c_int
         lib.vsamp_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
         lib.vsamp_uniforms.restype = ctypes.c_int
         lib.vsamp_last_error.restype = ctypes.c_char_p

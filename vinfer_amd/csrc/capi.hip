@@ -16,6 +16,7 @@
 #include "uniform.h"
 #include "verify.cuh"
 #include "logprobs.cuh"
+#include "lmhead.cuh"
 
 namespace {
 
@@ -560,6 +561,82 @@ int vsamp_logprobs(const vsamp_args* a, const int32_t* tokens, int32_t n_top, fl
     hipLaunchKernelGGL(vs::k_logprobs<float>, dim3(a->batch), dim3(vs::kThreads), 0, st, l);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_logprobs");
+}
+
+int vsamp_logprobs_tiles(const vsamp_args* a, const float* tile_max, const float* tile_sum, const int32_t* tokens,
+                         int32_t n_top, float* out_token_logprob, int32_t* out_top_ids, float* out_top_logprobs,
+                         void* stream) {
+  g_err.clear();
+  if (!a) return fail(VSAMP_E_ARG, "args is NULL");
+  if (a->dtype != VSAMP_BF16) return fail(VSAMP_E_DTYPE, "vsamp_logprobs_tiles takes the bf16 logits of vsamp_lm_head");
+  if (a->batch < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", a->batch);
+  if (a->vocab < 1 || a->vocab > kMaxVocab)
+    return fail(VSAMP_E_ARG, "vocab must be in [1, %lld], got %d", static_cast<long long>(kMaxVocab), a->vocab);
+  if (a->row_stride < a->vocab)
+    return fail(VSAMP_E_ARG, "row_stride (%lld) must be >= vocab (%d)", static_cast<long long>(a->row_stride),
+                a->vocab);
+  if (n_top < 0 || n_top > vs::kMaxTop) return fail(VSAMP_E_ARG, "n_top must be in [0, %d], got %d", vs::kMaxTop, n_top);
+  if ((tokens == nullptr) != (out_token_logprob == nullptr))
+    return fail(VSAMP_E_ARG, "tokens and out_token_logprob must both be set or both NULL");
+  if (n_top > 0 && (!out_top_ids || !out_top_logprobs))
+    return fail(VSAMP_E_ARG, "out_top_ids and out_top_logprobs must be set when n_top > 0");
+  if (a->batch == 0) return VSAMP_OK;
+  if (!a->logits || !tile_max || !tile_sum) return fail(VSAMP_E_ARG, "logits, tile_max and tile_sum must be set");
+  if (int rc = check_current_device()) return rc;
+  vs::LogprobArgs l;
+  l.logits = a->logits;
+  l.stride = a->row_stride;
+  l.V = a->vocab;
+  l.tokens = tokens;
+  l.n_top = n_top;
+  l.out_token = out_token_logprob;
+  l.out_top_ids = out_top_ids;
+  l.out_top = out_top_logprobs;
+  l.tmax = tile_max;
+  l.tsum = tile_sum;
+  l.nT = (a->vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
+  hipLaunchKernelGGL((vs::k_logprobs<uint16_t, true>), dim3(a->batch), dim3(vs::kThreads), 0,
+                     static_cast<hipStream_t>(stream), l);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_logprobs (tiles)");
+}
+
+int vsamp_lm_head(const vsamp_lm_head_args* a, void* stream) {
+  g_err.clear();
+  if (!a) return fail(VSAMP_E_ARG, "args is NULL");
+  if (a->batch < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", a->batch);
+  if (a->vocab < 1 || a->vocab > kMaxVocab)
+    return fail(VSAMP_E_ARG, "vocab must be in [1, %lld], got %d", static_cast<long long>(kMaxVocab), a->vocab);
+  if (a->dim < vs::kLmBK || a->dim % vs::kLmBK)
+    return fail(VSAMP_E_ARG, "dim must be a positive multiple of %d, got %d", vs::kLmBK, a->dim);
+  if (a->hidden_stride < a->dim || a->weight_stride < a->dim || a->logits_stride < a->vocab)
+    return fail(VSAMP_E_ARG, "strides must be >= dim (hidden, weight) and >= vocab (logits)");
+  if (a->batch == 0) return VSAMP_OK;
+  if (!a->hidden || !a->weight || !a->logits || !a->tile_max || !a->tile_sum)
+    return fail(VSAMP_E_ARG, "hidden, weight, logits, tile_max and tile_sum must be set");
+  if ((reinterpret_cast<uintptr_t>(a->hidden) | reinterpret_cast<uintptr_t>(a->weight)) & 15u ||
+      a->hidden_stride % 8 || a->weight_stride % 8)
+    return fail(VSAMP_E_ARG, "hidden and weight rows must be 16-byte aligned (aligned base, stride a multiple of 8)");
+  if (int rc = check_current_device()) return rc;
+  vs::LmHeadArgs l;
+  l.hidden = static_cast<const uint16_t*>(a->hidden);
+  l.ldh = a->hidden_stride;
+  l.W = static_cast<const uint16_t*>(a->weight);
+  l.ldw = a->weight_stride;
+  l.logits = static_cast<uint16_t*>(a->logits);
+  l.ldo = a->logits_stride;
+  l.tmax = a->tile_max;
+  l.tsum = a->tile_sum;
+  l.nT = (a->vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
+  l.B = a->batch;
+  l.d = a->dim;
+  l.V = a->vocab;
+  l.vec_out = !(reinterpret_cast<uintptr_t>(a->logits) & 15u) && a->logits_stride % 8 == 0;
+  static_assert(vs::kLmBN == VSAMP_LM_TILE, "the statistics' tile is the kernel's column tile");
+  const dim3 grid(l.nT, (a->batch + vs::kLmBM - 1) / vs::kLmBM);
+  hipLaunchKernelGGL(vs::k_lm_head, grid, dim3(vs::kLmThreads), 0, static_cast<hipStream_t>(stream), l);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_lm_head");
 }
 
 int vsamp_sample_states(const vsamp_args* a, void* out_states, void* stream) {

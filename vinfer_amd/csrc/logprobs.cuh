@@ -10,13 +10,23 @@
 // radix descent over that list, and the top n from it. A row whose top bins hold more than
 // kCandCap elements (massive ties) takes the n-th key over the row and its first members in
 // id order by two more passes.
+//
+// Tile mode (TILES, bf16 logits written by k_lm_head): the row's max and normaliser come from
+// the per-tile statistics (tile max and sum of exp(x - tile max) of every 128 logits:
+// S = sum_t s_t exp(m_t - M), in fp64), and the list from the tiles alone: theta, the n-th
+// largest tile max, is at most the n-th largest logit (the n largest tile maxima are n logits),
+// and every logit >= theta lies in a tile whose max is >= theta, so the elements >= theta of
+// those tiles (n of them unless tile maxima tie) hold every logit the top n can need. A row
+// with more than kTileCand such tiles takes the two passes above.
 #pragma once
 
 #include "sample.cuh"
 
 namespace vs {
 
-constexpr int kMaxTop = 32;  // most top logprobs per row
+constexpr int kMaxTop = 32;     // most top logprobs per row
+constexpr int kTileCand = 64;   // candidate tiles a tile-mode row reads (else two row passes)
+constexpr int kStatTile = 128;  // logits per statistics tile (k_lm_head's column tile)
 
 struct LogprobArgs {
   const void* logits;  // row r at logits + r * stride
@@ -27,9 +37,53 @@ struct LogprobArgs {
   float* out_token;       // [B] or null
   int32_t* out_top_ids;   // [B * n_top]
   float* out_top;         // [B * n_top]
+  const float* tmax;      // (tile mode) [B, nT] per-tile max and sum of exp(x - max)
+  const float* tsum;
+  int nT;
 };
 
-template <class Tin>
+// The key of the k-th largest (1-based, with multiplicity) of the 16-bit keys keys[0 .. nk) of
+// every thread (nk <= 4; k <= the number of keys): two rounds over the high and the low byte,
+// each a 256-bin LDS histogram that wave 0 walks from the top. `h` is 256 words, `sh` 4 words.
+__device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk, uint32_t k, uint32_t* h, uint32_t* sh) {
+  const int tid = threadIdx.x;
+  uint32_t hi = 0, above = 0;
+  for (int round = 0; round < 2; ++round) {
+    if (tid < 256) h[tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < nk && (round == 0 || (keys[i] >> 8) == hi)) atomicAdd(&h[round == 0 ? keys[i] >> 8 : keys[i] & 0xFFu], 1u);
+    }
+    __syncthreads();
+    if (tid < kWave) {
+      // lane l: bins 255 - 4l .. 252 - 4l, descending
+      uint32_t c[4], s4 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = h[255 - 4 * tid - i];
+        s4 += c[i];
+      }
+      uint32_t ex = above + wave_incl_scan<uint32_t>(s4) - s4;
+      if (ex < k && k <= ex + s4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (ex < k && k <= ex + c[i]) {
+            sh[0] = static_cast<uint32_t>(255 - 4 * tid - i);
+            sh[1] = ex;
+          }
+          ex += c[i];
+        }
+      }
+    }
+    __syncthreads();
+    if (round == 0) hi = sh[0];
+    above = sh[1];
+  }
+  return (hi << 8) | sh[0];
+}
+
+template <class Tin, bool TILES = false>
 __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
   constexpr int kBins = 8192;  // by the top 13 bits of the ordered key
   __shared__ uint32_t h13[kBins];  // (then the candidate list: kCandCap 8-byte entries)
@@ -51,6 +105,93 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
   row.eval = nullptr;
   row.nexc = 0;
   const int n = a.n_top;
+  if constexpr (TILES) exp_table_init();  // (published by the first barrier below)
+  Cand* cand = reinterpret_cast<Cand*>(h13);
+  float M = 0.0f;
+  bool finite = false;
+  double lse = 0.0;
+  bool front = true;  // (uniform) the row passes below are needed
+  if constexpr (TILES) {
+    // 1. the max and the normaliser from the tile statistics (thread t: tiles t + 1024 i)
+    const float* tm = a.tmax + static_cast<int64_t>(r) * a.nT;
+    const float* ts = a.tsum + static_cast<int64_t>(r) * a.nT;
+    float mt[4];
+    uint32_t mkt = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = tid + i * kThreads;
+      mt[i] = t < a.nT ? tm[t] : -INFINITY;
+      const uint32_t k = key_of(mt[i]);
+      mkt = k > mkt ? k : mkt;
+    }
+    mkt = static_cast<uint32_t>(block_max_u64(mkt, srch.red64));
+    M = val_of(mkt);
+    finite = mkt < key_of(INFINITY) && mkt > key_of(-INFINITY);
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = tid + i * kThreads;
+      if (finite && t < a.nT && mt[i] > -INFINITY)
+        s += static_cast<double>(ts[t]) * exp_nonpos(static_cast<double>(mt[i]) - static_cast<double>(M));
+    }
+    s = block_sum<double>(s, reinterpret_cast<double*>(srch.red64));
+    lse = static_cast<double>(M) + log(s);
+    if (n > 0) {
+      // 2. theta (16-bit key of the n-th largest tile max), the tiles whose max is >= it, and
+      // their elements >= theta into the list
+      uint32_t k16[4];
+      int nk = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        k16[i] = key_of(mt[i]) >> 16;  // (a bf16 value: the top half of its key; any NaN the largest)
+        nk += tid + i * kThreads < a.nT;
+      }
+      const uint32_t nnt = static_cast<uint32_t>(min(min(n, a.V), a.nT));
+      const uint32_t th = kth_key16(k16, nk, nnt, rdx.hcnt, sh);
+      uint32_t mine = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mine += i < nk && k16[i] >= th;
+      uint32_t ntile;
+      uint32_t at = block_excl_scan<uint32_t>(mine, rdx.hcnt, &ntile);
+      if (ntile <= static_cast<uint32_t>(kTileCand)) {  // (uniform)
+        int* ctile = reinterpret_cast<int*>(srch.tw);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (i < nk && k16[i] >= th) ctile[at++] = tid + i * kThreads;
+        if (tid == 0) sh[1] = 0;
+        __syncthreads();
+        const uint32_t thkey = key_of(val16(th));
+        // (every element's load first, then the list: kPer loads in flight per thread)
+        constexpr int kPer = kTileCand * kStatTile / kThreads;
+        float xs[kPer];
+        int ids[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int q = tid + k * kThreads;
+          ids[k] = q < static_cast<int>(ntile) * kStatTile ? ctile[q / kStatTile] * kStatTile + q % kStatTile : a.V;
+          xs[k] = load_one<Tin>(row.p, ids[k] < a.V ? ids[k] : 0);
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int id = ids[k];
+          const float x = xs[k];
+          const bool c = id < a.V && key_of(x) >= thkey;
+          const u64 bal = __ballot(c);  // (one counter update per wave round)
+          if (bal) {
+            const int leader = __ffsll(static_cast<long long>(bal)) - 1;
+            uint32_t pos = 0;
+            if (lane_id() == leader) pos = atomicAdd(&sh[1], static_cast<uint32_t>(__popcll(bal)));
+            pos = __builtin_amdgcn_readlane(pos, leader) + static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
+            if (c && pos < static_cast<uint32_t>(kCandCap)) cand[pos] = Cand{x, id};
+          }
+        }
+        front = false;
+      }
+    } else {
+      front = false;
+    }
+  }
+  if (front) {
   for (int i = tid; i < kBins; i += kThreads) h13[i] = 0;
   if (tid < 8) sh[tid] = 0;
   __syncthreads();
@@ -62,8 +203,11 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
     if (n > 0) atomicAdd(&h13[k >> 19], 1u);
   });
   mk = static_cast<uint32_t>(block_max_u64(mk, srch.red64));
-  const float M = val_of(mk);
-  const bool finite = mk < key_of(INFINITY) && mk > key_of(-INFINITY);
+  const bool tiles_lse = TILES;  // (the normaliser is the tile statistics' either way)
+  if (!tiles_lse) {
+    M = val_of(mk);
+    finite = mk < key_of(INFINITY) && mk > key_of(-INFINITY);
+  }
   // the bin of the n-th largest key (thread t sums bins 8191 - 8t .. 8184 - 8t, descending)
   uint32_t bin = 0;
   if (n > 0) {
@@ -88,10 +232,9 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
     bin = sh[0];
   }
   // 2. the sum of exponentials; the elements of the top bins to LDS
-  Cand* cand = reinterpret_cast<Cand*>(h13);
   double s = 0.0;
   for_each_ahead(row, [&](float x, int id) {
-    s += static_cast<double>(__expf(x - M));
+    if (!tiles_lse) s += static_cast<double>(__expf(x - M));
     if (n > 0) {
       const bool c = (key_of(x) >> 19) >= bin;
       const u64 bal = __ballot(c);  // (one counter update per wave round)
@@ -105,7 +248,8 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
     }
   });
   s = block_sum<double>(s, reinterpret_cast<double*>(srch.red64));
-  const double lse = static_cast<double>(M) + log(s);
+  if (!tiles_lse) lse = static_cast<double>(M) + log(s);
+  }  // (front)
   auto lp = [&](float x) -> float { return finite ? static_cast<float>(static_cast<double>(x) - lse) : NAN; };
   if (tid == 0 && a.out_token && a.tokens) {
     const int t = a.tokens[r];

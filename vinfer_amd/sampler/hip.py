@@ -220,6 +220,63 @@ class HipSampler:
         )
         return out_tok, ids, lps
 
+    def lm_head(self, hidden, weight):
+        """The LM head fused with the log-softmax statistics (``vsamp_lm_head``): bf16
+        ``logits [B, V] = hidden [B, d] @ weight [V, d]^T`` (fp32 accumulation, rounded to bf16, as
+        ``F.linear`` returns it; model.py:230-233) and, per row and 128 logits, their max and sum of
+        exp(x - max). Returns ``(logits, tile_max, tile_sum)``; the statistics feed
+        ``logprobs_tiles``."""
+        for name, t in (("hidden", hidden), ("weight", weight)):
+            if t.dtype != torch.bfloat16 or t.device.type != "cuda" or t.dim() != 2 or t.stride(1) != 1:
+                raise ValueError(f"{name} must be a bf16 2-D tensor on a GPU with unit stride along d")
+        B, d = hidden.shape
+        V, d2 = weight.shape
+        if d2 != d or weight.device != hidden.device:
+            raise ValueError(f"weight must be [V, {d}] on {hidden.device}, got {tuple(weight.shape)} on {weight.device}")
+        dev = hidden.device
+        nT = (V + _lib.LM_TILE - 1) // _lib.LM_TILE
+        logits = torch.empty(B, V, dtype=torch.bfloat16, device=dev)
+        tmax = torch.empty(B, nT, dtype=torch.float32, device=dev)
+        tsum = torch.empty(B, nT, dtype=torch.float32, device=dev)
+        a = _lib.VsampLmHeadArgs()
+        a.hidden, a.hidden_stride = hidden.data_ptr(), hidden.stride(0) if B > 1 else d
+        a.weight, a.weight_stride = weight.data_ptr(), weight.stride(0) if V > 1 else d
+        a.logits, a.logits_stride = logits.data_ptr(), V
+        a.tile_max, a.tile_sum = tmax.data_ptr(), tsum.data_ptr()
+        a.batch, a.dim, a.vocab = B, d, V
+        _lib.check(self._lib.vsamp_lm_head(ctypes.byref(a), self._stream(dev)))
+        return logits, tmax, tsum
+
+    def logprobs_tiles(self, logits, tile_max, tile_sum, tokens=None, n_top=0):
+        """``logprobs`` over the bf16 logits ``lm_head`` wrote, with its tile statistics
+        (``vsamp_logprobs_tiles``)."""
+        dev = self._device(logits)
+        if logits.dtype != torch.bfloat16:
+            raise ValueError("logprobs_tiles takes the bf16 logits of lm_head")
+        B, V = logits.shape
+        nT = (V + _lib.LM_TILE - 1) // _lib.LM_TILE
+        for name, t in (("tile_max", tile_max), ("tile_sum", tile_sum)):
+            if t.dtype != torch.float32 or t.device != dev or tuple(t.shape) != (B, nT) or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous float32 [{B}, {nT}] tensor on {dev}")
+        if not 0 <= n_top <= 32:
+            raise ValueError(f"n_top must be in [0, 32], got {n_top}")
+        a = _lib.VsampArgs()
+        a.logits = logits.data_ptr()
+        a.dtype = _DTYPES[logits.dtype]
+        a.batch, a.vocab = B, V
+        a.row_stride = logits.stride(0) if B > 1 else V
+        tok = self._vec(tokens.to(torch.int32) if tokens is not None else None, B, torch.int32, dev, "tokens")
+        out_tok = torch.empty(B, dtype=torch.float32, device=dev) if tok is not None else None
+        ids = torch.empty(B, n_top, dtype=torch.int32, device=dev)
+        lps = torch.empty(B, n_top, dtype=torch.float32, device=dev)
+        _lib.check(
+            self._lib.vsamp_logprobs_tiles(
+                ctypes.byref(a), tile_max.data_ptr(), tile_sum.data_ptr(), _ptr(tok), n_top, _ptr(out_tok),
+                ids.data_ptr() if n_top else None, lps.data_ptr() if n_top else None, self._stream(dev)
+            )
+        )
+        return out_tok, ids, lps
+
     def sample_states(self, logits, params, uniforms):
         """``sample_batch`` without histories, plus each row's sampling state (uint8 ``[B, 40]``,
         opaque) for a later ``verify`` of these rows as drafts (``draft_states``)."""
