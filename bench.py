@@ -434,6 +434,67 @@ def logprobs_bench(args) -> int:
     return 0
 
 
+def lm_head_bench(args) -> int:
+    """``--lm-head``: the LM head plus log-probabilities (token and top 20) at d=4096, V=151936,
+    B in {256, 64, 1}: unfused (torch's bf16 matmul, i.e. hipBLASLt, then ``vsamp_logprobs``'s two
+    passes over each row) against fused (``vsamp_lm_head``: the hand-written MFMA GEMM whose
+    epilogue writes the tile statistics, then ``vsamp_logprobs_tiles``). One JSON line per batch,
+    HIP events on the launch stream, synthetic bf16 operands."""
+    import math
+
+    import torch
+
+    from vinfer_amd.registry import BackendContext
+    from vinfer_amd.sampler import SAMPLER
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    s = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    d, V, n_top = 4096, 151936, 20
+    g = torch.Generator(device=dev).manual_seed(0)
+    W = (torch.randn(V, d, generator=g, device=dev) * (4 / math.sqrt(d))).to(torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+    for B in (256, 64, 1):
+        hidden = (torch.randn(B, d, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+        tokens = torch.randint(0, V, (B,), generator=g, device=dev, dtype=torch.int32)
+
+        def timed(fn, n=20):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(n):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / n
+
+        logits_t = hidden @ W.T
+        logits_f, tmax, tsum = s.lm_head(hidden, W)
+        us = {
+            "torch_matmul": timed(lambda: hidden @ W.T),
+            "logprobs_rows": timed(lambda: s.logprobs(logits_t, tokens, n_top)),
+            "lm_head_fused": timed(lambda: s.lm_head(hidden, W)),
+            "logprobs_tiles": timed(lambda: s.logprobs_tiles(logits_f, tmax, tsum, tokens, n_top)),
+        }
+        us["unfused_total"] = us["torch_matmul"] + us["logprobs_rows"]
+        us["fused_total"] = us["lm_head_fused"] + us["logprobs_tiles"]
+        same = float((logits_f == logits_t).float().mean())
+        nT = (V + 127) // 128
+        bytes_ = V * d * 2 + B * d * 2 + B * V * 2 + B * nT * 8
+        flops = 2.0 * B * d * V
+        t = us["lm_head_fused"] * 1e-6
+        print(json.dumps({"lm_head": {"batch": B, "dim": d, "vocab": V, "n_top": n_top}, "us": us,
+                          "fused_speedup": us["unfused_total"] / us["fused_total"],
+                          "k_lm_head": {"tflops": flops / t / 1e12, "mfma_frac_bf16": flops / t / 2.5e15,
+                                        "gbs": bytes_ / t / 1e9, "hbm_frac": bytes_ / t / 1e9 / HBM_PEAK_GBS,
+                                        "bytes": bytes_},
+                          "logits_equal_torch_frac": same}), flush=True)
+        del hidden, logits_t, logits_f, tmax, tsum
+    return 0
+
+
 def workloads_bench(args) -> int:
     """``--workloads``: every named sampler workload (``vinfer_amd.workloads.NAMES``), one JSON line
     each: the launch time (back-to-back launches between HIP events on the launch stream, after
@@ -541,6 +602,8 @@ def main() -> int:
     ap.add_argument("--verify", action="store_true", help="time the speculative-decoding verify instead")
     ap.add_argument("--logprobs", action="store_true", help="time the raw log-probabilities instead")
     ap.add_argument("--workloads", action="store_true", help="time every named workload (one line each)")
+    ap.add_argument("--lm-head", action="store_true",
+                    help="time the LM head + log-probabilities, fused against torch's matmul + vsamp_logprobs")
     ap.add_argument("--split-rows", action="store_true",
                     help="with --workloads: also time small bf16 batches with split rows (VSAMP_SPLIT_ROWS)")
     args = ap.parse_args()
@@ -561,6 +624,8 @@ def main() -> int:
         return logprobs_bench(args)
     if args.workloads:
         return workloads_bench(args)
+    if args.lm_head:
+        return lm_head_bench(args)
 
     import numpy as np
     import torch

@@ -633,8 +633,12 @@ int vsamp_lm_head(const vsamp_lm_head_args* a, void* stream) {
   l.V = a->vocab;
   l.vec_out = !(reinterpret_cast<uintptr_t>(a->logits) & 15u) && a->logits_stride % 8 == 0;
   static_assert(vs::kLmBN == VSAMP_LM_TILE, "the statistics' tile is the kernel's column tile");
-  const dim3 grid(l.nT, (a->batch + vs::kLmBM - 1) / vs::kLmBM);
-  hipLaunchKernelGGL(vs::k_lm_head, grid, dim3(vs::kLmThreads), 0, static_cast<hipStream_t>(stream), l);
+  // (batches of at most 64 rows: 64-row tiles, four times less MFMA work on padding)
+  if (a->batch <= 64)
+    hipLaunchKernelGGL(vs::k_lm_head<64>, dim3(l.nT, 1), dim3(vs::kLmThreads), 0, static_cast<hipStream_t>(stream), l);
+  else
+    hipLaunchKernelGGL(vs::k_lm_head<256>, dim3(l.nT, (a->batch + 255) / 256), dim3(vs::kLmThreads), 0,
+                       static_cast<hipStream_t>(stream), l);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_lm_head");
 }

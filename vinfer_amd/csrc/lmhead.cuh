@@ -5,20 +5,22 @@
 // log-softmax (k_logprobs in tile mode) takes the row's normaliser from those statistics and
 // reads only the few tiles that can hold its top n, instead of two passes over the row.
 //
-// MFMA tiling (gfx950, v_mfma_f32_32x32x16_bf16): a workgroup of 4 waves computes a 256 x 128
-// tile of the output (all rows of a batch of up to 256) over the hidden dimension in steps of
-// 64. Wave w owns rows 64w .. 64w + 63 and all 128 columns: 2 x 4 tiles of 32 x 32, 128 fp32
-// accumulators per lane. Both operands are K-contiguous, so a lane's 8 bf16 of an MFMA operand
-// (row l % 32, k 8 (l / 32) .. +7) are one 16-byte load: the hidden rows (2 MB at B = 256, read
-// by every workgroup, so they stay in L2) come straight from global memory into registers, one
-// step ahead; the weight tile, shared by the 4 waves, is staged through LDS (two buffers, rows
-// padded to 144 bytes so that each 8-lane group of a 16-byte read hits distinct banks), its
-// loads issued one step ahead. The weight is read once from HBM: 1.245 GB for V = 151936,
-// d = 4096 -- the kernel's bound at decode batches (2 B d V flops over 2 V d bytes: B flops per
-// byte, below the MFMA/HBM balance of about 312 at every B <= 256).
+// MFMA tiling (gfx950, v_mfma_f32_32x32x16_bf16): a workgroup of 8 waves computes a BM x 128
+// tile of the output (BM = 256, or 64 for batches of at most 64 rows) over the hidden dimension
+// in steps of 64. Both operands are K-contiguous rows, and both are staged through a ring of S
+// LDS stages (BM + 128 rows of 128 bytes each) by direct global-to-LDS loads
+// (global_load_lds_dwordx4: lane L of a load writes the 16 bytes at stage offset 16 L, so one
+// wave-wide load fills 8 rows): no registers hold data in flight, so S - 1 steps of both
+// operands are requested ahead (96 KB per CU for BM = 256) -- at decode batches the kernel
+// streams the 1.245 GB weight (V = 151936, d = 4096) and is bound by HBM (2 B d V flops over
+// 2 V d bytes: B flops per byte, below the MFMA/HBM balance of about 312 at every B <= 256).
+// Chunk c (16 bytes) of stage row r sits at slot c ^ (r % 8): the 8 lanes of a 16-byte LDS read
+// group (8 consecutive rows, one chunk) then hit 8 distinct 4-bank groups. Each wave owns a
+// (32 MT) x (32 NT) block of the tile: MT x NT accumulator tiles of 16 fp32 per lane; lane l's
+// MFMA operands are row l % 32, k 8 (l / 32) .. +7 of its A and B rows.
 //
-// Epilogue: the accumulators go to LDS as bf16 (a 256 x 128 tile, rows padded to 272 bytes);
-// thread t then owns row t of the tile: its max and its sum of exponentials (fp32 exp of
+// Epilogue: the accumulators go to LDS as bf16 (a BM x 128 tile, rows padded to 272 bytes);
+// thread t < BM then owns row t of the tile: its max and its sum of exponentials (fp32 exp of
 // x - max, summed in fp32); then the tile's bf16 logits are stored 16 bytes at a time.
 #pragma once
 
@@ -26,14 +28,28 @@
 
 namespace vs {
 
-constexpr int kLmBM = 256;         // rows per workgroup tile
-constexpr int kLmBN = 128;         // columns per tile (the statistics' tile)
-constexpr int kLmBK = 64;          // hidden-dimension step
-constexpr int kLmThreads = 256;    // 4 waves
-constexpr int kLmWStride = kLmBK + 8;   // LDS row stride of the weight tile (bf16)
-constexpr int kLmOStride = kLmBN + 8;   // LDS row stride of the output tile (bf16)
-constexpr int kLmWBuf = kLmBN * kLmWStride;  // bf16 per weight buffer
-constexpr int kLmLds = (2 * kLmWBuf > kLmBM * kLmOStride ? 2 * kLmWBuf : kLmBM * kLmOStride) * 2;  // bytes
+constexpr int kLmBN = 128;       // columns per tile (the statistics' tile)
+constexpr int kLmBK = 64;        // hidden-dimension step: 8 chunks of 16 bytes per row
+constexpr int kLmThreads = 512;  // 8 waves
+constexpr int kLmOStride = kLmBN + 8;  // LDS row stride of the output tile (bf16)
+
+template <int BM>
+struct LmTile;
+template <>
+struct LmTile<256> {
+  static constexpr int WM = 4, MT = 2, NT = 2, S = 3;  // waves over M; tiles per wave; stages
+};
+template <>
+struct LmTile<64> {
+  static constexpr int WM = 2, MT = 1, NT = 1, S = 5;
+};
+template <int BM>
+constexpr int lm_stage_bytes() { return (BM + kLmBN) * 128; }
+template <int BM>
+constexpr int lm_lds_bytes() {
+  return LmTile<BM>::S * lm_stage_bytes<BM>() > BM * kLmOStride * 2 ? LmTile<BM>::S * lm_stage_bytes<BM>()
+                                                                       : BM * kLmOStride * 2;
+}
 
 struct LmHeadArgs {
   const uint16_t* hidden;  // [B, d] bf16, row stride ldh (elements)
@@ -61,108 +77,119 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-// (one workgroup per CU: 4 waves, ~270 registers per lane with the accumulators and two steps
-// of operands in flight)
+// s_waitcnt with vmcnt(n) and the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// One wave-wide global_load_lds_dwordx4: lane L's 16 bytes at `src` go to LDS byte address
+// `lds` + 16 L (`lds` wave-uniform). Counted by vmcnt.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
+#if defined(__HIP_DEVICE_COMPILE__)  // (the host pass of hipcc parses device code too)
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(lds), "v"(src) : "memory", "m0");
+#endif
+}
+
+template <int BM>
 __global__ __launch_bounds__(kLmThreads, 1) void k_lm_head(LmHeadArgs a) {
-  __shared__ __align__(16) uint16_t lm_lds[kLmLds / 2];
+  using C = LmTile<BM>;
+  constexpr int S = C::S, MT = C::MT, NT = C::NT;
+  constexpr int STAGE = lm_stage_bytes<BM>();
+  constexpr int PW = (BM + kLmBN) / 64;  // wave-wide loads per wave per stage (8 rows each)
+  __shared__ __align__(16) uint8_t lds[lm_lds_bytes<BM>()];
   const int tid = threadIdx.x;
   const int l = lane_id();
   const int w = tid / kWave;
+  const int wm = w % C::WM, wn = w / C::WM;
   const int n0 = blockIdx.x * kLmBN;
-  const int m0 = blockIdx.y * kLmBM;
+  const int m0 = blockIdx.y * BM;
   const uint16_t* hid = as_global(a.hidden);
   const uint16_t* W = as_global(a.W);
-  // this lane's hidden rows (one per M tile; rows past the batch read the last row, unused)
-  const uint16_t* arow[2];
+  // this lane's sources: load j of the wave fills stage rows 8 i .. 8 i + 7 (i = w + 8 j), lane
+  // l the 16 bytes at slot l % 8 of row 8 i + l / 8, i.e. chunk (l % 8) ^ (l / 8) of that row
+  // (rows past the batch or the vocabulary read the last one, unused)
+  const uint16_t* src[PW];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int m = min(m0 + 64 * w + 32 * mt + (l & 31), a.B - 1);
-    arow[mt] = hid + static_cast<int64_t>(m) * a.ldh + 8 * (l >> 5);
+  for (int j = 0; j < PW; ++j) {
+    const int row = 8 * (w + 8 * j) + (l >> 3);
+    const int c = (l & 7) ^ (l >> 3);
+    src[j] = row < BM ? hid + static_cast<int64_t>(min(m0 + row, a.B - 1)) * a.ldh + 8 * c
+                      : W + static_cast<int64_t>(min(n0 + row - BM, a.V - 1)) * a.ldw + 8 * c;
   }
-  // the weight tile's 16-byte chunks this thread stages: chunk q = tid + 256 c -> row q / 8,
-  // part q % 8 (rows past the vocabulary read the last row, unused)
-  const uint16_t* wsrc[4];
-  int wdst[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int q = tid + kLmThreads * c;
-    const int row = q >> 3, part = q & 7;
-    wsrc[c] = W + static_cast<int64_t>(min(n0 + row, a.V - 1)) * a.ldw + 8 * part;
-    wdst[c] = row * kLmWStride + 8 * part;
-  }
-  f32x16_t acc[2][4];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x16_t{};
   const int nk = a.d / kLmBK;
-  auto load_a = [&](uint4 (&dst)[2][4], int k) {
+  // (through inline assembly: the compiler then neither sees the loads' LDS writes nor waits for
+  // them before every LDS read and barrier; the waits are the explicit ones below)
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const int wu = __builtin_amdgcn_readfirstlane(w);  // (the wave, in a scalar register: M0's operand)
+  auto issue = [&](int kt) {
+    const uint32_t stage = lds0 + static_cast<uint32_t>((kt % S) * STAGE);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) dst[mt][ks] = ld_global_u4(reinterpret_cast<const uint4*>(arow[mt] + k + 16 * ks));
+    for (int j = 0; j < PW; ++j) lds_dma16(src[j] + kt * kLmBK, stage + 1024u * (wu + 8 * j));
   };
-  auto load_w = [&](uint4 (&dst)[4], int k) {
+  f32x16_t acc[MT][NT];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) dst[c] = ld_global_u4(reinterpret_cast<const uint4*>(wsrc[c] + k));
-  };
-  auto store_w = [&](const uint4 (&src)[4], int buf) {
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) *reinterpret_cast<uint4*>(lm_lds + buf * kLmWBuf + wdst[c]) = src[c];
-  };
-  // Step kt reads weight buffer kt % 2 and the hidden operands of step kt (acur); it requests
-  // step kt + 1's hidden operands (anext) and step kt + 2's weight chunks (wnext: its LDS copy
-  // was made one step ago), and copies step kt + 1's weight chunks (wcur, requested one step
-  // ago) into the other buffer. The hidden loads go first: the wait for them at the next step
-  // then does not wait for the weight loads behind them. Past the last step the indices clamp
-  // (reloads, unused).
-  uint4 aA[2][4], aB[2][4], wA[4], wB[4];
-  load_a(aA, 0);
-  load_w(wA, 0);
-  load_w(wB, min(1, nk - 1) * kLmBK);
-  store_w(wA, 0);
-  lds_barrier();
-  auto step = [&](int kt, int buf, const uint4 (&acur)[2][4], uint4 (&anext)[2][4], const uint4 (&wcur)[4],
-                  uint4 (&wnext)[4]) {
-    load_a(anext, min(kt + 1, nk - 1) * kLmBK);
-    load_w(wnext, min(kt + 2, nk - 1) * kLmBK);
-    const uint16_t* wb = lm_lds + buf * kLmWBuf;
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x16_t{};
+  // (a uniform number of steps in flight; the waits below take the count of loads issued after
+  // the step they wait for)
+#pragma unroll
+  for (int s0 = 0; s0 < S - 1; ++s0)
+    if (s0 < nk) issue(s0);
+  const int ra0 = 32 * MT * wm + (l & 31);        // this lane's A row in its first tile
+  const int rb0 = 32 * NT * wn + (l & 31);        // and its weight row
+  for (int kt = 0; kt < nk; ++kt) {
+    // step kt's loads are done when at most min(S - 2, nk - 1 - kt) steps' loads are in flight
+    const int ahead = min(S - 2, nk - 1 - kt);  // (uniform)
+    if (ahead >= 3) wait_vm<3 * PW>();
+    else if (ahead == 2) wait_vm<2 * PW>();
+    else if (ahead == 1) wait_vm<PW>();
+    else wait_vm<0>();
+    lds_barrier();  // (every wave's loads of step kt are in; every wave is done with step kt - 1)
+    if (kt + S - 1 < nk) issue(kt + S - 1);  // (into step kt - 1's stage)
+    const uint8_t* stage = lds + (kt % S) * STAGE;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      bf16x8_t b[4];
+      const int c = 2 * ks + (l >> 5);
+      bf16x8_t av[MT], bv[NT];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        b[nt] = as_bf16x8(*reinterpret_cast<const uint4*>(wb + (32 * nt + (l & 31)) * kLmWStride + 16 * ks + 8 * (l >> 5)));
+      for (int mt = 0; mt < MT; ++mt) {
+        const int r = ra0 + 32 * mt;
+        av[mt] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + r * 128 + 16 * (c ^ (r & 7))));
+      }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int nt = 0; nt < NT; ++nt) {
+        const int r = BM + rb0 + 32 * nt;
+        bv[nt] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + r * 128 + 16 * (c ^ (r & 7))));
+      }
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(acur[mt][ks]), b[nt], acc[mt][nt], 0, 0, 0);
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
     }
-    store_w(wcur, buf ^ 1);  // (every wave finished reading that buffer one step ago)
-    lds_barrier();
-  };
-  for (int kt = 0; kt < nk; kt += 2) {
-    step(kt, 0, aA, aB, wB, wA);
-    if (kt + 1 < nk) step(kt + 1, 1, aB, aA, wA, wB);  // (uniform)
   }
+  lds_barrier();  // (every wave is done with the stages: the output tile goes over them)
   // ---- epilogue: the tile as bf16 in LDS (lane l, accumulator j of tile (mt, nt): row
-  // 64w + 32mt + 8(j / 4) + 4(l / 32) + j % 4, column 32nt + l % 32)
-  uint16_t* ot = lm_lds;
+  // 32 MT wm + 32 mt + 8 (j / 4) + 4 (l / 32) + j % 4, column 32 NT wn + 32 nt + l % 32)
+  uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int row = 64 * w + 32 * mt + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-        ot[row * kLmOStride + 32 * nt + (l & 31)] = static_cast<uint16_t>(bf16_rne(acc[mt][nt][j]));
+        const int row = 32 * MT * wm + 32 * mt + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
+        ot[row * kLmOStride + 32 * NT * wn + 32 * nt + (l & 31)] = static_cast<uint16_t>(bf16_rne(acc[mt][nt][j]));
       }
   lds_barrier();
-  // thread t: row t of the tile -- its max and sum of exponentials over the columns inside the
-  // vocabulary
+  // thread t < BM: row t of the tile -- its max and sum of exponentials over the columns inside
+  // the vocabulary
   const int ncol = min(kLmBN, a.V - n0);
-  {
+  if (tid < BM) {
     const int m = m0 + tid;
     uint4 v[kLmBN / 8];
 #pragma unroll
@@ -201,17 +228,17 @@ __global__ __launch_bounds__(kLmThreads, 1) void k_lm_head(LmHeadArgs a) {
   // the logits: 16 chunks of 16 bytes per row (q -> row q / 16, part q % 16); rows that are not
   // 16-byte aligned, and a chunk that crosses the end of the vocabulary, element by element
   uint16_t* out = as_global(a.logits);
-  for (int q = tid; q < kLmBM * (kLmBN / 8); q += kLmThreads) {
+  for (int q = tid; q < BM * (kLmBN / 8); q += kLmThreads) {
     const int row = q >> 4, part = q & 15;
     const int m = m0 + row;
     const int c0 = 8 * part;
     if (m >= a.B || c0 >= ncol) continue;
     uint16_t* dst = out + static_cast<int64_t>(m) * a.ldo + n0 + c0;
-    const uint16_t* src = ot + row * kLmOStride + c0;
+    const uint16_t* srcp = ot + row * kLmOStride + c0;
     if (a.vec_out && c0 + 8 <= ncol) {
-      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(srcp);
     } else {
-      for (int i = 0; i < min(8, ncol - c0); ++i) dst[i] = src[i];
+      for (int i = 0; i < min(8, ncol - c0); ++i) dst[i] = srcp[i];
     }
   }
 }
