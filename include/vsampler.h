@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 4
+#define VSAMP_ABI_VERSION 5
 
 /* Bytes of one row's sampling state (vsamp_sample_states), an opaque record. */
 #define VSAMP_ROW_STATE_BYTES 40

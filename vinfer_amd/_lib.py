@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 ROW_STATE_BYTES = 40
 
 VSAMP_BF16 = 0
