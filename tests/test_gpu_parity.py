@@ -450,6 +450,37 @@ def test_per_token_call_matches_the_batch():
     assert s.sample(torch.tensor([0.1, 3.0, -2.0], device=DEV), SamplingParams(temperature=0), 0, 0) == 1
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_per_token_call_matches_the_oracle(dtype):
+    # the engine's unchanged call (generate.py:129) at the model's vocabulary, one row per call,
+    # with penalties over a history passed as a list and as a device tensor, against the oracle
+    from oracle.sampler_oracle import sample_batch as oracle_batch
+
+    s = hip(dtype)
+    g = torch.Generator().manual_seed(5)
+    V = 151936
+    x = (torch.randn(V, generator=g) * 2).to(dtype)
+    row = x.to(DEV)
+    xs = x.float().numpy()
+    cases = [
+        (SamplingParams(temperature=0.7, top_k=20, top_p=0.8), []),
+        (SamplingParams(temperature=1.0, top_p=0.95, min_p=0.05, repetition_penalty=1.05, presence_penalty=0.5,
+                        frequency_penalty=0.2), list(range(0, 3000, 7)) + [5, 5, 5, V + 3, -1]),
+        (SamplingParams(temperature=0.0, repetition_penalty=1.3), [int(np.argmax(xs))]),
+    ]
+    print(f"per-token call V={V} {dtype}", flush=True)
+    for ci, (sp, hist) in enumerate(cases):
+        for pos in range(6):
+            h = torch.tensor(hist, dtype=torch.int32, device=DEV) if pos % 2 else hist
+            tok = s.sample(row, sp, 11 + ci, pos, history=h if sp.penalized else None)
+            hi = np.asarray(hist, dtype=np.int32)
+            res = oracle_batch(xs[None], [sp.temperature], [sp.top_k], [sp.top_p], [sp.min_p],
+                               [sp.repetition_penalty], [sp.presence_penalty], [sp.frequency_penalty],
+                               hi, np.array([0, len(hi)], np.int32), [uniform(11 + ci, pos)])[0]
+            if not classify_ties(res):
+                assert tok == res.token, (ci, pos, tok, res.token)
+
+
 def test_deterministic_and_stream_safe():
     w = workloads.make("mixed_bf16", batch=32).to(DEV)
     s = hip()

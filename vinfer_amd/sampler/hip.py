@@ -15,6 +15,7 @@ from __future__ import annotations
 import ctypes
 from collections.abc import Sequence
 
+import numpy as np
 import torch
 
 from vinfer_amd import _lib
@@ -48,6 +49,7 @@ class HipSampler:
         self.ctx = ctx
         self._lib = _lib.load()
         self._workspace = torch.empty(0, dtype=torch.uint8)
+        self._tokens: dict[torch.device, _TokenPath] = {}  # the per-token call's buffers
         # Split small bf16 batches' rows over several workgroups (VSAMP_SPLIT_ROWS): identical
         # results, slower than whole rows on MI355X at every batch measured, so off by default.
         self.split_rows = False
@@ -345,15 +347,81 @@ class HipSampler:
         history: Sequence[int] | torch.Tensor | None = None,
     ) -> int:
         require_history(params, history)
-        dev = logits.device
-        packed = pack_params([params], dev)
-        u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)
-        hist_ids = hist_offsets = None
-        if params.penalized and len(history) > 0:
-            hist_ids = torch.as_tensor(history, dtype=torch.int32).to(dev)
-            hist_offsets = torch.tensor([0, hist_ids.shape[0]], dtype=torch.int32, device=dev)
-        ids, _ = self.sample_batch(logits.reshape(1, -1), packed, u, hist_ids, hist_offsets)
-        return int(ids[0])
+        if logits.dim() != 1 and not (logits.dim() == 2 and logits.shape[0] == 1):
+            raise ValueError(f"sample takes one row of logits ([V] or [1, V]), got {tuple(logits.shape)}")
+        row = logits.reshape(-1)
+        if row.stride(0) != 1:
+            raise ValueError("logits must have unit stride")
+        dev = self._device(row.reshape(1, -1))
+        V = row.shape[0]
+        t = self._token_path(dev)
+        # the row's parameters, its uniform and its history's range: one pinned block, one copy
+        f = t.words.view(np.float32)
+        f[0], f[1], f[2] = params.temperature, params.top_p, params.min_p
+        f[3], f[4], f[5] = params.repetition_penalty, params.presence_penalty, params.frequency_penalty
+        t.words[6] = params.top_k
+        f[7] = uniform(seed, position)
+        n = len(history) if params.penalized else 0
+        a = t.args
+        a.logits, a.dtype, a.vocab, a.row_stride = row.data_ptr(), _DTYPES[row.dtype], V, V
+        a.hist_ids = a.hist_offsets = a.workspace = None
+        a.hist_total = a.workspace_bytes = 0
+        if n > 0:
+            if t.hist_host.shape[0] < n:
+                cap = max(n, 2 * t.hist_host.shape[0])
+                t.hist_host = torch.empty(cap, dtype=torch.int32, pin_memory=True)
+                t.hist_dev = torch.empty(cap, dtype=torch.int32, device=dev)
+            if isinstance(history, torch.Tensor) and history.device.type != "cpu":
+                t.hist_dev[:n].copy_(history.reshape(-1).to(torch.int32))
+            else:
+                t.hist_host.numpy()[:n] = np.asarray(history, dtype=np.int32).reshape(-1)
+                t.hist_dev[:n].copy_(t.hist_host[:n], non_blocking=True)
+            t.words[8], t.words[9] = 0, n
+            need = int(self._lib.vsamp_workspace_bytes(1, V, n))
+            if self._workspace.device != dev or self._workspace.numel() < need + 256:
+                self._workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+            a.hist_ids, a.hist_offsets, a.hist_total = t.hist_dev.data_ptr(), t.base + 32, n
+            a.workspace, a.workspace_bytes = (self._workspace.data_ptr() + 255) & ~255, need
+        t.block.copy_(t.words_t, non_blocking=True)
+        stream = torch.cuda.current_stream(dev)
+        _lib.check(self._lib.vsamp_sample(t.ref, ctypes.c_void_p(stream.cuda_stream)))
+        t.out.copy_(t.ids, non_blocking=True)
+        stream.synchronize()
+        return int(t.out_np[0])
+
+    def _token_path(self, dev: torch.device) -> "_TokenPath":
+        t = self._tokens.get(dev)
+        if t is None:
+            t = self._tokens[dev] = _TokenPath(dev)
+        return t
+
+
+class _TokenPath:
+    """The per-token call's buffers on one device, reused call after call: a pinned block of
+    the row's parameter words (temperature, top_p, min_p, the three penalties, top_k, the
+    uniform, the history's [0, n) range) with its device copy, pinned history staging, and the
+    drawn id's device and pinned slots. The call synchronises its stream before returning, so
+    a block is never rewritten while a copy from it is in flight (one caller thread per device,
+    as the engine's generation worker is)."""
+
+    def __init__(self, dev: torch.device) -> None:
+        self.words_t = torch.zeros(16, dtype=torch.int32, pin_memory=True)
+        self.words = self.words_t.numpy()
+        self.block = torch.zeros(16, dtype=torch.int32, device=dev)
+        self.base = self.block.data_ptr()
+        self.hist_host = torch.empty(0, dtype=torch.int32, pin_memory=True)
+        self.hist_dev = torch.empty(0, dtype=torch.int32, device=dev)
+        self.ids = torch.empty(1, dtype=torch.int32, device=dev)
+        self.out = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        self.out_np = self.out.numpy()
+        a = _lib.VsampArgs()
+        a.batch = 1
+        for i, name in enumerate(("temperature", "top_p", "min_p", "repetition_penalty", "presence_penalty",
+                                  "frequency_penalty", "top_k", "uniforms")):
+            setattr(a, name, self.base + 4 * i)
+        a.out_ids = self.ids.data_ptr()
+        self.args = a
+        self.ref = ctypes.byref(a)
 
 
 class PreparedStep:
