@@ -422,6 +422,33 @@ def test_temperature_division_merges_adjacent_fp32_values():
         assert ((pr[b] > 0) == r.kept).all(), b
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+def test_small_top_k_lists_with_tied_values(dtype):
+    # top-k candidate lists of at most 256 elements are sorted once and read by index (the K-th
+    # value, the top-p cutoff group, the draw): rows of values on a 0.25 grid give groups of
+    # equal values at the K-th value and at a cutoff that splits them, drafts sit inside those
+    # groups, and the same rows' probabilities check the kept sets
+    rng = np.random.default_rng(21)
+    B, V = 96, 3000
+    x = np.round(rng.normal(0, 2, (B, V)) * 4).astype(np.float32) / 4
+    params = pack_params([
+        SamplingParams(temperature=float(rng.choice([0.5, 1.0, 2.0])), top_k=int(rng.choice([1, 3, 10, 50, 200])),
+                       top_p=float(rng.choice([1.0, 0.3, 0.6, 0.9])), min_p=float(rng.choice([0.0, 0.0, 0.05, 0.2])))
+        for _ in range(B)])
+    order = np.argsort(-x, axis=1, kind="stable")
+    draft = torch.from_numpy(order[np.arange(B), rng.integers(0, 40, B)].astype(np.int32))
+    w = Workload("sorted", torch.from_numpy(x).to(dtype), params, torch.from_numpy(rng.random(B, dtype=np.float32)),
+                 None, None, draft)
+    check(w, max_tie_frac=0.1)
+    d = w.to(DEV)
+    pr = hip(dtype).probs(d.logits, d.params).cpu().double().numpy()
+    for b, r in enumerate(oracle(w, want_probs=True)):
+        if classify_ties(r):
+            continue
+        assert ((pr[b] > 0) == r.kept).all(), b
+        np.testing.assert_allclose(pr[b], r.probs, rtol=PROB_RTOL, atol=1e-30)
+
+
 def test_draw_frequencies_match_the_distribution():
     # 20,000 draws of one row with the package's uniforms: TV < 0.015 (test_sampler.py:24-38)
     logits = torch.tensor([2.0, 1.0, 0.5, 0.0, -1.0, -3.0])

@@ -59,6 +59,27 @@ __device__ __forceinline__ PenaltyArgs globalized(PenaltyArgs a) {
   return a;
 }
 
+// f(src[i], i) for every i in [0, n) of this thread (i = tid + j * kThreads), eight loads in
+// flight at a time: a loop that uses each load as it is issued waits a memory round trip per
+// iteration (16 of them for a history of 16K ids). Every load is issued, clamped into [0, n).
+// GLOBAL: src is global memory (global loads); otherwise it may be LDS too (flat loads).
+template <bool GLOBAL = true, class F>
+__device__ __forceinline__ void for_each_id(const int32_t* src, int n, F f) {
+  constexpr int kU = 8;
+  for (int i0 = threadIdx.x; i0 < n; i0 += kU * kThreads) {
+    int v[kU];
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+      const int32_t* q = src + min(i0 + k * kThreads, n - 1);
+      if constexpr (GLOBAL) v[k] = ld_global(q);
+      else v[k] = *q;
+    }
+#pragma unroll
+    for (int k = 0; k < kU; ++k)
+      if (i0 + k * kThreads < n) f(v[k], i0 + k * kThreads);
+  }
+}
+
 __device__ __forceinline__ float apply_penalty(float x, int c, float rep, float pres, float freq) {
   // Compiled with -ffp-contract=off: every operation below rounds on its own.
   x = (x > 0.0f) ? x / rep : x * rep;
@@ -98,29 +119,21 @@ constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 constexpr int kCountWords = 16384;
 constexpr int kHistCache = kChunk - kCountWords - 1024;
 
-// The penalised values of exceptions [0, n) whose (id, count) pairs are in the workspace, or for
-// e < staged in LDS: all loads of a thread are issued before any value is computed.
-template <class Tin>
-__device__ __forceinline__ void gather_values(const PenaltyArgs& a, const Tin* row, int h0, uint32_t n, const int2* stage,
-                              uint32_t staged, float rep, float pres, float freq, const ExcCache& ec) {
-  constexpr int kU = 4;
+// The penalised values of exceptions [0, n), whose (id, count) pairs pair(e) gives (from LDS or
+// the workspace): all loads of a thread are issued before any value is computed.
+template <class Tin, class P>
+__device__ __forceinline__ void gather_values(const PenaltyArgs& a, const Tin* row, int h0, uint32_t n, P pair,
+                                              float rep, float pres, float freq, const ExcCache& ec) {
+  constexpr int kU = 8;
   for (uint32_t e0 = threadIdx.x; e0 < n; e0 += kU * kThreads) {
     int id[kU], c[kU];
     float x[kU];
 #pragma unroll
     for (int k = 0; k < kU; ++k) {
       const uint32_t e = e0 + k * kThreads;
-      id[k] = 0;
-      c[k] = 0;
-      if (e < n) {
-        if (e < staged) {
-          id[k] = stage[e].x;
-          c[k] = stage[e].y;
-        } else {
-          id[k] = a.ws.exc_id[h0 + e];
-          c[k] = a.ws.exc_cnt[h0 + e];
-        }
-      }
+      const int2 q = e < n ? pair(e) : make_int2(0, 0);
+      id[k] = q.x;
+      c[k] = q.y;
     }
 #pragma unroll
     for (int k = 0; k < kU; ++k) x[k] = e0 + k * kThreads < n ? load_one<Tin>(row, id[k]) : 0.0f;
@@ -138,31 +151,32 @@ __device__ __forceinline__ void gather_values(const PenaltyArgs& a, const Tin* r
   }
 }
 
-// Long histories (more than kHashMaxL ids, at most 65535) over a vocabulary of at most kBmMaxV
-// ids: a presence bitmap of the vocabulary (one non-returning atomic per history id), the
-// exclusive prefix of its 64-bit words' popcounts, then u16 counts indexed by the rank of an id
-// among the distinct ids (prefix + popcount below it; a second pass over the history). Thread t
-// owns bitmap words kBmPer * t .. + kBmPer - 1 and writes their ids' (id, count) pairs in rank
-// order. Returns false (having written nothing) when the distinct ids do not fit: the caller
-// then counts in windows.
+// Histories of at most 65535 ids over a vocabulary of at most kBmMaxV ids: a presence bitmap of
+// the vocabulary (one non-returning atomic per history id), the exclusive prefix of its 64-bit
+// words' popcounts, then u16 counts indexed by the rank of an id among the distinct ids (prefix +
+// popcount below it; a second pass over the history). Thread t owns bitmap words kBmPer * t ..
+// + kBmPer - 1 and stages their ids in rank order in LDS, from where the workgroup writes the
+// (id, count) pairs coalesced (each thread straight to the workspace when they do not fit).
+// Returns false (having written nothing) when the distinct ids do not fit: the caller then counts
+// in windows.
 constexpr int kBmPer = 4;                       // 64-bit bitmap words per thread
 constexpr int kBmMaxV = 64 * kBmPer * kThreads;  // 262144
 template <class Tin>
-__device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, int r, uint32_t* lds, uint32_t* red, ExcCache ec,
-                                             int h0, int L, int V, bool on, int32_t* dc, float rep, float pres,
-                                             float freq, const Tin* row, const int32_t* hist, uint32_t* n_out) {
+__device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, uint32_t* words, uint32_t* red, ExcCache ec, int h0,
+                                             int L, int V, bool on, int32_t* dc, float rep, float pres, float freq,
+                                             const Tin* row, const int32_t* hist, uint32_t* n_out) {
   const int tid = threadIdx.x;
   const int nw = (V + 63) / 64;  // 64-bit bitmap words
-  u64* bm = reinterpret_cast<u64*>(lds);
-  uint16_t* pre = reinterpret_cast<uint16_t*>(lds + 2 * nw);  // u16 prefix per word
-  uint32_t* cnt = lds + 2 * nw + (nw + 1) / 2;                 // u16 counts by rank, in pairs
-  const int cap = 2 * (kChunk - (2 * nw + (nw + 1) / 2));       // ranks that fit
-  for (int i = tid; i < 2 * nw; i += kThreads) lds[i] = 0;
+  u64* bm = reinterpret_cast<u64*>(words);
+  const int head = 2 * nw + (nw + 1) / 2;
+  uint16_t* pre = reinterpret_cast<uint16_t*>(words + 2 * nw);  // u16 prefix per word
+  uint32_t* cnt = words + head;                                  // u16 counts by rank, in pairs
+  const int cap = 2 * (kChunk - head);                           // ranks that fit
+  for (int i = tid; i < 2 * nw; i += kThreads) words[i] = 0;
   lds_barrier();
-  for (int i = tid; i < L; i += kThreads) {
-    const int id = hist[i];
-    if (id >= 0 && id < V) atomicOr(&lds[id >> 5], 1u << (id & 31));
-  }
+  for_each_id(hist, L, [&](int id, int) {
+    if (id >= 0 && id < V) atomicOr(&words[id >> 5], 1u << (id & 31));
+  });
   lds_barrier();
   u64 w[kBmPer];
   uint32_t n = 0;
@@ -188,32 +202,58 @@ __device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, int r, uint32
   }
   for (int i = tid; i < static_cast<int>((total + 1) / 2); i += kThreads) cnt[i] = 0;
   lds_barrier();
-  for (int i = tid; i < L; i += kThreads) {
-    const int id = hist[i];
-    if (id < 0 || id >= V) continue;
+  for_each_id(hist, L, [&](int id, int) {
+    if (id < 0 || id >= V) return;
     const int wi = id >> 6;
     const uint32_t rank = pre[wi] + static_cast<uint32_t>(__popcll(bm[wi] & ((1ull << (id & 63)) - 1ull)));
     atomicAdd(&cnt[rank >> 1], 1u << ((rank & 1u) << 4));
-  }
+  });
   lds_barrier();
+  auto count_of = [&](uint32_t e) -> int { return static_cast<int>((cnt[e >> 1] >> ((e & 1u) << 4)) & 0xFFFFu); };
   // (id, count) pairs in rank order
+  int32_t* rid = reinterpret_cast<int32_t*>(cnt + (total + 1) / 2);
+  const uint32_t room = static_cast<uint32_t>(kChunk - head - static_cast<int>((total + 1) / 2));
+  if (total <= room) {  // (uniform)
 #pragma unroll
-  for (int k = 0; k < kBmPer; ++k) {
-    uint32_t e = pw[k];
-    for (u64 m = w[k]; m; m &= m - 1) {
-      const int id = 64 * (kBmPer * tid + k) + static_cast<int>(__builtin_ctzll(m));
-      const int c = static_cast<int>((cnt[e >> 1] >> ((e & 1u) << 4)) & 0xFFFFu);
+    for (int k = 0; k < kBmPer; ++k) {
+      uint32_t e = pw[k];
+      for (u64 m = w[k]; m; m &= m - 1) rid[e++] = 64 * (kBmPer * tid + k) + static_cast<int>(__builtin_ctzll(m));
+    }
+    lds_barrier();
+    for (uint32_t e = tid; e < total; e += kThreads) {
+      const int id = rid[e];
+      const int c = count_of(e);
       if (dc) dc[id] = c;
       if (on) {
         a.ws.exc_id[h0 + e] = id;
         a.ws.exc_cnt[h0 + e] = c;
       }
-      ++e;
     }
+    if (on)
+      gather_values<Tin>(a, row, h0, total, [&](uint32_t e) { return make_int2(rid[e], count_of(e)); }, rep, pres,
+                         freq, ec);
+  } else {
+#pragma unroll
+    for (int k = 0; k < kBmPer; ++k) {
+      uint32_t e = pw[k];
+      for (u64 m = w[k]; m; m &= m - 1) {
+        const int id = 64 * (kBmPer * tid + k) + static_cast<int>(__builtin_ctzll(m));
+        const int c = count_of(e);
+        if (dc) dc[id] = c;
+        if (on) {
+          a.ws.exc_id[h0 + e] = id;
+          a.ws.exc_cnt[h0 + e] = c;
+        }
+        ++e;
+      }
+    }
+    // the (id, count) pairs were written by other threads of this workgroup: full barrier
+    __syncthreads();
+    if (on)
+      gather_values<Tin>(a, row, h0, total,
+                         [&](uint32_t e) { return make_int2(a.ws.exc_id[h0 + e], a.ws.exc_cnt[h0 + e]); }, rep, pres,
+                         freq, ec);
   }
-  // the (id, count) pairs were written by other threads of this workgroup: full barrier
-  __syncthreads();
-  if (on) gather_values<Tin>(a, row, h0, total, nullptr, 0, rep, pres, freq, ec);
   *n_out = total;
   return true;
 }
@@ -255,9 +295,8 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
       cnts[i] = 0;
     }
     lds_barrier();
-    for (int i = tid; i < L; i += kThreads) {
-      const int id = hist[i];
-      if (id < 0 || id >= V) continue;
+    for_each_id(hist, L, [&](int id, int) {
+      if (id < 0 || id >= V) return;
       uint32_t h = (static_cast<uint32_t>(id) * 2654435761u) >> (32 - 14);  // Fibonacci hashing
       while (true) {
         const uint32_t prev = atomicCAS(&keys[h], kEmpty, static_cast<uint32_t>(id));
@@ -267,7 +306,7 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
         }
         h = (h + 1) & (kHashSlots - 1);
       }
-    }
+    });
     lds_barrier();
     // compaction: thread t owns slots 16t .. 16t + 15
     constexpr int kPer = kHashSlots / kThreads;
@@ -296,8 +335,9 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
       ++e;
     }
     lds_barrier();
-    if (on) gather_values<Tin>(a, row, h0, n_total, stage, n_total, rep, pres, freq, ec);
-  } else if (V <= kBmMaxV && L <= 0xFFFF && bitmap_count<Tin>(a, r, lds, red, ec, h0, L, V, on, dc, rep, pres, freq,
+    if (on)
+      gather_values<Tin>(a, row, h0, n_total, [&](uint32_t e) { return stage[e]; }, rep, pres, freq, ec);
+  } else if (V <= kBmMaxV && L <= 0xFFFF && bitmap_count<Tin>(a, lds, red, ec, h0, L, V, on, dc, rep, pres, freq,
                                                                 row, hist, &n_total)) {
     // (counted through a presence bitmap: two passes over the history)
   } else {
@@ -309,7 +349,7 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
     const bool wide = L > 0xFFFF;  // u16 counters hold any count of a shorter history
     const int window = wide ? kCountWords : 2 * kCountWords;
     const int nwin_words = window / 32;
-    for (int i = tid; i < Lc; i += kThreads) cache[i] = hist[i];
+    for_each_id(hist, Lc, [&](int id, int i) { cache[i] = id; });
     for (int i = tid; i < kCountWords; i += kThreads) cnt[i] = 0;
     for (int i = tid; i < 1024; i += kThreads) present[i] = 0;
     lds_barrier();
@@ -365,7 +405,10 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
     }
     // the (id, count) pairs were written by other threads of this workgroup: full barrier
     __syncthreads();
-    if (on) gather_values<Tin>(a, row, h0, n_total, nullptr, 0, rep, pres, freq, ec);
+    if (on)
+      gather_values<Tin>(a, row, h0, n_total,
+                         [&](uint32_t e) { return make_int2(a.ws.exc_id[h0 + e], a.ws.exc_cnt[h0 + e]); }, rep, pres,
+                         freq, ec);
   }
   if (tid == 0) a.ws.n_exc[r] = on ? n_total : 0u;
   lds_barrier();

@@ -444,10 +444,11 @@ __device__ __forceinline__ void build_bitmap(Row<Tin>& row, uint32_t* words) {
   const int nw = (row.nblk + 3) / 4;
   for (int i = threadIdx.x; i < nw; i += kThreads) words[i] = 0;
   lds_barrier();
-  for (int e = threadIdx.x; e < row.nexc; e += kThreads) {
-    const uint32_t id = static_cast<uint32_t>(row.eid[e]);
+  // (row.eid: the workspace on the generic path, LDS on the fast path)
+  for_each_id<false>(row.eid, row.nexc, [&](int v, int) {
+    const uint32_t id = static_cast<uint32_t>(v);
     atomicOr(&words[id >> 5], 1u << (id & 31u));
-  }
+  });
   lds_barrier();
   row.bm = reinterpret_cast<const uint8_t*>(words);
 }
@@ -492,13 +493,23 @@ __device__ __forceinline__ void hist_mass(uint32_t* hc, u64* hm, uint32_t digit,
   }
 }
 
-// Smallest key K in [lo, hi] with pred(val_of(K)); pred(val_of(hi)) must hold.
+// Smallest key K in [lo, hi] with pred(val_of(K)); pred(val_of(hi)) must hold and pred must be
+// monotone over the keys of [lo, hi]. One wave searches (every lane calls, every lane gets the
+// key): each round tests 64 keys spread over [lo, hi] and keeps the span between the last
+// failing and the first passing one, so a 32-bit range takes 6 rounds where a bisection takes 32
+// serial steps.
 template <class P>
-__device__ uint32_t bisect_key(uint32_t lo, uint32_t hi, P pred) {
-  while (lo < hi) {
-    const uint32_t mid = lo + ((hi - lo) >> 1);
-    if (pred(val_of(mid))) hi = mid;
-    else lo = mid + 1;
+__device__ __forceinline__ uint32_t bisect_key_wave(uint32_t lo, uint32_t hi, P pred) {
+  const u64 l1 = static_cast<u64>(lane_id()) + 1u;
+  while (lo < hi) {  // (uniform)
+    const u64 span = hi - lo;
+    const uint32_t probe = lo + static_cast<uint32_t>((span * l1) >> 6);  // lane 63 probes hi
+    const u64 ok = __ballot(pred(val_of(probe)));
+    const int f = __ffsll(static_cast<long long>(ok)) - 1;  // (lane 63's probe always passes)
+    const uint32_t hi2 = __builtin_amdgcn_readlane(probe, f);
+    const uint32_t below = __builtin_amdgcn_readlane(probe, f > 0 ? f - 1 : 0);
+    lo = f > 0 ? below + 1u : lo;
+    hi = hi2;
   }
   return hi;
 }
@@ -982,6 +993,195 @@ __device__ __forceinline__ int chunk_pick(const u64* cm, int mode, double target
   return 16 * L + q;
 }
 
+// ---- generic path: small top-k lists, sorted ---------------------------------------------------
+// A top-k candidate list of at most kSortCap elements is sorted once, by descending value and
+// then ascending id (the draw's order), and the rest of the row's work reads it by index: the
+// K-th largest is entry K - 1, and wave 0 alone finds the top-p cutoff group and the drawn
+// element from the exclusive prefix of the masses, with the comparisons the radix descents make
+// on their digits (so both give the same groups; see sorted_tail).
+constexpr int kSortCap = 256;  // four entries per lane of wave 0
+static_assert(kMatchOffset + 2 * kCandCap + 2 * kSortCap <= kChunk, "the sort's staging must fit");
+
+// Sorts c[0, n), n <= kSortCap, in place (rank by counting; tmp holds n entries). Every thread
+// calls; the sorted list is visible on return.
+__device__ __forceinline__ void sort_cands(Cand* c, int n, Cand* tmp) {
+  const int i = threadIdx.x;
+  if (i < n) {
+    const Cand me = c[i];
+    const uint32_t km = key_of(me.x);
+    uint32_t rank = 0;
+    for (int j = 0; j < n; ++j) {  // (j uniform: one broadcast read per wave)
+      const Cand o = c[j];
+      const uint32_t ko = key_of(o.x);
+      rank += (ko > km || (ko == km && o.id < me.id)) ? 1u : 0u;
+    }
+    tmp[rank] = me;
+  }
+  lds_barrier();
+  if (i < n) c[i] = tmp[i];
+  lds_barrier();
+}
+
+// Top-p cutoff and draw over a sorted list c[0, n) that holds every element >= k.x0 (the kept
+// set is a prefix of it). Wave 0 computes; on success the results reach k and the row's outputs
+// are written (returns true); when no group qualifies as the cutoff (which the radix descent
+// would resolve on its own terms) nothing is changed and it returns false.
+//
+// Equivalence with radix_mass: with E_i the exclusive prefix of the masses in list order, a
+// digit's or a key group's "mass above" is E at its first element. kCutoff keeps the lowest group
+// whose double(E) < P: the E are non-decreasing, so that is the group of the last element with
+// double(E_i) < P. kCross takes the group with double(E_g) <= t < double(E_g + M_g); those
+// intervals tile [0, double(S)), and so do the elements' [double(E_i), double(E_i + q_i)) inside
+// them, so it is the group of the one element whose interval holds t.
+template <bool STATE, class Tin>
+__device__ __forceinline__ bool sorted_tail(const SampleArgs& a, const Row<Tin>& row, const RowParams& p,
+                                            GenericSmem& g, Search& s, const Cand* c, int n, float mz, Kept& k,
+                                            int r) {
+  // results: hcnt[0] ok, [1] cutoff key, [2] first index of the cutoff group, [3] its size,
+  // [4] kept members r, [5] partial, [6] draw index; bq[0] S, bq[1] mass above the cutoff,
+  // bq[2] mass of one member of the cutoff group
+  uint32_t* res = g.rdx.hcnt;
+  u64* resq = g.rdx.bq;
+  if (threadIdx.x < kWave) {
+    const int l = lane_id();
+    const float T = p.T;
+    const uint32_t k0 = key_of(k.x0);
+    uint32_t key[4];
+    u64 q[4];
+    u64 ls = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int i = 4 * l + t;
+      const float x = i < n ? c[i].x : 0.0f;
+      const bool in = i < n && key_of(x) >= k0;
+      key[t] = in ? key_of(x) : 0u;  // (0: below every kept key)
+      q[t] = in ? mass_q(ptilde(x, T, mz)) : 0ull;
+      ls += q[t];
+    }
+    const u64 incl = wave_incl_scan<u64>(ls);
+    u64 E[4];
+    E[0] = incl - ls;
+#pragma unroll
+    for (int t = 1; t < 4; ++t) E[t] = E[t - 1] + q[t - 1];
+    const u64 S0 = dpp::last(incl);
+    // sums over the kept elements of one key group: count above / in, mass above / in
+    auto group = [&](uint32_t gk, uint32_t* f, uint32_t* cnt, u64* above, u64* mass) {
+      uint32_t cf = 0, cg = 0;
+      u64 ma = 0, mg = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bool kept = key[t] != 0u;
+        cf += kept && key[t] > gk ? 1u : 0u;
+        cg += kept && key[t] == gk ? 1u : 0u;
+        ma += kept && key[t] > gk ? q[t] : 0ull;
+        mg += kept && key[t] == gk ? q[t] : 0ull;
+      }
+      *f = wave_sum<uint32_t>(cf);
+      *cnt = wave_sum<uint32_t>(cg);
+      *above = wave_sum<u64>(ma);
+      *mass = wave_sum<u64>(mg);
+    };
+    bool ok = true;
+    u64 S = S0;
+    uint32_t ck = 0, fc = 0, nc = 0, rr = 0;
+    u64 mabove = 0, qc = 0;
+    bool partial = false, has_cut = false;
+    if (p.tp < 1.0f) {
+      const double P = static_cast<double>(p.tp) * static_cast<double>(S0);
+      uint32_t below = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) below += key[t] != 0u && static_cast<double>(E[t]) < P ? 1u : 0u;
+      const uint32_t nb = wave_sum<uint32_t>(below);
+      ok = nb > 0;
+      if (ok) {
+        const int js = static_cast<int>(nb) - 1;  // the last element with E < P
+        ck = key_of(c[js].x);
+        u64 massc;
+        group(ck, &fc, &nc, &mabove, &massc);
+        qc = nc ? massc / nc : 0ull;
+        rr = nc;
+        if (qc > 0) {
+          const double cr = ceil((P - static_cast<double>(mabove)) / static_cast<double>(qc));
+          rr = cr < 1.0 ? 1u : (cr >= static_cast<double>(nc) ? nc : static_cast<uint32_t>(cr));
+        }
+        partial = rr < nc;
+        has_cut = true;
+        S = mabove + static_cast<u64>(rr) * qc;
+      }
+    }
+    uint32_t di = 0;
+    if (ok && !a.out_probs) {
+      const u64 td = static_cast<u64>(static_cast<double>(p.u) * static_cast<double>(S));
+      const u64 tdc = td < S ? td : S - 1;
+      if (has_cut && tdc >= mabove && qc > 0) {
+        di = fc + static_cast<uint32_t>((tdc - mabove) / qc);
+      } else {
+        // the group holding tdc among the elements >= x0 (x0 raised to the cutoff value when
+        // the cutoff group is whole)
+        const uint32_t kx = has_cut && !partial ? ck : k0;
+        const double tt = static_cast<double>(tdc);
+        // (the one element whose interval holds tdc: the lane and slot that saw it)
+        uint32_t mine = 0xFFFFFFFFu;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (key[t] != 0u && key[t] >= kx && static_cast<double>(E[t]) <= tt && tt < static_cast<double>(E[t] + q[t]))
+            mine = key[t];
+        const u64 hl = __ballot(mine != 0xFFFFFFFFu);
+        ok = hl != 0ull;
+        if (ok) {
+          const uint32_t dk = __builtin_amdgcn_readlane(mine, __ffsll(static_cast<long long>(hl)) - 1);
+          uint32_t fd, nd;
+          u64 maboved, massd;
+          group(dk, &fd, &nd, &maboved, &massd);
+          const u64 qd = nd ? massd / nd : 0ull;
+          u64 j = qd ? (tdc - maboved) / qd : 0ull;
+          if (j >= nd) j = nd ? nd - 1 : 0;
+          di = fd + static_cast<uint32_t>(j);
+        }
+      }
+    }
+    if (l == 0) {
+      res[0] = ok ? 1u : 0u;
+      res[1] = ck;
+      res[2] = fc;
+      res[3] = nc;
+      res[4] = rr;
+      res[5] = partial ? 1u : 0u;
+      res[6] = di;
+      res[7] = has_cut ? 1u : 0u;
+      resq[0] = S;
+      resq[1] = mabove;
+      resq[2] = qc;
+    }
+  }
+  __syncthreads();
+  if (!res[0]) {
+    __syncthreads();
+    return false;
+  }
+  k.S = resq[0];
+  if (res[7]) {
+    k.has_cut = true;
+    k.vc = val_of(res[1]);
+    k.qc = resq[2];
+    k.mabove_c = resq[1];
+    k.r = res[4];
+    k.partial = res[5] != 0u;
+    if (!k.partial) k.x0 = k.vc;
+  }
+  const uint32_t fc = res[2];
+  const int draw = a.out_probs ? 0 : c[res[6]].id;
+  __syncthreads();
+  // the id of the cutoff group's r-th member (resolve_idr's), from the list
+  if (k.partial) {
+    bool need = STATE || a.out_probs != nullptr;
+    if (!need && p.draft >= 0 && p.draft < row.V && a.out_dprob) need = value_of(row, p.draft, &s.vslot) == k.vc;
+    if (need) k.idr = c[fc + k.r - 1].id;
+  }
+  finish<STATE>(a, row, p, mz, k, draw, &s.vslot, r);
+  return true;
+}
+
 template <bool STATE, class Tin>
 __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g,
                                             FastSmem& f, int r) {
@@ -999,12 +1199,13 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     __syncthreads();
   }
   u64 best = 0;
-  for_each(row, [&](float x, int id) {
+  auto visit = [&](float x, int id) {
     const uint32_t key = key_of(x);
     const u64 kq = (static_cast<u64>(key) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(id));
     best = kq > best ? kq : best;
     if (topk) atomicAdd(&h13[key >> 19], 1u);
-  });
+  };
+  for_each(row, visit);
   best = block_max_u64(best, s.red64);  // (its barriers also end the histogram)
   const uint32_t mkey = static_cast<uint32_t>(best >> 32);
   const int imax = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
@@ -1018,6 +1219,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
   }
   const uint32_t lo_key = key_of(-INFINITY);
   uint32_t topbin = 0, ntop = kCandCap + 1u;  // the top-k candidates: bins >= topbin, ntop of them
+  bool sorted = false;                          // (and sorted, when few)
   if (topk) {  // top-k: keep z >= kth largest z (sampler.py:53-55)
     // the bin of the K-th largest key (thread t sums bins 8191 - 8t .. 8184 - 8t, descending),
     // then the K'-th largest of that bin's elements, copied to LDS when they fit
@@ -1063,21 +1265,26 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     __syncthreads();
     const uint32_t nb = g.rdx.ncand;
     ntop = nb;
+    sorted = nb <= static_cast<uint32_t>(kSortCap) && K <= nb;  // (uniform)
+    if (sorted) sort_cands(cand, static_cast<int>(nb), cand + kCandCap);
     const CandList bl{cand, static_cast<int>(nb)};
-    const uint32_t kkey = nb <= static_cast<uint32_t>(kCandCap) ? radix_kth(row, &bl, K, g.rdx)
-                                                                : radix_kth(row, nullptr, K, g.rdx);
-    if (threadIdx.x == 0) {
+    const uint32_t kkey = sorted ? key_of(cand[K - 1].x)
+                          : nb <= static_cast<uint32_t>(kCandCap) ? radix_kth(row, &bl, K, g.rdx)
+                                                                  : radix_kth(row, nullptr, K, g.rdx);
+    if (threadIdx.x < kWave) {
       const float kz = val_of(kkey) / T;
-      g.rdx.bk[2] = bisect_key(lo_key, kkey, [&](float x) { return x / T >= kz; });
+      const uint32_t kx = bisect_key_wave(lo_key, kkey, [&](float x) { return x / T >= kz; });
+      if (lane_id() == 0) g.rdx.bk[2] = kx;
     }
     __syncthreads();
     k.x0 = val_of(g.rdx.bk[2]);
     __syncthreads();
   }
   if (p.mp > 0.0f) {  // min-p: keep exp(z - max z) >= min_p
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < kWave) {
       const double dmp = static_cast<double>(p.mp);
-      g.rdx.bk[3] = bisect_key(lo_key, mkey, [&](float x) { return ptilde(x, T, mz) >= dmp; });
+      const uint32_t kx = bisect_key_wave(lo_key, mkey, [&](float x) { return ptilde(x, T, mz) >= dmp; });
+      if (lane_id() == 0) g.rdx.bk[3] = kx;
     }
     __syncthreads();
     const float xm = val_of(g.rdx.bk[3]);
@@ -1090,6 +1297,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
   // (uniform) the top-k candidates already hold every element >= x0: no pass over the row
   const bool reuse = ntop <= static_cast<uint32_t>(kCandCap) && (key_of(k.x0) >> 19) >= topbin;
   const bool listable = k.x0 > -INFINITY;  // (uniform) a threshold: usually few candidates
+  if (sorted && reuse && sorted_tail<STATE>(a, row, p, g, s, cand, static_cast<int>(ntop), mz, k, r)) return;
   if (reuse) {
     const float x0 = k.x0;
     for (int i = threadIdx.x; i < static_cast<int>(ntop); i += kThreads)
