@@ -368,10 +368,10 @@ __device__ __forceinline__ uint32_t Row<float>::load(int b, float v[kBlk]) const
 // blocks, exceptions spread over the workgroup. The groups of kDepth stripes wholly inside an
 // aligned row have their loads (and lane masks) issued together, ahead of the work on them.
 template <class Tin, class F>
-__device__ __forceinline__ void for_each_ahead(const Row<Tin>& row, F f) {
+__device__ __forceinline__ void for_each_ahead(const Row<Tin>& row, F f, int j0 = 0) {
   constexpr int kDepth = 2;  // (measured on logprobs and fp32 rows: 2 beats 4 and 8)
   const int whole = row.vec ? row.V / kBlk / kThreads : 0;  // (uniform) such stripes
-  int j = 0;
+  int j = j0;  // (the stripes below j0, a multiple of kDepth, were visited by the caller)
   for (; j + kDepth <= whole; j += kDepth) {
     WholeBlock<Tin> q[kDepth];
     uint32_t masked[kDepth];
@@ -1000,6 +1000,11 @@ __device__ __forceinline__ int chunk_pick(const u64* cm, int mode, double target
 // element from the exclusive prefix of the masses, with the comparisons the radix descents make
 // on their digits (so both give the same groups; see sorted_tail).
 constexpr int kSortCap = 256;  // four entries per lane of wave 0
+// Streaming top-k candidates (fp32 rows): K at most kStreamK, at most kStreamCap staged elements
+// (in LDS after the candidate list: the sort's staging, unused until then).
+constexpr int kStreamK = 384;
+constexpr int kStreamCap = 1536;
+static_assert(kMatchOffset + 2 * kCandCap + 2 * kStreamCap <= kChunk, "the staged candidates must fit");
 static_assert(kMatchOffset + 2 * kCandCap + 2 * kSortCap <= kChunk, "the sort's staging must fit");
 
 // Sorts c[0, n), n <= kSortCap, in place (rank by counting; tmp holds n entries). Every thread
@@ -1205,8 +1210,93 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     best = kq > best ? kq : best;
     if (topk) atomicAdd(&h13[key >> 19], 1u);
   };
-  for_each(row, visit);
+  // The bin of the kk-th largest key so far (thread t sums bins 8191 - 8t .. 8184 - 8t,
+  // descending) to g.rdx.bk[0], the count above that bin to bk[1]; every thread calls, a
+  // barrier publishes. (bk[0] keeps its value when fewer than kk keys were counted.)
+  auto find_bin = [&](uint32_t kk) {
+    uint32_t c8[8], s8 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      c8[i] = h13[kTopBins - 1 - 8 * threadIdx.x - i];
+      s8 += c8[i];
+    }
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan<uint32_t>(s8, g.rdx.hcnt, &tot);  // (hcnt: free until the descent)
+    if (ex < kk && kk <= ex + s8) {
+      uint32_t above = ex;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (above < kk && kk <= above + c8[i]) {
+          g.rdx.bk[0] = static_cast<uint32_t>(kTopBins - 1 - 8 * threadIdx.x - i);
+          g.rdx.bk[1] = above;
+        }
+        above += c8[i];
+      }
+    }
+  };
+  // fp32 rows with a small top-k: the first kStreamDepth stripes sample the row, and the bin of
+  // their m-th largest key (m about twice the K-th's share of the sample) bounds the candidates
+  // from below; the rest of the pass appends every element in that bin or above to a staging
+  // list, which then holds the top-k candidates without a second pass over the row (checked
+  // below: it must have kept all of them and hold the K-th largest)
+  constexpr int kStreamDepth = 2;
+  Cand* stage = reinterpret_cast<Cand*>(reinterpret_cast<uint32_t*>(&g) + kMatchOffset + 2 * kCandCap);
+  const bool stream = sizeof(Tin) == 4 && topk && p.K <= kStreamK && row.vec &&
+                      row.V / kBlk / kThreads >= kStreamDepth;  // (uniform)
+  uint32_t tau_bin = 0;
+  if (stream) {
+    if (threadIdx.x == 0) {
+      g.rdx.bk[0] = 0;  // (the sample too small: every element is a candidate, the list overflows)
+      g.rdx.bk[2] = 0;  // staged candidates
+    }
+    WholeBlock<Tin> q[kStreamDepth];
+    uint32_t masked[kStreamDepth];
+#pragma unroll
+    for (int k = 0; k < kStreamDepth; ++k) {
+      const int b = k * kThreads + threadIdx.x;
+      q[k].load(row.p, b);
+      masked[k] = row.bm ? row.bm[b] : 0u;
+    }
+    float v[kStreamDepth][kBlk];
+#pragma unroll
+    for (int k = 0; k < kStreamDepth; ++k) {
+      q[k].values(v[k]);
+#pragma unroll
+      for (int i = 0; i < kBlk; ++i)
+        if (!(masked[k] & (1u << i))) visit(v[k][i], (k * kThreads + static_cast<int>(threadIdx.x)) * kBlk + i);
+    }
+    __syncthreads();  // (the sample's histogram is complete)
+    constexpr u64 kSample = static_cast<u64>(kStreamDepth) * kThreads * kBlk;
+    find_bin(static_cast<uint32_t>((2ull * static_cast<u64>(p.K) * kSample + static_cast<u64>(V) - 1) / V) + 2u);
+    __syncthreads();
+    tau_bin = g.rdx.bk[0];
+    auto append = [&](float x, int id) {
+      const bool c = (key_of(x) >> 19) >= tau_bin;
+      const u64 bal = __ballot(c);  // (one counter update per wave round)
+      if (bal) {
+        const int leader = __ffsll(static_cast<long long>(bal)) - 1;
+        uint32_t at = 0;
+        if (lane_id() == leader) at = atomicAdd(&g.rdx.bk[2], static_cast<uint32_t>(__popcll(bal)));
+        at = __builtin_amdgcn_readlane(at, leader) +
+             static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
+        if (c && at < static_cast<uint32_t>(kStreamCap)) stage[at] = Cand{x, id};
+      }
+    };
+#pragma unroll
+    for (int k = 0; k < kStreamDepth; ++k) {
+#pragma unroll
+      for (int i = 0; i < kBlk; ++i)
+        if (!(masked[k] & (1u << i))) append(v[k][i], (k * kThreads + static_cast<int>(threadIdx.x)) * kBlk + i);
+    }
+    for_each_ahead(row, [&](float x, int id) {
+      visit(x, id);
+      append(x, id);
+    }, kStreamDepth);
+  } else {
+    for_each(row, visit);
+  }
   best = block_max_u64(best, s.red64);  // (its barriers also end the histogram)
+  const uint32_t nstage = stream ? g.rdx.bk[2] : 0u;
   const uint32_t mkey = static_cast<uint32_t>(best >> 32);
   const int imax = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
   const float xmax = val_of(mkey);
@@ -1224,25 +1314,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     // the bin of the K-th largest key (thread t sums bins 8191 - 8t .. 8184 - 8t, descending),
     // then the K'-th largest of that bin's elements, copied to LDS when they fit
     const uint32_t K = static_cast<uint32_t>(p.K);
-    uint32_t c8[8], s8 = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      c8[i] = h13[kTopBins - 1 - 8 * threadIdx.x - i];
-      s8 += c8[i];
-    }
-    uint32_t tot;
-    const uint32_t ex = block_excl_scan<uint32_t>(s8, g.rdx.hcnt, &tot);  // (hcnt: free until the descent)
-    if (ex < K && K <= ex + s8) {
-      uint32_t above = ex;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (above < K && K <= above + c8[i]) {
-          g.rdx.bk[0] = static_cast<uint32_t>(kTopBins - 1 - 8 * threadIdx.x - i);
-          g.rdx.bk[1] = above;
-        }
-        above += c8[i];
-      }
-    }
+    find_bin(K);
     if (threadIdx.x == 0) g.rdx.ncand = 0;
     __syncthreads();  // (every read of the bins is done: the candidates go over them)
     // every element of that bin and the bins above (at most K - 1 of those): the K-th largest of
@@ -1250,7 +1322,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     const uint32_t bin = g.rdx.bk[0];
     topbin = bin;
     Cand* cand = reinterpret_cast<Cand*>(h13);
-    for_each(row, [&](float x, int id) {
+    auto take = [&](float x, int id) {
       const bool c = (key_of(x) >> 19) >= bin;
       const u64 bal = __ballot(c);  // (one counter update per wave round)
       if (bal) {
@@ -1261,7 +1333,14 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
              static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
         if (c && at < static_cast<uint32_t>(kCandCap)) cand[at] = Cand{x, id};
       }
-    });
+    };
+    // the staged list holds every element in bins >= tau_bin when it did not overflow; it holds
+    // the K-th largest when that bin is at or above tau_bin
+    if (stream && nstage <= static_cast<uint32_t>(kStreamCap) && bin >= tau_bin) {
+      for (int i = threadIdx.x; i < static_cast<int>(nstage); i += kThreads) take(stage[i].x, stage[i].id);
+    } else {
+      for_each(row, take);
+    }
     __syncthreads();
     const uint32_t nb = g.rdx.ncand;
     ntop = nb;
