@@ -109,8 +109,10 @@ struct ExcCache {
   int cap;
 };
 
-// Counting: a row whose history has at most kHashMaxL ids counts them in an LDS hash table
-// (16384 slots of (id, count), at most 75 % full); longer histories count in windows of ids.
+// Counting: through a presence bitmap of the vocabulary (bitmap_count, below) when the
+// vocabulary, the history and its distinct ids fit; otherwise a history of at most kHashMaxL ids
+// in an LDS hash table (16384 slots of (id, count), at most 75 % full), a longer one in windows
+// of ids.
 constexpr int kHashSlots = 16384;
 constexpr int kHashMaxL = 12288;
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
@@ -158,20 +160,25 @@ __device__ __forceinline__ void gather_values(const PenaltyArgs& a, const Tin* r
 // + kBmPer - 1 and stages their ids in rank order in LDS, from where the workgroup writes the
 // (id, count) pairs coalesced (each thread straight to the workspace when they do not fit).
 // Returns false (having written nothing) when the distinct ids do not fit: the caller then counts
-// in windows.
+// another way. The arrays start at LDS word kPenBitmapOffset, so the bitmap (bit id of 32-bit word
+// id / 32) is where the sampling kernel's generic path keeps its bitmap of penalised ids, and
+// stays there on return.
 constexpr int kBmPer = 4;                       // 64-bit bitmap words per thread
 constexpr int kBmMaxV = 64 * kBmPer * kThreads;  // 262144
+constexpr int kPenBitmapOffset = 5120;
 template <class Tin>
-__device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, uint32_t* words, uint32_t* red, ExcCache ec, int h0,
+__device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, uint32_t* lds, uint32_t* red, ExcCache ec, int h0,
                                              int L, int V, bool on, int32_t* dc, float rep, float pres, float freq,
                                              const Tin* row, const int32_t* hist, uint32_t* n_out) {
   const int tid = threadIdx.x;
   const int nw = (V + 63) / 64;  // 64-bit bitmap words
+  uint32_t* words = lds + kPenBitmapOffset;
+  constexpr int kRoom = kChunk - kPenBitmapOffset;  // words from the bitmap on
   u64* bm = reinterpret_cast<u64*>(words);
   const int head = 2 * nw + (nw + 1) / 2;
   uint16_t* pre = reinterpret_cast<uint16_t*>(words + 2 * nw);  // u16 prefix per word
   uint32_t* cnt = words + head;                                  // u16 counts by rank, in pairs
-  const int cap = 2 * (kChunk - head);                           // ranks that fit
+  const int cap = 2 * (kRoom - head);                            // ranks that fit
   for (int i = tid; i < 2 * nw; i += kThreads) words[i] = 0;
   lds_barrier();
   for_each_id(hist, L, [&](int id, int) {
@@ -212,7 +219,7 @@ __device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, uint32_t* wor
   auto count_of = [&](uint32_t e) -> int { return static_cast<int>((cnt[e >> 1] >> ((e & 1u) << 4)) & 0xFFFFu); };
   // (id, count) pairs in rank order
   int32_t* rid = reinterpret_cast<int32_t*>(cnt + (total + 1) / 2);
-  const uint32_t room = static_cast<uint32_t>(kChunk - head - static_cast<int>((total + 1) / 2));
+  const uint32_t room = static_cast<uint32_t>(kRoom - head - static_cast<int>((total + 1) / 2));
   if (total <= room) {  // (uniform)
 #pragma unroll
     for (int k = 0; k < kBmPer; ++k) {
@@ -262,8 +269,11 @@ __device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, uint32_t* wor
 // Writes the row's exceptions to the workspace (global memory: a reader in the same workgroup
 // needs a __syncthreads() first) and, up to ec.cap of them, to `ec` in LDS (visible on return).
 // With dense_counts set, also writes every id's count. Returns the number of exceptions.
+// *bitmap_out (when given) tells whether the penalised ids' bitmap is left in LDS from word
+// kPenBitmapOffset on (bitmap_count's).
 template <class Tin>
-__device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, uint32_t* lds, uint32_t* red, ExcCache ec) {
+__device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, uint32_t* lds, uint32_t* red, ExcCache ec,
+                                                  bool* bitmap_out = nullptr) {
   const int tid = threadIdx.x;
   const int V = a.V;
   const int h0 = a.off ? a.off[r * a.hstep] : 0;
@@ -286,7 +296,11 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
     __syncthreads();  // the zeros land before the counts below overwrite some of them
   }
   uint32_t n_total = 0;
-  if (L <= kHashMaxL) {
+  bool bitmap = false;
+  if (V <= kBmMaxV && L <= 0xFFFF && bitmap_count<Tin>(a, lds, red, ec, h0, L, V, on, dc, rep, pres, freq, row,
+                                                        hist, &n_total)) {
+    bitmap = true;  // (counted through a presence bitmap: two passes over the history)
+  } else if (L <= kHashMaxL) {
     // ---- one pass: an (id -> count) hash table in LDS ----
     uint32_t* keys = lds;
     uint32_t* cnts = lds + kHashSlots;
@@ -337,9 +351,6 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
     lds_barrier();
     if (on)
       gather_values<Tin>(a, row, h0, n_total, [&](uint32_t e) { return stage[e]; }, rep, pres, freq, ec);
-  } else if (V <= kBmMaxV && L <= 0xFFFF && bitmap_count<Tin>(a, lds, red, ec, h0, L, V, on, dc, rep, pres, freq,
-                                                                row, hist, &n_total)) {
-    // (counted through a presence bitmap: two passes over the history)
   } else {
     // ---- long histories: count a window of ids at a time ----
     uint32_t* cnt = lds;
@@ -411,6 +422,7 @@ __device__ __forceinline__ uint32_t penalty_phase(const PenaltyArgs& a, int r, u
                          freq, ec);
   }
   if (tid == 0) a.ws.n_exc[r] = on ? n_total : 0u;
+  if (bitmap_out) *bitmap_out = bitmap && on;
   lds_barrier();
   return on ? n_total : 0u;
 }

@@ -119,7 +119,7 @@ struct GenericSmem {
 //   [0, kBitmapOffset)                          Search and Radix scratch
 //   [kBitmapOffset, kBitmapOffset + 16384)      per-block lane masks of penalised ids (V / 8 bytes)
 //   [kMatchOffset, kMatchOffset + kMatchWords)  the draw's per-block count cells
-constexpr int kBitmapOffset = 5120;
+constexpr int kBitmapOffset = kPenBitmapOffset;  // (where the penalty pass's bitmap path leaves its bitmap)
 constexpr int kMatchOffset = kBitmapOffset + 16384;
 
 constexpr int kMaxL = 128;     // penalised values in one chunk the fast path can resolve
@@ -364,6 +364,10 @@ __device__ __forceinline__ uint32_t Row<float>::load(int b, float v[kBlk]) const
   return valid;
 }
 
+// Stripes in flight in for_each_ahead's rolling window (0: groups of kDepth stripes, each group's
+// loads issued together and used before the next group's).
+constexpr int kRollDepth = 2;
+
 // Visit every element of the row once: bulk lanes through `f(x, id)` in the calling thread's
 // blocks, exceptions spread over the workgroup. The groups of kDepth stripes wholly inside an
 // aligned row have their loads (and lane masks) issued together, ahead of the work on them.
@@ -372,6 +376,38 @@ __device__ __forceinline__ void for_each_ahead(const Row<Tin>& row, F f, int j0 
   constexpr int kDepth = 2;  // (measured on logprobs and fp32 rows: 2 beats 4 and 8)
   const int whole = row.vec ? row.V / kBlk / kThreads : 0;  // (uniform) such stripes
   int j = j0;  // (the stripes below j0, a multiple of kDepth, were visited by the caller)
+  if constexpr (kRollDepth > 0) {
+    // a rolling window: as stripe j's values are taken out of slot k, the slot's next load
+    // (stripe j + kRollDepth) is issued, so kRollDepth stripes stay in flight
+    constexpr int D = kRollDepth;
+    const int end = j0 + (whole - j0) / D * D;  // (uniform)
+    if (end > j0) {
+      WholeBlock<Tin> q[D];
+      uint32_t masked[D];
+#pragma clang loop unroll(full)
+      for (int k = 0; k < D; ++k) {
+        const int b = (j0 + k) * kThreads + threadIdx.x;
+        q[k].load(row.p, b);
+        masked[k] = row.bm ? row.bm[b] : 0u;
+      }
+      for (; j < end; j += D) {
+#pragma clang loop unroll(full)
+        for (int k = 0; k < D; ++k) {
+          const int b = (j + k) * kThreads + threadIdx.x;
+          float v[kBlk];
+          q[k].values(v);
+          const uint32_t m = masked[k];
+          // (the last window reloads its own stripes: in bounds, and never used)
+          const int bn = (j + D + k < end ? j + D + k : j + k) * kThreads + threadIdx.x;
+          q[k].load(row.p, bn);
+          masked[k] = row.bm ? row.bm[bn] : 0u;
+#pragma unroll
+          for (int i = 0; i < kBlk; ++i)
+            if (!(m & (1u << i))) f(v[i], b * kBlk + i);
+        }
+      }
+    }
+  }
   for (; j + kDepth <= whole; j += kDepth) {
     WholeBlock<Tin> q[kDepth];
     uint32_t masked[kDepth];
@@ -999,6 +1035,11 @@ __device__ __forceinline__ int chunk_pick(const u64* cm, int mode, double target
 // K-th largest is entry K - 1, and wave 0 alone finds the top-p cutoff group and the drawn
 // element from the exclusive prefix of the masses, with the comparisons the radix descents make
 // on their digits (so both give the same groups; see sorted_tail).
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
+
 constexpr int kSortCap = 256;  // four entries per lane of wave 0
 // Streaming top-k candidates (fp32 rows): K at most kStreamK, at most kStreamCap staged elements
 // (in LDS after the candidate list: the sort's staging, unused until then).
@@ -1187,12 +1228,17 @@ __device__ __forceinline__ bool sorted_tail(const SampleArgs& a, const Row<Tin>&
   return true;
 }
 
+// have_bitmap: the penalty pass left the penalised ids' bitmap at kBitmapOffset.
 template <bool STATE, class Tin>
 __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, const RowParams& p, GenericSmem& g,
-                                            FastSmem& f, int r) {
+                                            FastSmem& f, int r, bool have_bitmap = false) {
   const int V = row.V;
   Search& s = g.srch;
-  if (row.nexc > 0) build_bitmap(row, reinterpret_cast<uint32_t*>(&g) + kBitmapOffset);
+  if (row.nexc > 0) {
+    uint32_t* words = reinterpret_cast<uint32_t*>(&g) + kBitmapOffset;
+    if (have_bitmap) row.bm = reinterpret_cast<const uint8_t*>(words);
+    else build_bitmap(row, words);
+  }
   // max (and first index of the max; NaN counts as the max); with top-k, in the same pass, a
   // histogram of the keys' top 13 bits
   const bool topk = p.K > 0 && p.K < V;  // (uniform)
@@ -1203,13 +1249,14 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     for (int i = threadIdx.x; i < kTopBins; i += kThreads) h13[i] = 0;
     __syncthreads();
   }
+  // The row's max: greedy rows (T <= 0) need its first index too, through ordered (key, id)
+  // pairs; the others only its value, through fmax and a NaN flag (a NaN row's token, its first
+  // NaN, is searched for afterwards), which costs a pass over an fp32 row a fraction of the
+  // vector instructions
+  const bool greedy = !(p.T > 0.0f);  // (uniform)
   u64 best = 0;
-  auto visit = [&](float x, int id) {
-    const uint32_t key = key_of(x);
-    const u64 kq = (static_cast<u64>(key) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(id));
-    best = kq > best ? kq : best;
-    if (topk) atomicAdd(&h13[key >> 19], 1u);
-  };
+  float vmax = -INFINITY;
+  uint32_t vnan = 0;
   // The bin of the kk-th largest key so far (thread t sums bins 8191 - 8t .. 8184 - 8t,
   // descending) to g.rdx.bk[0], the count above that bin to bk[1]; every thread calls, a
   // barrier publishes. (bk[0] keeps its value when fewer than kk keys were counted.)
@@ -1237,68 +1284,92 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
   // fp32 rows with a small top-k: the first kStreamDepth stripes sample the row, and the bin of
   // their m-th largest key (m about twice the K-th's share of the sample) bounds the candidates
   // from below; the rest of the pass appends every element in that bin or above to a staging
-  // list, which then holds the top-k candidates without a second pass over the row (checked
-  // below: it must have kept all of them and hold the K-th largest)
+  // list, which then holds the top-k candidates without a second pass over the row, and no
+  // longer counts keys (checked below: the list must have kept all of them and hold the K-th
+  // largest; its own histogram then gives the K-th largest's bin)
   constexpr int kStreamDepth = 2;
   Cand* stage = reinterpret_cast<Cand*>(reinterpret_cast<uint32_t*>(&g) + kMatchOffset + 2 * kCandCap);
   const bool stream = sizeof(Tin) == 4 && topk && p.K <= kStreamK && row.vec &&
                       row.V / kBlk / kThreads >= kStreamDepth;  // (uniform)
   uint32_t tau_bin = 0;
-  if (stream) {
-    if (threadIdx.x == 0) {
-      g.rdx.bk[0] = 0;  // (the sample too small: every element is a candidate, the list overflows)
-      g.rdx.bk[2] = 0;  // staged candidates
-    }
-    WholeBlock<Tin> q[kStreamDepth];
-    uint32_t masked[kStreamDepth];
-#pragma unroll
-    for (int k = 0; k < kStreamDepth; ++k) {
-      const int b = k * kThreads + threadIdx.x;
-      q[k].load(row.p, b);
-      masked[k] = row.bm ? row.bm[b] : 0u;
-    }
-    float v[kStreamDepth][kBlk];
-#pragma unroll
-    for (int k = 0; k < kStreamDepth; ++k) {
-      q[k].values(v[k]);
-#pragma unroll
-      for (int i = 0; i < kBlk; ++i)
-        if (!(masked[k] & (1u << i))) visit(v[k][i], (k * kThreads + static_cast<int>(threadIdx.x)) * kBlk + i);
-    }
-    __syncthreads();  // (the sample's histogram is complete)
-    constexpr u64 kSample = static_cast<u64>(kStreamDepth) * kThreads * kBlk;
-    find_bin(static_cast<uint32_t>((2ull * static_cast<u64>(p.K) * kSample + static_cast<u64>(V) - 1) / V) + 2u);
-    __syncthreads();
-    tau_bin = g.rdx.bk[0];
-    auto append = [&](float x, int id) {
-      const bool c = (key_of(x) >> 19) >= tau_bin;
-      const u64 bal = __ballot(c);  // (one counter update per wave round)
-      if (bal) {
-        const int leader = __ffsll(static_cast<long long>(bal)) - 1;
-        uint32_t at = 0;
-        if (lane_id() == leader) at = atomicAdd(&g.rdx.bk[2], static_cast<uint32_t>(__popcll(bal)));
-        at = __builtin_amdgcn_readlane(at, leader) +
-             static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
-        if (c && at < static_cast<uint32_t>(kStreamCap)) stage[at] = Cand{x, id};
+  auto first_pass = [&](auto greedy_c) {
+    constexpr bool kGreedy = decltype(greedy_c)::value;
+    auto visit_max = [&](float x, int id) {
+      if constexpr (kGreedy) {
+        const u64 kq = (static_cast<u64>(key_of(x)) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(id));
+        best = kq > best ? kq : best;
+      } else {
+        vmax = fmaxf(vmax, x);
+        vnan |= x != x ? 1u : 0u;
       }
     };
+    auto visit = [&](float x, int id) {
+      visit_max(x, id);
+      if (topk) atomicAdd(&h13[key_of(x) >> 19], 1u);
+    };
+    if (stream) {
+      if (threadIdx.x == 0) {
+        g.rdx.bk[0] = 0;  // (the sample too small: every element is a candidate, the list overflows)
+        g.rdx.bk[2] = 0;  // staged candidates
+      }
+      WholeBlock<Tin> q[kStreamDepth];
+      uint32_t masked[kStreamDepth];
 #pragma unroll
-    for (int k = 0; k < kStreamDepth; ++k) {
+      for (int k = 0; k < kStreamDepth; ++k) {
+        const int b = k * kThreads + threadIdx.x;
+        q[k].load(row.p, b);
+        masked[k] = row.bm ? row.bm[b] : 0u;
+      }
+      float v[kStreamDepth][kBlk];
 #pragma unroll
-      for (int i = 0; i < kBlk; ++i)
-        if (!(masked[k] & (1u << i))) append(v[k][i], (k * kThreads + static_cast<int>(threadIdx.x)) * kBlk + i);
+      for (int k = 0; k < kStreamDepth; ++k) {
+        q[k].values(v[k]);
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i)
+          if (!(masked[k] & (1u << i))) visit(v[k][i], (k * kThreads + static_cast<int>(threadIdx.x)) * kBlk + i);
+      }
+      __syncthreads();  // (the sample's histogram is complete)
+      constexpr u64 kSample = static_cast<u64>(kStreamDepth) * kThreads * kBlk;
+      find_bin(static_cast<uint32_t>((2ull * static_cast<u64>(p.K) * kSample + static_cast<u64>(V) - 1) / V) + 2u);
+      __syncthreads();
+      tau_bin = g.rdx.bk[0];
+      // (x >= tau_x is key_of(x) >> 19 >= tau_bin for every non-NaN x: tau_x is the bin's
+      // least value, or -inf below the least finite key's bin; a NaN row samples a point)
+      const float tau_x = val_of(max(tau_bin << 19, key_of(-INFINITY)));
+      auto append = [&](float x, int id) {
+        const bool c = x >= tau_x;
+        const u64 bal = __ballot(c);  // (one counter update per wave round)
+        if (bal) {
+          const int leader = __ffsll(static_cast<long long>(bal)) - 1;
+          uint32_t at = 0;
+          if (lane_id() == leader) at = atomicAdd(&g.rdx.bk[2], static_cast<uint32_t>(__popcll(bal)));
+          at = __builtin_amdgcn_readlane(at, leader) +
+               static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
+          if (c && at < static_cast<uint32_t>(kStreamCap)) stage[at] = Cand{x, id};
+        }
+      };
+#pragma unroll
+      for (int k = 0; k < kStreamDepth; ++k) {
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i)
+          if (!(masked[k] & (1u << i))) append(v[k][i], (k * kThreads + static_cast<int>(threadIdx.x)) * kBlk + i);
+      }
+      for_each_ahead(row, [&](float x, int id) {
+        visit_max(x, id);
+        append(x, id);
+      }, kStreamDepth);
+    } else {
+      for_each(row, visit);
     }
-    for_each_ahead(row, [&](float x, int id) {
-      visit(x, id);
-      append(x, id);
-    }, kStreamDepth);
-  } else {
-    for_each(row, visit);
-  }
+  };
+  if (greedy) first_pass(BoolC<true>{});
+  else first_pass(BoolC<false>{});
+  if (!greedy) best = static_cast<u64>(vnan ? 0xFFFFFFFFu : key_of(vmax)) << 32;
   best = block_max_u64(best, s.red64);  // (its barriers also end the histogram)
   const uint32_t nstage = stream ? g.rdx.bk[2] : 0u;
   const uint32_t mkey = static_cast<uint32_t>(best >> 32);
-  const int imax = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+  int imax = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+  if (!greedy && mkey == 0xFFFFFFFFu) imax = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, s);
   const float xmax = val_of(mkey);
   const float T = p.T;
   const float mz = xmax / T;
@@ -1314,6 +1385,19 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
     // the bin of the K-th largest key (thread t sums bins 8191 - 8t .. 8184 - 8t, descending),
     // then the K'-th largest of that bin's elements, copied to LDS when they fit
     const uint32_t K = static_cast<uint32_t>(p.K);
+    // (streamed: the histogram holds the sample only; the staged list's keys, or when it cannot
+    // serve, another pass over the row's, replace it)
+    const bool staged = stream && nstage >= K && nstage <= static_cast<uint32_t>(kStreamCap);  // (uniform)
+    if (stream) {
+      for (int i = threadIdx.x; i < kTopBins; i += kThreads) h13[i] = 0;
+      __syncthreads();
+      if (staged) {
+        for (int i = threadIdx.x; i < static_cast<int>(nstage); i += kThreads) atomicAdd(&h13[key_of(stage[i].x) >> 19], 1u);
+      } else {
+        for_each(row, [&](float x, int) { atomicAdd(&h13[key_of(x) >> 19], 1u); });
+      }
+      __syncthreads();
+    }
     find_bin(K);
     if (threadIdx.x == 0) g.rdx.ncand = 0;
     __syncthreads();  // (every read of the bins is done: the candidates go over them)
@@ -1334,9 +1418,9 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
         if (c && at < static_cast<uint32_t>(kCandCap)) cand[at] = Cand{x, id};
       }
     };
-    // the staged list holds every element in bins >= tau_bin when it did not overflow; it holds
-    // the K-th largest when that bin is at or above tau_bin
-    if (stream && nstage <= static_cast<uint32_t>(kStreamCap) && bin >= tau_bin) {
+    // the staged list holds every element in bins >= tau_bin when it did not overflow, so the
+    // K-th largest when it has at least K of them
+    if (staged) {
       for (int i = threadIdx.x; i < static_cast<int>(nstage); i += kThreads) take(stage[i].x, stage[i].id);
     } else {
       for_each(row, take);
@@ -2688,14 +2772,15 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   p.u = p.u >= 0.0f ? p.u : 0.0f;
   // the generic path: the penalty pass writes the penalised ids and values to the workspace
   int ne = 0;
-  if (PEN) ne = static_cast<int>(penalty_phase<Tin>(a.pen, r, big, f.red32, ExcCache{nullptr, nullptr, 0}));
+  bool have_bitmap = false;
+  if (PEN) ne = static_cast<int>(penalty_phase<Tin>(a.pen, r, big, f.red32, ExcCache{nullptr, nullptr, 0}, &have_bitmap));
   __syncthreads();
   if (ne > 0) {
     row.nexc = ne;
     row.eid = a.ws.exc_id + p.h0;
     row.eval = a.ws.exc_val + p.h0;
   }
-  generic_row<STATE>(a, row, p, g, f, r);
+  generic_row<STATE>(a, row, p, g, f, r, have_bitmap);
 }
 
 }  // namespace vs
