@@ -633,8 +633,17 @@ int vsamp_lm_head(const vsamp_lm_head_args* a, void* stream) {
   l.V = a->vocab;
   l.vec_out = !(reinterpret_cast<uintptr_t>(a->logits) & 15u) && a->logits_stride % 8 == 0;
   static_assert(vs::kLmBN == VSAMP_LM_TILE, "the statistics' tile is the kernel's column tile");
-  // (batches of at most 64 rows: 64-row tiles, four times less MFMA work on padding)
-  if (a->batch <= 64)
+  // (one row: a matrix-vector product, for the hidden sizes it is built for; batches of at most
+  // 64 rows: 64-row tiles, four times less MFMA work on padding)
+  const int cpl = a->dim % 512 == 0 ? a->dim / 512 : 0;  // hidden chunks per lane
+  if (a->batch == 1 && (cpl == 1 || cpl == 2 || cpl == 4 || cpl == 8)) {
+    const dim3 grid(l.nT), block(vs::kGvThreads);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (cpl == 1) hipLaunchKernelGGL(vs::k_lm_gemv<1>, grid, block, 0, st, l);
+    else if (cpl == 2) hipLaunchKernelGGL(vs::k_lm_gemv<2>, grid, block, 0, st, l);
+    else if (cpl == 4) hipLaunchKernelGGL(vs::k_lm_gemv<4>, grid, block, 0, st, l);
+    else hipLaunchKernelGGL(vs::k_lm_gemv<8>, grid, block, 0, st, l);
+  } else if (a->batch <= 64)
     hipLaunchKernelGGL(vs::k_lm_head<64>, dim3(l.nT, 1), dim3(vs::kLmThreads), 0, static_cast<hipStream_t>(stream), l);
   else
     hipLaunchKernelGGL(vs::k_lm_head<256>, dim3(l.nT, (a->batch + 255) / 256), dim3(vs::kLmThreads), 0,

@@ -195,6 +195,10 @@ template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ int mov(int x) {
   return static_cast<int>(mov<CTRL, ROW_MASK>(static_cast<uint32_t>(x)));
 }
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float mov(float x) {
+  return __uint_as_float(mov<CTRL, ROW_MASK>(__float_as_uint(x)));
+}
 
 // Lane 63's value, in every lane.
 __device__ __forceinline__ uint32_t last(uint32_t x) { return __builtin_amdgcn_readlane(x, 63); }
@@ -207,6 +211,7 @@ __device__ __forceinline__ u64 last(u64 x) {
 __device__ __forceinline__ double last(double x) {
   return __longlong_as_double(static_cast<long long>(last(static_cast<u64>(__double_as_longlong(x)))));
 }
+__device__ __forceinline__ float last(float x) { return __uint_as_float(last(__float_as_uint(x))); }
 
 // Reduction with an associative, commutative op: every 16-lane row ends with its row total in
 // all lanes, then rows 1 and 3 fold in rows 0 and 2, then row 3 folds in rows 0 + 1.
