@@ -235,7 +235,7 @@ def decode_loop(args) -> int:
     if K:
         sampler_us = timed(lambda: hip.sample_batch(logits, params, u))
     else:
-        ranges = torch.tensor([[s.slot * dec._hist_row, s.slot * dec._hist_row + s.hist_len] for s in seqs],
+        ranges = torch.tensor([[s.slot * dec._hist_row, s.slot * dec._hist_row + int(dec._hist_len[s.slot])] for s in seqs],
                               dtype=torch.int32, device=dev)
         sampler_us = timed(lambda: hip.sample_batch(logits, params, u, dec.hist, ranges))
     out = {

@@ -55,7 +55,7 @@ class TextStream(Protocol):
     def flush(self) -> str: ...
 
 
-@dataclass
+@dataclass(slots=True)
 class Step:
     """One generated token of a request (generate.py:20-24)."""
 
@@ -145,10 +145,22 @@ class _Seq:
     stream: TextStream | None
     slot: int = -1
     position: int = 0  # position of the next token to sample (= tokens in the sequence so far)
-    hist_len: int = 0  # ids in the slot's history row
     generated: list[int] = field(default_factory=list)
     # (speculative loop) a token the draft model has not been fed yet: (token, position)
     draft_gap: tuple[int, int] | None = None
+
+
+@dataclass(eq=False)
+class _Group:
+    """What a step needs of one membership (the sequences of a draw, in order) that does not
+    change from step to step: built when the membership changes, not per step."""
+
+    slots: np.ndarray  # int64 [n]
+    seeds: np.ndarray  # int64 [n]
+    pen: np.ndarray  # bool [n]: rows with penalties
+    pen_slots: np.ndarray  # int64: the slots of those rows
+    params: PackedParams
+    n_top: int  # largest top_logprobs of a row asking for log-probabilities, or -1 if none asks
 
 
 class BatchDecoder:
@@ -180,11 +192,12 @@ class BatchDecoder:
         self._next_rid = 0
         # Logits of the last model step, not yet sampled: (sequences, [n, V]).
         self._pending: tuple[list[_Seq], torch.Tensor] | None = None
-        self._packed: dict[tuple[int, ...], PackedParams] = {}
+        self._groups: dict[tuple[int, ...], _Group] = {}
         self._lp: list = []  # this step's log-probability launches
         # One history row per slot; the extra column takes the id drawn at the last position.
         self._hist_row = max_seq_len + 1
         self.hist = torch.zeros(num_slots * self._hist_row, dtype=torch.int32, device=model.device)
+        self._hist_len = np.zeros(num_slots, dtype=np.int64)  # ids in each slot's history row
         # [0]: the sampler's inputs (uniforms, ranges: 3 words a row), [1]: the model's (3 a row)
         self._stage = (_Staging(model.device, 6 * num_slots), _Staging(model.device, 3 * num_slots))
 
@@ -250,12 +263,13 @@ class BatchDecoder:
         drawn = [self._draw(seqs, logits, st, c) for (seqs, logits), c in zip(groups, cols)]
         seqs = [s for g in groups for s in g[0]]
         tokens = torch.cat(drawn).tolist() if len(drawn) > 1 else drawn[0].tolist()  # the one wait
-        lp_of = self._host_logprobs()
+        lp_of = self._host_logprobs() if self._lp else None
         out: list[tuple[int, Step]] = []
         going: list[_Seq] = []
+        advance = self._advance
         for s, tok in zip(seqs, tokens):
-            step = self._advance(s, tok)
-            if s.params.logprobs:
+            step = advance(s, tok)
+            if lp_of is not None and s.params.logprobs:
                 step.logprob, top = lp_of[id(s)]
                 step.top_logprobs = top[: s.params.top_logprobs] if s.params.top_logprobs else None
             out.append((s.rid, step))
@@ -263,13 +277,17 @@ class BatchDecoder:
                 going.append(s)
             else:
                 self._retire(s)
-        self._free.sort(reverse=True)
+        if len(going) < len(seqs):
+            self._free.sort(reverse=True)
         if going:
             st = self._stage[1]
             st.reset()
             n = len(going)
-            at = st.put(np.array([[s.slot for s in going], [s.generated[-1] for s in going],
-                                  [s.position - 1 for s in going]], dtype=np.int32).reshape(-1))
+            at = st.reserve(3 * n)
+            v = st.host_view(at, 3 * n).reshape(3, n)
+            v[0] = np.fromiter((s.slot for s in going), np.int32, n)
+            v[1] = np.fromiter((s.generated[-1] for s in going), np.int32, n)
+            v[2] = np.fromiter((s.position for s in going), np.int32, n) - 1
             st.send()
             slots, toks, pos = st.device(at, 3 * n).view(3, n).long()
             self._pending = (going, self.model.decode(slots, toks, pos))
@@ -300,37 +318,48 @@ class BatchDecoder:
             s.slot = self._free.pop()
             s.position = len(s.prompt)
             prompt = torch.tensor(s.prompt, dtype=torch.int64)
-            s.hist_len = 0
+            self._hist_len[s.slot] = 0
             if s.params.penalized and self.penalize_prompt:
                 base = s.slot * self._hist_row
                 self.hist[base : base + len(s.prompt)] = prompt.to(torch.int32).to(dev)
-                s.hist_len = len(s.prompt)
+                self._hist_len[s.slot] = len(s.prompt)
             rows.append(self.model.prefill(s.slot, prompt.to(dev)).reshape(-1))
             self._running[s.rid] = s
             seqs.append(s)
         return (seqs, torch.stack(rows)) if seqs else None
 
-    def _params(self, seqs: list[_Seq], dev: torch.device) -> PackedParams:
+    def _group(self, seqs: list[_Seq], dev: torch.device) -> _Group:
         key = tuple(s.rid for s in seqs)
-        packed = self._packed.get(key)
-        if packed is None:
-            if len(self._packed) > 64:  # memberships change as requests come and go
-                self._packed.clear()
-            packed = self._packed[key] = pack_params([s.params for s in seqs], dev)
-        return packed
+        g = self._groups.get(key)
+        if g is None:
+            if len(self._groups) > 64:  # memberships change as requests come and go
+                self._groups.clear()
+            ps = [s.params for s in seqs]
+            slots = np.array([s.slot for s in seqs], dtype=np.int64)
+            pen = np.array([p.penalized for p in ps], dtype=bool)
+            lps = [p.top_logprobs for p in ps if p.logprobs]
+            g = self._groups[key] = _Group(slots, np.array([p.seed for p in ps], dtype=np.int64), pen, slots[pen],
+                                           pack_params(ps, dev), max(lps) if lps else -1)
+        return g
+
+    def _params(self, seqs: list[_Seq], dev: torch.device) -> PackedParams:
+        return self._group(seqs, dev).params
 
     def _stage_draw(self, st: _Staging, seqs: list[_Seq]) -> tuple[int, int | None]:
         """Stage one group's uniforms and (when a row has penalties) history ranges."""
         n = len(seqs)
+        g = self._group(seqs, self.model.device)
         at_u = st.reserve(n)
-        position_uniforms([s.params.seed for s in seqs], [s.position for s in seqs],
+        position_uniforms(g.seeds, np.fromiter((s.position for s in seqs), np.int64, n),
                           out=st.host_view(at_u, n).view(np.float32))
-        if not any(s.params.penalized for s in seqs):
+        if not g.pen_slots.size:
             return at_u, None
         # Rows without penalties get an empty range (their slot's history is not kept).
-        base = np.array([s.slot for s in seqs], dtype=np.int64) * self._hist_row
-        ln = np.array([s.hist_len if s.params.penalized else 0 for s in seqs], dtype=np.int64)
-        at_r = st.put(np.stack([base, base + ln], axis=1).astype(np.int32).reshape(-1))
+        at_r = st.reserve(2 * n)
+        r = st.host_view(at_r, 2 * n).reshape(n, 2)
+        base = g.slots * self._hist_row
+        r[:, 0] = base
+        r[:, 1] = base + np.where(g.pen, self._hist_len[g.slots], 0)
         return at_u, at_r
 
     def _draw(self, seqs: list[_Seq], logits: torch.Tensor, st: _Staging, cols) -> torch.Tensor:
@@ -339,19 +368,17 @@ class BatchDecoder:
         n = len(seqs)
         at_u, at_r = cols
         u = st.device(at_u, n).view(torch.float32)
-        params = self._params(seqs, logits.device)
+        g = self._group(seqs, logits.device)
         if at_r is None:
-            ids, _ = self.sampler.sample_batch(logits, params, u)
+            ids, _ = self.sampler.sample_batch(logits, g.params, u)
         else:
             ranges = st.device(at_r, 2 * n).view(n, 2)
-            ids, _ = self.sampler.sample_batch(logits, params, u, self.hist, ranges)
+            ids, _ = self.sampler.sample_batch(logits, g.params, u, self.hist, ranges)
             # The drawn id joins its row's history right behind the range just used.
             self.hist.index_copy_(0, ranges[:, 1].long(), ids)
-            for s in seqs:
-                s.hist_len += s.params.penalized
-        if any(s.params.logprobs for s in seqs):
-            n_top = max(s.params.top_logprobs for s in seqs)
-            tok_lp, top_ids, top_lp = self.sampler.logprobs(logits, ids, n_top)
+            self._hist_len[g.pen_slots] += 1
+        if g.n_top >= 0:
+            tok_lp, top_ids, top_lp = self.sampler.logprobs(logits, ids, g.n_top)
             self._lp.append((seqs, tok_lp, top_ids, top_lp))
         return ids
 
