@@ -61,8 +61,9 @@ def tile_stats(logits: torch.Tensor):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("B,d,V", [(1, 64, 1000), (1, 512, 3001), (1, 2048, 20000), (1, 4096, 151936),
-                                   (3, 128, 4099), (17, 512, 20000), (100, 192, 9000), (300, 256, 5000),
-                                   (600, 64, 2100), (256, 4096, 151936)])
+                                   (2, 1024, 7001), (3, 2048, 20000), (4, 4096, 151936), (3, 128, 4099),
+                                   (17, 512, 20000), (100, 192, 9000), (300, 256, 5000), (600, 64, 2100),
+                                   (256, 4096, 151936)])
 def test_gpu_lm_head_matches_torch_fp32(B, d, V):
     print(f"lm_head B={B} d={d} V={V}", flush=True)
     hidden, weight = operands(B + d + V, B, d, V)
@@ -104,7 +105,8 @@ def check_logprobs_tiles(logits, tmax, tsum, tokens, n_top, oracle_rows=()):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("B,d,V,n_top", [(4, 256, 1000, 5), (9, 512, 20000, 20), (256, 4096, 151936, 20),
-                                         (2, 128, 151936, 32), (5, 64, 300, 0), (1, 4096, 151936, 20)])
+                                         (2, 128, 151936, 32), (5, 64, 300, 0), (1, 4096, 151936, 20),
+                                         (3, 4096, 151936, 20)])
 def test_gpu_logprobs_tiles_equal_logprobs(B, d, V, n_top):
     print(f"logprobs_tiles B={B} d={d} V={V} n_top={n_top}", flush=True)
     hidden, weight = operands(7 * B + V, B, d, V)

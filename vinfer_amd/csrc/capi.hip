@@ -633,16 +633,18 @@ int vsamp_lm_head(const vsamp_lm_head_args* a, void* stream) {
   l.V = a->vocab;
   l.vec_out = !(reinterpret_cast<uintptr_t>(a->logits) & 15u) && a->logits_stride % 8 == 0;
   static_assert(vs::kLmBN == VSAMP_LM_TILE, "the statistics' tile is the kernel's column tile");
-  // (one row: a matrix-vector product, for the hidden sizes it is built for; batches of at most
-  // 64 rows: 64-row tiles, four times less MFMA work on padding)
+  // (up to 4 rows: matrix-vector products, for the hidden sizes they are built for; batches of
+  // at most 64 rows: 64-row tiles, four times less MFMA work on padding)
   const int cpl = a->dim % 512 == 0 ? a->dim / 512 : 0;  // hidden chunks per lane
-  if (a->batch == 1 && (cpl == 1 || cpl == 2 || cpl == 4 || cpl == 8)) {
+  if (a->batch <= 4 && (cpl == 1 || cpl == 2 || cpl == 4 || cpl == 8)) {
+    const int nb = a->batch == 1 ? 1 : a->batch == 2 ? 2 : 4;
     const dim3 grid(l.nT), block(vs::kGvThreads);
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (cpl == 1) hipLaunchKernelGGL(vs::k_lm_gemv<1>, grid, block, 0, st, l);
-    else if (cpl == 2) hipLaunchKernelGGL(vs::k_lm_gemv<2>, grid, block, 0, st, l);
-    else if (cpl == 4) hipLaunchKernelGGL(vs::k_lm_gemv<4>, grid, block, 0, st, l);
-    else hipLaunchKernelGGL(vs::k_lm_gemv<8>, grid, block, 0, st, l);
+#define VS_GEMV(C, N) if (cpl == C && nb == N) hipLaunchKernelGGL((vs::k_lm_gemv<C, N>), grid, block, 0, st, l)
+    VS_GEMV(1, 1); VS_GEMV(2, 1); VS_GEMV(4, 1); VS_GEMV(8, 1);
+    VS_GEMV(1, 2); VS_GEMV(2, 2); VS_GEMV(4, 2); VS_GEMV(8, 2);
+    VS_GEMV(1, 4); VS_GEMV(2, 4); VS_GEMV(4, 4); VS_GEMV(8, 4);
+#undef VS_GEMV
   } else if (a->batch <= 64)
     hipLaunchKernelGGL(vs::k_lm_head<64>, dim3(l.nT, 1), dim3(vs::kLmThreads), 0, static_cast<hipStream_t>(stream), l);
   else

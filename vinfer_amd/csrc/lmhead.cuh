@@ -243,15 +243,15 @@ __global__ __launch_bounds__(kLmThreads, 1) void k_lm_head(LmHeadArgs a) {
   }
 }
 
-// ---- one batch row: a matrix-vector product ---------------------------------------------------
-// At B = 1 the 64-row tile above loads 63 rows of padding beside each step's weight (a CU's
-// intake, not the HBM, bounds the kernel), so one row takes a kernel of its own: each workgroup
-// computes one 128-column statistics tile, each wave 16 of its weight rows. Lane l holds chunks
-// l + 64 c (c < CPL, d = 512 CPL) of the hidden row in registers and reads the same chunks of
-// each weight row with plain 16-byte loads, three rows ahead; a row's dot product is the lanes'
-// fp32 sums of bf16 pair products (v_dot2) added over the wave. The epilogue is the tile's
-// statistics and its bf16 logits, as above.
-constexpr int kGvThreads = 512;  // 8 waves, 16 rows each
+// ---- a few batch rows: matrix-vector products -------------------------------------------------
+// At B <= 4 the 64-row tile above loads 60 or more rows of padding beside each step's weight (a
+// CU's intake, not the HBM, bounds the kernel), so these batches take a kernel of their own:
+// each workgroup computes one 128-column statistics tile for every row, each wave 16 of its
+// weight rows. Lane l holds chunks l + 64 c (c < CPL, d = 512 CPL) of the NB hidden rows in
+// registers and reads the same chunks of each weight row with plain 16-byte loads, a window of
+// rows ahead; a logit is the lanes' fp32 sums of bf16 pair products (v_dot2) added over the
+// wave. The epilogue is each row's tile statistics and bf16 logits, as above.
+constexpr int kGvThreads = 512;  // 8 waves, 16 weight rows each
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float dot8(uint4 w, uint4 h, float acc) {
@@ -261,19 +261,23 @@ __device__ __forceinline__ float dot8(uint4 w, uint4 h, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), __builtin_bit_cast(bf16x2_t, h.w), acc, false);
 }
 
-template <int CPL>
+// NB hidden rows (B <= NB; rows past the batch repeat its last row, unused)
+template <int CPL, int NB>
 __global__ __launch_bounds__(kGvThreads, 1) void k_lm_gemv(LmHeadArgs a) {
   constexpr int kRowsPerWave = kLmBN / (kGvThreads / kWave);  // 16
-  constexpr int kRing = 4;  // rows in flight per wave
+  constexpr int kRing = NB == 1 ? 4 : 2;  // weight rows in flight per wave (registers: hidden + ring)
   static_assert(kRowsPerWave % kRing == 0, "whole groups of rows");
-  __shared__ float lg[kLmBN];  // the tile's logits, rounded to bf16
+  __shared__ float lg[NB][kLmBN];  // the tile's logits, rounded to bf16
   const int l = lane_id();
   const int w = threadIdx.x / kWave;
   const int n0 = blockIdx.x * kLmBN;
-  const uint4* hid = reinterpret_cast<const uint4*>(as_global(a.hidden));
-  uint4 hv[CPL];
+  uint4 hv[NB][CPL];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) hv[c] = hid[l + 64 * c];
+  for (int b = 0; b < NB; ++b) {
+    const uint4* hid = reinterpret_cast<const uint4*>(as_global(a.hidden) + static_cast<int64_t>(min(b, a.B - 1)) * a.ldh);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) hv[b][c] = hid[l + 64 * c];
+  }
   // row i of this wave: n0 + kRowsPerWave w + i (rows past the vocabulary read the last one)
   auto load_row = [&](int i, uint4 (&dst)[CPL]) {
     const uint4* r = reinterpret_cast<const uint4*>(
@@ -282,33 +286,42 @@ __global__ __launch_bounds__(kGvThreads, 1) void k_lm_gemv(LmHeadArgs a) {
     for (int c = 0; c < CPL; ++c) dst[c] = r[l + 64 * c];
   };
   // a rolling window: slot k holds row kRing g + k and is reloaded with the next group's row as
-  // soon as its dot product is taken (the last group, peeled, reloads nothing)
+  // soon as its dot products are taken (the last group, peeled, reloads nothing)
   uint4 rb[kRing][CPL];
 #pragma unroll
   for (int k = 0; k < kRing; ++k) load_row(k, rb[k]);
   auto group = [&](int g, bool reload) {
 #pragma unroll
     for (int k = 0; k < kRing; ++k) {
-      float s0 = 0.0f, s1 = 0.0f;
+      float s[NB];
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        if (c & 1) s1 = dot8(rb[k][c], hv[c], s1);
-        else s0 = dot8(rb[k][c], hv[c], s0);
+      for (int b = 0; b < NB; ++b) {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          if (c & 1) s1 = dot8(rb[k][c], hv[b][c], s1);
+          else s0 = dot8(rb[k][c], hv[b][c], s0);
+        }
+        s[b] = s0 + s1;
       }
       if (reload) load_row(kRing * (g + 1) + k, rb[k]);
-      const float v = wave_sum<float>(s0 + s1);
-      if (l == 0) lg[kRowsPerWave * w + kRing * g + k] = __uint_as_float(bf16_rne(v) << 16);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float v = wave_sum<float>(s[b]);
+        if (l == 0) lg[b][kRowsPerWave * w + kRing * g + k] = __uint_as_float(bf16_rne(v) << 16);
+      }
     }
   };
 #pragma unroll 1
   for (int g = 0; g < kRowsPerWave / kRing - 1; ++g) group(g, true);
   group(kRowsPerWave / kRing - 1, false);
   __syncthreads();
-  if (w != 0) return;
-  // wave 0: the statistics over the columns inside the vocabulary (lane l: columns l, l + 64),
-  // then the bf16 logits, 16 bytes per lane
+  if (w >= NB || w >= a.B) return;
+  // wave b < B: row b's statistics over the columns inside the vocabulary (lane l: columns l,
+  // l + 64), then its bf16 logits, 16 bytes per lane
+  const int b = w;
   const int ncol = min(kLmBN, a.V - n0);
-  const float x0 = lg[l], x1 = lg[l + 64];
+  const float x0 = lg[b][l], x1 = lg[b][l + 64];
   uint32_t mk = 0;
   if (l < ncol) mk = key_of(x0);
   if (l + 64 < ncol) mk = max(mk, key_of(x1));
@@ -321,16 +334,16 @@ __global__ __launch_bounds__(kGvThreads, 1) void k_lm_gemv(LmHeadArgs a) {
   }
   e = wave_sum<float>(e);
   if (l == 0) {
-    a.tmax[blockIdx.x] = mx;
-    a.tsum[blockIdx.x] = e;
+    a.tmax[static_cast<int64_t>(b) * a.nT + blockIdx.x] = mx;
+    a.tsum[static_cast<int64_t>(b) * a.nT + blockIdx.x] = e;
   }
-  uint16_t* out = as_global(a.logits) + n0;
+  uint16_t* out = as_global(a.logits) + static_cast<int64_t>(b) * a.ldo + n0;
   const int c0 = 8 * l;
   if (l < kLmBN / 8 && c0 < ncol) {
     uint32_t q[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      q[i] = (__float_as_uint(lg[c0 + 2 * i]) >> 16) | (__float_as_uint(lg[c0 + 2 * i + 1]) & 0xFFFF0000u);
+      q[i] = (__float_as_uint(lg[b][c0 + 2 * i]) >> 16) | (__float_as_uint(lg[b][c0 + 2 * i + 1]) & 0xFFFF0000u);
     if (a.vec_out && c0 + 8 <= ncol) {
       *reinterpret_cast<uint4*>(out + c0) = make_uint4(q[0], q[1], q[2], q[3]);
     } else {
