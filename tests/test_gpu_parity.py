@@ -449,6 +449,27 @@ def test_small_top_k_lists_with_tied_values(dtype):
         np.testing.assert_allclose(pr[b], r.probs, rtol=PROB_RTOL, atol=1e-30)
 
 
+@pytest.mark.parametrize("order", ["ascending", "descending", "shuffled"])
+def test_streamed_top_k_candidates_fall_back_on_ordered_rows(order):
+    # fp32 rows with a small top-k take their candidates from a sample of the row's first
+    # stripes: ascending rows (the sample holds the smallest values) overflow the staged list,
+    # descending rows (it holds the largest) stage fewer than K; both fall back to counting the
+    # row and a candidate pass, and must give the oracle's ids
+    rng = np.random.default_rng(31)
+    B, V = 12, 151936
+    x = rng.normal(0, 2, (B, V)).astype(np.float32)
+    if order == "ascending":
+        x.sort(axis=1)
+    elif order == "descending":
+        x = -np.sort(-x, axis=1)
+    params = pack_params([SamplingParams(temperature=float(rng.choice([0.7, 1.0])), top_k=int(k), top_p=0.9)
+                          for k in rng.choice([5, 50, 300], B)])
+    draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
+    w = Workload("ordered", torch.from_numpy(np.ascontiguousarray(x)), params,
+                 torch.from_numpy(rng.random(B, dtype=np.float32)), None, None, draft)
+    check(w, max_tie_frac=0.1)
+
+
 def test_draw_frequencies_match_the_distribution():
     # 20,000 draws of one row with the package's uniforms: TV < 0.015 (test_sampler.py:24-38)
     logits = torch.tensor([2.0, 1.0, 0.5, 0.0, -1.0, -3.0])
