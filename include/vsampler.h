@@ -9,6 +9,9 @@
  *
  * Conventions (all entry points):
  *  - Every buffer is caller-allocated device memory; the library never allocates or frees.
+ *    vsamp_sample's parameter columns, history (ids and offsets) and out_ids may also be pinned
+ *    host memory mapped into the device's address space (hipHostMalloc): the kernels read and
+ *    write them with plain loads and stores, so a one-row call needs no copy either way.
  *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the null stream).
  *    Nothing synchronises the host.
  *  - Return 0 on success, a VSAMP_E_* code otherwise; vsamp_last_error() then describes the
