@@ -186,30 +186,41 @@ def decode_loop(args) -> int:
         g = torch.Generator(device=dev).manual_seed(7)
         draft.head = (draft.head.float() + torch.randn(draft.head.shape, generator=g, device=dev)
                       * draft.head.float().std() * 0.5).to(torch.bfloat16)
-        dec = SpeculativeDecoder(model, hip, draft_model=draft, num_draft=K, num_slots=B, max_seq_len=L)
-    else:
-        dec = BatchDecoder(model, hip, num_slots=B, max_seq_len=L, penalize_prompt=True)
-    rng = np.random.default_rng(1001)
-    ks = (0, 20, 50, 1000)
-    for i in range(B):
-        kw = dict(max_tokens=L - 64, ignore_eos=True, seed=int(rng.integers(0, 2**62)))
-        if not K:
-            kw.update(repetition_penalty=1.05, presence_penalty=0.5, frequency_penalty=0.2)
-        if i % 4 == 0:
-            kw.update(temperature=0.0)
+
+    def run(graphs: bool):
+        """The loop's timed iterations: (decoder, us per iteration, tokens)."""
+        if K:
+            dec = SpeculativeDecoder(model, hip, draft_model=draft, num_draft=K, num_slots=B, max_seq_len=L)
         else:
-            kw.update(temperature=float(rng.uniform(0.3, 1.5)), top_k=ks[i % 4], top_p=float(rng.uniform(0.5, 1.0)))
-        dec.submit(rng.integers(0, V, size=32).tolist(), SamplingParams(**kw))
-    for _ in range(args.warmup):
-        dec.step()
-    torch.cuda.synchronize()
+            # (graphs: the steady membership's iterations replay two captured HIP graphs)
+            dec = BatchDecoder(model, hip, num_slots=B, max_seq_len=L, penalize_prompt=True, graphs=graphs)
+        rng = np.random.default_rng(1001)
+        ks = (0, 20, 50, 1000)
+        for i in range(B):
+            kw = dict(max_tokens=L - 64, ignore_eos=True, seed=int(rng.integers(0, 2**62)))
+            if not K:
+                kw.update(repetition_penalty=1.05, presence_penalty=0.5, frequency_penalty=0.2)
+            if i % 4 == 0:
+                kw.update(temperature=0.0)
+            else:
+                kw.update(temperature=float(rng.uniform(0.3, 1.5)), top_k=ks[i % 4],
+                          top_p=float(rng.uniform(0.5, 1.0)))
+            dec.submit(rng.integers(0, V, size=32).tolist(), SamplingParams(**kw))
+        for _ in range(args.warmup):
+            dec.step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        n_tok = 0
+        for _ in range(args.steps):
+            n_tok += len(dec.step())
+        torch.cuda.synchronize()
+        return dec, (time.perf_counter() - t0) / args.steps * 1e6, n_tok
+
     steps = args.steps
-    t0 = time.perf_counter()
-    n_tok = 0
-    for _ in range(steps):
-        n_tok += len(dec.step())
-    torch.cuda.synchronize()
-    loop_us = (time.perf_counter() - t0) / steps * 1e6
+    eager_us = None
+    if not K:
+        _, eager_us, _ = run(False)
+    dec, loop_us, n_tok = run(not K)
 
     # the two device parts alone, on the same shapes
     slots = torch.arange(B, device=dev)
@@ -266,6 +277,9 @@ def decode_loop(args) -> int:
         },
         "tokens_per_iteration": n_tok / args.steps,
         "us_per_step_loop": loop_us,
+        "graphs": not K,
+        "graph_iterations": getattr(dec, "graph_steps", 0),
+        "us_per_step_loop_without_graphs": eager_us,
         "us_model_step_alone": model_us,
         "us_sampler_call_alone": sampler_us,
         "us_host_and_rest": loop_us - model_us - sampler_us,

@@ -12,6 +12,8 @@ test-local one (``WholeTextStream``) stands in for the engine's.
 
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -273,6 +275,32 @@ def test_gpu_batched_tokens_equal_one_sequence_at_a_time():
 
 
 @pytest.mark.gpu
+def test_gpu_graph_replays_give_the_per_token_tokens():
+    """graphs=True: a membership that holds for two iterations is captured into HIP graphs and
+    replayed while it holds (the program's own eager steps, admissions and waits in between);
+    every token of every request still equals the per-token loop's. One request's tenth token is
+    made a stop id, so requests also end mid-run on a drawn stop (the replayed model step's row
+    of a stopped request is dropped)."""
+    dev = torch.device("cuda", 0)
+    model = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    reqs = [(p, dataclasses.replace(sp, max_tokens=24 + 3 * i))
+            for i, (p, sp) in enumerate(mixed_requests(10, model.vocab_size, seed=11))]
+    first = one_at_a_time(model, hip, reqs[0][0], reqs[0][1], penalize_prompt=True)
+    eos = frozenset({first[9].token_id})
+    print("decode loop with graphs: 10 requests, 6 slots, V 151936 bf16", flush=True)
+    dec = BatchDecoder(model, hip, num_slots=6, max_seq_len=160, penalize_prompt=True, eos_token_ids=eos,
+                       graphs=True, graph_after=2)
+    rids = [dec.submit(p, sp) for p, sp in reqs]
+    done = dec.run()
+    assert dec.graph_steps > 20
+    for i, ((prompt, sp), rid) in enumerate(zip(reqs, rids)):
+        want = one_at_a_time(model, hip, prompt, sp, eos=eos, penalize_prompt=True)
+        assert done[rid] == want, f"request {i}"
+    assert done[rids[0]][-1].finish_reason == "stop" and len(done[rids[0]]) <= 10
+
+
+@pytest.mark.gpu
 def test_gpu_decode_loop_rows_match_the_oracle():
     """Each token the loop draws is the oracle's token for the same logits row, history and
     uniform (rows the tie classifier flags excepted)."""
@@ -300,6 +328,11 @@ def test_gpu_decode_loop_rows_match_the_oracle():
             tok, pos = st.token_id, pos + 1
             history.append(tok)
     assert checked > 20
+
+
+def test_graphs_need_a_gpu_model_and_a_prepared_sampler(cpu_model, ref_sampler):
+    with pytest.raises(ValueError, match="graphs need"):
+        BatchDecoder(cpu_model, ref_sampler, num_slots=2, max_seq_len=16, graphs=True)
 
 
 def test_the_model_hears_when_a_slot_is_released(cpu_model, ref_sampler):

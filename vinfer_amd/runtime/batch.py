@@ -22,6 +22,17 @@ stop strings are not checked.
 Requests join whenever a slot is free (prefill, then their first token is sampled in the same
 iteration as everyone else's next token) and leave as soon as they finish, freeing their slot.
 
+An iteration launches the next model step right behind the draw, on the drawn ids as they lie
+on the device, and waits only for those ids: the host's per-request logic then runs while the
+GPU computes the model step. A request that draws a stop token has had that step computed too;
+its row is dropped (and ``release`` of its slot comes after that step was enqueued).
+
+With ``graphs=True`` (a GPU model whose ``decode`` can be captured), a membership that stays the
+same for ``graph_after`` iterations is captured into two HIP graphs -- the inputs' copy, the
+draw, the history append and the ids' copy back; then the model step on the drawn ids, into the
+logits buffer the draw reads -- and each later iteration of that membership replays them: two
+graph launches instead of a dozen torch and library calls.
+
 Histories for the penalties live on the device, one row of ``max_seq_len + 1`` ids per slot,
 and are handed to the sampler as per-row ranges (no per-step packing): a sampled id is written
 into its row on the device right after the draw. A row's history is the request's generated
@@ -85,7 +96,8 @@ def check_request(prompt_len: int, params: SamplingParams, max_seq_len: int) -> 
 class DecodeModel(Protocol):
     """What the loop needs of a model: a prefill into a slot and a batched one-token step. A
     model may also define ``release(slot)``, called when a slot's request ends (where a state
-    pool would free it, generate.py:146)."""
+    pool would free it, generate.py:146), possibly after one more ``decode`` of that slot was
+    enqueued (the step launched before the request's last token was known to be a stop)."""
 
     device: torch.device
 
@@ -114,10 +126,11 @@ class _Staging:
     def reset(self) -> None:
         self.n = 0
 
-    def reserve(self, n: int) -> int:
-        if self.n + n > self.np.shape[0]:
+    def reserve(self, n: int, align: int = 1) -> int:
+        at = -(-self.n // align) * align
+        if at + n > self.np.shape[0]:
             raise RuntimeError("staging buffer too small")
-        at, self.n = self.n, self.n + n
+        self.n = at + n
         return at
 
     def put(self, words: np.ndarray) -> int:
@@ -161,6 +174,23 @@ class _Group:
     pen_slots: np.ndarray  # int64: the slots of those rows
     params: PackedParams
     n_top: int  # largest top_logprobs of a row asking for log-probabilities, or -1 if none asks
+    key: tuple[int, ...]  # the request ids, in order
+
+
+@dataclass(eq=False)
+class _StepGraphs:
+    """A membership's captured iteration: the draw's graph (inputs' copy, sampler, history
+    append, ids to ``ids_host``) and the model step's (into ``logits``), with what they hold."""
+
+    key: tuple[int, ...]
+    draw: "torch.cuda.CUDAGraph"
+    model: "torch.cuda.CUDAGraph"
+    stage: _Staging
+    logits: torch.Tensor
+    prep: object  # the sampler's prepared launch (its buffers must outlive the graphs)
+    ids_host: torch.Tensor
+    ids_np: np.ndarray
+    pen_slots: np.ndarray
 
 
 class BatchDecoder:
@@ -175,9 +205,13 @@ class BatchDecoder:
         text_stream: Callable[[tuple[str, ...]], TextStream] | None = None,
         seed: int = 0,
         penalize_prompt: bool = False,
+        graphs: bool = False,
+        graph_after: int = 4,
     ) -> None:
         if num_slots < 1 or max_seq_len < 1:
             raise ValueError("num_slots and max_seq_len must be >= 1")
+        if graphs and (model.device.type != "cuda" or not hasattr(sampler, "prepare_batch")):
+            raise ValueError("graphs need a model on a GPU and a sampler with prepare_batch")
         self.model = model
         self.sampler = sampler
         self.num_slots = num_slots
@@ -198,8 +232,20 @@ class BatchDecoder:
         self._hist_row = max_seq_len + 1
         self.hist = torch.zeros(num_slots * self._hist_row, dtype=torch.int32, device=model.device)
         self._hist_len = np.zeros(num_slots, dtype=np.int64)  # ids in each slot's history row
-        # [0]: the sampler's inputs (uniforms, ranges: 3 words a row), [1]: the model's (3 a row)
-        self._stage = (_Staging(model.device, 6 * num_slots), _Staging(model.device, 3 * num_slots))
+        # One step's inputs, one copy: uniforms and ranges (3 words a row), then the next model
+        # step's slots, positions and row indices (int64: 6 words a row), with alignment.
+        self._stage = (_Staging(model.device, 9 * num_slots + 8),)
+        # the drawn ids' host copy, and the event after it (the iteration's one wait)
+        cuda = model.device.type == "cuda"
+        self._ids_host = torch.empty(num_slots, dtype=torch.int32, pin_memory=cuda)
+        self._ids_np = self._ids_host.numpy()
+        self._ids_ready = torch.cuda.Event() if cuda else None
+        self.graphs = graphs
+        self.graph_after = graph_after
+        self._graph: _StepGraphs | None = None
+        self._graph_key: tuple[int, ...] | None = None  # the last eligible membership and its run
+        self._graph_run = 0
+        self.graph_steps = 0  # iterations run by replaying graphs
 
     # ---- requests ------------------------------------------------------------------------------
     def submit(self, prompt_ids: list[int], params: SamplingParams) -> int:
@@ -254,44 +300,131 @@ class BatchDecoder:
             groups.append(admitted)
         if not groups:
             return []
-        # The sampler's per-row inputs of every group go to the device in one copy.
-        st = self._stage[0]
-        st.reset()
-        cols = [self._stage_draw(st, seqs) for seqs, _ in groups]
-        st.send()
-        self._lp = []
-        drawn = [self._draw(seqs, logits, st, c) for (seqs, logits), c in zip(groups, cols)]
         seqs = [s for g in groups for s in g[0]]
-        tokens = torch.cat(drawn).tolist() if len(drawn) > 1 else drawn[0].tolist()  # the one wait
+        n = len(seqs)
+        # rows whose next model step is launched before their token is known: all but the rows
+        # drawing their last token by max_tokens
+        nxt = [i for i, s in enumerate(seqs) if len(s.generated) + 1 < s.params.max_tokens]
+        m = len(nxt)
+        key = None
+        if self.graphs and admitted is None and m == n:
+            g = self._group(seqs, self.model.device)
+            key = g.key if g.n_top < 0 else None
+        if key is not None and key == self._graph_key:
+            self._graph_run += 1
+        else:
+            self._graph_key, self._graph_run = key, 0
+        self._lp = []
+        if key is not None and (self._graph_run >= self.graph_after or (self._graph and self._graph.key == key)):
+            tokens, nxt_logits = self._graph_step(key, seqs, groups[0][1])
+        else:
+            tokens, nxt_logits = self._eager_step(groups, seqs, nxt)
         lp_of = self._host_logprobs() if self._lp else None
         out: list[tuple[int, Step]] = []
         going: list[_Seq] = []
+        keep: list[int] = []  # the rows of nxt_logits that go on
         advance = self._advance
-        for s, tok in zip(seqs, tokens):
+        j = 0  # position in nxt
+        for i, (s, tok) in enumerate(zip(seqs, tokens)):
             step = advance(s, tok)
             if lp_of is not None and s.params.logprobs:
                 step.logprob, top = lp_of[id(s)]
                 step.top_logprobs = top[: s.params.top_logprobs] if s.params.top_logprobs else None
             out.append((s.rid, step))
+            launched = j < m and nxt[j] == i
             if step.finish_reason is None:
                 going.append(s)
+                keep.append(j)
             else:
                 self._retire(s)
-        if len(going) < len(seqs):
+            j += launched
+        if len(going) < n:
             self._free.sort(reverse=True)
         if going:
-            st = self._stage[1]
-            st.reset()
-            n = len(going)
-            at = st.reserve(3 * n)
-            v = st.host_view(at, 3 * n).reshape(3, n)
-            v[0] = np.fromiter((s.slot for s in going), np.int32, n)
-            v[1] = np.fromiter((s.generated[-1] for s in going), np.int32, n)
-            v[2] = np.fromiter((s.position for s in going), np.int32, n) - 1
-            st.send()
-            slots, toks, pos = st.device(at, 3 * n).view(3, n).long()
-            self._pending = (going, self.model.decode(slots, toks, pos))
+            if len(keep) < m:
+                nxt_logits = nxt_logits.index_select(0, torch.tensor(keep, device=nxt_logits.device))
+            self._pending = (going, nxt_logits)
         return out
+
+    def _stage_step(self, st: _Staging, groups, seqs: list[_Seq], nxt) -> tuple[list, int]:
+        """Stage a step's inputs: each group's uniforms and ranges, then the next model step's
+        slots, positions and rows (int64). Returns the groups' columns and the model's offset."""
+        st.reset()
+        cols = [self._stage_draw(st, g) for g, _ in groups]
+        m = len(nxt)
+        at_m = st.reserve(6 * m, align=2)
+        if m:
+            v = st.host_view(at_m, 6 * m).view(np.int64).reshape(3, m)
+            v[0] = np.fromiter((seqs[i].slot for i in nxt), np.int64, m)
+            v[1] = np.fromiter((seqs[i].position for i in nxt), np.int64, m)  # the drawn token's
+            v[2] = nxt
+        return cols, at_m
+
+    def _eager_step(self, groups, seqs: list[_Seq], nxt) -> tuple[list[int], torch.Tensor | None]:
+        """Draw every group, launch the next model step on the drawn ids, wait for the ids."""
+        n, m = len(seqs), len(nxt)
+        st = self._stage[0]
+        cols, at_m = self._stage_step(st, groups, seqs, nxt)
+        st.send()
+        drawn = [self._draw(g, logits, st, c) for (g, logits), c in zip(groups, cols)]
+        ids = torch.cat(drawn) if len(drawn) > 1 else drawn[0]
+        if self._ids_ready is not None:
+            self._ids_host[:n].copy_(ids, non_blocking=True)
+            self._ids_ready.record()
+        else:
+            self._ids_host[:n].copy_(ids)
+        nxt_logits = None
+        if m:
+            mv = st.device(at_m, 6 * m).view(torch.int64).view(3, m)
+            toks = ids if m == n else ids.index_select(0, mv[2])
+            nxt_logits = self.model.decode(mv[0], toks.long(), mv[1])
+        if self._ids_ready is not None:
+            self._ids_ready.synchronize()  # (the draws, not the model step behind them)
+        return self._ids_np[:n].tolist(), nxt_logits
+
+    def _graph_step(self, key, seqs: list[_Seq], logits: torch.Tensor) -> tuple[list[int], torch.Tensor]:
+        """One iteration of a captured membership: the inputs staged at the captured offsets,
+        the draw's graph, the event the host waits for, the model step's graph."""
+        gs = self._graph
+        if gs is None or gs.key != key:
+            self._graph = None  # (the old graphs' memory goes back before the new capture)
+            gs = self._graph = self._capture(key, seqs, logits)
+        if logits is not gs.logits:  # (the first replay: the eager model step's rows)
+            gs.logits.copy_(logits)
+        n = len(seqs)
+        self._stage_step(gs.stage, [(seqs, None)], seqs, range(n))
+        gs.draw.replay()
+        self.graph_steps += 1
+        self._ids_ready.record()
+        gs.model.replay()
+        self._ids_ready.synchronize()
+        if gs.pen_slots.size:
+            self._hist_len[gs.pen_slots] += 1
+        return gs.ids_np[:n].tolist(), gs.logits
+
+    def _capture(self, key, seqs: list[_Seq], logits: torch.Tensor) -> "_StepGraphs":
+        n = len(seqs)
+        dev = logits.device
+        g = self._group(seqs, dev)
+        st = _Staging(dev, 9 * n + 8)
+        cols, at_m = self._stage_step(st, [(seqs, None)], seqs, range(n))
+        at_u, at_r = cols[0]
+        x = torch.empty_like(logits)  # the draw's logits, which the model step's graph rewrites
+        u = st.device(at_u, n).view(torch.float32)
+        ranges = None if at_r is None else st.device(at_r, 2 * n).view(n, 2)
+        prep = self.sampler.prepare_batch(x, g.params, u, None if ranges is None else self.hist, ranges)
+        ids_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+        mv = st.device(at_m, 6 * n).view(torch.int64).view(3, n)
+        draw, model = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(draw):
+            st.dev[: st.n].copy_(st.host[: st.n], non_blocking=True)
+            prep.launch()
+            if ranges is not None:  # the drawn id joins its row's history behind the range used
+                self.hist.index_copy_(0, ranges[:, 1].long(), prep.ids)
+            ids_host.copy_(prep.ids, non_blocking=True)
+        with torch.cuda.graph(model, pool=draw.pool()):
+            x.copy_(self.model.decode(mv[0], prep.ids.long(), mv[1]))
+        return _StepGraphs(key, draw, model, st, x, prep, ids_host, ids_host.numpy(), g.pen_slots)
 
     def run(self) -> dict[int, list[Step]]:
         """Step until every queued request has finished; each request's steps in order."""
@@ -339,7 +472,7 @@ class BatchDecoder:
             pen = np.array([p.penalized for p in ps], dtype=bool)
             lps = [p.top_logprobs for p in ps if p.logprobs]
             g = self._groups[key] = _Group(slots, np.array([p.seed for p in ps], dtype=np.int64), pen, slots[pen],
-                                           pack_params(ps, dev), max(lps) if lps else -1)
+                                           pack_params(ps, dev), max(lps) if lps else -1, key)
         return g
 
     def _params(self, seqs: list[_Seq], dev: torch.device) -> PackedParams:
