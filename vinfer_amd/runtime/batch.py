@@ -28,10 +28,14 @@ GPU computes the model step. A request that draws a stop token has had that step
 its row is dropped (and ``release`` of its slot comes after that step was enqueued).
 
 With ``graphs=True`` (a GPU model whose ``decode`` can be captured), a membership that stays the
-same for ``graph_after`` iterations is captured into two HIP graphs -- the inputs' copy, the
-draw, the history append and the ids' copy back; then the model step on the drawn ids, into the
-logits buffer the draw reads -- and each later iteration of that membership replays them: two
-graph launches instead of a dozen torch and library calls.
+same for ``graph_after`` iterations is captured into HIP graphs -- the inputs' copy, the draw,
+the history append, the ids' copy back, then the model step on the drawn ids into the logits
+buffer the draw reads -- and its later iterations replay them: one graph launch instead of a
+dozen torch and library calls, the staged inputs moved on in place, and the host polls the
+ids' pinned copy instead of waiting for an event. Two such graphs alternate so that, while no
+request waits for a free slot, the next iteration is launched before the host takes this one's
+ids: the host's per-request work then overlaps the GPU's whole iteration. When a row ends, the
+iteration already in flight still draws it; that token is dropped.
 
 Histories for the penalties live on the device, one row of ``max_seq_len + 1`` ids per slot,
 and are handed to the sampler as per-row ranges (no per-step packing): a sampled id is written
@@ -179,18 +183,29 @@ class _Group:
 
 @dataclass(eq=False)
 class _StepGraphs:
-    """A membership's captured iteration: the draw's graph (inputs' copy, sampler, history
-    append, ids to ``ids_host``) and the model step's (into ``logits``), with what they hold."""
+    """A membership's two captured iterations (graph slots 0 and 1, launched alternately), the
+    buffers they hold, and the host views of their staged inputs. Iteration t (counted from the
+    eager state) draws every row at position pos0 + t with history end ends0 + t (rows with
+    penalties) -- every row moves on by one per iteration while the membership lasts."""
 
     key: tuple[int, ...]
-    draw: "torch.cuda.CUDAGraph"
-    model: "torch.cuda.CUDAGraph"
-    stage: _Staging
+    graphs: list
+    keep: list  # per slot: staging, the sampler's prepared launch, the ids' pinned copy
     logits: torch.Tensor
-    prep: object  # the sampler's prepared launch (its buffers must outlive the graphs)
-    ids_host: torch.Tensor
-    ids_np: np.ndarray
+    ids_np: list  # per slot: the drawn ids' pinned copy (numpy view)
     pen_slots: np.ndarray
+    slots: np.ndarray
+    pen: np.ndarray
+    base: np.ndarray  # the rows' history rows' first index
+    pos0: np.ndarray
+    ends0: np.ndarray | None  # (None: no row has penalties)
+    pos: list  # per slot: staged positions (int64 view)
+    seeds: np.ndarray
+    u: list  # per slot: staged uniforms
+    ends: list  # per slot: staged history ends (or None)
+    pen_inc: np.ndarray  # 1 for a row with penalties (its history grows by one a step), else 0
+    t: int = 0  # the next iteration to launch
+    next: int = 0  # the slot it goes to
 
 
 class BatchDecoder:
@@ -246,6 +261,7 @@ class BatchDecoder:
         self._graph_key: tuple[int, ...] | None = None  # the last eligible membership and its run
         self._graph_run = 0
         self.graph_steps = 0  # iterations run by replaying graphs
+        self._inflight: tuple[_StepGraphs, int, list[_Seq]] | None = None  # (graphs, slot, rows)
 
     # ---- requests ------------------------------------------------------------------------------
     def submit(self, prompt_ids: list[int], params: SamplingParams) -> int:
@@ -291,6 +307,8 @@ class BatchDecoder:
     def step(self) -> list[tuple[int, Step]]:
         """Admit what fits, draw one token for every running request, advance the model.
         Returns ``(request id, Step)`` per request that produced a token."""
+        if self._inflight is not None:
+            return self._step_inflight()
         groups = []
         if self._pending is not None:
             groups.append(self._pending)
@@ -340,10 +358,45 @@ class BatchDecoder:
             j += launched
         if len(going) < n:
             self._free.sort(reverse=True)
-        if going:
+        if going and self._inflight is None:  # (with an iteration in flight, it draws them next)
             if len(keep) < m:
                 nxt_logits = nxt_logits.index_select(0, torch.tensor(keep, device=nxt_logits.device))
             self._pending = (going, nxt_logits)
+        return out
+
+    def _step_inflight(self) -> list[tuple[int, Step]]:
+        """An iteration whose graph was launched by the previous call: launch the one after it
+        first when every row is still running and no request waits for a free slot, then take
+        its ids. A row that ended meanwhile (a stop, a cancel) has its token dropped; without a
+        following launch the model step's rows of the rows going on become the pending logits."""
+        gs, slot, rows = self._inflight
+        self._inflight = None
+        alive = [s.rid in self._running for s in rows]
+        if all(alive) and not (self._waiting and self._free):
+            self._launch(gs, 1 - slot)
+            self._inflight = (gs, 1 - slot, rows)
+        tokens = self._wait_ids(gs, slot)
+        out: list[tuple[int, Step]] = []
+        going: list[_Seq] = []
+        keep: list[int] = []
+        advance = self._advance
+        for i, (s, tok) in enumerate(zip(rows, tokens)):
+            if not alive[i]:
+                continue
+            step = advance(s, tok)
+            out.append((s.rid, step))
+            if step.finish_reason is None:
+                going.append(s)
+                keep.append(i)
+            else:
+                self._retire(s)
+        if len(going) < len(rows):
+            self._free.sort(reverse=True)
+        if going and self._inflight is None:
+            x = gs.logits
+            if len(keep) < len(rows):
+                x = x.index_select(0, torch.tensor(keep, device=x.device))
+            self._pending = (going, x)
         return out
 
     def _stage_step(self, st: _Staging, groups, seqs: list[_Seq], nxt) -> tuple[list, int]:
@@ -383,48 +436,94 @@ class BatchDecoder:
         return self._ids_np[:n].tolist(), nxt_logits
 
     def _graph_step(self, key, seqs: list[_Seq], logits: torch.Tensor) -> tuple[list[int], torch.Tensor]:
-        """One iteration of a captured membership: the inputs staged at the captured offsets,
-        the draw's graph, the event the host waits for, the model step's graph."""
+        """An iteration of a captured membership from the eager state: launch it, launch the next
+        one too when no request waits for a free slot (it is then in flight when this returns),
+        and take this one's ids."""
         gs = self._graph
         if gs is None or gs.key != key:
             self._graph = None  # (the old graphs' memory goes back before the new capture)
             gs = self._graph = self._capture(key, seqs, logits)
-        if logits is not gs.logits:  # (the first replay: the eager model step's rows)
+        if logits is not gs.logits:  # (the eager model step's rows)
             gs.logits.copy_(logits)
-        n = len(seqs)
-        self._stage_step(gs.stage, [(seqs, None)], seqs, range(n))
-        gs.draw.replay()
+        # (positions move on from the rows' own: the captured offsets are relative to them)
+        gs.pos0[:] = np.fromiter((s.position for s in seqs), np.int64, len(seqs))
+        if gs.ends0 is not None:
+            gs.ends0[:] = gs.base + np.where(gs.pen, self._hist_len[gs.slots], 0)
+        gs.t = 0
+        slot = gs.next
+        self._launch(gs, slot)
+        if not (self._waiting and self._free):
+            self._launch(gs, 1 - slot)
+            self._inflight = (gs, 1 - slot, seqs)
+        return self._wait_ids(gs, slot), gs.logits
+
+    def _launch(self, gs: "_StepGraphs", slot: int) -> None:
+        """Stage iteration gs.t's inputs in the slot's buffers and launch its graph."""
+        t = gs.t
+        gs.t += 1
+        gs.next = 1 - slot
+        pos = gs.pos[slot]
+        np.add(gs.pos0, t, out=pos)
+        position_uniforms(gs.seeds, pos, out=gs.u[slot])
+        if gs.ends0 is not None:
+            np.add(gs.ends0, t * gs.pen_inc, out=gs.ends[slot])
+        gs.ids_np[slot][:] = -1  # (drawn ids are >= 0)
+        gs.graphs[slot].replay()
         self.graph_steps += 1
-        self._ids_ready.record()
-        gs.model.replay()
-        self._ids_ready.synchronize()
+
+    def _wait_ids(self, gs: "_StepGraphs", slot: int) -> list[int]:
+        """The slot's drawn ids, by polling their pinned copy (the graph writes it before its
+        model step, which runs on meanwhile)."""
+        ids = gs.ids_np[slot]
+        spins = 0
+        while (ids < 0).any():
+            spins += 1
+            if spins == 1 << 20:  # (long past any draw: the graph's end settles it)
+                torch.cuda.current_stream(gs.logits.device).synchronize()
+                if (ids < 0).any():
+                    raise RuntimeError("the drawn ids never reached the host")
         if gs.pen_slots.size:
             self._hist_len[gs.pen_slots] += 1
-        return gs.ids_np[:n].tolist(), gs.logits
+        return ids.tolist()
 
     def _capture(self, key, seqs: list[_Seq], logits: torch.Tensor) -> "_StepGraphs":
+        """Two graphs of the membership's iteration (launched alternately, each with its own
+        staged inputs, so one can be launched while the other's ids are still awaited): the
+        inputs' copy, the draw from ``x``, the history append, the ids to pinned memory, the
+        model step on them into ``x``."""
         n = len(seqs)
         dev = logits.device
         g = self._group(seqs, dev)
-        st = _Staging(dev, 9 * n + 8)
-        cols, at_m = self._stage_step(st, [(seqs, None)], seqs, range(n))
-        at_u, at_r = cols[0]
-        x = torch.empty_like(logits)  # the draw's logits, which the model step's graph rewrites
-        u = st.device(at_u, n).view(torch.float32)
-        ranges = None if at_r is None else st.device(at_r, 2 * n).view(n, 2)
-        prep = self.sampler.prepare_batch(x, g.params, u, None if ranges is None else self.hist, ranges)
-        ids_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
-        mv = st.device(at_m, 6 * n).view(torch.int64).view(3, n)
-        draw, model = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-        with torch.cuda.graph(draw):
-            st.dev[: st.n].copy_(st.host[: st.n], non_blocking=True)
-            prep.launch()
-            if ranges is not None:  # the drawn id joins its row's history behind the range used
-                self.hist.index_copy_(0, ranges[:, 1].long(), prep.ids)
-            ids_host.copy_(prep.ids, non_blocking=True)
-        with torch.cuda.graph(model, pool=draw.pool()):
-            x.copy_(self.model.decode(mv[0], prep.ids.long(), mv[1]))
-        return _StepGraphs(key, draw, model, st, x, prep, ids_host, ids_host.numpy(), g.pen_slots)
+        x = torch.empty_like(logits)  # the draw's logits, which each graph's model step rewrites
+        graphs, keep, pos, us, ends, ids_np = [], [], [], [], [], []
+        for _ in range(2):
+            st = _Staging(dev, 9 * n + 8)
+            cols, at_m = self._stage_step(st, [(seqs, None)], seqs, range(n))
+            at_u, at_r = cols[0]
+            u = st.device(at_u, n).view(torch.float32)
+            ranges = None if at_r is None else st.device(at_r, 2 * n).view(n, 2)
+            prep = self.sampler.prepare_batch(x, g.params, u, None if ranges is None else self.hist, ranges)
+            ids_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+            mv = st.device(at_m, 6 * n).view(torch.int64).view(3, n)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                st.dev[: st.n].copy_(st.host[: st.n], non_blocking=True)
+                prep.launch()
+                if ranges is not None:  # the drawn id joins its row's history behind the range used
+                    self.hist.index_copy_(0, ranges[:, 1].long(), prep.ids)
+                ids_host.copy_(prep.ids, non_blocking=True)
+                x.copy_(self.model.decode(mv[0], prep.ids.long(), mv[1]))
+            graphs.append(graph)
+            keep.append((st, prep, ids_host))
+            # host views of the staged words that move from one iteration to the next
+            pos.append(st.host_view(at_m, 6 * n).view(np.int64).reshape(3, n)[1])
+            us.append(st.host_view(at_u, n).view(np.float32))
+            ends.append(None if at_r is None else st.host_view(at_r, 2 * n).reshape(n, 2)[:, 1])
+            ids_np.append(ids_host.numpy())
+        pen = g.pen
+        return _StepGraphs(key, graphs, keep, x, ids_np, g.pen_slots, g.slots, pen, g.slots * self._hist_row,
+                           np.zeros(n, np.int64), None if ends[0] is None else np.zeros(n, np.int32), pos, g.seeds,
+                           us, ends, pen.astype(np.int32))
 
     def run(self) -> dict[int, list[Step]]:
         """Step until every queued request has finished; each request's steps in order."""
