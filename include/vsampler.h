@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 5
+#define VSAMP_ABI_VERSION 6
 
 /* Bytes of one row's sampling state (vsamp_sample_states), an opaque record. */
 #define VSAMP_ROW_STATE_BYTES 40
@@ -44,6 +44,13 @@ extern "C" {
  * identical either way. On MI355X it is slower than whole rows at every batch measured (the
  * slices' merge needs device-scope fences), so it is off unless asked for. */
 #define VSAMP_SPLIT_ROWS 2u
+/* History append (with VSAMP_HIST_RANGES, vsamp_sample only): each row's drawn id is also
+ * written to hist_ids[end] of its range (the entry right behind the ids it was penalised by),
+ * so a decode loop's history grows on the device without a call of its own. hist_ids must be
+ * writable and hold that entry; no row's range may contain another row's end. No reference
+ * counterpart: for callers that keep per-row histories on the device (a batched decode loop).
+ * Needs penalties on (a history and a penalty column). */
+#define VSAMP_HIST_APPEND 4u
 
 enum vsamp_dtype { VSAMP_BF16 = 0, VSAMP_F32 = 1 };
 
@@ -105,7 +112,7 @@ typedef struct vsamp_args {
   void* workspace;
   size_t workspace_bytes;
 
-  uint32_t flags; /* VSAMP_HIST_RANGES and / or VSAMP_SPLIT_ROWS, or 0 */
+  uint32_t flags; /* VSAMP_HIST_RANGES, VSAMP_SPLIT_ROWS, VSAMP_HIST_APPEND, or 0 */
   uint32_t reserved1;
 } vsamp_args;
 

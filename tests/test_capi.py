@@ -84,7 +84,9 @@ def _args(**kw):
         ({"batch": -1}, 1, "batch"),
         ({"uniforms": None}, 1, "uniforms"),
         ({"out_ids": None}, 1, "out_ids"),
-        ({"flags": 4}, 1, "flags"),
+        ({"flags": 8}, 1, "flags"),
+        ({"flags": 4}, 1, "VSAMP_HIST_APPEND goes with VSAMP_HIST_RANGES"),
+        ({"flags": 5}, 1, "VSAMP_HIST_APPEND needs penalties"),
         ({"draft_ids": 0x4000}, 1, "draft"),
         ({"hist_ids": 0x5000, "hist_total": 10}, 1, "hist"),
         ({"logits": None}, 1, "logits"),

@@ -184,6 +184,37 @@ def test_history_ranges_give_the_csr_results(dtype):
         assert not bad, bad[:10]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_history_append_writes_each_draw_behind_its_range(dtype):
+    """VSAMP_HIST_APPEND: the same draws as without it, each row's id written at its range's end
+    and nothing else of the buffer changed. Histories sit in per-slot regions in a shuffled
+    order, as the decode loop keeps them (fast path and hash table at 151936 / 200000 for bf16;
+    the generic path for fp32)."""
+    for V, seed in ((151936, 31), (200000, 32)):
+        w = random_workload(seed, 24, V, dtype, hist_len=3000)
+        off = w.hist_offsets.tolist()
+        B = w.batch
+        cap = max(off[b + 1] - off[b] for b in range(B)) + 3
+        buf = torch.full((B * cap,), -5, dtype=torch.int32)  # (ids outside [0, V) are ignored)
+        ranges = [None] * B
+        for slot, b in enumerate(np.random.default_rng(seed).permutation(B)):
+            n = off[b + 1] - off[b]
+            buf[slot * cap : slot * cap + n] = w.hist_ids[off[b] : off[b + 1]]
+            ranges[b] = (slot * cap, slot * cap + n)
+        d = w.to(DEV)
+        s = hip(dtype)
+        hb = buf.to(DEV)
+        rg = torch.tensor(ranges, dtype=torch.int32, device=DEV)
+        print(f"history append V={V} {dtype}", flush=True)
+        a = s.sample_batch(d.logits, d.params, d.uniforms, hb, rg, d.draft_ids)
+        hb2 = hb.clone()
+        b_ = s.sample_batch(d.logits, d.params, d.uniforms, hb2, rg, d.draft_ids, append_history=True)
+        assert torch.equal(a[0], b_[0]) and torch.equal(a[1], b_[1])
+        want = hb.clone()
+        want[rg[:, 1].long()] = a[0]
+        assert torch.equal(hb2, want)
+
+
 @pytest.mark.parametrize("name,B", [("mixed_bf16", 64), ("peaked_flat", 64), ("verify_bf16", 24), ("large_fp32", 12), ("single_fp32", 1)])
 def test_workload_rows_match_the_oracle(name, B):
     check(workloads.make(name, batch=B), max_tie_frac=0.1)

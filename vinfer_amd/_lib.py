@@ -11,13 +11,14 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 ROW_STATE_BYTES = 40
 
 VSAMP_BF16 = 0
 VSAMP_F32 = 1
 VSAMP_HIST_RANGES = 1
 VSAMP_SPLIT_ROWS = 2
+VSAMP_HIST_APPEND = 4
 
 STATUS = {0: "ok", 1: "VSAMP_E_ARG", 2: "VSAMP_E_DTYPE", 3: "VSAMP_E_HIP", 4: "VSAMP_E_WORKSPACE", 5: "VSAMP_E_DEVICE"}
 

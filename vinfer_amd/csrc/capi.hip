@@ -173,11 +173,18 @@ int scratch_of_current_device(void** out) {
   return VSAMP_OK;
 }
 
+bool wants_penalties(const vsamp_args* a);
+
 int validate(const vsamp_args* a, bool need_draw) {
   if (!a) return fail(VSAMP_E_ARG, "args is NULL");
-  if (a->flags & ~(VSAMP_HIST_RANGES | VSAMP_SPLIT_ROWS))
-    return fail(VSAMP_E_ARG, "flags must be a combination of VSAMP_HIST_RANGES and VSAMP_SPLIT_ROWS, got %u",
+  if (a->flags & ~(VSAMP_HIST_RANGES | VSAMP_SPLIT_ROWS | VSAMP_HIST_APPEND))
+    return fail(VSAMP_E_ARG,
+                "flags must be a combination of VSAMP_HIST_RANGES, VSAMP_SPLIT_ROWS and VSAMP_HIST_APPEND, got %u",
                 a->flags);
+  if ((a->flags & VSAMP_HIST_APPEND) && (!need_draw || !(a->flags & VSAMP_HIST_RANGES)))
+    return fail(VSAMP_E_ARG, "VSAMP_HIST_APPEND goes with VSAMP_HIST_RANGES, in a call that draws");
+  if ((a->flags & VSAMP_HIST_APPEND) && !wants_penalties(a))
+    return fail(VSAMP_E_ARG, "VSAMP_HIST_APPEND needs penalties on (a history and a penalty column)");
   if (a->dtype != VSAMP_BF16 && a->dtype != VSAMP_F32)
     return fail(VSAMP_E_DTYPE, "unsupported logits dtype %d (VSAMP_BF16=0, VSAMP_F32=1)", a->dtype);
   if (a->batch < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", a->batch);
@@ -254,6 +261,8 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
                vs::RowState* state = nullptr, int param_div = 1) {
   const bool pen = wants_penalties(a);
   if (state && pen) return fail(VSAMP_E_ARG, "row states are written without penalties only");
+  if ((a->flags & VSAMP_HIST_APPEND) && (state || probs))
+    return fail(VSAMP_E_ARG, "VSAMP_HIST_APPEND goes with a call that draws from penalised rows");
   vs::SampleArgs s;
   std::memset(&s, 0, sizeof s);
   if (pen) {
@@ -263,6 +272,8 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
     s.pen = penalty_args(a, s.ws);
     s.has_exc = 1;
     s.off = a->hist_offsets;
+    // (the drawn id goes behind each row's range: the caller's history buffer is writable)
+    if (a->flags & VSAMP_HIST_APPEND) s.hist_out = const_cast<int32_t*>(a->hist_ids);
   }
   s.logits = a->logits;
   s.stride = a->row_stride;

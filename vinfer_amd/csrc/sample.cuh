@@ -54,6 +54,7 @@ struct SampleArgs {
   const float* u;
   const int32_t* draft;
   int32_t* out_ids;
+  int32_t* hist_out;  // when non-null, each row's drawn id also goes to hist_out[its history's end]
   float* out_dprob;
   float* out_probs;  // probs mode when non-null
   int64_t probs_stride;
@@ -965,6 +966,7 @@ __device__ __forceinline__ void finish(const SampleArgs& a, const Row<Tin>& row,
   if (tid == 0) {
     a.out_ids[r] = tok;
     if (a.out_dprob) a.out_dprob[r] = static_cast<float>(dprob);
+    if (a.hist_out) a.hist_out[p.h1] = tok;  // (STATE launches carry no history: never set there)
   }
 }
 
@@ -2720,6 +2722,7 @@ __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
   a.u = as_global(a.u);
   a.draft = as_global(a.draft);
   a.out_ids = as_global(a.out_ids);
+  a.hist_out = as_global(a.hist_out);
   a.out_dprob = as_global(a.out_dprob);
   a.out_probs = as_global(a.out_probs);
   a.out_state = as_global(a.out_state);

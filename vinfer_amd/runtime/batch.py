@@ -101,7 +101,9 @@ class DecodeModel(Protocol):
     """What the loop needs of a model: a prefill into a slot and a batched one-token step. A
     model may also define ``release(slot)``, called when a slot's request ends (where a state
     pool would free it, generate.py:146), possibly after one more ``decode`` of that slot was
-    enqueued (the step launched before the request's last token was known to be a stop)."""
+    enqueued (the step launched before the request's last token was known to be a stop), and
+    ``decode_into(slots, tokens, positions, out)``, ``decode`` writing its logits into ``out``
+    (the captured loop then needs no copy of them)."""
 
     device: torch.device
 
@@ -256,6 +258,7 @@ class BatchDecoder:
         self._ids_np = self._ids_host.numpy()
         self._ids_ready = torch.cuda.Event() if cuda else None
         self.graphs = graphs
+        self._appends = bool(getattr(sampler, "appends_history", False))
         self.graph_after = graph_after
         self._graph: _StepGraphs | None = None
         self._graph_key: tuple[int, ...] | None = None  # the last eligible membership and its run
@@ -495,6 +498,7 @@ class BatchDecoder:
         dev = logits.device
         g = self._group(seqs, dev)
         x = torch.empty_like(logits)  # the draw's logits, which each graph's model step rewrites
+        decode_into = getattr(self.model, "decode_into", None)
         graphs, keep, pos, us, ends, ids_np = [], [], [], [], [], []
         for _ in range(2):
             st = _Staging(dev, 9 * n + 8)
@@ -502,17 +506,22 @@ class BatchDecoder:
             at_u, at_r = cols[0]
             u = st.device(at_u, n).view(torch.float32)
             ranges = None if at_r is None else st.device(at_r, 2 * n).view(n, 2)
-            prep = self.sampler.prepare_batch(x, g.params, u, None if ranges is None else self.hist, ranges)
+            append = {"append_history": True} if ranges is not None and self._appends else {}
+            prep = self.sampler.prepare_batch(x, g.params, u, None if ranges is None else self.hist, ranges,
+                                              **append)
             ids_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
             mv = st.device(at_m, 6 * n).view(torch.int64).view(3, n)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 st.dev[: st.n].copy_(st.host[: st.n], non_blocking=True)
                 prep.launch()
-                if ranges is not None:  # the drawn id joins its row's history behind the range used
+                if ranges is not None and not append:  # the drawn id joins its row's history
                     self.hist.index_copy_(0, ranges[:, 1].long(), prep.ids)
                 ids_host.copy_(prep.ids, non_blocking=True)
-                x.copy_(self.model.decode(mv[0], prep.ids.long(), mv[1]))
+                if decode_into is not None:
+                    decode_into(mv[0], prep.ids.long(), mv[1], x)
+                else:
+                    x.copy_(self.model.decode(mv[0], prep.ids.long(), mv[1]))
             graphs.append(graph)
             keep.append((st, prep, ids_host))
             # host views of the staged words that move from one iteration to the next
@@ -604,10 +613,14 @@ class BatchDecoder:
         if at_r is None:
             ids, _ = self.sampler.sample_batch(logits, g.params, u)
         else:
+            # The drawn id joins its row's history right behind the range just used (by the
+            # sampler's own launch when it can).
             ranges = st.device(at_r, 2 * n).view(n, 2)
-            ids, _ = self.sampler.sample_batch(logits, g.params, u, self.hist, ranges)
-            # The drawn id joins its row's history right behind the range just used.
-            self.hist.index_copy_(0, ranges[:, 1].long(), ids)
+            if self._appends:
+                ids, _ = self.sampler.sample_batch(logits, g.params, u, self.hist, ranges, append_history=True)
+            else:
+                ids, _ = self.sampler.sample_batch(logits, g.params, u, self.hist, ranges)
+                self.hist.index_copy_(0, ranges[:, 1].long(), ids)
             self._hist_len[g.pen_slots] += 1
         if g.n_top >= 0:
             tok_lp, top_ids, top_lp = self.sampler.logprobs(logits, ids, g.n_top)

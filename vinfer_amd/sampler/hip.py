@@ -50,6 +50,8 @@ class HipSampler:
         self._lib = _lib.load()
         self._workspace = torch.empty(0, dtype=torch.uint8)
         self._tokens: dict[torch.device, _TokenPath] = {}  # the per-token call's buffers
+        # sample_batch / prepare_batch take append_history (VSAMP_HIST_APPEND)
+        self.appends_history = True
         # Split small bf16 batches' rows over several workgroups (VSAMP_SPLIT_ROWS): identical
         # results, slower than whole rows on MI355X at every batch measured, so off by default.
         self.split_rows = False
@@ -72,7 +74,8 @@ class HipSampler:
             raise ValueError(f"{name} must be a {dtype} [{n}] tensor on {dev}")
         return t.contiguous()
 
-    def _args(self, logits, params, hist_ids, hist_offsets, uniforms=None, draft_ids=None, param_rows=None):
+    def _args(self, logits, params, hist_ids, hist_offsets, uniforms=None, draft_ids=None, param_rows=None,
+              append_history=False):
         dev = self._device(logits)
         B, V = logits.shape
         P = B if param_rows is None else param_rows  # parameter entries (verify: one per sequence)
@@ -121,6 +124,8 @@ class HipSampler:
         a.hist_offsets = _ptr(hist_offsets) if hist_total else None
         a.hist_total = hist_total
         a.flags = (flags if hist_total else 0) | (_lib.VSAMP_SPLIT_ROWS if self.split_rows else 0)
+        if append_history:  # (the library checks that ranges and a penalty column come with it)
+            a.flags |= _lib.VSAMP_HIST_APPEND
         if uniforms is not None:
             uniforms = self._vec(uniforms, P, torch.float32, dev, "uniforms")
             a.uniforms = _ptr(uniforms)
@@ -144,11 +149,13 @@ class HipSampler:
         return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
     # ---- the interface ----------------------------------------------------------------------
-    def prepare_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
+    def prepare_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None,
+                      append_history=False):
         """A reusable launch of ``sample_batch`` on fixed buffers: every check and the argument
         block are done once; ``PreparedStep.launch()`` then only enqueues the kernel. Outputs
         land in ``PreparedStep.ids`` / ``.draft_prob``; inputs may be refilled in place."""
-        a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids)
+        a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids,
+                             append_history=append_history)
         if a.workspace_bytes:  # a private workspace: steps prepared together may overlap
             ws = torch.empty(a.workspace_bytes + 256, dtype=torch.uint8, device=logits.device)
             a.workspace = (ws.data_ptr() + 255) & ~255
@@ -160,8 +167,12 @@ class HipSampler:
         a.out_draft_prob = _ptr(dprob)
         return PreparedStep(self._lib, a, keep, ids, dprob)
 
-    def sample_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
-        a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids)
+    def sample_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None,
+                     append_history=False):
+        """``SamplerBackend.sample_batch``; with ``append_history`` (per-row ranges into a writable
+        ``hist_ids``, penalties on) each row's drawn id is also written at its range's end."""
+        a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids,
+                             append_history=append_history)
         dev = logits.device
         B = logits.shape[0]
         ids = torch.empty(B, dtype=torch.int32, device=dev)

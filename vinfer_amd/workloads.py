@@ -179,6 +179,11 @@ class SyntheticLM:
         h = self.emb[tokens] + self.pos[positions % 64]
         return h @ self.head
 
+    def decode_into(self, slots: torch.Tensor, tokens: torch.Tensor, positions: torch.Tensor,
+                    out: torch.Tensor) -> None:
+        """``decode`` with its logits written into ``out`` ``[B, V]``."""
+        torch.matmul(self.emb[tokens] + self.pos[positions % 64], self.head, out=out)
+
     def prefill(self, slot: int, prompt_ids: torch.Tensor) -> torch.Tensor:
         n = int(prompt_ids.shape[0])
         last = prompt_ids[n - 1 :]
