@@ -509,6 +509,53 @@ def lm_head_bench(args) -> int:
     return 0
 
 
+def regimes_bench(args) -> int:
+    """``--regimes``: the headline batch (B=256, V=151936 bf16) split by regime: its flat rows
+    alone, its peaked rows alone, each with and without the rows' histories, then the mixed
+    batch itself. One JSON line each, timed as ``--workloads`` times a workload (the launches
+    of a variant follow each other in this order, which a counter run pairs with dispatches)."""
+    import dataclasses
+
+    import torch
+
+    from vinfer_amd.registry import BackendContext
+    from vinfer_amd.sampler import SAMPLER
+    from vinfer_amd.workloads import make
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    s = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    stream = torch.cuda.current_stream(dev)
+    K = max(1, args.steps // 4)
+    variants = []
+    for regime in ("flat", "peaked"):
+        w = make("peaked_flat", regime=regime)
+        variants.append((regime, True, w))
+        variants.append((regime, False, dataclasses.replace(w, hist_ids=None, hist_offsets=None)))
+    variants.append(("mixed (the headline batch)", True, make("peaked_flat")))
+    for regime, hist, w in variants:
+        d = w.to(dev)
+        sets = [d.logits] + [torch.roll(d.logits, shifts=7919 * i, dims=1).contiguous() for i in range(1, N_SETS)]
+        steps = [s.prepare_batch(x, d.params, d.uniforms, d.hist_ids, d.hist_offsets) for x in sets]
+        for i in range(args.warmup):
+            steps[i % len(steps)].launch(stream.cuda_stream)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(K):
+            steps[i % len(steps)].launch(stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / K
+        algo = w.algorithmic_bytes()
+        print(json.dumps({"workload": "peaked_flat", "regime": regime, "histories": hist, "batch": w.batch,
+                          "vocab": w.vocab, "us_per_launch": us, "rows_per_s": w.batch / (us * 1e-6),
+                          "launches": K, "warmup": args.warmup, "input_sets": len(sets), "algorithmic_bytes": algo,
+                          "roofline_frac": algo / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}), flush=True)
+        del steps, sets, d
+    return 0
+
+
 def workloads_bench(args) -> int:
     """``--workloads``: every named sampler workload (``vinfer_amd.workloads.NAMES``), one JSON line
     each: the launch time (back-to-back launches between HIP events on the launch stream, after
@@ -616,6 +663,8 @@ def main() -> int:
     ap.add_argument("--verify", action="store_true", help="time the speculative-decoding verify instead")
     ap.add_argument("--logprobs", action="store_true", help="time the raw log-probabilities instead")
     ap.add_argument("--workloads", action="store_true", help="time every named workload (one line each)")
+    ap.add_argument("--regimes", action="store_true",
+                    help="time the headline batch's flat and peaked rows apart, with and without histories")
     ap.add_argument("--lm-head", action="store_true",
                     help="time the LM head + log-probabilities, fused against torch's matmul + vsamp_logprobs")
     ap.add_argument("--split-rows", action="store_true",
@@ -636,6 +685,8 @@ def main() -> int:
         return verify_bench(args)
     if args.logprobs:
         return logprobs_bench(args)
+    if args.regimes:
+        return regimes_bench(args)
     if args.workloads:
         return workloads_bench(args)
     if args.lm_head:
