@@ -2700,7 +2700,26 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
       row.bm = reinterpret_cast<const uint8_t*>(bmw);
     }
   }
-  resolve_idr<STATE>(a, row, p, k, srch);
+  // the partial cutoff group's r-th member (row states, probabilities, a draft inside that group):
+  // the member search from the kept low bytes, as for the draw, where its cells fit (then cleared
+  // again for the draw's search), else a pass over the row
+  if (k.partial) {
+    bool need = STATE || a.out_probs != nullptr;
+    if (!need && p.draft >= 0 && p.draft < row.V && a.out_dprob) need = value_of(row, p.draft, &srch.vslot) == k.vc;
+    if (need) {  // (uniform)
+      int id = -1;
+      if (cells_fit) {
+        uint8_t* cells = reinterpret_cast<uint8_t*>(hist + kMatchOffset);
+        id = select_member(row, f, ne, k.vc, static_cast<u64>(k.r - 1), cells, mxk, low);
+        const int ncq = cells_per(row) * kThreads / 16;
+        for (int i = tid; i < ncq; i += kThreads) reinterpret_cast<uint4*>(cells)[i] = make_uint4(0, 0, 0, 0);
+        if (tid == 0) f.si[6] = -1;
+        lds_barrier();
+      }
+      const float vc = k.vc;
+      k.idr = id >= 0 ? id : find_first(row, [&](float x, int) -> u64 { return x == vc; }, static_cast<u64>(k.r - 1), srch);
+    }
+  }
   int draw = 0;
   if (!a.out_probs) {
     if constexpr (SPLIT) draw = split_find(a, row, f, ne, vd, j, srch, hist + kMatchOffset, recs);
