@@ -330,18 +330,23 @@ __device__ __forceinline__ void residual_item(const VerifyArgs& a, int b, int sl
         }
       }
     }
+    // The stripe sums go to the other slices as relaxed agent-scope atomic stores, which are
+    // coherent across the XCDs' L2s by themselves; each writer waits for its stores to complete
+    // (vmcnt counts stores too) before the workgroup barrier and the counter's atomic add, and
+    // the last slice loads them with agent-scope atomic loads only after that add has returned.
+    // Device-scope fences (an L2 write-back and an invalidate per slice, ~15 us of a call)
+    // are not needed for these few words; nothing else crosses workgroups here.
     __syncthreads();
     if (tid < j_end - j_begin) {
       u64 t = 0;
       for (int w = 0; w < kWaves; ++w) t += cell[w][tid];
-      a.sums[b * kMaxStripes + j_begin + tid] = t;
-      __threadfence();
+      __hip_atomic_store(&a.sums[b * kMaxStripes + j_begin + tid], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
     if (tid == 0) si[2] = static_cast<int>(atomicAdd(&a.done[b], 1u));
     __syncthreads();
     if (si[2] != slices - 1) return;  // (uniform) another slice finishes the row
-    __threadfence();
     // 2. (last slice) stripe totals; the stripe where the running sum passes floor(m * R / 2^24)
     if (wv == 0) {
       const int j = lane_id();
