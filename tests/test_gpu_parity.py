@@ -532,7 +532,8 @@ def test_per_token_call_matches_the_batch():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
 def test_per_token_call_matches_the_oracle(dtype):
     # the engine's unchanged call (generate.py:129) at the model's vocabulary, one row per call,
-    # with penalties over a history passed as a list and as a device tensor, against the oracle
+    # with penalties over a history passed as a list, a device int32 tensor (read in place), a
+    # host int64 tensor and a device int64 tensor, against the oracle
     from oracle.sampler_oracle import sample_batch as oracle_batch
 
     s = hip(dtype)
@@ -549,8 +550,9 @@ def test_per_token_call_matches_the_oracle(dtype):
     ]
     print(f"per-token call V={V} {dtype}", flush=True)
     for ci, (sp, hist) in enumerate(cases):
-        for pos in range(6):
-            h = torch.tensor(hist, dtype=torch.int32, device=DEV) if pos % 2 else hist
+        for pos in range(8):
+            h = [hist, torch.tensor(hist, dtype=torch.int32, device=DEV), torch.tensor(hist, dtype=torch.int64),
+                 torch.tensor(hist, dtype=torch.int64, device=DEV)][pos % 4]
             tok = s.sample(row, sp, 11 + ci, pos, history=h if sp.penalized else None)
             hi = np.asarray(hist, dtype=np.int32)
             res = oracle_batch(xs[None], [sp.temperature], [sp.top_k], [sp.top_p], [sp.min_p],

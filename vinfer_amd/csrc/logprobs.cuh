@@ -83,10 +83,166 @@ __device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk,
   return (hi << 8) | sh[0];
 }
 
+// bf16 rows in one pass: the row's 16-bit key histogram (u16 counts, two keys a word) gives the
+// max, the normaliser (each populated key's count times the fp32 exponential of its value, summed
+// in fp64: the terms the per-element sum adds) and the n-th largest key; each thread keeps the
+// three largest elements it read (packed key and position, by a min/max insertion), and those
+// >= the n-th key are the candidate list, complete unless some thread's third is >= that key.
+// Returns false, with no output written, for a row it does not serve -- unaligned, a NaN, an
+// infinite or no finite max, a key count past 2^16, an n-th largest value <= 0 (where -0.0 and
+// +0.0 would need their ties by id), an incomplete list -- and the caller runs its two passes.
+// On success `kn32` is the n-th largest key as an ordered 32-bit key.
+__device__ __forceinline__ bool lp_one_pass(const LogprobArgs& a, const Row<uint16_t>& row, uint32_t* hist, Cand* cand,
+                                            uint32_t* sh, uint32_t* red32, u64* red64, float& M, bool& finite,
+                                            double& lse, uint32_t& kn32) {
+  const int tid = threadIdx.x;
+  const int V = row.V;
+  const int n = a.n_top;
+  if (!row.vec) return false;  // (uniform)
+  const int nfull = V / kBlk;
+  // (a row without a whole block loads a constant block instead, unused)
+  const uint4* blocks = reinterpret_cast<const uint4*>(nfull > 0 ? row.p : g_unused_block);
+  // blocks tid + 1024 m; kAhead of them in flight while the previous kAhead are counted
+  constexpr int kAhead = 4;
+  uint4 d[kAhead];
+#pragma unroll
+  for (int k = 0; k < kAhead; ++k) d[k] = ld_global_u4(blocks + min(k * kThreads + tid, max(nfull - 1, 0)));
+  for (int i = tid; i < 32768 / 4; i += kThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0, 0, 0, 0);
+  if (tid < 8) sh[tid] = 0;
+  __syncthreads();
+  // This thread's three largest elements as packed words (key << 16 | 0xFFFF - its position
+  // among the thread's elements: equal keys keep the first); the position is 8m + e for element
+  // e of block tid + 1024m, and 4096 for the ragged tail's one.
+  uint32_t t1 = 0, t2 = 0, t3 = 0;
+  auto keep = [&](uint32_t k, uint32_t pos) {
+    const uint32_t pk = (k << 16) | (0xFFFFu - pos);
+    const uint32_t x = min(t1, pk);
+    t1 = max(t1, pk);
+    const uint32_t y = min(t2, x);
+    t2 = max(t2, x);
+    t3 = max(t3, y);
+  };
+  const int rounds = (nfull + kAhead * kThreads - 1) / (kAhead * kThreads);  // (uniform)
+  for (int it = 0; it < rounds; ++it) {
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) {
+      const int m = it * kAhead + k;
+      const uint4 q = d[k];
+      d[k] = ld_global_u4(blocks + min((m + kAhead) * kThreads + tid, max(nfull - 1, 0)));
+      if (m * kThreads + tid < nfull) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // ordered keys of both halves at once: xor with (sign ? 0xFFFF : 0x8000)
+          const uint32_t s2 = (w[j] >> 15) & 0x00010001u;
+          const uint32_t k2 = w[j] ^ (s2 * 0x7FFFu | 0x80008000u);
+          const uint32_t klo = k2 & 0xFFFFu, khi = k2 >> 16;
+          atomicAdd(&hist[klo >> 1], 1u << ((klo & 1u) << 4));
+          atomicAdd(&hist[khi >> 1], 1u << ((khi & 1u) << 4));
+          keep(klo, static_cast<uint32_t>(8 * m + 2 * j));
+          keep(khi, static_cast<uint32_t>(8 * m + 2 * j + 1));
+        }
+      }
+    }
+  }
+  for (int i = nfull * kBlk + tid; i < V; i += kThreads) {  // (fewer than kBlk elements: tid < 8)
+    const uint32_t k = ok16(ld_global(row.p + i));
+    atomicAdd(&hist[k >> 1], 1u << ((k & 1u) << 4));
+    keep(k, 4096u);
+  }
+  __syncthreads();
+  // the max (keys 0x0080 .. 0xFF7F are the finite values; below and above them lie -inf, +inf
+  // and the NaNs)
+  const uint32_t mk = static_cast<uint32_t>(block_max_u64(static_cast<u64>(t1 >> 16), red64));
+  if (!(mk > 0x007Fu && mk < 0xFF80u)) return false;  // (uniform)
+  M = val16(mk);
+  finite = true;
+  // the normaliser: words tid + 1024 i (the populated keys spread over every thread), each key's
+  // count times its exponential; then the count of this thread's 64 consecutive keys (words
+  // 32 tid .. 32 tid + 31)
+  double s = 0.0;
+  uint32_t nan = 0;
+#pragma unroll 4
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t wd = hist[tid + i * kThreads];
+    if (!wd) continue;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t cnt = h ? wd >> 16 : wd & 0xFFFFu;
+      const uint32_t key = 2u * (tid + i * kThreads) + h;
+      if (key < 0x007Fu || key > 0xFF80u) nan += cnt;
+      else if (cnt) s += static_cast<double>(cnt) * static_cast<double>(__expf(val16(key) - M));
+    }
+  }
+  uint32_t c = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint4 v4 = reinterpret_cast<const uint4*>(hist + 32 * tid)[(q + tid) & 7];  // (rotated: banks)
+    c += (v4.x & 0xFFFFu) + (v4.x >> 16) + (v4.y & 0xFFFFu) + (v4.y >> 16) + (v4.z & 0xFFFFu) + (v4.z >> 16) +
+         (v4.w & 0xFFFFu) + (v4.w >> 16);
+  }
+  if (nan) sh[4] = 1;  // (read after the scan's barriers)
+  uint32_t total;
+  const uint32_t ex = block_excl_scan<uint32_t>(c, red32, &total);
+  if (total != static_cast<uint32_t>(V) || sh[4]) {  // (uniform: a count wrapped, or NaNs)
+    __syncthreads();  // (every thread has read the flag before the two passes reset sh)
+    return false;
+  }
+  s = block_sum<double>(s, reinterpret_cast<double*>(red64));
+  lse = static_cast<double>(M) + log(s);
+  if (n <= 0) return true;
+  // the n-th largest key: the thread whose keys hold it walks its counts from the top
+  const uint32_t nn = static_cast<uint32_t>(n) < static_cast<uint32_t>(V) ? static_cast<uint32_t>(n)
+                                                                         : static_cast<uint32_t>(V);
+  const uint32_t above = total - ex - c;  // elements in the keys above this thread's
+  if (above < nn && nn <= above + c) {
+    uint32_t wc[32];  // (one thread: its words, all loads issued before the walk)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint4 v4 = reinterpret_cast<const uint4*>(hist + 32 * tid)[q];
+      wc[4 * q] = v4.x;
+      wc[4 * q + 1] = v4.y;
+      wc[4 * q + 2] = v4.z;
+      wc[4 * q + 3] = v4.w;
+    }
+    uint32_t run = above;
+#pragma unroll
+    for (int i = 31; i >= 0; --i) {
+#pragma unroll
+      for (int h = 1; h >= 0; --h) {
+        const uint32_t cnt = h ? wc[i] >> 16 : wc[i] & 0xFFFFu;
+        if (run < nn && nn <= run + cnt) {
+          sh[5] = 64u * tid + 2u * i + h;
+          sh[7] = run + cnt;  // elements >= it
+        }
+        run += cnt;
+      }
+    }
+  }
+  __syncthreads();  // (the histogram is dead: the list goes over it)
+  const uint32_t kn = sh[5];
+  const bool positive = val16(kn) > 0.0f;  // (uniform)
+  if (positive) {
+    auto id_of = [&](uint32_t pk) -> int {
+      const uint32_t pos = 0xFFFFu - (pk & 0xFFFFu);
+      return pos == 4096u ? nfull * kBlk + tid : static_cast<int>(((pos >> 3) * kThreads + tid) * kBlk + (pos & 7u));
+    };
+    if ((t3 >> 16) >= kn && t3) sh[6] = 1;  // (this thread may hold more of them than it kept)
+    if (t1 && (t1 >> 16) >= kn) cand[atomicAdd(&sh[1], 1u)] = Cand{val16(t1 >> 16), id_of(t1)};
+    if (t2 && (t2 >> 16) >= kn) cand[atomicAdd(&sh[1], 1u)] = Cand{val16(t2 >> 16), id_of(t2)};
+  }
+  __syncthreads();
+  const bool ok = positive && !sh[6] && sh[1] == sh[7];
+  __syncthreads();  // (every thread has the verdict before the two passes of a fallback reset sh)
+  kn32 = key_of(val16(kn));
+  return ok;
+}
+
 template <class Tin, bool TILES = false>
 __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
   constexpr int kBins = 8192;  // by the top 13 bits of the ordered key
-  __shared__ uint32_t h13[kBins];  // (then the candidate list: kCandCap 8-byte entries)
+  constexpr bool kOnePass = sizeof(Tin) == 2 && !TILES;  // (bf16 rows: one pass over a 16-bit histogram)
+  __shared__ uint32_t h13[kOnePass ? 32768 : kBins];  // (then the candidate list: kCandCap 8-byte entries)
   __shared__ Radix rdx;
   __shared__ Search srch;
   __shared__ Cand top[kMaxTop];
@@ -191,6 +347,11 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
       front = false;
     }
   }
+  uint32_t kn32 = 0;  // (one pass) the n-th largest key, known from the histogram
+  if constexpr (kOnePass) {
+    if (lp_one_pass(a, row, h13, cand, sh, rdx.hcnt, srch.red64, M, finite, lse, kn32)) front = false;  // (uniform)
+  }
+  const bool known = kOnePass && !front;
   if (front) {
   for (int i = tid; i < kBins; i += kThreads) h13[i] = 0;
   if (tid < 8) sh[tid] = 0;
@@ -263,92 +424,112 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
                                                                             : static_cast<uint32_t>(a.V);
   const bool listed = nc <= static_cast<uint32_t>(kCandCap);
   const CandList cl{cand, static_cast<int>(listed ? nc : 0)};
-  const uint32_t kk = listed ? radix_kth(row, &cl, nn, rdx) : radix_kth(row, nullptr, nn, rdx);
-  // 4. the elements above it (fewer than nn), then the first of those equal to it by id
-  if (tid == 0) sh[2] = 0;
-  __syncthreads();
-  if (listed) {
-    for (int i = tid; i < static_cast<int>(nc); i += kThreads) {
-      const Cand c = cand[i];
-      if (key_of(c.x) > kk) {
-        const uint32_t at = atomicAdd(&sh[2], 1u);
-        if (at < static_cast<uint32_t>(kMaxTop)) top[at] = c;
-      }
-    }
-  } else {
-    for_each(row, [&](float x, int id) {
-      if (key_of(x) > kk) {
-        const uint32_t at = atomicAdd(&sh[2], 1u);
-        if (at < static_cast<uint32_t>(kMaxTop)) top[at] = Cand{x, id};
-      }
-    });
-  }
-  __syncthreads();
-  const uint32_t na = sh[2];
-  const uint32_t need = nn - na;
-  if (listed) {
-    // a tied entry's place: the tied entries with a smaller id
-    for (int i = tid; i < static_cast<int>(nc); i += kThreads) {
-      const Cand c = cand[i];
-      if (key_of(c.x) != kk) continue;
+  const uint32_t kk = known ? kn32 : listed ? radix_kth(row, &cl, nn, rdx) : radix_kth(row, nullptr, nn, rdx);
+  if (known && nc <= static_cast<uint32_t>(kWave)) {  // (uniform)
+    // 4/5. (one pass, a short list: every element >= the n-th key) wave 0 ranks the list by
+    // descending value, then ascending id, and writes the first nn
+    if (tid < kWave) {
+      const bool v = static_cast<uint32_t>(tid) < nc;
+      const Cand c = v ? cand[tid] : Cand{0.0f, 0};
+      const uint32_t kc = key_of(c.x);
       uint32_t rank = 0;
-      for (int j = 0; j < static_cast<int>(nc); ++j) rank += key_of(cand[j].x) == kk && cand[j].id < c.id;
-      if (rank < need) top[na + rank] = c;
+      for (int j = 0; j < static_cast<int>(nc); ++j) {
+        const Cand o = cand[j];
+        const uint32_t ko = key_of(o.x);
+        rank += ko > kc || (ko == kc && o.id < c.id);
+      }
+      if (v && rank < nn) {
+        a.out_top_ids[static_cast<int64_t>(r) * n + rank] = c.id;
+        a.out_top[static_cast<int64_t>(r) * n + rank] = lp(c.x);
+      }
     }
   } else {
-    // the ties' per-stripe counts, then their places stripe by stripe (ascending id)
-    const int wv = tid / kWave;
-    for (int j = 0; j < row.nstripes; ++j) {
-      const int b = j * kThreads + tid;
-      uint32_t c = 0;
-      if (b < row.nblk) {
-        float v[kBlk];
-        const uint32_t valid = row.load(b, v);
-#pragma unroll
-        for (int i = 0; i < kBlk; ++i) c += (valid >> i & 1u) && key_of(v[i]) == kk;
-      }
-      c = wave_sum<uint32_t>(c);
-      if (lane_id() == 0) srch.cell[wv][j] = c;
-    }
+    // 4. the elements above it (fewer than nn), then the first of those equal to it by id
+    if (tid == 0) sh[2] = 0;
     __syncthreads();
-    uint32_t done = 0;
-    for (int j = 0; j < row.nstripes && done < need; ++j) {
-      uint32_t cj = 0;
-      for (int w = 0; w < kWaves; ++w) cj += static_cast<uint32_t>(srch.cell[w][j]);
-      if (cj == 0) continue;  // (uniform)
-      const int b = j * kThreads + tid;
-      float v[kBlk];
-      const uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
-      uint32_t c = 0;
-#pragma unroll
-      for (int i = 0; i < kBlk; ++i) c += (valid >> i & 1u) && key_of(v[i]) == kk;
-      uint32_t tot;
-      uint32_t at = done + block_excl_scan<uint32_t>(c, rdx.hcnt, &tot);
-#pragma unroll
-      for (int i = 0; i < kBlk; ++i) {
-        if ((valid >> i & 1u) && key_of(v[i]) == kk) {
-          if (at < need) top[na + at] = Cand{v[i], b * kBlk + i};
-          ++at;
+    if (listed) {
+      for (int i = tid; i < static_cast<int>(nc); i += kThreads) {
+        const Cand c = cand[i];
+        if (key_of(c.x) > kk) {
+          const uint32_t at = atomicAdd(&sh[2], 1u);
+          if (at < static_cast<uint32_t>(kMaxTop)) top[at] = c;
         }
       }
-      done += tot;
-      __syncthreads();
+    } else {
+      for_each(row, [&](float x, int id) {
+        if (key_of(x) > kk) {
+          const uint32_t at = atomicAdd(&sh[2], 1u);
+          if (at < static_cast<uint32_t>(kMaxTop)) top[at] = Cand{x, id};
+        }
+      });
     }
-  }
-  __syncthreads();
-  // 5. order: descending value, ascending id (the ties are last, already in id order)
-  if (tid < static_cast<int>(nn)) {
-    const Cand c = top[tid];
-    uint32_t rank = tid;
-    if (tid < static_cast<int>(na)) {
-      rank = 0;
-      for (int j = 0; j < static_cast<int>(na); ++j) {
-        const Cand o = top[j];
-        rank += key_of(o.x) > key_of(c.x) || (key_of(o.x) == key_of(c.x) && o.id < c.id);
+    __syncthreads();
+    const uint32_t na = sh[2];
+    const uint32_t need = nn - na;
+    if (listed) {
+      // a tied entry's place: the tied entries with a smaller id
+      for (int i = tid; i < static_cast<int>(nc); i += kThreads) {
+        const Cand c = cand[i];
+        if (key_of(c.x) != kk) continue;
+        uint32_t rank = 0;
+        for (int j = 0; j < static_cast<int>(nc); ++j) rank += key_of(cand[j].x) == kk && cand[j].id < c.id;
+        if (rank < need) top[na + rank] = c;
+      }
+    } else {
+      // the ties' per-stripe counts, then their places stripe by stripe (ascending id)
+      const int wv = tid / kWave;
+      for (int j = 0; j < row.nstripes; ++j) {
+        const int b = j * kThreads + tid;
+        uint32_t c = 0;
+        if (b < row.nblk) {
+          float v[kBlk];
+          const uint32_t valid = row.load(b, v);
+  #pragma unroll
+          for (int i = 0; i < kBlk; ++i) c += (valid >> i & 1u) && key_of(v[i]) == kk;
+        }
+        c = wave_sum<uint32_t>(c);
+        if (lane_id() == 0) srch.cell[wv][j] = c;
+      }
+      __syncthreads();
+      uint32_t done = 0;
+      for (int j = 0; j < row.nstripes && done < need; ++j) {
+        uint32_t cj = 0;
+        for (int w = 0; w < kWaves; ++w) cj += static_cast<uint32_t>(srch.cell[w][j]);
+        if (cj == 0) continue;  // (uniform)
+        const int b = j * kThreads + tid;
+        float v[kBlk];
+        const uint32_t valid = b < row.nblk ? row.load(b, v) : 0u;
+        uint32_t c = 0;
+  #pragma unroll
+        for (int i = 0; i < kBlk; ++i) c += (valid >> i & 1u) && key_of(v[i]) == kk;
+        uint32_t tot;
+        uint32_t at = done + block_excl_scan<uint32_t>(c, rdx.hcnt, &tot);
+  #pragma unroll
+        for (int i = 0; i < kBlk; ++i) {
+          if ((valid >> i & 1u) && key_of(v[i]) == kk) {
+            if (at < need) top[na + at] = Cand{v[i], b * kBlk + i};
+            ++at;
+          }
+        }
+        done += tot;
+        __syncthreads();
       }
     }
-    a.out_top_ids[static_cast<int64_t>(r) * n + rank] = c.id;
-    a.out_top[static_cast<int64_t>(r) * n + rank] = lp(c.x);
+    __syncthreads();
+    // 5. order: descending value, ascending id (the ties are last, already in id order)
+    if (tid < static_cast<int>(nn)) {
+      const Cand c = top[tid];
+      uint32_t rank = tid;
+      if (tid < static_cast<int>(na)) {
+        rank = 0;
+        for (int j = 0; j < static_cast<int>(na); ++j) {
+          const Cand o = top[j];
+          rank += key_of(o.x) > key_of(c.x) || (key_of(o.x) == key_of(c.x) && o.id < c.id);
+        }
+      }
+      a.out_top_ids[static_cast<int64_t>(r) * n + rank] = c.id;
+      a.out_top[static_cast<int64_t>(r) * n + rank] = lp(c.x);
+    }
   }
   for (int i = static_cast<int>(nn) + tid; i < n; i += kThreads) {  // n > V: the rest are empty
     a.out_top_ids[static_cast<int64_t>(r) * n + i] = -1;
