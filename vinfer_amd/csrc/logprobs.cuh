@@ -191,32 +191,21 @@ __device__ __forceinline__ bool lp_one_pass(const LogprobArgs& a, const Row<uint
   s = block_sum<double>(s, reinterpret_cast<double*>(red64));
   lse = static_cast<double>(M) + log(s);
   if (n <= 0) return true;
-  // the n-th largest key: the thread whose keys hold it walks its counts from the top
+  // the n-th largest key: the wave of the thread whose keys hold it takes them, one a lane from
+  // the top, and scans their counts
   const uint32_t nn = static_cast<uint32_t>(n) < static_cast<uint32_t>(V) ? static_cast<uint32_t>(n)
                                                                          : static_cast<uint32_t>(V);
   const uint32_t above = total - ex - c;  // elements in the keys above this thread's
-  if (above < nn && nn <= above + c) {
-    uint32_t wc[32];  // (one thread: its words, all loads issued before the walk)
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint4 v4 = reinterpret_cast<const uint4*>(hist + 32 * tid)[q];
-      wc[4 * q] = v4.x;
-      wc[4 * q + 1] = v4.y;
-      wc[4 * q + 2] = v4.z;
-      wc[4 * q + 3] = v4.w;
-    }
-    uint32_t run = above;
-#pragma unroll
-    for (int i = 31; i >= 0; --i) {
-#pragma unroll
-      for (int h = 1; h >= 0; --h) {
-        const uint32_t cnt = h ? wc[i] >> 16 : wc[i] & 0xFFFFu;
-        if (run < nn && nn <= run + cnt) {
-          sh[5] = 64u * tid + 2u * i + h;
-          sh[7] = run + cnt;  // elements >= it
-        }
-        run += cnt;
-      }
+  const u64 owner = __ballot(above < nn && nn <= above + c);
+  if (owner) {  // (uniform over the wave)
+    const int ol = __ffsll(static_cast<long long>(owner)) - 1;
+    const uint32_t oa = __builtin_amdgcn_readlane(above, ol);
+    const uint32_t key = 64u * static_cast<uint32_t>((tid & ~(kWave - 1)) + ol) + 63u - static_cast<uint32_t>(lane_id());
+    const uint32_t cnt = hcount(hist, key);
+    const uint32_t run = oa + wave_incl_scan<uint32_t>(cnt) - cnt;
+    if (run < nn && nn <= run + cnt) {
+      sh[5] = key;
+      sh[7] = run + cnt;  // elements >= it
     }
   }
   __syncthreads();  // (the histogram is dead: the list goes over it)
