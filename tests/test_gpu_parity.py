@@ -515,6 +515,43 @@ def test_draw_frequencies_match_the_distribution():
         assert 0.5 * (freq - expected).abs().sum() < 0.015
 
 
+@pytest.mark.parametrize("pen", [False, True], ids=["plain", "penalties"])
+def test_greedy_rows_take_the_first_of_repeated_maxima(pen):
+    """Greedy bf16 rows whose max repeats: the first id holding it (the member search from the
+    pass's kept low bytes, or the row pass), against the oracle; rows of signed zeros, a max
+    only a penalised value reaches, and maxima in the ragged tail included."""
+    from oracle.sampler_oracle import sample_batch as oracle_batch
+
+    rng = np.random.default_rng(41 + pen)
+    rows, V = [], 151939  # (a ragged tail of 3 elements)
+    for b in range(24):
+        x = rng.normal(0, 1, V).astype(np.float32)
+        m = float(rng.choice([2.0, 3.5, 7.0]))
+        k = int(rng.integers(1, 40))
+        x[rng.choice(V, size=k, replace=False)] = m
+        if b % 6 == 1:
+            x[:] = 0.0
+            x[rng.choice(V, size=V // 2, replace=False)] = -0.0
+        if b % 6 == 2:
+            x[V - 1] = m  # the last element (the tail) is one of the maxima
+        rows.append(x)
+    x = torch.from_numpy(np.stack(rows)).to(torch.bfloat16)
+    B = x.shape[0]
+    sp = SamplingParams(temperature=0.0, repetition_penalty=0.5 if pen else 1.0)  # (0.5: negative rows gain)
+    hist = [rng.integers(0, V, 200).tolist() for _ in range(B)] if pen else [[] for _ in range(B)]
+    hi, ho = pack_history(hist)
+    u = torch.zeros(B)
+    s = hip(torch.bfloat16)
+    print(f"greedy repeated maxima pen={pen}", flush=True)
+    ids, _ = s.sample_batch(x.to(DEV), pack_params([sp] * B, DEV), u.to(DEV), hi.to(DEV) if pen else None,
+                            ho.to(DEV) if pen else None)
+    xs = x.float().numpy()
+    res = oracle_batch(xs, [0.0] * B, [0] * B, [1.0] * B, [0.0] * B, [sp.repetition_penalty] * B, [0.0] * B,
+                       [0.0] * B, hi.numpy(), ho.numpy(), [0.0] * B)
+    got = ids.cpu().tolist()
+    assert got == [r.token for r in res]
+
+
 def test_per_token_call_matches_the_batch():
     s = hip(torch.bfloat16)
     logits = (torch.randn(1000) * 2).to(torch.bfloat16).to(DEV)

@@ -2498,7 +2498,18 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
     if (f.plan.nnan) k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
     else if (!(T > 0.0f)) {
       int pt = -1;
-      if constexpr (SPLIT) pt = split_find(a, row, f, ne, xmax, 0ull, srch, hist + kMatchOffset, recs);
+      if constexpr (SPLIT) {
+        pt = split_find(a, row, f, ne, xmax, 0ull, srch, hist + kMatchOffset, recs);
+      } else if (!a.out_probs && cells_per(row) * kThreads <= 4 * kMatchWords) {  // (uniform)
+        // the first id holding the max, by the member search from the kept low bytes (as the
+        // draw's member) instead of a pass over the row
+        uint8_t* cells = reinterpret_cast<uint8_t*>(hist + kMatchOffset);
+        const int ncq = cells_per(row) * kThreads / 16;
+        for (int i = tid; i < ncq; i += kThreads) reinterpret_cast<uint4*>(cells)[i] = make_uint4(0, 0, 0, 0);
+        if (tid == 0) f.si[6] = -1;
+        lds_barrier();
+        pt = select_member(row, f, ne, xmax, 0ull, cells, mxk, low);
+      }
       k.point = pt >= 0 ? pt : find_first(row, [&](float x, int) -> u64 { return x == xmax; }, 0ull, srch);
     }
     else if (!degenerate(row, p, mkey, 0, mz, srch, k)) k.point = 0;
