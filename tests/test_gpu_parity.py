@@ -398,6 +398,34 @@ def test_few_penalised_values_inside_the_walked_chunk():
     check(Workload("walk_chunk", x, params, u, hi, ho, None), max_tie_frac=0.25)
 
 
+@pytest.mark.parametrize("shift", ["frequency", "presence"])
+def test_many_penalised_values_share_the_walked_keys(shift):
+    # every logit is one of the 64 bf16 values 1 + k/128 (one chunk), and about 100 distinct
+    # ids per row are penalised, so the top-k count, top-p cutoff and draw walks all land on keys
+    # that hold the bf16 value together with penalised values: a frequency penalty of 2^-10 per
+    # occurrence leaves up to three distinct fp32 values inside the key below (above its bf16
+    # value); a presence penalty of 2^-7 moves values exactly onto the next bf16 value down
+    rng = np.random.default_rng(17 if shift == "frequency" else 18)
+    B, V = 32, 2048
+    vals = (1.0 + np.arange(64) / 128.0).astype(np.float32)
+    x = torch.from_numpy(vals[rng.integers(0, 64, (B, V))]).to(torch.bfloat16)
+    hist = []
+    for _ in range(B):
+        ids = rng.permutation(V)[:100]
+        reps = rng.integers(1, 4, ids.size)
+        hist.append(np.repeat(ids, reps).tolist())
+    hi, ho = pack_history(hist)
+    freq, pres = (2.0**-10, 0.0) if shift == "frequency" else (0.0, 2.0**-7)
+    params = pack_params(
+        [SamplingParams(temperature=float(rng.choice([0.7, 1.0])), top_k=int(rng.choice([0, 0, 100, 700])),
+                        top_p=float(rng.choice([0.3, 0.5, 0.8, 1.0])), presence_penalty=pres,
+                        frequency_penalty=freq)
+         for _ in range(B)]
+    )
+    u = torch.from_numpy(rng.random(B, dtype=np.float32))
+    check(Workload(f"walk_keys_{shift}", x, params, u, hi, ho, None), max_tie_frac=0.5)
+
+
 @pytest.mark.parametrize("V", [151936, 157248, 157249, 200000])  # presence bitmap up to 157248, then hash
 def test_bf16_rows_the_histogram_path_hands_to_the_generic_path(V):
     # histories the bf16 histogram path does not count itself: longer than its table takes,

@@ -160,7 +160,6 @@ struct __align__(16) FastSmem {
   u64 lq[kMaxL];            //   and mass
   uint32_t binc[kWave];     // per-key counts / masses of penalised values inside that chunk
   u64 binm[kWave];
-  uint32_t nl;
   uint32_t pchunk[2];  // the chunks that hold penalised values lie in [pchunk[0], pchunk[1]]
   uint32_t red32[kWaves];
   u64 red64[2 * kWaves];
@@ -1650,30 +1649,41 @@ struct WalkResult {
 __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& f, int ne, int c, int mode, u64 above,
                                                 double target, float x0, float T, float mz) {
   const int l = lane_id();
+  const u64 lower = (1ull << l) - 1ull;
   f.binc[l] = 0;
   f.binm[l] = 0;
-  if (l == 0) f.nl = 0;
-  // the chunk's penalised values: per-key counts and masses, and a list of (key, mass)
+  // the chunk's penalised values: first a list of their keys, compacted by ballot (a cheap pass
+  // over all of them), then one list entry per lane: its mass, and the per-key counts and masses
   const bool has_pen = static_cast<uint32_t>(c) >= f.pchunk[0] && static_cast<uint32_t>(c) <= f.pchunk[1];
-  for (int e = l; has_pen && e < ne; e += kWave) {
-    const float x = f.eval[e];
-    const uint32_t key = key_of(x);
-    const uint32_t top = key >> 16;
-    if (chunk_of16(top) != c) continue;
-    if (mode != kWalkCount && !(x >= x0)) continue;
-    const u64 q = mode == kWalkCount ? 0ull : mass_q(ptilde(x, T, mz));
-    const int lane = static_cast<int>(65535u - 64u * static_cast<uint32_t>(c) - top);
-    atomicAdd(&f.binc[lane], 1u);
-    atomicAdd(&f.binm[lane], q);
-    const uint32_t i = atomicAdd(&f.nl, 1u);
-    if (i < kMaxL) {
-      f.lkey[i] = key;
-      f.lq[i] = q;
+  uint32_t nl = 0;
+  // (four values a lane per step: 16-byte reads of eval, whose length is a multiple of 4)
+  static_assert(kExcCap % 4 == 0, "eval is read four values at a time");
+  for (int e0 = 0; has_pen && e0 < ne; e0 += 4 * kWave) {  // (uniform)
+    const int e = e0 + 4 * l;
+    const float4 x4 = e < ne ? *reinterpret_cast<const float4*>(&f.eval[e]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t key = key_of(xs[j]);
+      const bool in = e + j < ne && chunk_of16(key >> 16) == c && (mode == kWalkCount || xs[j] >= x0);
+      const u64 b = __ballot(in);
+      const uint32_t at = nl + static_cast<uint32_t>(__popcll(b & lower));
+      if (in && at < static_cast<uint32_t>(kMaxL)) f.lkey[at] = key;
+      nl += static_cast<uint32_t>(__popcll(b));
     }
   }
-  wave_lds_sync();  // (the lanes' counts, masses and list entries are in)
   WalkResult res;
-  res.ok = lds_peek(&f.nl) <= kMaxL;
+  res.ok = nl <= static_cast<uint32_t>(kMaxL);
+  wave_lds_sync();  // (the list's keys and the zeroed per-key sums are in)
+  for (uint32_t i = static_cast<uint32_t>(l); res.ok && i < nl; i += kWave) {
+    const uint32_t key = f.lkey[i];
+    const u64 q = mode == kWalkCount ? 0ull : mass_q(ptilde(val_of(key), T, mz));
+    f.lq[i] = q;
+    const int lane = static_cast<int>(65535u - 64u * static_cast<uint32_t>(c) - (key >> 16));
+    atomicAdd(&f.binc[lane], 1u);
+    atomicAdd(&f.binm[lane], q);
+  }
+  wave_lds_sync();  // (the lanes' counts, masses and list masses are in)
   res.key = 0;
   res.n = 0;
   res.q = 0;
@@ -1711,79 +1721,116 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
     res.above = abw;
     return res;
   }
-  // The key mixes its bf16 value with penalised values: lane 0 walks its items in descending
-  // order.
-  uint32_t rkey = bkey, rn = 0;
-  u64 rq = 0, rab = abw;
-  if (l == 0) {
-    // move this key's penalised values to the front of the list, then sort them (descending)
-    int n = 0;
-    const uint32_t nl = lds_peek(&f.nl);
-    for (uint32_t i = 0; i < nl; ++i) {
-      if ((f.lkey[i] >> 16) == Kw) {
-        const uint32_t tk = f.lkey[n];
-        const u64 tq = f.lq[n];
-        f.lkey[n] = f.lkey[i];
-        f.lq[n] = f.lq[i];
-        f.lkey[i] = tk;
-        f.lq[i] = tq;
-        ++n;
+  // The key mixes its bf16 value with penalised values: its groups of equal values (the bulk
+  // value's, with the penalised values equal to it, and the other penalised values') are resolved
+  // by the whole wave. The list (at most 2 x 64 entries) is compacted to this key's entries; each
+  // entry sums the weight of the entries above it and finds its equals (the first of them stands
+  // for the group), and a wave max picks the hit group: the smallest value for the cutoff (hits
+  // are the values whose weight above is below the target), the only one otherwise.
+  static_assert(kMaxL <= 2 * kWave, "two list entries per lane");
+  const bool counting = mode == kWalkCount;
+  uint32_t ek[2];
+  u64 eq[2];
+  bool em[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t i = static_cast<uint32_t>(l + kWave * h);
+    ek[h] = i < nl ? f.lkey[i] : 0u;
+    eq[h] = i < nl ? f.lq[i] : 0ull;
+    em[h] = i < nl && (ek[h] >> 16) == Kw;
+  }
+  const u64 b0 = __ballot(em[0]), b1 = __ballot(em[1]);
+  const int n0 = __popcll(b0);
+  const int n = n0 + __popcll(b1);
+  wave_lds_sync();  // (every lane has read its entries before the list is overwritten)
+  if (em[0]) {
+    const int at = __popcll(b0 & lower);
+    f.lkey[at] = ek[0];
+    f.lq[at] = eq[0];
+  }
+  if (em[1]) {
+    const int at = n0 + __popcll(b1 & lower);
+    f.lkey[at] = ek[1];
+    f.lq[at] = eq[1];
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = l + kWave * h;
+    ek[h] = i < n ? f.lkey[i] : 0u;
+    eq[h] = i < n ? f.lq[i] : 0ull;
+  }
+  u64 above_w[2] = {0ull, 0ull}, eq_m[2] = {0ull, 0ull};
+  uint32_t eq_n[2] = {0u, 0u};
+  bool first[2] = {true, true};
+  for (int q = 0; q < n; ++q) {  // (uniform)
+    const int ql = q & (kWave - 1);
+    const uint32_t kq = __builtin_amdgcn_readlane(q < kWave ? ek[0] : ek[1], ql);
+    const u64 qq = readlane64(q < kWave ? eq[0] : eq[1], ql);
+    const u64 wq = counting ? 1ull : qq;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (kq > ek[h]) {
+        above_w[h] += wq;
+      } else if (kq == ek[h]) {
+        eq_n[h] += 1u;
+        eq_m[h] += qq;
+        if (q < l + kWave * h) first[h] = false;
       }
-    }
-    for (int i = 1; i < n; ++i) {
-      const uint32_t kk = f.lkey[i];
-      const u64 qq = f.lq[i];
-      int jj = i - 1;
-      while (jj >= 0 && f.lkey[jj] < kk) {
-        f.lkey[jj + 1] = f.lkey[jj];
-        f.lq[jj + 1] = f.lq[jj];
-        --jj;
-      }
-      f.lkey[jj + 1] = kk;
-      f.lq[jj + 1] = qq;
-    }
-    // merge with the bulk value (cbw members of mass qbw each), walking distinct values
-    u64 acc = abw;
-    int ie = 0;
-    bool bulk_done = cbw == 0;
-    while (ie < n || !bulk_done) {
-      uint32_t vkey;
-      if (bulk_done) vkey = f.lkey[ie];
-      else if (ie < n && f.lkey[ie] > bkey) vkey = f.lkey[ie];
-      else vkey = bkey;
-      uint32_t gn = 0;
-      u64 gm = 0, gq = 0;
-      if (!bulk_done && vkey == bkey) {
-        gn += cbw;
-        gm += cbw * qbw;
-        gq = qbw;
-        bulk_done = true;
-      }
-      while (ie < n && f.lkey[ie] == vkey) {
-        gn += 1;
-        gm += f.lq[ie];
-        gq = f.lq[ie];
-        ++ie;
-      }
-      const u64 gw = mode == kWalkCount ? static_cast<u64>(gn) : gm;
-      bool h;
-      if (mode == kWalkCount) h = static_cast<double>(acc) < target && target <= static_cast<double>(acc + gw);
-      else if (mode == kWalkCutoff) h = gn > 0 && static_cast<double>(acc) < target;
-      else h = gw > 0 && static_cast<double>(acc) <= target && target < static_cast<double>(acc + gw);
-      if (h) {
-        rkey = vkey;
-        rn = gn;
-        rq = gq;
-        rab = acc;
-        if (mode != kWalkCutoff) break;
-      }
-      acc += gw;
     }
   }
-  res.key = __builtin_amdgcn_readlane(rkey, 0);
-  res.n = __builtin_amdgcn_readlane(rn, 0);
-  res.q = readlane64(rq, 0);
-  res.above = readlane64(rab, 0);
+  auto hits = [&](u64 acc, uint32_t gn, u64 gw) -> bool {
+    if (mode == kWalkCount) return static_cast<double>(acc) < target && target <= static_cast<double>(acc + gw);
+    if (mode == kWalkCutoff) return gn > 0 && static_cast<double>(acc) < target;
+    return gw > 0 && static_cast<double>(acc) <= target && target < static_cast<double>(acc + gw);
+  };
+  // (the wave max's order: cutoff walks want the smallest key, the others the largest; 0 = none)
+  auto order = [&](uint32_t key) -> u64 {
+    return mode == kWalkCutoff ? 0x100000000ull - key : static_cast<u64>(key) + 1ull;
+  };
+  const bool bulk = cbw > 0;
+  const u64 bw = counting ? static_cast<u64>(cbw) : static_cast<u64>(cbw) * qbw;
+  u64 best = 0, acc_h[2];
+  uint32_t gn_h[2];
+  bool hit_h[2];
+  u64 above_b = 0;
+  bool eq_b = false;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const bool valid = l + kWave * h < n;
+    const bool same = bulk && ek[h] == bkey;
+    acc_h[h] = abw + above_w[h] + (bulk && bkey > ek[h] ? bw : 0ull);
+    gn_h[h] = eq_n[h] + (same ? cbw : 0u);
+    const u64 gm = eq_m[h] + (same ? static_cast<u64>(cbw) * qbw : 0ull);
+    hit_h[h] = valid && first[h] && hits(acc_h[h], gn_h[h], counting ? static_cast<u64>(gn_h[h]) : gm);
+    if (hit_h[h] && order(ek[h]) > best) best = order(ek[h]);
+    if (valid && ek[h] > bkey) above_b += counting ? 1ull : eq[h];
+    if (valid && ek[h] == bkey) eq_b = true;
+  }
+  best = wave_max_u64(best);
+  above_b = abw + wave_sum<u64>(above_b);
+  // the bulk value's own group, when no penalised value equals it
+  const bool hit_b = bulk && __ballot(eq_b) == 0 && hits(above_b, cbw, bw);
+  if (hit_b && order(bkey) > best) best = order(bkey);
+  if (best == 0) {  // (no group hit: the bulk key, none kept)
+    res.key = bkey;
+    res.above = abw;
+    return res;
+  }
+  if (hit_b && best == order(bkey)) {
+    res.key = bkey;
+    res.n = cbw;
+    res.q = qbw;
+    res.above = above_b;
+    return res;
+  }
+  const u64 w0 = __ballot(hit_h[0] && order(ek[0]) == best), w1 = __ballot(hit_h[1] && order(ek[1]) == best);
+  const bool hi = w0 == 0;
+  const int at = __ffsll(static_cast<long long>(hi ? w1 : w0)) - 1;
+  res.key = __builtin_amdgcn_readlane(hi ? ek[1] : ek[0], at);
+  res.n = __builtin_amdgcn_readlane(hi ? gn_h[1] : gn_h[0], at);
+  res.q = readlane64(hi ? eq[1] : eq[0], at);
+  res.above = readlane64(hi ? acc_h[1] : acc_h[0], at);
   return res;
 }
 
