@@ -250,6 +250,11 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
   return v;
 }
 
+// Set bits of a wave mask in the lanes below this one (v_mbcnt: two instructions).
+__device__ __forceinline__ uint32_t lanes_below(u64 m) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+}
+
 // A 64-bit value of one lane, in every lane.
 __device__ __forceinline__ u64 readlane64(u64 x, int lane) {
   const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), lane);

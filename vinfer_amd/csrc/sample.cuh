@@ -1649,12 +1649,14 @@ struct WalkResult {
 __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& f, int ne, int c, int mode, u64 above,
                                                 double target, float x0, float T, float mz) {
   const int l = lane_id();
-  const u64 lower = (1ull << l) - 1ull;
   f.binc[l] = 0;
   f.binm[l] = 0;
   // the chunk's penalised values: first a list of their keys, compacted by ballot (a cheap pass
-  // over all of them), then one list entry per lane: its mass, and the per-key counts and masses
+  // over all of them), then one list entry per lane: its mass, and the per-key counts and masses.
+  // (A row that reaches a walk holds no NaN, so a value's key needs no NaN case; -0.0 takes
+  // +0.0's key. The chunk's keys are klo .. klo + 2^22 - 1.)
   const bool has_pen = static_cast<uint32_t>(c) >= f.pchunk[0] && static_cast<uint32_t>(c) <= f.pchunk[1];
+  const uint32_t klo = (65535u - 64u * static_cast<uint32_t>(c) - 63u) << 16;
   uint32_t nl = 0;
   // (four values a lane per step: 16-byte reads of eval, whose length is a multiple of 4)
   static_assert(kExcCap % 4 == 0, "eval is read four values at a time");
@@ -1664,10 +1666,12 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
     const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t key = key_of(xs[j]);
-      const bool in = e + j < ne && chunk_of16(key >> 16) == c && (mode == kWalkCount || xs[j] >= x0);
+      const uint32_t bits = __float_as_uint(xs[j]);
+      const uint32_t key =
+          xs[j] == 0.0f ? 0x80000000u : bits ^ (static_cast<uint32_t>(static_cast<int32_t>(bits) >> 31) | 0x80000000u);
+      const bool in = e + j < ne && key - klo < (1u << 22) && (mode == kWalkCount || xs[j] >= x0);
       const u64 b = __ballot(in);
-      const uint32_t at = nl + static_cast<uint32_t>(__popcll(b & lower));
+      const uint32_t at = nl + lanes_below(b);
       if (in && at < static_cast<uint32_t>(kMaxL)) f.lkey[at] = key;
       nl += static_cast<uint32_t>(__popcll(b));
     }
@@ -1744,12 +1748,12 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
   const int n = n0 + __popcll(b1);
   wave_lds_sync();  // (every lane has read its entries before the list is overwritten)
   if (em[0]) {
-    const int at = __popcll(b0 & lower);
+    const int at = static_cast<int>(lanes_below(b0));
     f.lkey[at] = ek[0];
     f.lq[at] = eq[0];
   }
   if (em[1]) {
-    const int at = n0 + __popcll(b1 & lower);
+    const int at = n0 + static_cast<int>(lanes_below(b1));
     f.lkey[at] = ek[1];
     f.lq[at] = eq[1];
   }
@@ -1760,14 +1764,19 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
     ek[h] = i < n ? f.lkey[i] : 0u;
     eq[h] = i < n ? f.lq[i] : 0ull;
   }
-  u64 above_w[2] = {0ull, 0ull}, eq_m[2] = {0ull, 0ull};
+  // (the loop's key and mass are uniform: the bulk value's weight above and its equal entries
+  // are summed in scalar registers)
+  const bool bulk = cbw > 0;
+  u64 above_w[2] = {0ull, 0ull}, eq_m[2] = {0ull, 0ull}, above_b = abw;
   uint32_t eq_n[2] = {0u, 0u};
-  bool first[2] = {true, true};
+  bool first[2] = {true, true}, eq_b = false;
   for (int q = 0; q < n; ++q) {  // (uniform)
     const int ql = q & (kWave - 1);
     const uint32_t kq = __builtin_amdgcn_readlane(q < kWave ? ek[0] : ek[1], ql);
     const u64 qq = readlane64(q < kWave ? eq[0] : eq[1], ql);
     const u64 wq = counting ? 1ull : qq;
+    if (kq > bkey) above_b += wq;
+    if (kq == bkey) eq_b = true;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       if (kq > ek[h]) {
@@ -1784,17 +1793,14 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
     if (mode == kWalkCutoff) return gn > 0 && static_cast<double>(acc) < target;
     return gw > 0 && static_cast<double>(acc) <= target && target < static_cast<double>(acc + gw);
   };
-  // (the wave max's order: cutoff walks want the smallest key, the others the largest; 0 = none)
-  auto order = [&](uint32_t key) -> u64 {
-    return mode == kWalkCutoff ? 0x100000000ull - key : static_cast<u64>(key) + 1ull;
-  };
-  const bool bulk = cbw > 0;
+  // (the wave max's order: cutoff walks want the smallest key, the others the largest; 0 = none,
+  // which no key in a walk takes: keys 0 and 0xFFFFFFFF are NaNs)
+  auto order = [&](uint32_t key) -> uint32_t { return mode == kWalkCutoff ? ~key : key; };
   const u64 bw = counting ? static_cast<u64>(cbw) : static_cast<u64>(cbw) * qbw;
-  u64 best = 0, acc_h[2];
+  uint32_t best = 0;
+  u64 acc_h[2];
   uint32_t gn_h[2];
   bool hit_h[2];
-  u64 above_b = 0;
-  bool eq_b = false;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const bool valid = l + kWave * h < n;
@@ -1804,13 +1810,10 @@ __device__ __forceinline__ WalkResult wave_walk(const uint32_t* hist, FastSmem& 
     const u64 gm = eq_m[h] + (same ? static_cast<u64>(cbw) * qbw : 0ull);
     hit_h[h] = valid && first[h] && hits(acc_h[h], gn_h[h], counting ? static_cast<u64>(gn_h[h]) : gm);
     if (hit_h[h] && order(ek[h]) > best) best = order(ek[h]);
-    if (valid && ek[h] > bkey) above_b += counting ? 1ull : eq[h];
-    if (valid && ek[h] == bkey) eq_b = true;
   }
-  best = wave_max_u64(best);
-  above_b = abw + wave_sum<u64>(above_b);
+  best = dpp::reduce(best, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
   // the bulk value's own group, when no penalised value equals it
-  const bool hit_b = bulk && __ballot(eq_b) == 0 && hits(above_b, cbw, bw);
+  const bool hit_b = bulk && !eq_b && hits(above_b, cbw, bw);
   if (hit_b && order(bkey) > best) best = order(bkey);
   if (best == 0) {  // (no group hit: the bulk key, none kept)
     res.key = bkey;
