@@ -426,6 +426,28 @@ def test_many_penalised_values_share_the_walked_keys(shift):
     check(Workload(f"walk_keys_{shift}", x, params, u, hi, ho, None), max_tie_frac=0.5)
 
 
+@pytest.mark.parametrize("V", [200003, 262144, 300001])
+def test_long_bf16_rows_search_their_later_blocks(V):
+    # rows past the blocks whose low bytes the pass keeps (V > 155,648): the member search reads
+    # a later block again only when its largest key reaches the drawn value's, and every block
+    # past 270,336 ids; rows of 16 distinct values (members in every block), and N(0, s) rows
+    # (the drawn value in the upper tail), greedy and sampled, with and without histories
+    rng = np.random.default_rng(V)
+    B = 24
+    g = torch.Generator().manual_seed(V)
+    x = torch.randn(B, V, generator=g) * 2.5
+    x[::3] = torch.from_numpy(rng.integers(-8, 8, (len(range(0, B, 3)), V)).astype(np.float32) / 4.0)
+    params = pack_params(
+        [SamplingParams(temperature=float(rng.choice([0.0, 0.6, 1.0])), top_k=int(rng.choice([0, 0, 40])),
+                        top_p=float(rng.choice([1.0, 0.95, 0.5])), repetition_penalty=float(rng.choice([1.0, 1.2])))
+         for _ in range(B)]
+    )
+    hist = [rng.integers(0, V, int(rng.integers(0, 200))).tolist() for _ in range(B)]
+    hi, ho = pack_history(hist)
+    u = torch.from_numpy(rng.random(B, dtype=np.float32))
+    check(Workload(f"long_rows_{V}", x.to(torch.bfloat16), params, u, hi, ho, None), max_tie_frac=0.25)
+
+
 @pytest.mark.parametrize("V", [151936, 157248, 157249, 200000])  # presence bitmap up to 157248, then hash
 def test_bf16_rows_the_histogram_path_hands_to_the_generic_path(V):
     # histories the bf16 histogram path does not count itself: longer than its table takes,
