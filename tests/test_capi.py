@@ -27,6 +27,14 @@ def test_library_is_built_and_loads():
     assert lib.vsamp_abi_version() == _lib.ABI_VERSION
 
 
+def test_abi_version_is_one_number_everywhere():
+    # the header's version, the binding's, and the one the integration guide's snippet asserts
+    header = int(re.search(r"#define VSAMP_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    guide = (HEADER.parents[1] / "INTEGRATION.md").read_text()
+    snippet = int(re.search(r"^VSAMP_ABI_VERSION = (\d+)", guide, re.M).group(1))
+    assert header == _lib.ABI_VERSION == snippet
+
+
 def test_every_declared_symbol_is_exported():
     names = declared()
     assert names == sorted(_lib.EXPORTS)
