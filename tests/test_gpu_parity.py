@@ -426,6 +426,31 @@ def test_many_penalised_values_share_the_walked_keys(shift):
     check(Workload(f"walk_keys_{shift}", x, params, u, hi, ho, None), max_tie_frac=0.5)
 
 
+@pytest.mark.parametrize("n_pen", [60, 64, 65, 120, 128, 129])
+def test_one_walked_key_holds_many_equal_penalised_values(n_pen):
+    # four distinct bf16 values (1 + k/128, k = 0..3: one chunk); n_pen ids of value 1 + 3/128
+    # are penalised by 2^-7 onto 1 + 2/128 exactly, so one key holds n_pen equal penalised values
+    # (both halves of the walk's list past 64) merged with that bf16 value's own group; past 128
+    # in the chunk the row goes to the generic path
+    rng = np.random.default_rng(n_pen)
+    B, V = 16, 4096
+    vals = (1.0 + np.arange(4) / 128.0).astype(np.float32)
+    xs = vals[rng.integers(0, 4, (B, V))]
+    hist = []
+    for b in range(B):
+        top = np.flatnonzero(xs[b] == vals[3])
+        hist.append(rng.choice(top, n_pen, replace=False).tolist())
+    x = torch.from_numpy(xs).to(torch.bfloat16)
+    hi, ho = pack_history(hist)
+    params = pack_params(
+        [SamplingParams(temperature=1.0, top_k=int(rng.choice([0, 0, 1500, 3000])),
+                        top_p=float(rng.choice([0.2, 0.45, 0.7, 1.0])), presence_penalty=2.0**-7)
+         for _ in range(B)]
+    )
+    u = torch.from_numpy(rng.random(B, dtype=np.float32))
+    check(Workload(f"equal_penalised_{n_pen}", x, params, u, hi, ho, None), max_tie_frac=0.5)
+
+
 @pytest.mark.parametrize("V", [200003, 262144, 300001])
 def test_long_bf16_rows_search_their_later_blocks(V):
     # rows past the blocks whose low bytes the pass keeps (V > 155,648): the member search reads
