@@ -114,13 +114,19 @@ __device__ __forceinline__ bool lp_one_pass(const LogprobArgs& a, const Row<uint
   // among the thread's elements: equal keys keep the first); the position is 8m + e for element
   // e of block tid + 1024m, and 4096 for the ragged tail's one.
   uint32_t t1 = 0, t2 = 0, t3 = 0;
+  // (t1 >= t2 >= t3 throughout: the new second is the median of t1, t2 and the word, the new
+  // third the median of t2, t3 and the word; v_med3_u32 takes each in one instruction)
+  auto med3 = [](uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t d;
+    asm("v_med3_u32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+  };
   auto keep = [&](uint32_t k, uint32_t pos) {
     const uint32_t pk = (k << 16) | (0xFFFFu - pos);
-    const uint32_t x = min(t1, pk);
+    const uint32_t n3 = med3(t2, t3, pk);
+    t2 = med3(t1, t2, pk);
     t1 = max(t1, pk);
-    const uint32_t y = min(t2, x);
-    t2 = max(t2, x);
-    t3 = max(t3, y);
+    t3 = n3;
   };
   const int rounds = (nfull + kAhead * kThreads - 1) / (kAhead * kThreads);  // (uniform)
   for (int it = 0; it < rounds; ++it) {
