@@ -16,7 +16,15 @@ constexpr double kMassScale = 4398046511104.0;  // 2^42
 
 typedef unsigned long long u64;
 typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ ushort2_t ones2() { return ushort2_t{1, 1}; }
+// Ordered 16-bit keys (unsigned order = numeric order) of both bf16 values of a word at once:
+// each half xor (sign ? 0xFFFF : 0x8000), the sign spread over its half by a packed arithmetic
+// shift (v_pk_ashrrev_i16).
+__device__ __forceinline__ uint32_t ok16x2(uint32_t w) {
+  const short2_t sg = __builtin_bit_cast(short2_t, w) >> static_cast<short>(15);
+  return w ^ (__builtin_bit_cast(uint32_t, sg) | 0x80008000u);
+}
 
 // ---- global pointers --------------------------------------------------------------------------
 // Pointers that reach a kernel inside an argument struct are generic: loads through them compile

@@ -140,8 +140,7 @@ __device__ __forceinline__ bool lp_one_pass(const LogprobArgs& a, const Row<uint
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           // ordered keys of both halves at once: xor with (sign ? 0xFFFF : 0x8000)
-          const uint32_t s2 = (w[j] >> 15) & 0x00010001u;
-          const uint32_t k2 = w[j] ^ (s2 * 0x7FFFu | 0x80008000u);
+          const uint32_t k2 = ok16x2(w[j]);
           const uint32_t klo = k2 & 0xFFFFu, khi = k2 >> 16;
           atomicAdd(&hist[klo >> 1], 1u << ((klo & 1u) << 4));
           atomicAdd(&hist[khi >> 1], 1u << ((khi & 1u) << 4));

@@ -48,8 +48,7 @@ __device__ __forceinline__ void slice_hist(const uint16_t* row, int V, int G, in
   for (int k = 0; k < kAhead; ++k) q[k] = ld_global_u4(blocks + min(b0 + tid + k * kThreads, last));
   auto add2 = [&](uint32_t w) {
     // ordered keys of both halves at once: xor with (sign ? 0xFFFF : 0x8000)
-    const uint32_t s2 = (w >> 15) & 0x00010001u;
-    const uint32_t k2 = w ^ (s2 * 0x7FFFu | 0x80008000u);
+    const uint32_t k2 = ok16x2(w);
     const uint32_t klo = k2 & 0xFFFFu, khi = k2 >> 16;
     atomicAdd(&hist[klo >> 1], 1u << ((klo & 1u) << 4));
     atomicAdd(&hist[khi >> 1], 1u << ((khi & 1u) << 4));
