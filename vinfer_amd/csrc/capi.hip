@@ -40,7 +40,11 @@ int hip_fail(hipError_t e, const char* what) {
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_dev_ok[kMaxDevices];  // 0 unknown, 1 gfx950, 2 not
 std::atomic<int> g_dev_cus[kMaxDevices];  // compute units of a checked device
-constexpr int kMaxResidualSlices = 2;      // workgroups per rejected row of a verify call (measured: 1, 4 slower)
+// Workgroups per rejected row of a verify call, at most (the launch takes the largest power of two
+// that gives every (row, slice) item a workgroup of its own: 4 for ~50 rejected rows on 256 CUs).
+// Measured with the slices' fence-free hand-off (B = 192, K = 1, V = 262144): 2 slices 155.3 us
+// per call, 4, 8 or 16 136.0-136.4.
+constexpr int kMaxResidualSlices = 8;
 
 int check_device(int dev, char* why, size_t n) {
   int count = 0;
