@@ -723,28 +723,36 @@ class SpeculativeDecoder(BatchDecoder):
         self._free.sort(reverse=True)
         return out
 
-    def _uniforms(self, seqs: list[_Seq], offsets: range, c: int, dev: torch.device) -> torch.Tensor:
-        """[len(seqs), len(offsets)] uniforms of stream c at positions s.position + offset."""
-        seeds = [s.params.seed for s in seqs for _ in offsets]
-        pos = [-(4 * (s.position + o) + c) for s in seqs for o in offsets]
-        u = position_uniforms(seeds, pos)
-        return torch.from_numpy(u).view(len(seqs), len(offsets)).to(dev)
-
     def _speculate(self, seqs: list[_Seq]) -> list[tuple[int, Step]]:
         K = self.num_draft
         n = len(seqs)
         dev = self.model.device
-        params = self._params(seqs, dev)
-        slots = torch.tensor([s.slot for s in seqs], dtype=torch.int64, device=dev)
-        last = torch.tensor([s.generated[-1] for s in seqs], dtype=torch.int64, device=dev)
-        pos0 = torch.tensor([s.position - 1 for s in seqs], dtype=torch.int64, device=dev)  # the last token's
-        u_draft = self._uniforms(seqs, range(K), 1, dev)
+        g = self._group(seqs, dev)
+        params = g.params
+        # the step's host inputs in two copies: slots, last tokens and their positions; then every
+        # uniform of the step, of streams c = 1 (draft draws, [K, n]: one contiguous row per
+        # draft), 2 (acceptance) and 3 (residual) ([n, K] each) at positions + 0 .. K - 1, and
+        # 4 (bonus) at position + K
+        position = np.fromiter((s.position for s in seqs), np.int64, n)
+        ints = np.stack([g.slots, np.fromiter((s.generated[-1] for s in seqs), np.int64, n), position - 1])
+        offs = np.arange(K, dtype=np.int64)
+        at = position[:, None] + offs[None, :]  # [n, K]
+        useeds = np.concatenate([np.tile(g.seeds, K), np.repeat(g.seeds, K), np.repeat(g.seeds, K), g.seeds])
+        upos = np.concatenate([-(4 * at.T + 1).ravel(), -(4 * at + 2).ravel(), -(4 * at + 3).ravel(),
+                               -(4 * (position + K) + 4)])
+        u = torch.from_numpy(position_uniforms(useeds, upos)).to(dev)
+        ints_d = torch.from_numpy(ints).to(dev)
+        slots, last, pos0 = ints_d[0], ints_d[1], ints_d[2]  # (pos0: the last token's position)
+        nk = n * K
+        u_draft = u[:nk].view(K, n)
+        u_accept, u_residual, u_bonus = u[nk:2 * nk].view(n, K), u[2 * nk:3 * nk].view(n, K), u[3 * nk:]
         # the last draft of a fully accepted block reaches the draft model first (logits unused)
         gap = [s for s in seqs if s.draft_gap is not None]
         if gap:
-            self.draft_model.decode(*(torch.tensor(v, dtype=torch.int64, device=self.draft_model.device) for v in
-                                      ([s.slot for s in gap], [s.draft_gap[0] for s in gap],
-                                       [s.draft_gap[1] for s in gap])))
+            gd = torch.from_numpy(np.array([[s.slot for s in gap], [s.draft_gap[0] for s in gap],
+                                            [s.draft_gap[1] for s in gap]], dtype=np.int64))
+            gd = gd.to(self.draft_model.device)
+            self.draft_model.decode(gd[0], gd[1], gd[2])
             for s in gap:
                 s.draft_gap = None
         # the draft proposes K tokens
@@ -754,10 +762,10 @@ class SpeculativeDecoder(BatchDecoder):
         for j in range(K):
             logits = self.draft_model.decode(slots, x, pos0 + j)
             if with_states:
-                ids, st = self.sampler.sample_states(logits, params, u_draft[:, j].contiguous())
+                ids, st = self.sampler.sample_states(logits, params, u_draft[j])
                 states.append(st)
             else:
-                ids, _ = self.sampler.sample_batch(logits, params, u_draft[:, j].contiguous())
+                ids, _ = self.sampler.sample_batch(logits, params, u_draft[j])
             draft_rows.append(logits)
             drafts.append(ids)
             x = ids.long()
@@ -772,9 +780,7 @@ class SpeculativeDecoder(BatchDecoder):
             target = self.model.decode(slots.repeat_interleave(K + 1), toks.reshape(-1),
                                        (pos0.view(n, 1) + steps).reshape(-1)).view(n, K + 1, -1)
         tokens, counts = self.sampler.verify(
-            target, torch.stack(draft_rows, dim=1), drafts_t, params,
-            self._uniforms(seqs, range(K), 2, dev), self._uniforms(seqs, range(K), 3, dev),
-            self._uniforms(seqs, range(K, K + 1), 4, dev).view(n),
+            target, torch.stack(draft_rows, dim=1), drafts_t, params, u_accept, u_residual, u_bonus,
             draft_states=torch.stack(states, dim=1) if with_states else None,
         )
         tokens, counts = tokens.tolist(), counts.tolist()  # the iteration's wait
