@@ -4,7 +4,7 @@ The oracle decides in fp64 with ties by ascending id; the engine decides in fp32
 unstable sort (src/vinfer/runtime/sampler.py:52-64). ``oracle/fp32_rule.py`` redoes the engine's
 fp32 steps with torch's CPU kernels and flags the rows on which the engine's rule itself is
 ambiguous (equal probabilities straddling the top-p cutoff, a cutoff inside the fp32 summation
-band, min-p within 4 ulp, a draw on a prefix boundary). Here, on rows of every survey shape:
+band, min-p within 4 ulp, a draw on a prefix boundary). Here, on rows of every benchmark workload shape:
 wherever the engine's rule is not ambiguous, its kept set equals the oracle's, for both the
 ascending-id order and torch.sort's own order of equal probabilities, and the fp32 draw picks
 the oracle's token. The tie counts per shape are the ones the parity reports quote.
