@@ -395,10 +395,21 @@ class HipSampler:
             a.hist_ids, a.hist_offsets, a.hist_total = hist_ptr, t.base + 32, n
             a.workspace, a.workspace_bytes = (self._workspace.data_ptr() + 255) & ~255, need
         stream = torch.cuda.current_stream(dev)
+        out = t.out_np
+        out[0] = -1
         _lib.check(self._lib.vsamp_sample(t.ref, ctypes.c_void_p(stream.cuda_stream)))
-        stream.synchronize()
+        # the kernel writes the id last, after every read of the parameters and the history: the
+        # call returns as soon as the id reaches the pinned word (sooner than a stream
+        # synchronisation returns), and a synchronisation settles it past any draw's time
+        spins = 0
+        while out[0] < 0:
+            spins += 1
+            if spins == 1 << 20:
+                stream.synchronize()
+                if out[0] < 0:
+                    raise RuntimeError("the drawn id never reached the host")
         del keep
-        return int(t.out_np[0])
+        return int(out[0])
 
     def _token_path(self, dev: torch.device) -> "_TokenPath":
         t = self._tokens.get(dev)
@@ -413,8 +424,9 @@ class _TokenPath:
     no copy either way, 6 us less per call than a copy in and a copy out): the row's parameter
     words (temperature, top_p, min_p, the three penalties, top_k, the uniform, the history's
     [0, n) range), the history of a call that passes it from the host, and the drawn id. The
-    call synchronises its stream before returning, so nothing here is rewritten while a kernel
-    reads it (one caller thread per device, as the engine's generation worker is)."""
+    call returns once the kernel has written the id, which it does after its last read of the
+    rest, so nothing here is rewritten while a kernel reads it (one caller thread per device, as
+    the engine's generation worker is)."""
 
     def __init__(self, dev: torch.device) -> None:
         self.words_t = torch.zeros(16, dtype=torch.int32, pin_memory=True)
