@@ -28,6 +28,9 @@ import time
 
 METRIC = "sampled rows/sec + µs/step at B=256, V=151936 bf16; % HBM roofline"
 HBM_PEAK_GBS = 8000.0
+# What "dtype" stands for: the sampling decisions are taken on fp32 z, as the engine's are.
+ARITHMETIC = ("bf16/fp32 logits widened exactly to fp32; z = x / T in fp32 (IEEE division); "
+              "exp(z - max z) in fp64; masses as u64 fixed point (units of 2^-42), summed exactly")
 N_SETS = 4
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "k_sample_bf16_peaked_flat_B256.md")
 COPY_PROBE_BYTES = 1 << 30  # bytes read (and written) by one launch of the copy probe
@@ -261,7 +264,8 @@ def decode_loop(args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64",
+        "dtype": "f32",
+        "arithmetic": ARITHMETIC,
         "data": "synthetic",
         "config": {
             "workload": "decode_loop",
@@ -365,7 +369,8 @@ def verify_bench(args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64",
+        "dtype": "f32",
+        "arithmetic": ARITHMETIC,
         "data": "synthetic",
         "config": {"workload": "verify_k1", "batch": B, "num_draft": K, "vocab": V, "logits_dtype": "bf16",
                    "temperature": "U[0.5,1.2]", "top_p": 0.95, "draft": "target + N(0, 0.5^2)"},
@@ -434,7 +439,8 @@ def logprobs_bench(args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64",
+        "dtype": "f32",
+        "arithmetic": ARITHMETIC,
         "data": "synthetic",
         "config": {"workload": "logprobs_peaked_flat", "batch": w.batch, "vocab": w.vocab, "logits_dtype": "bf16",
                    "n_top": 20, "input_sets": N_SETS},
@@ -787,7 +793,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64",
+        "dtype": "f32",
+        "arithmetic": ARITHMETIC,
         "data": "synthetic",
         "config": {
             "workload": "peaked_flat",

@@ -746,3 +746,48 @@ def test_split_rows_equal_whole_rows(B, V, pad, pen):
         assert torch.equal(i1, i2) and torch.equal(p1.view(torch.int32), p2.view(torch.int32))
     ties, bad = compare_ids(i1, oracle(w), p1)
     assert not bad, bad[:10]
+
+
+@pytest.mark.parametrize("pen", [False, True], ids=["plain", "penalties"])
+def test_split_rows_replayed_from_a_graph(pen):
+    # A HIP graph keeps the arguments of the launch it captured, the rows' arrival epoch among
+    # them: each replay must still finish every row (the last slice sets the arrival count back
+    # to 0 under that epoch). Three replays with new logits and uniforms each, eager work between
+    # them, against whole-row launches of the same inputs and the oracle.
+    B, V = 4, 151936
+    s = hip(torch.bfloat16)
+    w0 = random_workload(31 + pen, B, V, torch.bfloat16, penalties=pen, hist_len=300 if pen else 0)
+    w0.params.top_k[::2] = 0
+    d0 = w0.to(DEV)
+    x = d0.logits.clone()
+    u = d0.uniforms.clone()
+    hi, ho = (d0.hist_ids, d0.hist_offsets) if pen else (None, None)
+    s.split_rows = True
+    try:
+        st = s.prepare_batch(x, d0.params, u, hi, ho, d0.draft_ids)
+    finally:
+        s.split_rows = False
+    assert st._args.flags & _lib.VSAMP_SPLIT_ROWS
+    print(f"split rows in a graph B={B} V={V} penalties={pen}", flush=True)
+    st.launch()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st.launch()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        fresh = random_workload(100 * rep + 7 + pen, B, V, torch.bfloat16, penalties=False)
+        w = Workload(f"replay {rep}", fresh.logits, w0.params, fresh.uniforms, w0.hist_ids, w0.hist_offsets,
+                     w0.draft_ids)
+        x.copy_(w.logits.to(DEV))
+        u.copy_(w.uniforms.to(DEV))
+        st.ids.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        got, gp = st.ids.cpu(), st.draft_prob.cpu()
+        want, wp = s.sample_batch(x, d0.params, u, hi, ho, d0.draft_ids)  # (whole rows, eager)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want.cpu()), (rep, got, want)
+        assert torch.equal(gp.view(torch.int32), wp.cpu().view(torch.int32))
+        ties, bad = compare_ids(got, oracle(w), gp)
+        assert not bad, (rep, bad[:10])

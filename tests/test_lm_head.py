@@ -106,7 +106,7 @@ def check_logprobs_tiles(logits, tmax, tsum, tokens, n_top, oracle_rows=()):
 @pytest.mark.gpu
 @pytest.mark.parametrize("B,d,V,n_top", [(4, 256, 1000, 5), (9, 512, 20000, 20), (256, 4096, 151936, 20),
                                          (2, 128, 151936, 32), (5, 64, 300, 0), (1, 4096, 151936, 20),
-                                         (3, 4096, 151936, 20)])
+                                         (3, 4096, 151936, 20), (2, 64, 300, 20), (3, 64, 12, 20)])
 def test_gpu_logprobs_tiles_equal_logprobs(B, d, V, n_top):
     print(f"logprobs_tiles B={B} d={d} V={V} n_top={n_top}", flush=True)
     hidden, weight = operands(7 * B + V, B, d, V)

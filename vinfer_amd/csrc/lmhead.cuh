@@ -87,9 +87,22 @@ __device__ __forceinline__ void wait_vm() {
 
 // One wave-wide global_load_lds_dwordx4: lane L's 16 bytes at `src` go to LDS byte address
 // `lds` + 16 L (`lds` wave-uniform). Counted by vmcnt.
+// The LDS address goes in M0, which the compiler reserves: the statement saves M0 in a scalar
+// register of its own and restores it after the load has been issued, so M0 holds the
+// compiler's value again when the statement ends. The s_nop is the one wait state the ISA asks
+// for between an SALU write of M0 and an LDS DMA that reads it.
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
 #if defined(__HIP_DEVICE_COMPILE__)  // (the host pass of hipcc parses device code too)
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(lds), "v"(src) : "memory", "m0");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
 #endif
 }
 

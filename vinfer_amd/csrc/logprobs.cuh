@@ -286,9 +286,11 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
     }
     s = block_sum<double>(s, reinterpret_cast<double*>(srch.red64));
     lse = static_cast<double>(M) + log(s);
-    if (n > 0) {
+    if (n > 0 && a.nT >= min(n, a.V)) {
       // 2. theta (16-bit key of the n-th largest tile max), the tiles whose max is >= it, and
-      // their elements >= theta into the list
+      // their elements >= theta into the list. (With fewer tiles than the n = min(n_top, V)
+      // elements asked for, the smallest tile max need not reach the n-th largest logit: such
+      // rows take the row passes below.)
       uint32_t k16[4];
       int nk = 0;
 #pragma unroll
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
         k16[i] = key_of(mt[i]) >> 16;  // (a bf16 value: the top half of its key; any NaN the largest)
         nk += tid + i * kThreads < a.nT;
       }
-      const uint32_t nnt = static_cast<uint32_t>(min(min(n, a.V), a.nT));
+      const uint32_t nnt = static_cast<uint32_t>(min(n, a.V));
       const uint32_t th = kth_key16(k16, nk, nnt, rdx.hcnt, sh);
       uint32_t mine = 0;
 #pragma unroll
@@ -337,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
         }
         front = false;
       }
-    } else {
+    } else if (n == 0) {
       front = false;
     }
   }

@@ -2078,10 +2078,10 @@ __device__ __forceinline__ int split_find(const SampleArgs& a, const Row<uint16_
       for (int t = 0; t < (k2 != k1 ? 2 : 1); ++t) {
         const uint32_t key = t ? k2 : k1;
         const uint32_t ch = (65535u - key) >> 6;
-        const uint32_t e = ld_global(reinterpret_cast<const uint16_t*>(rec + kSliceEmap) + ch);
+        const uint32_t e = ld_dev<uint16_t>(reinterpret_cast<const uint16_t*>(rec + kSliceEmap) + ch);
         if (e != kNoEntry) {
           const uint32_t w0 = 32768u - 32u * ch - 32u;  // the chunk's first histogram word
-          const uint32_t word = ld_global(reinterpret_cast<const uint32_t*>(rec + kSliceData) + 32u * e + ((key >> 1) - w0));
+          const uint32_t word = ld_dev<uint32_t>(reinterpret_cast<const uint32_t*>(rec + kSliceData) + 32u * e + ((key >> 1) - w0));
           c += (word >> ((key & 1u) << 4)) & 0xFFFFu;
         }
       }

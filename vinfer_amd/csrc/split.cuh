@@ -12,11 +12,45 @@
 // found in one slice: the records give each slice's count of the drawn value, so only the slice
 // holding the member is searched. Nothing waits for another workgroup: the others exit after
 // counting themselves in.
+//
+// The records cross workgroups, and XCDs, within the launch. They are written with agent-scope
+// relaxed atomic stores and read with agent-scope relaxed atomic loads (`st_dev` / `ld_dev`).
+// On gfx950 these are plain vector stores and loads with the SC1 bit set (device scope): a
+// store is written through the writer's L2 to the device's coherence point, and a load returns
+// the device-coherent copy rather than a line a reader's L2 may still hold from an earlier
+// launch. Each writer waits for its own stores to complete (`s_waitcnt vmcnt(0)`) before the
+// workgroup barrier that precedes the arrival's atomic, so the slice that sees the count reach
+// G reads complete records. This takes the place of a release fence in every writer and an
+// acquire fence in the reader, which on this GPU write back or invalidate the whole L2 of the
+// XCD (the fence pair took ~6 us of each arrival). The HIP memory model alone does not promise this
+// ordering for relaxed atomics; the SC1 encoding of gfx950's agent-scope atomics does.
 #pragma once
 
 #include "common.cuh"
 
 namespace vs {
+
+// Device-coherent stores and loads (agent-scope relaxed atomics: SC1 on gfx950), for data that
+// another workgroup of the same launch reads.
+template <class T>
+__device__ __forceinline__ void st_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T ld_dev(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u4(uint4* p, uint4 v) {
+  u64* q = reinterpret_cast<u64*>(p);
+  st_dev<u64>(q, (static_cast<u64>(v.y) << 32) | v.x);
+  st_dev<u64>(q + 1, (static_cast<u64>(v.w) << 32) | v.z);
+}
+__device__ __forceinline__ uint4 ld_dev_u4(const uint4* p) {
+  const u64* q = reinterpret_cast<const u64*>(p);
+  const u64 a = ld_dev<u64>(q), b = ld_dev<u64>(q + 1);
+  return make_uint4(static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b),
+                    static_cast<uint32_t>(b >> 32));
+}
 
 // One slice record: data[1024][32] u32 | idx[1024] u16 | emap[1024] u16 | n u32 (256-aligned).
 constexpr size_t kSliceData = 0;
@@ -78,6 +112,7 @@ __device__ __forceinline__ void slice_hist(const uint16_t* row, int V, int G, in
 
 // Writes the slice record of `hist` (complete and published by the caller's barrier) to `rec`:
 // thread t takes chunk t (keys 65535 - 64t - 63 .. 65535 - 64t, words 32768 - 32t - 32 ..).
+// Every store is device-coherent, and each thread waits for its stores to complete.
 __device__ __forceinline__ void slice_record(const uint32_t* hist, uint8_t* rec, uint32_t* red) {
   const int tid = threadIdx.x;
   const int w0 = 32768 - 32 * tid - 32;
@@ -94,25 +129,24 @@ __device__ __forceinline__ void slice_record(const uint32_t* hist, uint8_t* rec,
   if (nz) {
     uint4* dst = reinterpret_cast<uint4*>(rec + kSliceData) + 8 * pos;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) dst[s] = c[s];
-    reinterpret_cast<uint16_t*>(rec + kSliceIdx)[pos] = static_cast<uint16_t>(tid);
+    for (int s = 0; s < 8; ++s) st_dev_u4(dst + s, c[s]);
+    st_dev<uint16_t>(reinterpret_cast<uint16_t*>(rec + kSliceIdx) + pos, static_cast<uint16_t>(tid));
   }
-  reinterpret_cast<uint16_t*>(rec + kSliceEmap)[tid] = nz ? static_cast<uint16_t>(pos) : kNoEntry;
-  if (tid == 0) *reinterpret_cast<uint32_t*>(rec + kSliceN) = n;
+  st_dev<uint16_t>(reinterpret_cast<uint16_t*>(rec + kSliceEmap) + tid, nz ? static_cast<uint16_t>(pos) : kNoEntry);
+  if (tid == 0) st_dev<uint32_t>(reinterpret_cast<uint32_t*>(rec + kSliceN), n);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Counts this workgroup's slice in at the row's arrival word and tells whether it is the row's
-// last (then every other slice's record is visible to it). The word holds (epoch << 16 | count):
-// a word left by another launch (another epoch, or never written) restarts the count at 1, so
-// the workspace needs no clearing between launches. `flag` is an LDS word.
-// The device-scope fences are taken by thread 0 alone, ordered after (release) and before
-// (acquire) the other threads' accesses by the workgroup barriers: each fence writes back or
-// invalidates the whole L2 of the XCD, and one per workgroup is enough (one per wave made a
-// launch of 256 workgroups four times slower).
+// last (then every other slice's record is complete, read with ld_dev). The word holds
+// (epoch << 16 | count): a word left by another launch (another epoch, or never written)
+// restarts the count at 1, so the workspace needs no clearing between launches. The last slice
+// sets the count back to 0 under the same epoch, so a replay of the launch with the same
+// arguments (a HIP graph keeps the epoch it was captured with) counts from 0 again. `flag` is
+// an LDS word.
 __device__ __forceinline__ bool slice_arrive(u64* word, u64 epoch, int G, int* flag) {
-  __syncthreads();  // (every wave's record stores have completed)
+  __syncthreads();  // (every thread's record stores have completed: slice_record's vmcnt(0))
   if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // (the workgroup's record stores are visible first)
     const u64 tag = epoch & 0xFFFFFFFFFFFFull;
     u64 old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     u64 now = 0;
@@ -126,8 +160,8 @@ __device__ __forceinline__ bool slice_arrive(u64* word, u64 epoch, int G, int* f
       old = seen;
     }
     *flag = static_cast<int>(now & 0xFFFFu);
-    if ((now & 0xFFFFu) == static_cast<u64>(G))
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // (the other slices' records are read after this)
+    // (every slice of this launch has counted itself in: nothing else touches the word now)
+    if ((now & 0xFFFFu) == static_cast<u64>(G)) st_dev<u64>(word, tag << 16);
   }
   __syncthreads();
   return *flag == G;
@@ -140,7 +174,7 @@ __device__ __forceinline__ void slice_merge(const uint8_t* recs, int G, int own,
   const int tid = threadIdx.x;
   if (tid < kWave) {
     const uint32_t n = tid < G && tid != own
-                           ? ld_global(reinterpret_cast<const uint32_t*>(recs + static_cast<size_t>(tid) * kSliceRecord + kSliceN))
+                           ? ld_dev<uint32_t>(reinterpret_cast<const uint32_t*>(recs + static_cast<size_t>(tid) * kSliceRecord + kSliceN))
                            : 0u;
     const uint32_t u = 8u * n;
     const uint32_t inc = wave_incl_scan<uint32_t>(u);
@@ -164,8 +198,8 @@ __device__ __forceinline__ void slice_merge(const uint8_t* recs, int G, int own,
       }
       const uint32_t e = (U - pre[lo]) >> 3;
       const uint8_t* rec = recs + static_cast<size_t>(lo) * kSliceRecord;
-      ch[k] = ld_global(reinterpret_cast<const uint16_t*>(rec + kSliceIdx) + e);
-      q[k] = ld_global_u4(reinterpret_cast<const uint4*>(rec + kSliceData) + 8 * e + (U & 7u));
+      ch[k] = ld_dev<uint16_t>(reinterpret_cast<const uint16_t*>(rec + kSliceIdx) + e);
+      q[k] = ld_dev_u4(reinterpret_cast<const uint4*>(rec + kSliceData) + 8 * e + (U & 7u));
     }
 #pragma unroll
     for (int k = 0; k < kAhead; ++k) {

@@ -335,7 +335,11 @@ __device__ __forceinline__ void residual_item(const VerifyArgs& a, int b, int sl
     // (vmcnt counts stores too) before the workgroup barrier and the counter's atomic add, and
     // the last slice loads them with agent-scope atomic loads only after that add has returned.
     // Device-scope fences (an L2 write-back and an invalidate per slice, ~15 us of a call)
-    // are not needed for these few words; nothing else crosses workgroups here.
+    // are not needed for these few words; nothing else crosses workgroups here. This rests on
+    // gfx950's encoding rather than on the HIP memory model, which orders relaxed atomics only
+    // through a release/acquire pair: an agent-scope atomic store or load is a vector store or
+    // load with the SC1 bit (device scope), written through the writer's L2 and read from the
+    // device's coherence point, and vmcnt(0) returns once the store has reached that point.
     __syncthreads();
     if (tid < j_end - j_begin) {
       u64 t = 0;

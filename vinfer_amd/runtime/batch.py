@@ -57,7 +57,8 @@ import torch
 
 from vinfer_amd._lib import position_uniforms
 from vinfer_amd.sampler.base import SamplerBackend
-from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params
+from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params, penalized
+from vinfer_amd.sampling import field as param_field
 
 
 class TextStream(Protocol):
@@ -348,9 +349,10 @@ class BatchDecoder:
         j = 0  # position in nxt
         for i, (s, tok) in enumerate(zip(seqs, tokens)):
             step = advance(s, tok)
-            if lp_of is not None and s.params.logprobs:
+            if lp_of is not None and param_field(s.params, "logprobs"):
                 step.logprob, top = lp_of[id(s)]
-                step.top_logprobs = top[: s.params.top_logprobs] if s.params.top_logprobs else None
+                n_top = param_field(s.params, "top_logprobs")
+                step.top_logprobs = top[:n_top] if n_top else None
             out.append((s.rid, step))
             launched = j < m and nxt[j] == i
             if step.finish_reason is None:
@@ -560,7 +562,7 @@ class BatchDecoder:
             s.position = len(s.prompt)
             prompt = torch.tensor(s.prompt, dtype=torch.int64)
             self._hist_len[s.slot] = 0
-            if s.params.penalized and self.penalize_prompt:
+            if penalized(s.params) and self.penalize_prompt:
                 base = s.slot * self._hist_row
                 self.hist[base : base + len(s.prompt)] = prompt.to(torch.int32).to(dev)
                 self._hist_len[s.slot] = len(s.prompt)
@@ -577,8 +579,8 @@ class BatchDecoder:
                 self._groups.clear()
             ps = [s.params for s in seqs]
             slots = np.array([s.slot for s in seqs], dtype=np.int64)
-            pen = np.array([p.penalized for p in ps], dtype=bool)
-            lps = [p.top_logprobs for p in ps if p.logprobs]
+            pen = np.array([penalized(p) for p in ps], dtype=bool)
+            lps = [param_field(p, "top_logprobs") for p in ps if param_field(p, "logprobs")]
             g = self._groups[key] = _Group(slots, np.array([p.seed for p in ps], dtype=np.int64), pen, slots[pen],
                                            pack_params(ps, dev), max(lps) if lps else -1, key)
         return g
@@ -633,7 +635,7 @@ class BatchDecoder:
         for seqs, tok_lp, top_ids, top_lp in self._lp:
             tl, ti, tv = tok_lp.tolist(), top_ids.tolist(), top_lp.tolist()
             for i, s in enumerate(seqs):
-                if s.params.logprobs:
+                if param_field(s.params, "logprobs"):
                     out[id(s)] = (tl[i], list(zip(ti[i], tv[i])))
         return out
 
@@ -687,9 +689,9 @@ class SpeculativeDecoder(BatchDecoder):
         self._ready: list[_Seq] = []  # sequences with a first token, waiting for an iteration
 
     def submit(self, prompt_ids: list[int], params: SamplingParams) -> int:
-        if params.penalized:
+        if penalized(params):
             raise ValueError("speculative decoding applies no penalties")
-        if params.logprobs:
+        if param_field(params, "logprobs"):
             raise ValueError("speculative decoding reports no log-probabilities")
         # positions up to prompt + max_tokens - 1 + num_draft are scored (the last block's drafts)
         check_request(len(prompt_ids), dataclasses.replace(params, max_tokens=params.max_tokens + self.num_draft),

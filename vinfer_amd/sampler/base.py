@@ -15,7 +15,7 @@ from typing import Protocol
 import torch
 
 from vinfer_amd.registry import BackendRegistry
-from vinfer_amd.sampling import PackedParams, SamplingParams
+from vinfer_amd.sampling import PackedParams, SamplingParams, penalized
 
 
 class SamplerBackend(Protocol):
@@ -113,7 +113,7 @@ def require_history(params: SamplingParams, history) -> None:
     """``ValueError`` when ``params`` turns a penalty on and no history was passed: the engine's
     per-token call (src/vinfer/runtime/generate.py:129) passes none, and silently sampling
     without the penalties would be a fallback (kernels/registry.py:5-7 rules those out)."""
-    if params.penalized and history is None:
+    if penalized(params) and history is None:
         raise ValueError(
             "repetition/presence/frequency penalties need the request's token history: "
             "pass history= (the token ids so far, empty for the first token)"

@@ -13,6 +13,7 @@ synchronising, except ``sample`` which returns a Python ``int`` as the engine's 
 from __future__ import annotations
 
 import ctypes
+import threading
 from collections.abc import Sequence
 
 import numpy as np
@@ -21,7 +22,7 @@ import torch
 from vinfer_amd import _lib
 from vinfer_amd.registry import BackendContext
 from vinfer_amd.sampler.base import SAMPLER, require_history
-from vinfer_amd.sampling import PackedParams, SamplingParams, pack_params, uniform
+from vinfer_amd.sampling import PackedParams, SamplingParams, field, pack_params, penalized, uniform
 
 _DTYPES = {torch.bfloat16: _lib.VSAMP_BF16, torch.float32: _lib.VSAMP_F32}
 
@@ -48,8 +49,10 @@ class HipSampler:
     def __init__(self, ctx: BackendContext) -> None:
         self.ctx = ctx
         self._lib = _lib.load()
-        self._workspace = torch.empty(0, dtype=torch.uint8)
-        self._tokens: dict[torch.device, _TokenPath] = {}  # the per-token call's buffers
+        # Per calling thread: the workspaces by device and the per-token call's buffers. A
+        # thread's calls on one device are ordered (one stream, or the per-token call's wait), so
+        # its buffers are never rewritten while a kernel reads them; two threads never share one.
+        self._local = threading.local()
         # sample_batch / prepare_batch take append_history (VSAMP_HIST_APPEND)
         self.appends_history = True
         # Split small bf16 batches' rows over several workgroups (VSAMP_SPLIT_ROWS): identical
@@ -136,10 +139,7 @@ class HipSampler:
         ws_bytes = self._lib.vsamp_split_workspace_bytes if self.split_rows else self._lib.vsamp_workspace_bytes
         need = int(ws_bytes(B, V, hist_total))
         if need:
-            if self._workspace.device != dev or self._workspace.numel() < need + 256:
-                self._workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
-            base = self._workspace.data_ptr()
-            a.workspace = (base + 255) & ~255
+            a.workspace = self._workspace(dev, need)
             a.workspace_bytes = need
         keep = (logits, cols, hist_ids, hist_offsets, uniforms, draft_ids)
         return a, keep
@@ -197,9 +197,7 @@ class HipSampler:
         dev = logits.device
         need = int(self._lib.vsamp_workspace_bytes(B, V, a.hist_total))
         if a.workspace_bytes < need:
-            if self._workspace.device != dev or self._workspace.numel() < need + 256:
-                self._workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
-            a.workspace = (self._workspace.data_ptr() + 255) & ~255
+            a.workspace = self._workspace(dev, need)
             a.workspace_bytes = need
         out = torch.empty(B, V, dtype=torch.float32, device=dev)
         counts = torch.empty(B, V, dtype=torch.int32, device=dev)
@@ -368,11 +366,13 @@ class HipSampler:
         t = self._token_path(dev)
         # the row's parameters, its uniform and its history's range: one pinned block, one copy
         f = t.words.view(np.float32)
-        f[0], f[1], f[2] = params.temperature, params.top_p, params.min_p
-        f[3], f[4], f[5] = params.repetition_penalty, params.presence_penalty, params.frequency_penalty
+        f[0], f[1], f[2] = params.temperature, params.top_p, field(params, "min_p")
+        f[3] = field(params, "repetition_penalty")
+        f[4] = field(params, "presence_penalty")
+        f[5] = field(params, "frequency_penalty")
         t.words[6] = params.top_k
         f[7] = uniform(seed, position)
-        n = len(history) if params.penalized else 0
+        n = len(history) if penalized(params) else 0
         a = t.args
         a.logits, a.dtype, a.vocab, a.row_stride = row.data_ptr(), _DTYPES[row.dtype], V, V
         a.hist_ids = a.hist_offsets = a.workspace = None
@@ -390,10 +390,8 @@ class HipSampler:
                 hist_ptr = t.hist_host.data_ptr()
             t.words[8], t.words[9] = 0, n
             need = int(self._lib.vsamp_workspace_bytes(1, V, n))
-            if self._workspace.device != dev or self._workspace.numel() < need + 256:
-                self._workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
             a.hist_ids, a.hist_offsets, a.hist_total = hist_ptr, t.base + 32, n
-            a.workspace, a.workspace_bytes = (self._workspace.data_ptr() + 255) & ~255, need
+            a.workspace, a.workspace_bytes = self._workspace(dev, need), need
         stream = torch.cuda.current_stream(dev)
         out = t.out_np
         out[0] = -1
@@ -412,10 +410,19 @@ class HipSampler:
         return int(out[0])
 
     def _token_path(self, dev: torch.device) -> "_TokenPath":
-        t = self._tokens.get(dev)
+        paths = self._local.__dict__.setdefault("paths", {})
+        t = paths.get(dev)
         if t is None:
-            t = self._tokens[dev] = _TokenPath(dev)
+            t = paths[dev] = _TokenPath(dev)
         return t
+
+    def _workspace(self, dev: torch.device, need: int) -> int:
+        """A 256-byte aligned device workspace of ``need`` bytes, this thread's for ``dev``."""
+        spaces = self._local.__dict__.setdefault("workspaces", {})
+        w = spaces.get(dev)
+        if w is None or w.numel() < need + 256:
+            w = spaces[dev] = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+        return (w.data_ptr() + 255) & ~255
 
 
 class _TokenPath:
@@ -425,8 +432,8 @@ class _TokenPath:
     words (temperature, top_p, min_p, the three penalties, top_k, the uniform, the history's
     [0, n) range), the history of a call that passes it from the host, and the drawn id. The
     call returns once the kernel has written the id, which it does after its last read of the
-    rest, so nothing here is rewritten while a kernel reads it (one caller thread per device, as
-    the engine's generation worker is)."""
+    rest, so nothing here is rewritten while a kernel reads it. Each calling thread has its own
+    (the engine calls from one generation worker thread, serial.py:40)."""
 
     def __init__(self, dev: torch.device) -> None:
         self.words_t = torch.zeros(16, dtype=torch.int32, pin_memory=True)

@@ -18,7 +18,7 @@ import torch
 
 from vinfer_amd.registry import BackendContext
 from vinfer_amd.sampler.base import SAMPLER, require_history
-from vinfer_amd.sampling import SamplingParams, pack_params, uniform
+from vinfer_amd.sampling import SamplingParams, pack_params, penalized, uniform
 
 
 def _penalize(x: torch.Tensor, hist: torch.Tensor, rep, pres, freq):
@@ -229,7 +229,7 @@ class ReferenceSampler:
         require_history(params, history)
         dev = logits.device
         hist = off = None
-        if params.penalized and len(history) > 0:
+        if penalized(params) and len(history) > 0:
             hist = torch.as_tensor(history, dtype=torch.int32).to(dev)
             off = torch.tensor([0, hist.numel()], dtype=torch.int32, device=dev)
         u = torch.tensor([uniform(seed, position)], dtype=torch.float32, device=dev)

@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import torch
 
-from vinfer_amd.sampling.params import SamplingParams
+from vinfer_amd.sampling.params import SamplingParams, field
 
 F32_FIELDS = (
     "temperature",
@@ -74,8 +74,9 @@ class PackedParams:
 def pack_params(
     params: Sequence[SamplingParams], device: torch.device | str = "cpu"
 ) -> PackedParams:
-    """Pack one ``SamplingParams`` per row."""
-    cols = {k: torch.tensor([getattr(p, k) for p in params], dtype=torch.float32) for k in F32_FIELDS}
+    """Pack one params object per row: this package's ``SamplingParams`` or the engine's own
+    (sampler.py:18-27), whose missing extension fields pack as their off values."""
+    cols = {k: torch.tensor([field(p, k) for p in params], dtype=torch.float32) for k in F32_FIELDS}
     top_k = torch.tensor([p.top_k for p in params], dtype=torch.int32)
     return PackedParams(top_k=top_k, **cols).to(device)
 

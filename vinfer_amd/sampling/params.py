@@ -70,11 +70,37 @@ class SamplingParams:
 
     @property
     def penalized(self) -> bool:
-        return (
-            self.repetition_penalty != 1.0
-            or self.presence_penalty != 0.0
-            or self.frequency_penalty != 0.0
-        )
+        return penalized(self)
+
+
+# The extension fields and their off values. The engine's own SamplingParams (sampler.py:18-27)
+# has none of them; every reader below takes them with ``field`` so that an object of the
+# engine's class, or of that class with some of these fields added, is read as "off" for each
+# field it lacks.
+EXTENSION_DEFAULTS: dict[str, float | int | bool] = {
+    "repetition_penalty": 1.0,
+    "presence_penalty": 0.0,
+    "frequency_penalty": 0.0,
+    "min_p": 0.0,
+    "logprobs": False,
+    "top_logprobs": 0,
+}
+
+
+def field(params, name: str):
+    """``params.<name>``; for an extension field the object lacks, its off value."""
+    if name in EXTENSION_DEFAULTS:
+        return getattr(params, name, EXTENSION_DEFAULTS[name])
+    return getattr(params, name)
+
+
+def penalized(params) -> bool:
+    """Whether any of the three penalties is on for ``params`` (any params object)."""
+    return (
+        field(params, "repetition_penalty") != 1.0
+        or field(params, "presence_penalty") != 0.0
+        or field(params, "frequency_penalty") != 0.0
+    )
 
 
 def position_seed(seed: int, position: int) -> int:
