@@ -515,6 +515,81 @@ def lm_head_bench(args) -> int:
     return 0
 
 
+def lm_head_sample_bench(args) -> int:
+    """``--lm-head-sample``: the LM head plus the draw at d=4096, V=151936, B in {1, 64}, for three
+    kinds of rows without penalties: greedy, peaked (one logit far above the rest: the hidden
+    state near one weight row; T 1.0, top-p 0.95, min-p 0.05 as the headline's peaked rows) and
+    top-k (T 0.7, top-k 20, top-p 0.8). Unfused: torch's bf16 matmul, then ``sample_batch``;
+    fused: ``vsamp_lm_head``, then ``sample_tiles`` over its tile maxima; each draw a prepared
+    launch. Both draws are also run on the fused logits, whose ids must agree. One JSON line per
+    (batch, kind), HIP events on the launch stream, synthetic bf16 operands."""
+    import math
+
+    import torch
+
+    from vinfer_amd.registry import BackendContext
+    from vinfer_amd.sampler import SAMPLER
+    from vinfer_amd.sampling import SamplingParams, pack_params
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    s = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    d, V = 4096, 151936
+    g = torch.Generator(device=dev).manual_seed(0)
+    W = (torch.randn(V, d, generator=g, device=dev) * (4 / math.sqrt(d))).to(torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, n=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+    kinds = {
+        "greedy": SamplingParams(temperature=0.0),
+        "peaked": SamplingParams(temperature=1.0, top_p=0.95, min_p=0.05),
+        "top_k": SamplingParams(temperature=0.7, top_k=20, top_p=0.8),
+    }
+    for B in (1, 64):
+        for kind, sp in kinds.items():
+            hidden = torch.randn(B, d, generator=g, device=dev) * 0.5
+            if kind == "peaked":
+                rows = torch.randint(0, V, (B,), generator=g, device=dev)
+                hidden = hidden * 0.1 + 3.0 * W[rows].float()
+            hidden = hidden.to(torch.bfloat16)
+            params = pack_params([sp] * B, dev)
+            u = torch.rand(B, generator=g, device=dev)
+            logits_t = hidden @ W.T
+            logits_f, tmax, _ = s.lm_head(hidden, W)
+            a, _ = s.sample_tiles(logits_f, tmax, params, u)
+            b, _ = s.sample_batch(logits_f, params, u)
+            # (the draws as prepared launches: argument blocks built once, as a decode loop does)
+            st_rows = s.prepare_batch(logits_t, params, u)
+            st_tiles = s.prepare_tiles(logits_f, tmax, params, u)
+            us = {
+                "torch_matmul": timed(lambda: hidden @ W.T),
+                "sample_batch": timed(lambda: st_rows.launch(stream.cuda_stream)),
+                "lm_head_fused": timed(lambda: s.lm_head(hidden, W)),
+                "sample_tiles": timed(lambda: st_tiles.launch(stream.cuda_stream)),
+            }
+            us["unfused_total"] = us["torch_matmul"] + us["sample_batch"]
+            us["fused_total"] = us["lm_head_fused"] + us["sample_tiles"]
+            print(json.dumps({"lm_head_sample": {"batch": B, "dim": d, "vocab": V, "rows": kind,
+                                                 "params": {"temperature": sp.temperature, "top_k": sp.top_k,
+                                                            "top_p": sp.top_p, "min_p": sp.min_p}},
+                              "us": us, "fused_speedup": us["unfused_total"] / us["fused_total"],
+                              "draw_speedup": us["sample_batch"] / us["sample_tiles"],
+                              "ids_equal": bool(torch.equal(a, b))}), flush=True)
+            del hidden, logits_t, logits_f, tmax
+    return 0
+
+
 def regimes_bench(args) -> int:
     """``--regimes``: the headline batch (B=256, V=151936 bf16) split by regime: its flat rows
     alone, its peaked rows alone, each with and without the rows' histories, then the mixed
@@ -562,15 +637,83 @@ def regimes_bench(args) -> int:
     return 0
 
 
+def workload_cpu_baseline(w, budget_s: float = 3.0) -> dict:
+    """The CPU reference sampler on the workload, one row per call as the engine's ``sample``
+    runs (sampler.py:68-77): torch's CPU kernels on the engine's fp32 rule plus the extensions
+    (oracle/fp32_rule.py:torch_cpu_sample), with torch's default thread count on this host and
+    with one thread; the median per-row time of each. single_fp32 (one row per step) is timed
+    as 1000 steps, each on a new row and uniform of the same generator; the other workloads
+    cycle through their rows for ``budget_s``. Beside it, the numpy fp64 oracle on one thread."""
+    import numpy as np
+    import torch
+
+    from oracle.fp32_rule import torch_cpu_sample  # the checker's CPU restatement, timed as the baseline
+    from oracle.sampler_oracle import sample_batch
+    from vinfer_amd.workloads import make
+
+    steps = 1000 if w.batch == 1 else None
+    src = make(w.name if w.name != "single_bf16" else "single_fp32", batch=steps) if steps else w
+    if w.logits.dtype == torch.bfloat16 and src is not w:
+        src.logits = src.logits.to(torch.bfloat16)
+    p = src.params
+    empty = torch.zeros(0, dtype=torch.int32)
+
+    def row(b):
+        h = src.hist_ids[int(src.hist_offsets[b]) : int(src.hist_offsets[b + 1])] if src.hist_ids is not None else empty
+        return (src.logits[b], h, float(p.temperature[b]), int(p.top_k[b]), float(p.top_p[b]), float(p.min_p[b]),
+                float(p.repetition_penalty[b]), float(p.presence_penalty[b]), float(p.frequency_penalty[b]),
+                float(src.uniforms[b]))
+
+    def timed(threads):
+        torch.set_num_threads(threads)
+        per = []
+        t0 = time.perf_counter()
+        b = 0
+        while (b < steps) if steps else (time.perf_counter() - t0 < budget_s):
+            args = row(b % src.batch)
+            t1 = time.perf_counter()
+            torch_cpu_sample(*args)
+            per.append(time.perf_counter() - t1)
+            b += 1
+        return {"rows_per_s": len(per) / sum(per), "median_us_per_row": float(np.median(per)) * 1e6,
+                "rows": len(per), "threads": threads}
+
+    default_threads = torch.get_num_threads()
+    every = timed(default_threads)
+    one = timed(1)
+    torch.set_num_threads(default_threads)
+    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    cols = [f(getattr(w.params, k)) for k in ("temperature", "top_k", "top_p", "min_p", "repetition_penalty",
+                                               "presence_penalty", "frequency_penalty")]
+    hist = w.hist_ids.numpy() if w.hist_ids is not None else np.zeros(0, np.int32)
+    off = w.hist_offsets.numpy() if w.hist_offsets is not None else np.zeros(w.batch + 1, np.int32)
+    x, u = f(w.logits), f(w.uniforms)
+    dr = w.draft_ids.numpy() if w.draft_ids is not None else None
+    rows, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        r = rows % w.batch
+        sample_batch(x[r : r + 1], *[c[r : r + 1] for c in cols], hist, off[r : r + 2], u[r : r + 1],
+                     None if dr is None else dr[r : r + 1])
+        rows += 1
+    dt = time.perf_counter() - t0
+    what = (f"{every['rows']} steps of one new row each" if steps else
+            f"{every['rows']} rows of the workload (cycling through its {w.batch} rows)")
+    return {"value": every["rows_per_s"], "unit": "rows/s", "cores": default_threads, "kind": "port",
+            "sample": f"{what}, one row per call: torch CPU fp32 sampler on {default_threads} threads",
+            "median_us_per_row": every["median_us_per_row"], "single_thread": one,
+            "numpy_oracle_fp64_one_thread": {"value": rows / dt, "unit": "rows/s", "rows": rows,
+                                             "seconds": round(dt, 2)},
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "torch": torch.__version__}
+
+
 def workloads_bench(args) -> int:
     """``--workloads``: every named sampler workload (``vinfer_amd.workloads.NAMES``), one JSON line
     each: the launch time (back-to-back launches between HIP events on the launch stream, after
     warmup; inputs rotated over four copies when they fit in 8 GB), the HBM roofline fraction of
-    its algorithmic bytes, and the CPU oracle on a bounded sample of its rows."""
+    its algorithmic bytes, and the CPU reference sampler beside it (``workload_cpu_baseline``)."""
     import numpy as np
     import torch
 
-    from oracle.sampler_oracle import sample_batch  # the checker, timed here as the baseline
     from vinfer_amd.registry import BackendContext
     from vinfer_amd.sampler import SAMPLER
     from vinfer_amd.workloads import NAMES, make
@@ -616,23 +759,7 @@ def workloads_bench(args) -> int:
         if args.split_rows and w.logits.dtype == torch.bfloat16 and w.batch <= 128:
             out["us_per_launch_split_rows"] = timed(True)  # (VSAMP_SPLIT_ROWS: identical ids)
         if not args.no_cpu:
-            f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
-            p = w.params
-            cols = [f(getattr(p, k)) for k in ("temperature", "top_k", "top_p", "min_p", "repetition_penalty",
-                                                "presence_penalty", "frequency_penalty")]
-            hist = w.hist_ids.numpy() if w.hist_ids is not None else np.zeros(0, np.int32)
-            off = w.hist_offsets.numpy() if w.hist_offsets is not None else np.zeros(w.batch + 1, np.int32)
-            x, u = f(w.logits), f(w.uniforms)
-            dr = w.draft_ids.numpy() if w.draft_ids is not None else None
-            rows, t0 = 0, time.perf_counter()
-            while time.perf_counter() - t0 < 3.0:
-                r = rows % w.batch
-                sample_batch(x[r : r + 1], *[c[r : r + 1] for c in cols], hist, off[r : r + 2], u[r : r + 1],
-                             None if dr is None else dr[r : r + 1])
-                rows += 1
-            dt = time.perf_counter() - t0
-            out["cpu_baseline"] = {"value": rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
-                                   "sample": f"{rows} rows of the workload (cycling), numpy fp64 oracle; {dt:.1f} s"}
+            out["cpu_baseline"] = workload_cpu_baseline(w)
         print(json.dumps(out), flush=True)
         del sets, d
         torch.cuda.empty_cache()
@@ -673,6 +800,8 @@ def main() -> int:
                     help="time the headline batch's flat and peaked rows apart, with and without histories")
     ap.add_argument("--lm-head", action="store_true",
                     help="time the LM head + log-probabilities, fused against torch's matmul + vsamp_logprobs")
+    ap.add_argument("--lm-head-sample", action="store_true",
+                    help="time the LM head plus the draw, fused (tile maxima) against unfused")
     ap.add_argument("--split-rows", action="store_true",
                     help="with --workloads: also time small bf16 batches with split rows (VSAMP_SPLIT_ROWS)")
     args = ap.parse_args()
@@ -695,6 +824,8 @@ def main() -> int:
         return regimes_bench(args)
     if args.workloads:
         return workloads_bench(args)
+    if args.lm_head_sample:
+        return lm_head_sample_bench(args)
     if args.lm_head:
         return lm_head_bench(args)
 

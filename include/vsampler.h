@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 6
+#define VSAMP_ABI_VERSION 7
 
 /* Bytes of one row's sampling state (vsamp_sample_states), an opaque record. */
 #define VSAMP_ROW_STATE_BYTES 40
@@ -246,6 +246,18 @@ int vsamp_lm_head(const vsamp_lm_head_args* args, void* stream);
 int vsamp_logprobs_tiles(const vsamp_args* args, const float* tile_max, const float* tile_sum, const int32_t* tokens,
                          int32_t n_top, float* out_token_logprob, int32_t* out_top_ids, float* out_top_logprobs,
                          void* stream);
+
+/* vsamp_sample over bf16 logits that vsamp_lm_head wrote, with its tile maxima (`tile_max`
+ * [batch, ceil(vocab / VSAMP_LM_TILE)]: the max of every VSAMP_LM_TILE logits of a row). Same
+ * outputs as vsamp_sample on the same arguments, bit for bit. Rows the maxima decide are
+ * decided from a few tiles instead of a pass over the row: greedy rows (the first max lies in
+ * the first tile whose max is the row max) and rows sampled with top-k <= 256 or min-p (every
+ * kept token lies in a tile whose max reaches a bound taken from the maxima), without
+ * penalties. Every other row (penalties, top-p alone, NaN or infinite rows, more than 64
+ * candidate tiles or 256 candidate tokens) takes vsamp_sample's row passes in the same launch.
+ * Replaces the sampler call after the engine's LM head (models/qwen/model.py:230-233 ->
+ * runtime/sampler.py:68-77) when the LM head is vsamp_lm_head. */
+int vsamp_sample_tiles(const vsamp_args* args, const float* tile_max, void* stream);
 
 /* Host function (no device work): the draw's uniform of (seeds[i], positions[i]) into out[i],
  * i < n, all host memory. u = (splitmix64(position_seed(seed, position)) >> 40) * 2^-24, where

@@ -1,0 +1,176 @@
+"""The draw over the LM head's logits with its tile maxima (``vsamp_sample_tiles``).
+
+``sample_tiles`` must give exactly what ``sample_batch`` gives on the same logits and arguments:
+the same ids and the same draft probabilities, bit for bit, whether a row is decided from a few
+tiles (greedy rows, and top-k or min-p rows, without penalties) or takes the row passes
+(penalties, top-p alone, NaN and infinite rows, too many candidates). Both are then checked
+against the oracle on every non-tie row. Logits come from ``vsamp_lm_head`` (real GEMM output,
+with peaked rows made by a hidden state close to one weight row) and from crafted rows whose
+tile maxima the test computes (ties of the max across tiles, signed zeros, -inf, NaN and +inf
+rows, massive ties at the top-k boundary)."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from tests.parity import compare_ids, oracle
+from vinfer_amd import _lib
+from vinfer_amd.registry import BackendContext
+from vinfer_amd.sampler import SAMPLER
+from vinfer_amd.sampling import SamplingParams, pack_history, pack_params
+from vinfer_amd.workloads import Workload
+
+DEV = torch.device("cuda", 0)
+TILE = _lib.LM_TILE
+
+
+def hip():
+    return SAMPLER.resolve("hip", BackendContext(DEV, torch.bfloat16))
+
+
+def tile_max(logits: torch.Tensor) -> torch.Tensor:
+    """The max of every TILE logits of each row (a NaN is the largest), fp32 [B, nT]."""
+    B, V = logits.shape
+    nT = (V + TILE - 1) // TILE
+    x = torch.full((B, nT * TILE), -math.inf, dtype=torch.float32, device=logits.device)
+    x[:, :V] = logits.float()
+    return x.view(B, nT, TILE).amax(dim=2).contiguous()
+
+
+def mixed_params(rng, B, V, penalties_every=0):
+    """Every kind of row: greedy, top-k (some past the list's 256), min-p, both, top-p alone."""
+    out = []
+    for b in range(B):
+        kind = b % 8
+        kw = dict(temperature=float(rng.choice([0.3, 0.7, 1.0, 1.5])))
+        if kind == 0:
+            kw = dict(temperature=0.0)
+        elif kind == 1:
+            kw.update(top_k=int(rng.choice([1, 5, 20, 50, 256, 300])))
+        elif kind == 2:
+            kw.update(min_p=float(rng.choice([0.05, 0.3, 1.0])))
+        elif kind == 3:
+            kw.update(top_k=int(rng.choice([20, 50])), min_p=0.1, top_p=float(rng.choice([0.5, 0.9])))
+        elif kind == 4:
+            kw.update(top_p=0.9)  # (top-p alone: the row passes)
+        elif kind == 5:
+            kw.update(top_k=20, top_p=float(rng.choice([0.8, 1e-6])))
+        elif kind == 6:
+            kw.update(min_p=0.05, top_p=0.95)
+        else:
+            kw.update(top_k=int(rng.choice([1, 2, V - 1])))
+        if penalties_every and b % penalties_every == penalties_every - 1:
+            kw.update(repetition_penalty=1.3, frequency_penalty=0.5)
+        out.append(SamplingParams(**kw))
+    return out
+
+
+def check(logits, params, seed, hist=None, label=""):
+    B, V = logits.shape
+    rng = np.random.default_rng(seed)
+    s = hip()
+    tm = tile_max(logits)
+    pp = pack_params(params)
+    u = torch.from_numpy(rng.random(B, dtype=np.float32))
+    draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
+    if hist is not None:
+        hi, ho = pack_history(hist)
+    else:
+        hi = ho = None
+    d = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    print(f"sample_tiles {label} B={B} V={V}", flush=True)
+    a, ap = s.sample_tiles(logits, tm, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
+    b, bp = s.sample_batch(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu()), (label, a.cpu(), b.cpu())
+    assert torch.equal(ap.cpu().view(torch.int32), bp.cpu().view(torch.int32)), label
+    w = Workload(label, logits.cpu(), pp, u, hi, ho, draft)
+    ties, bad = compare_ids(a.cpu(), oracle(w), ap.cpu())
+    assert not bad, (label, bad[:10])
+    return a
+
+
+def lm_logits(seed, B, d, V, peaked=0.0):
+    """bf16 logits of vsamp_lm_head; with `peaked` > 0 each hidden row is that multiple of one
+    weight row plus noise, so one logit stands far above the rest."""
+    g = torch.Generator().manual_seed(seed)
+    weight = (torch.randn(V, d, generator=g) / math.sqrt(d) * 4).to(torch.bfloat16)
+    hidden = torch.randn(B, d, generator=g) * 0.5
+    if peaked:
+        rows = torch.randint(0, V, (B,), generator=g)
+        hidden = hidden * 0.1 + peaked * weight[rows].float()
+    logits, tmax, _ = hip().lm_head(hidden.to(torch.bfloat16).to(DEV), weight.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(tmax, tile_max(logits))  # (the kernel's maxima are the rows' own)
+    return logits
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,d,V,peaked", [(16, 512, 20000, 0.0), (32, 1024, 151936, 0.0), (64, 4096, 151936, 3.0),
+                                          (8, 256, 300, 0.0), (1, 4096, 151936, 3.0)])
+def test_gpu_sample_tiles_on_lm_head_logits(B, d, V, peaked):
+    logits = lm_logits(B * 7 + V, B, d, V, peaked)
+    rng = np.random.default_rng(B + V)
+    check(logits, mixed_params(rng, B, V), B + d, label=f"lm_head peaked={peaked}")
+
+
+@pytest.mark.gpu
+def test_gpu_sample_tiles_with_penalties_and_histories():
+    # rows with penalties take the row passes; rows without them in the same launch do not
+    B, d, V = 24, 1024, 151936
+    logits = lm_logits(5, B, d, V)
+    rng = np.random.default_rng(9)
+    hist = [rng.integers(-2, V + 2, int(rng.integers(0, 300))).tolist() for _ in range(B)]
+    check(logits, mixed_params(rng, B, V, penalties_every=3), 11, hist=hist, label="penalties")
+
+
+@pytest.mark.gpu
+def test_gpu_sample_tiles_on_crafted_rows():
+    V = 4099  # 33 tiles, the last one partial
+    g = torch.Generator().manual_seed(3)
+    rows = []
+    base = torch.randn(V, generator=g)
+    # the max in three tiles: greedy takes the first of them
+    x = base.clone()
+    x[[700, 300, 4098]] = 9.0
+    rows.append(x)
+    # the max is zero, +0 in a late tile and -0 in an earlier one (equal values)
+    x = -base.abs() - 1.0
+    x[2000] = 0.0
+    x[129] = -0.0
+    rows.append(x)
+    rows.append(torch.full((V,), -math.inf))  # every logit -inf
+    x = base.clone()
+    x[1500] = float("nan")  # a NaN: the row passes
+    rows.append(x)
+    x = base.clone()
+    x[17] = math.inf  # an infinite logit
+    rows.append(x)
+    rows.append(torch.full((V,), 0.25))  # one value everywhere
+    x = (base * 0.01).clone()  # a few values, massive ties at every boundary
+    rows.append(x)
+    x = base.clone()
+    x[:300] = 5.0  # 300 equal values above the rest: a top-k 20 boundary inside the tie
+    rows.append(x)
+    logits = torch.stack(rows).to(torch.bfloat16).to(DEV)
+    B = logits.shape[0]
+    for T, kw in [(0.0, {}), (1.0, dict(top_k=20)), (0.7, dict(min_p=0.3)), (1.2, dict(top_k=5, min_p=0.05)),
+                  (1.0, dict(top_k=1)), (0.5, dict(top_k=20, top_p=0.5))]:
+        params = [SamplingParams(temperature=T, **kw) for _ in range(B)]
+        check(logits, params, int(T * 10) + len(kw), label=f"crafted T={T} {kw}")
+
+
+@pytest.mark.gpu
+def test_gpu_sample_tiles_rejects_bad_arguments():
+    s = hip()
+    logits = torch.zeros(2, 1000, dtype=torch.bfloat16, device=DEV)
+    pp = pack_params([SamplingParams(), SamplingParams()], DEV)
+    u = torch.zeros(2, dtype=torch.float32, device=DEV)
+    with pytest.raises(ValueError, match="tile_max"):
+        s.sample_tiles(logits, torch.zeros(2, 7, device=DEV), pp, u)
+    with pytest.raises(ValueError, match="bf16"):
+        s.sample_tiles(logits.float(), torch.zeros(2, 8, device=DEV), pp, u)

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 ROW_STATE_BYTES = 40
 
 VSAMP_BF16 = 0
@@ -35,6 +35,7 @@ EXPORTS = (
     "vsamp_uniforms",
     "vsamp_logprobs",
     "vsamp_logprobs_tiles",
+    "vsamp_sample_tiles",
     "vsamp_lm_head",
     "vsamp_sample_states",
     "vsamp_verify",
@@ -184,6 +185,8 @@ def load() -> ctypes.CDLL:
             ctypes.c_void_p,
         ]
         lib.vsamp_logprobs_tiles.restype = ctypes.c_int
+        lib.vsamp_sample_tiles.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p, ctypes.c_void_p]
+        lib.vsamp_sample_tiles.restype = ctypes.c_int
         lib.vsamp_lm_head.argtypes = [ctypes.POINTER(VsampLmHeadArgs), ctypes.c_void_p]
         lib.vsamp_lm_head.restype = ctypes.c_int
         lib.vsamp_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]

@@ -262,7 +262,7 @@ int launch_penalties(const vs::PenaltyArgs& p, int B, hipStream_t st) {
 
 template <class Tin>
 int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStream_t st,
-               vs::RowState* state = nullptr, int param_div = 1) {
+               vs::RowState* state = nullptr, int param_div = 1, const float* tile_max = nullptr) {
   const bool pen = wants_penalties(a);
   if (state && pen) return fail(VSAMP_E_ARG, "row states are written without penalties only");
   if ((a->flags & VSAMP_HIST_APPEND) && (state || probs))
@@ -295,6 +295,16 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
   s.out_state = state;
   s.param_div = param_div;
   s.nrows = a->batch;
+  if (tile_max) {  // (bf16 rows with the LM head's tile maxima: no split rows, no states)
+    s.tile_max = tile_max;
+    s.nT = (a->vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
+    if (pen)
+      hipLaunchKernelGGL((vs::k_sample<Tin, true, false, false, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
+    else
+      hipLaunchKernelGGL((vs::k_sample<Tin, false, false, false, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_sample (tile maxima)");
+  }
   // Small batches of bf16 rows, when asked for: split rows if the workspace holds the records.
   const int G = (a->flags & VSAMP_SPLIT_ROWS) ? split_slices(a->batch, a->vocab) : 1;
   if (sizeof(Tin) == 2 && !state && !probs && G >= 2 && a->workspace &&
@@ -383,6 +393,16 @@ int vsamp_sample(const vsamp_args* a, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   return a->dtype == VSAMP_BF16 ? run_sample<uint16_t>(a, nullptr, 0, st)
                                 : run_sample<float>(a, nullptr, 0, st);
+}
+
+int vsamp_sample_tiles(const vsamp_args* a, const float* tile_max, void* stream) {
+  g_err.clear();
+  if (int rc = validate(a, true)) return rc;
+  if (a->dtype != VSAMP_BF16) return fail(VSAMP_E_DTYPE, "vsamp_sample_tiles takes the bf16 logits of vsamp_lm_head");
+  if (a->batch == 0) return VSAMP_OK;
+  if (!tile_max) return fail(VSAMP_E_ARG, "tile_max is NULL");
+  if (int rc = check_current_device()) return rc;
+  return run_sample<uint16_t>(a, nullptr, 0, static_cast<hipStream_t>(stream), nullptr, 1, tile_max);
 }
 
 int vsamp_sample_noalloc(const vsamp_args* a, void* stream) {

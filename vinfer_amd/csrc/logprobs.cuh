@@ -26,7 +26,6 @@ namespace vs {
 
 constexpr int kMaxTop = 32;     // most top logprobs per row
 constexpr int kTileCand = 64;   // candidate tiles a tile-mode row reads (else two row passes)
-constexpr int kStatTile = 128;  // logits per statistics tile (k_lm_head's column tile)
 
 struct LogprobArgs {
   const void* logits;  // row r at logits + r * stride
@@ -41,47 +40,6 @@ struct LogprobArgs {
   const float* tsum;
   int nT;
 };
-
-// The key of the k-th largest (1-based, with multiplicity) of the 16-bit keys keys[0 .. nk) of
-// every thread (nk <= 4; k <= the number of keys): two rounds over the high and the low byte,
-// each a 256-bin LDS histogram that wave 0 walks from the top. `h` is 256 words, `sh` 4 words.
-__device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk, uint32_t k, uint32_t* h, uint32_t* sh) {
-  const int tid = threadIdx.x;
-  uint32_t hi = 0, above = 0;
-  for (int round = 0; round < 2; ++round) {
-    if (tid < 256) h[tid] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i < nk && (round == 0 || (keys[i] >> 8) == hi)) atomicAdd(&h[round == 0 ? keys[i] >> 8 : keys[i] & 0xFFu], 1u);
-    }
-    __syncthreads();
-    if (tid < kWave) {
-      // lane l: bins 255 - 4l .. 252 - 4l, descending
-      uint32_t c[4], s4 = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        c[i] = h[255 - 4 * tid - i];
-        s4 += c[i];
-      }
-      uint32_t ex = above + wave_incl_scan<uint32_t>(s4) - s4;
-      if (ex < k && k <= ex + s4) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (ex < k && k <= ex + c[i]) {
-            sh[0] = static_cast<uint32_t>(255 - 4 * tid - i);
-            sh[1] = ex;
-          }
-          ex += c[i];
-        }
-      }
-    }
-    __syncthreads();
-    if (round == 0) hi = sh[0];
-    above = sh[1];
-  }
-  return (hi << 8) | sh[0];
-}
 
 // bf16 rows in one pass: the row's 16-bit key histogram (u16 counts, two keys a word) gives the
 // max, the normaliser (each populated key's count times the fp32 exponential of its value, summed

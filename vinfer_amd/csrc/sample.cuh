@@ -70,6 +70,9 @@ struct SampleArgs {
   u64 epoch;        // this launch's tag (48 bits), distinct from every earlier launch's
   int G;            // slices per row (0: one workgroup per row)
   int nrows;        // B
+  // (vsamp_sample_tiles) the rows' tile maxima [B, nT], one per kStatTile logits
+  const float* tile_max;
+  int nT;
 };
 
 // The row of this workgroup.
@@ -2792,6 +2795,210 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   return true;
 }
 
+// ---- rows decided from the LM head's tile maxima (vsamp_sample_tiles) ------------------------
+// k_lm_head writes, beside the bf16 logits, the max of every kStatTile consecutive logits of a
+// row (as a value: the max of bf16 values, NaN the largest). For some rows those maxima bound
+// where every token the draw can keep lies, and the row is decided from a few tiles:
+//   * greedy rows: the first id holding the row max lies in the first tile whose max equals the
+//     row max (as values: -0 equals +0), and only that tile is read;
+//   * rows sampled at T > 0 with top-k (K <= kSortCap) or min-p: every kept token has
+//     x >= xlo, where for top-k xlo is the least x with fl(x / T) >= fl(theta / T), theta the
+//     K-th largest tile max (the K largest tile maxima are K logits, so theta is at most the
+//     K-th largest logit, whose z every kept token reaches), and for min-p the least x whose
+//     p~ = exp(fl(x / T) - max z) reaches min_p; a kept token then lies in a tile whose max is
+//     >= xlo. The elements >= xlo of those tiles (at most kTileRowTiles tiles, at most
+//     kSortCap elements) are sorted as the generic path sorts its short lists, the exact top-k
+//     and min-p thresholds taken from them, and sorted_tail finishes the row: the same
+//     cutoff, masses and draw as a pass over the row.
+// Rows with penalties, NaN maxima, infinite scaled logits, top-p alone, or more candidates than
+// that take the row passes (the caller's path) as if no tile maxima were given.
+constexpr int kStatTile = 128;      // logits per statistics tile (k_lm_head's column tile)
+constexpr int kTileRowTiles = 64;   // candidate tiles a row decided from its tiles reads at most
+
+// The key of the k-th largest (1-based, with multiplicity) of the 16-bit keys keys[0 .. nk) of
+// every thread (nk <= 4; k <= the number of keys): two rounds over the high and the low byte,
+// each a 256-bin LDS histogram that wave 0 walks from the top. `h` is 256 words, `sh` 4 words.
+__device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk, uint32_t k, uint32_t* h, uint32_t* sh) {
+  const int tid = threadIdx.x;
+  uint32_t hi = 0, above = 0;
+  for (int round = 0; round < 2; ++round) {
+    if (tid < 256) h[tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < nk && (round == 0 || (keys[i] >> 8) == hi)) atomicAdd(&h[round == 0 ? keys[i] >> 8 : keys[i] & 0xFFu], 1u);
+    }
+    __syncthreads();
+    if (tid < kWave) {
+      // lane l: bins 255 - 4l .. 252 - 4l, descending
+      uint32_t c[4], s4 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = h[255 - 4 * tid - i];
+        s4 += c[i];
+      }
+      uint32_t ex = above + wave_incl_scan<uint32_t>(s4) - s4;
+      if (ex < k && k <= ex + s4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (ex < k && k <= ex + c[i]) {
+            sh[0] = static_cast<uint32_t>(255 - 4 * tid - i);
+            sh[1] = ex;
+          }
+          ex += c[i];
+        }
+      }
+    }
+    __syncthreads();
+    if (round == 0) hi = sh[0];
+    above = sh[1];
+  }
+  return (hi << 8) | sh[0];
+}
+
+// Returns true when the row was decided (outputs written) from its tile maxima; false, having
+// written nothing, when it needs the row passes. Every thread calls; `p.u` is clamped to >= 0.
+template <bool PEN>
+__device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t>& row, const RowParams& p, GenericSmem& g,
+                                         int r) {
+  const int tid = threadIdx.x;
+  const int V = row.V;
+  const int nT = a.nT;
+  const bool pen_on = PEN && p.h1 > p.h0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
+  const bool greedy = !(p.T > 0.0f);
+  const bool topk = p.K > 0 && p.K < V;
+  // (uniform)
+  if (pen_on || a.out_probs || a.out_state || nT > 4 * kThreads) return false;
+  if (!greedy && (!(topk || p.mp > 0.0f) || (topk && (p.K > kSortCap || p.K > nT)))) return false;
+  uint32_t* sh = g.rdx.bk;
+  // the tile maxima: thread t takes tiles t + i * kThreads
+  const float* tm = a.tile_max + static_cast<int64_t>(r) * nT;
+  float mt[4];
+  uint32_t kt[4];
+  uint32_t mk = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = tid + i * kThreads;
+    mt[i] = t < nT ? ld_global(tm + t) : -INFINITY;
+    kt[i] = t < nT ? key_of(mt[i]) : 0u;  // (0: below every key)
+    mk = kt[i] > mk ? kt[i] : mk;
+  }
+  mk = static_cast<uint32_t>(block_max_u64(mk, g.srch.red64));
+  if (mk > key_of(INFINITY)) return false;  // a NaN: the row passes find the first one
+  const float M = val_of(mk);
+  Kept k;
+  if (greedy) {
+    // the first tile whose max is the row max, then its first element equal to it
+    uint32_t first = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t = static_cast<uint32_t>(tid + i * kThreads);
+      if (t < static_cast<uint32_t>(nT) && mt[i] == M) first = t < first ? t : first;
+    }
+    first = ~static_cast<uint32_t>(block_max_u64(~first, g.srch.red64));
+    if (first >= static_cast<uint32_t>(nT)) return false;  // (tile maxima not of these logits)
+    uint32_t id = 0xFFFFFFFFu;
+    if (tid < kStatTile) {
+      const int i = static_cast<int>(first) * kStatTile + tid;
+      if (i < V && load_one<uint16_t>(row.p, i) == M) id = static_cast<uint32_t>(i);
+    }
+    id = ~static_cast<uint32_t>(block_max_u64(~id, g.srch.red64));
+    if (id >= static_cast<uint32_t>(V)) return false;  // (tile maxima not of these logits)
+    k.point = static_cast<int>(id);
+    finish<false>(a, row, p, 0.0f, k, 0, &g.srch.vslot, r);
+    return true;
+  }
+  const float T = p.T;
+  const float mz = M / T;
+  if (!(mz > -INFINITY && mz < INFINITY)) return false;  // point rows: the row passes
+  // xlo: no kept token lies below it (wave 0 bisects; the others wait at the barrier)
+  const uint32_t lo_key = key_of(-INFINITY);
+  float theta = -INFINITY;
+  if (topk) {
+    uint32_t k16[4];
+    int nk = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      k16[i] = kt[i] >> 16;  // (a bf16 value's key is the top half of its fp32 key)
+      nk += tid + i * kThreads < nT ? 1 : 0;
+    }
+    theta = val16(kth_key16(k16, nk, static_cast<uint32_t>(p.K), g.rdx.hcnt, sh + 2));
+  }
+  if (tid < kWave) {
+    float xlo = -INFINITY, xm = -INFINITY;
+    if (topk) {
+      const float zt = theta / T;
+      xlo = val_of(wave_bisect(lo_key, key_of(theta), key_of(zt * T), [&](float x) { return x / T >= zt; }));
+    }
+    if (p.mp > 0.0f) {
+      const double dmp = static_cast<double>(p.mp);
+      const float guess = T * (mz + __logf(p.mp));
+      xm = val_of(wave_bisect(lo_key, mk, key_of(guess), [&](float x) { return ptilde(x, T, mz) >= dmp; }));
+    }
+    if (tid == 0) {
+      reinterpret_cast<float*>(sh)[0] = xlo > xm ? xlo : xm;
+      reinterpret_cast<float*>(sh)[1] = xm;
+    }
+  }
+  lds_barrier();
+  const float xlo = reinterpret_cast<const float*>(sh)[0];
+  const float xm = reinterpret_cast<const float*>(sh)[1];
+  // the tiles that can hold a kept token, listed in LDS
+  uint32_t mine = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) mine += tid + i * kThreads < nT && mt[i] >= xlo ? 1u : 0u;
+  uint32_t ntile;
+  uint32_t at = block_excl_scan<uint32_t>(mine, g.rdx.hcnt, &ntile);
+  if (ntile > static_cast<uint32_t>(kTileRowTiles)) return false;  // (uniform)
+  int* ctile = reinterpret_cast<int*>(g.srch.tw);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (tid + i * kThreads < nT && mt[i] >= xlo) ctile[at++] = tid + i * kThreads;
+  if (tid == 0) sh[2] = 0;
+  lds_barrier();
+  // their elements >= xlo, into the candidate list (every element's load first)
+  Cand* c = reinterpret_cast<Cand*>(reinterpret_cast<uint32_t*>(&g) + kMatchOffset);
+  constexpr int kPer = kTileRowTiles * kStatTile / kThreads;
+  float xs[kPer];
+  int ids[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int e = tid + q * kThreads;
+    ids[q] = e < static_cast<int>(ntile) * kStatTile ? ctile[e / kStatTile] * kStatTile + e % kStatTile : V;
+    xs[q] = load_one<uint16_t>(row.p, ids[q] < V ? ids[q] : 0);
+  }
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const bool in = ids[q] < V && xs[q] >= xlo;
+    const u64 bal = __ballot(in);  // (one counter update per wave)
+    if (bal) {
+      const int leader = __ffsll(static_cast<long long>(bal)) - 1;
+      uint32_t pos = 0;
+      if (lane_id() == leader) pos = atomicAdd(&sh[2], static_cast<uint32_t>(__popcll(bal)));
+      pos = __builtin_amdgcn_readlane(pos, leader) + static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
+      if (in && pos < static_cast<uint32_t>(kSortCap)) c[pos] = Cand{xs[q], ids[q]};
+    }
+  }
+  lds_barrier();
+  const int n = static_cast<int>(sh[2]);
+  if (n > kSortCap || n < 1) return false;  // (uniform)
+  sort_cands(c, n, c + kCandCap);
+  // the exact thresholds: the K-th largest element's z (when the list holds K elements; else
+  // min-p's threshold, above the K-th largest, binds) and min-p's
+  if (tid < kWave) {
+    float x0 = xm;
+    if (topk && n >= p.K) {
+      const float kz = c[p.K - 1].x / T;
+      const float xk = val_of(wave_bisect(lo_key, key_of(c[p.K - 1].x), key_of(kz * T), [&](float x) { return x / T >= kz; }));
+      x0 = xk > x0 ? xk : x0;
+    }
+    if (tid == 0) reinterpret_cast<float*>(sh)[3] = x0;
+  }
+  lds_barrier();
+  k.x0 = reinterpret_cast<const float*>(sh)[3];
+  return sorted_tail<false>(a, row, p, g, g.srch, c, n, mz, k, r);
+}
+
 __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
   a.logits = as_global(a.logits);
   a.temp = as_global(a.temp);
@@ -2810,12 +3017,15 @@ __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
   a.pen = globalized(a.pen);
   a.slices = as_global(a.slices);
   a.arrive = as_global(a.arrive);
+  a.tile_max = as_global(a.tile_max);
   return a;
 }
 
 // STATE: also write each row's RowState (the speculative verify's launches; never with PEN).
 // SPLIT: a bf16 split-row launch (grid B * G).
-template <class Tin, bool PEN, bool STATE = false, bool SPLIT = false>
+// TILES: bf16 rows with their tile maxima (a.tile_max): the rows tile_row can decide are decided
+// from a few tiles, the others take the row passes below.
+template <class Tin, bool PEN, bool STATE = false, bool SPLIT = false, bool TILES = false>
 __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   const SampleArgs a = globalized(a_);
   // 128 KB: the key histogram (or the generic path's penalty counts), then the id-search /
@@ -2843,6 +3053,14 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   row.eid = f.eid;   // the fast path keeps the penalised ids and values in LDS
   row.eval = f.eval;
   GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
+  if constexpr (TILES && sizeof(Tin) == 2 && !STATE && !SPLIT) {
+    if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
+    lds_barrier();
+    RowParams pt = f.prm;
+    pt.u = pt.u >= 0.0f ? pt.u : 0.0f;
+    if (tile_row<PEN>(a, row, pt, g, r)) return;
+    lds_barrier();  // (every thread is done with the tile path's LDS)
+  }
   if constexpr (sizeof(Tin) == 2) {
     if (fast_row<PEN, STATE, SPLIT>(a, row, f.prm, big, f, g.srch, pw, r)) return;
     lds_barrier();  // (every thread is done with the fast path's LDS; f.prm is set)

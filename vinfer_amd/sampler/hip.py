@@ -288,6 +288,44 @@ class HipSampler:
         )
         return out_tok, ids, lps
 
+    def _check_tiles(self, logits, tile_max) -> None:
+        dev = self._device(logits)
+        if logits.dtype != torch.bfloat16:
+            raise ValueError("sample_tiles takes the bf16 logits of lm_head")
+        B, V = logits.shape
+        nT = (V + _lib.LM_TILE - 1) // _lib.LM_TILE
+        if (tile_max.dtype != torch.float32 or tile_max.device != dev or tuple(tile_max.shape) != (B, nT)
+                or not tile_max.is_contiguous()):
+            raise ValueError(f"tile_max must be a contiguous float32 [{B}, {nT}] tensor on {dev}")
+
+    def sample_tiles(self, logits, tile_max, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
+        """``sample_batch`` over the bf16 logits ``lm_head`` wrote, with its tile maxima
+        (``vsamp_sample_tiles``): the same ids and draft probabilities, with greedy, top-k and
+        min-p rows without penalties decided from a few tiles."""
+        self._check_tiles(logits, tile_max)
+        dev = logits.device
+        B = logits.shape[0]
+        a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids)
+        a.flags &= ~_lib.VSAMP_SPLIT_ROWS
+        ids = torch.empty(B, dtype=torch.int32, device=dev)
+        dprob = torch.empty(B, dtype=torch.float32, device=dev) if draft_ids is not None else None
+        a.out_ids = ids.data_ptr()
+        a.out_draft_prob = _ptr(dprob)
+        _lib.check(self._lib.vsamp_sample_tiles(ctypes.byref(a), tile_max.data_ptr(), self._stream(dev)))
+        del keep
+        return ids, dprob
+
+    def prepare_tiles(self, logits, tile_max, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
+        """``prepare_batch`` for ``sample_tiles``: a reusable launch on fixed buffers (the logits
+        and tile maxima may be rewritten in place between launches)."""
+        self._check_tiles(logits, tile_max)
+        split, self.split_rows = self.split_rows, False
+        try:
+            st = self.prepare_batch(logits, params, uniforms, hist_ids, hist_offsets, draft_ids)
+        finally:
+            self.split_rows = split
+        return PreparedStep(self._lib, st._args, st._keep + (tile_max,), st.ids, st.draft_prob, tile_max)
+
     def sample_states(self, logits, params, uniforms):
         """``sample_batch`` without histories, plus each row's sampling state (uint8 ``[B, 40]``,
         opaque) for a later ``verify`` of these rows as drafts (``draft_states``)."""
@@ -455,16 +493,20 @@ class _TokenPath:
 class PreparedStep:
     """One batch's sampler launch with its argument block built (see ``prepare_batch``)."""
 
-    def __init__(self, lib, args, keep, ids, dprob) -> None:
+    def __init__(self, lib, args, keep, ids, dprob, tile_max=None) -> None:
         self._lib, self._args, self._keep = lib, args, keep
         self._ref = ctypes.byref(args)
         self.ids, self.draft_prob = ids, dprob
+        self._tiles = None if tile_max is None else ctypes.c_void_p(tile_max.data_ptr())
 
     def launch(self, stream: int | None = None) -> None:
         """Enqueue the step on ``stream`` (a hipStream_t as int; default: torch's current)."""
         if stream is None:
             stream = torch.cuda.current_stream(self.ids.device).cuda_stream
-        code = self._lib.vsamp_sample(self._ref, ctypes.c_void_p(stream))
+        if self._tiles is None:
+            code = self._lib.vsamp_sample(self._ref, ctypes.c_void_p(stream))
+        else:
+            code = self._lib.vsamp_sample_tiles(self._ref, self._tiles, ctypes.c_void_p(stream))
         if code:
             _lib.check(code)
 
