@@ -720,7 +720,10 @@ def workloads_bench(args) -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    for name in NAMES + ("single_bf16",):
+    names = NAMES + ("single_bf16",)
+    if args.only:
+        names = tuple(n for n in names if n in args.only.split(","))
+    for name in names:
         if name == "single_bf16":  # the per-token row in the model's dtype
             w = make("single_fp32")
             w.logits = w.logits.to(torch.bfloat16)
@@ -765,6 +768,8 @@ def workloads_bench(args) -> int:
         torch.cuda.empty_cache()
     # the engine's per-token call, unchanged (generate.py:129): sample(logits[V], params, seed,
     # position) -> int, host work and the id's copy back included
+    if args.only and "per_token" not in args.only.split(","):
+        return 0
     from vinfer_amd.sampling import SamplingParams
 
     for dtype in (torch.bfloat16, torch.float32):
@@ -800,6 +805,8 @@ def main() -> int:
                     help="time the headline batch's flat and peaked rows apart, with and without histories")
     ap.add_argument("--lm-head", action="store_true",
                     help="time the LM head + log-probabilities, fused against torch's matmul + vsamp_logprobs")
+    ap.add_argument("--only", default="",
+                    help="with --workloads: a comma-separated subset of the workloads (per_token: the per-token call)")
     ap.add_argument("--lm-head-sample", action="store_true",
                     help="time the LM head plus the draw, fused (tile maxima) against unfused")
     ap.add_argument("--split-rows", action="store_true",
