@@ -193,7 +193,9 @@ def decode_loop(args) -> int:
     def run(graphs: bool):
         """The loop's timed iterations: (decoder, us per iteration, tokens)."""
         if K:
-            dec = SpeculativeDecoder(model, hip, draft_model=draft, num_draft=K, num_slots=B, max_seq_len=L)
+            # (graphs: a steady membership's iterations replay one captured HIP graph)
+            dec = SpeculativeDecoder(model, hip, draft_model=draft, num_draft=K, num_slots=B, max_seq_len=L,
+                                     graphs=graphs)
         else:
             # (graphs: the steady membership's iterations replay two captured HIP graphs)
             dec = BatchDecoder(model, hip, num_slots=B, max_seq_len=L, penalize_prompt=True, graphs=graphs)
@@ -220,10 +222,8 @@ def decode_loop(args) -> int:
         return dec, (time.perf_counter() - t0) / args.steps * 1e6, n_tok
 
     steps = args.steps
-    eager_us = None
-    if not K:
-        _, eager_us, _ = run(False)
-    dec, loop_us, n_tok = run(not K)
+    _, eager_us, eager_tok = run(False)
+    dec, loop_us, n_tok = run(True)
 
     # the two device parts alone, on the same shapes
     slots = torch.arange(B, device=dev)
@@ -281,9 +281,10 @@ def decode_loop(args) -> int:
         },
         "tokens_per_iteration": n_tok / args.steps,
         "us_per_step_loop": loop_us,
-        "graphs": not K,
+        "graphs": True,
         "graph_iterations": getattr(dec, "graph_steps", 0),
         "us_per_step_loop_without_graphs": eager_us,
+        "tokens_per_iteration_without_graphs": eager_tok / args.steps,
         "us_model_step_alone": model_us,
         "us_sampler_call_alone": sampler_us,
         "us_host_and_rest": loop_us - model_us - sampler_us,

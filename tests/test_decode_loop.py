@@ -512,3 +512,61 @@ def test_gpu_speculative_greedy_equals_the_plain_loop():
     want = run_batched(model, hip, reqs, num_slots=4)
     got = run_speculative(model, draft, hip, reqs, num_slots=4, K=2)
     assert got == want
+
+
+def spec_requests(n: int, vocab: int, seed: int = 0) -> list[tuple[list[int], SamplingParams]]:
+    """Requests speculation can serve (no penalties): greedy, top-k, top-p, min-p, stop ids."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        prompt = rng.integers(0, vocab, size=int(rng.integers(1, 12))).tolist()
+        kw = dict(max_tokens=int(rng.integers(20, 45)), seed=int(rng.integers(0, 2**62)))
+        kind = i % 5
+        if kind == 0:
+            kw.update(temperature=0.0)
+        elif kind == 1:
+            kw.update(temperature=0.8, top_k=int(rng.choice([5, 20, 50])))
+        elif kind == 2:
+            kw.update(temperature=1.1, top_p=0.8)
+        elif kind == 3:
+            kw.update(min_p=0.1, top_p=0.95)
+        else:
+            kw.update(temperature=0.7, stop_token_ids=tuple(int(t) for t in rng.integers(0, vocab, 40)))
+        out.append((prompt, SamplingParams(**kw)))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [2, 3])
+def test_gpu_speculative_graph_replays_give_the_eager_tokens(K):
+    """graphs=True: a membership that holds for two iterations is captured into a HIP graph and
+    replayed while it holds; every request's steps must equal the eager loop's, and graph
+    replays must have happened."""
+    from vinfer_amd.runtime import SpeculativeDecoder
+
+    dev = torch.device("cuda", 0)
+    model = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+    draft = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev, seed=1)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    reqs = spec_requests(9, 151936, seed=K)
+    print(f"speculative graphs: 9 requests, 4 slots, K={K}, V 151936 bf16", flush=True)
+    want = run_speculative(model, draft, hip, reqs, num_slots=4, K=K, max_seq_len=64)
+    dec = SpeculativeDecoder(model, hip, draft_model=draft, num_draft=K, num_slots=4, max_seq_len=64,
+                             graphs=True, graph_after=2)
+    rids = [dec.submit(p, sp) for p, sp in reqs]
+    done = dec.run()
+    assert dec.graph_steps > 5, dec.graph_steps
+    assert [done[r] for r in rids] == want
+
+
+@pytest.mark.gpu
+def test_gpu_speculative_graphs_greedy_equals_the_plain_loop():
+    dev = torch.device("cuda", 0)
+    model = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev)
+    draft = SyntheticLM(151936, dim=64, scale=3.0, dtype=torch.bfloat16, device=dev, seed=1)
+    hip = SAMPLER.resolve("hip", BackendContext(dev, torch.bfloat16))
+    reqs = greedy_requests(10, 151936, seed=5)
+    print("speculative greedy with graphs: 10 requests, K=2, V 151936 bf16", flush=True)
+    want = run_batched(model, hip, reqs, num_slots=4)
+    got = run_speculative(model, draft, hip, reqs, num_slots=4, K=2, graphs=True, graph_after=2)
+    assert got == want

@@ -104,7 +104,9 @@ class DecodeModel(Protocol):
     pool would free it, generate.py:146), possibly after one more ``decode`` of that slot was
     enqueued (the step launched before the request's last token was known to be a stop), and
     ``decode_into(slots, tokens, positions, out)``, ``decode`` writing its logits into ``out``
-    (the captured loop then needs no copy of them)."""
+    (the captured loop then needs no copy of them; ``out`` may be a row-strided view), and
+    ``stateless = True`` when its slots keep no state (a speculative loop then does not feed it
+    tokens whose logits it does not use)."""
 
     device: torch.device
 
@@ -209,6 +211,24 @@ class _StepGraphs:
     pen_inc: np.ndarray  # 1 for a row with penalties (its history grows by one a step), else 0
     t: int = 0  # the next iteration to launch
     next: int = 0  # the slot it goes to
+
+
+@dataclass(eq=False)
+class _SpecGraph:
+    """A membership's captured speculative iteration: the inputs' copy (slots, last tokens, the
+    token before each last one and its position, the draft steps' and the target's positions,
+    every uniform of the iteration), the draft model fed that earlier token (unless it keeps no
+    state), K draft steps and draws, the target's step, the verify, and its tokens and counts
+    copied to pinned memory (the counts last: the host polls them)."""
+
+    key: tuple[int, ...]
+    graph: object
+    keep: list
+    ints: np.ndarray  # int64 [4 + K + (K + 1), n]: slots, last, earlier token, its position, positions
+    u: np.ndarray  # float32 [(3K + 1) n]
+    useeds: np.ndarray  # int64 [(3K + 1) n]
+    tokens_np: np.ndarray  # int32 [n, K + 1]
+    counts_np: np.ndarray  # int32 [n]
 
 
 class BatchDecoder:
@@ -687,6 +707,12 @@ class SpeculativeDecoder(BatchDecoder):
         self.draft_model = draft_model
         self.num_draft = num_draft
         self._ready: list[_Seq] = []  # sequences with a first token, waiting for an iteration
+        self._spec_graph: _SpecGraph | None = None
+        self._spec_key: tuple[int, ...] | None = None  # the last membership and its run
+        self._spec_run = 0
+        # (graphs) an iteration launched before the host took the previous one's tokens:
+        # (its graph, its sequences)
+        self._spec_inflight: tuple[_SpecGraph, list[_Seq]] | None = None
 
     def submit(self, prompt_ids: list[int], params: SamplingParams) -> int:
         if penalized(params):
@@ -700,10 +726,13 @@ class SpeculativeDecoder(BatchDecoder):
 
     def step(self) -> list[tuple[int, Step]]:
         out: list[tuple[int, Step]] = []
-        spec = [s for s in self._ready if s.rid in self._running]
-        self._ready = []
-        if spec:
-            out += self._speculate(spec)
+        if self._spec_inflight is not None:
+            out += self._take_inflight()
+        else:
+            spec = [s for s in self._ready if s.rid in self._running]
+            self._ready = []
+            if spec:
+                out += self._speculate(spec)
         admitted = self._admit()
         if admitted is not None:
             seqs, logits = admitted
@@ -726,6 +755,14 @@ class SpeculativeDecoder(BatchDecoder):
         return out
 
     def _speculate(self, seqs: list[_Seq]) -> list[tuple[int, Step]]:
+        if self.graphs:
+            key = tuple(s.rid for s in seqs)
+            if key == self._spec_key:
+                self._spec_run += 1
+            else:
+                self._spec_key, self._spec_run = key, 0
+            if self._spec_run >= self.graph_after or (self._spec_graph is not None and self._spec_graph.key == key):
+                return self._speculate_graph(key, seqs)
         K = self.num_draft
         n = len(seqs)
         dev = self.model.device
@@ -750,6 +787,10 @@ class SpeculativeDecoder(BatchDecoder):
         u_accept, u_residual, u_bonus = u[nk:2 * nk].view(n, K), u[2 * nk:3 * nk].view(n, K), u[3 * nk:]
         # the last draft of a fully accepted block reaches the draft model first (logits unused)
         gap = [s for s in seqs if s.draft_gap is not None]
+        if gap and getattr(self.draft_model, "stateless", False):
+            for s in gap:  # (a draft model without state needs no feed)
+                s.draft_gap = None
+            gap = []
         if gap:
             gd = torch.from_numpy(np.array([[s.slot for s in gap], [s.draft_gap[0] for s in gap],
                                             [s.draft_gap[1] for s in gap]], dtype=np.int64))
@@ -786,6 +827,13 @@ class SpeculativeDecoder(BatchDecoder):
             draft_states=torch.stack(states, dim=1) if with_states else None,
         )
         tokens, counts = tokens.tolist(), counts.tolist()  # the iteration's wait
+        return self._emit(seqs, tokens, counts)
+
+    def _emit(self, seqs: list[_Seq], tokens: list[list[int]], counts: list[int],
+              ready: bool = True) -> list[tuple[int, Step]]:
+        """Each sequence's emitted tokens through the per-request logic; the ones going on wait
+        for the next iteration (unless it is already in flight: ``ready`` false)."""
+        K = self.num_draft
         out: list[tuple[int, Step]] = []
         for s, row, c in zip(seqs, tokens, counts):
             if c == K + 1:  # every draft kept: the draft model has not seen the last one
@@ -797,5 +845,194 @@ class SpeculativeDecoder(BatchDecoder):
                     self._retire(s)
                     break
             else:
-                self._ready.append(s)
+                if ready:
+                    self._ready.append(s)
         return out
+
+    # ---- the iteration as a HIP graph -----------------------------------------------------------
+    def _speculate_graph(self, key: tuple[int, ...], seqs: list[_Seq]) -> list[tuple[int, Step]]:
+        """The iteration of a membership that held for ``graph_after`` iterations, replayed from a
+        HIP graph: the host stages the inputs, replays and polls the counts; then, while no
+        request waits for a free slot, it launches the next iteration on inputs derived from
+        these tokens before it runs this iteration's per-request logic, which then overlaps the
+        GPU's work. Every sequence's draft model is fed the token before its last one, at its
+        position (a sequence whose previous block was fully accepted needs it; for the others it
+        repeats a step already taken, which a model whose state is indexed by position, as the
+        loop's overwriting of rejected positions already assumes, takes unchanged; a draft model
+        without state is not fed)."""
+        gs = self._spec_graph
+        if gs is None or gs.key != key:
+            self._spec_graph = None  # (the old graph's memory goes back before the new capture)
+            gs = self._spec_graph = self._capture_spec(key, seqs)
+        self._stage_spec(gs, seqs, None, None)
+        self._launch_spec(gs)
+        tokens, counts = self._wait_spec(gs)
+        return self._after_spec(gs, seqs, tokens, counts)
+
+    def _take_inflight(self) -> list[tuple[int, Step]]:
+        """The iteration launched ahead by the previous step: its tokens for the sequences still
+        running (a sequence that ended meanwhile has its block dropped)."""
+        gs, seqs = self._spec_inflight
+        self._spec_inflight = None
+        tokens, counts = self._wait_spec(gs)
+        alive = [s.rid in self._running for s in seqs]
+        if all(alive):
+            return self._after_spec(gs, seqs, tokens, counts)
+        keep = [i for i, a in enumerate(alive) if a]
+        live = [seqs[i] for i in keep]
+        for s in live:
+            s.draft_gap = None
+        return self._emit(live, [tokens[i] for i in keep], [counts[i] for i in keep])
+
+    def _after_spec(self, gs: _SpecGraph, seqs: list[_Seq], tokens: list[list[int]],
+                    counts: list[int]) -> list[tuple[int, Step]]:
+        """Launch the next iteration ahead when the membership can hold, then emit."""
+        ahead = not (self._waiting and self._free) and not self._ready
+        if ahead:
+            self._stage_spec(gs, seqs, tokens, counts)
+            self._launch_spec(gs)
+            self._spec_inflight = (gs, seqs)
+        for s in seqs:
+            s.draft_gap = None  # (the graph feeds every sequence the token before its last)
+        return self._emit(seqs, tokens, counts, ready=not ahead)
+
+    def _spec_uniforms(self, gs: _SpecGraph, position: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
+        """Every uniform of an iteration at ``position`` (the next token's, per sequence): the
+        draft draws ([K, n]), acceptances and residuals ([n, K] each) and the bonus ([n])."""
+        K = self.num_draft
+        at = position[:, None] + np.arange(K, dtype=np.int64)[None, :]
+        upos = np.concatenate([-(4 * at.T + 1).ravel(), -(4 * at + 2).ravel(), -(4 * at + 3).ravel(),
+                               -(4 * (position + K) + 4)])
+        return position_uniforms(gs.useeds, upos, out=out)
+
+    def _launch_spec(self, gs: _SpecGraph) -> None:
+        gs.counts_np[:] = -1  # (counts are >= 1)
+        gs.graph.replay()
+        self.graph_steps += 1
+
+    def _wait_spec(self, gs: _SpecGraph) -> tuple[list[list[int]], list[int]]:
+        spins = 0
+        while (gs.counts_np < 0).any():
+            spins += 1
+            if spins == 1 << 20:  # (long past any iteration: the graph's end settles it)
+                torch.cuda.current_stream(self.model.device).synchronize()
+                if (gs.counts_np < 0).any():
+                    raise RuntimeError("the verified tokens never reached the host")
+        return gs.tokens_np.tolist(), gs.counts_np.tolist()
+
+    def _stage_spec(self, gs: _SpecGraph, seqs: list[_Seq], tokens, counts) -> None:
+        """An iteration's inputs into the graph's pinned staging words (the graph's first node
+        copies them to the device): from the sequences as they stand, or, with ``tokens`` and
+        ``counts`` of an iteration whose per-request logic has not run yet, as they stand after
+        it."""
+        n = len(seqs)
+        K = self.num_draft
+        ints = gs.ints
+        if tokens is None:
+            position = np.fromiter((s.position for s in seqs), np.int64, n)
+            ints[1] = np.fromiter((s.generated[-1] for s in seqs), np.int64, n)
+            # the token at position - 2: the second-to-last generated one, or the prompt's last
+            ints[2] = np.fromiter((s.generated[-2] if len(s.generated) >= 2 else s.prompt[-1] for s in seqs),
+                                  np.int64, n)
+        else:
+            c = np.asarray(counts, dtype=np.int64)
+            tk = np.asarray(tokens, dtype=np.int64)
+            rows = np.arange(n)
+            position = np.fromiter((s.position for s in seqs), np.int64, n) + c
+            ints[1] = tk[rows, c - 1]
+            last = np.fromiter((s.generated[-1] for s in seqs), np.int64, n)
+            ints[2] = np.where(c >= 2, tk[rows, np.maximum(c - 2, 0)], last)
+        ints[3] = position - 2
+        ints[4:4 + K] = position[None, :] - 1 + np.arange(K, dtype=np.int64)[:, None]  # draft steps
+        # the target's positions, sequence-major: token c of sequence b at b (K + 1) + c
+        ints[4 + K:].reshape(-1)[:] = (position[:, None] - 1 + np.arange(K + 1, dtype=np.int64)[None, :]).reshape(-1)
+        self._spec_uniforms(gs, position, out=gs.u)
+
+    def _capture_spec(self, key: tuple[int, ...], seqs: list[_Seq]) -> _SpecGraph:
+        n = len(seqs)
+        K = self.num_draft
+        dev = self.model.device
+        g = self._group(seqs, dev)
+        params = g.params
+        rows = 4 + K + (K + 1)
+        st = _Staging(dev, 2 * rows * n + (3 * K + 1) * n + 8)
+        at_i = st.reserve(2 * rows * n, align=2)
+        at_u = st.reserve((3 * K + 1) * n)
+        ints = st.host_view(at_i, 2 * rows * n).view(np.int64).reshape(rows, n)
+        u_host = st.host_view(at_u, (3 * K + 1) * n).view(np.float32)
+        ints[0] = g.slots
+        gs = _SpecGraph(key, None, [], ints, u_host,
+                        np.concatenate([np.tile(g.seeds, K), np.repeat(g.seeds, K), np.repeat(g.seeds, K), g.seeds]),
+                        np.zeros((n, K + 1), np.int32), np.zeros(n, np.int32))
+        self._stage_spec(gs, seqs, None, None)
+        d = st.device(at_i, 2 * rows * n).view(torch.int64).view(rows, n)
+        slots, last, gtok, gpos = d[0], d[1], d[2], d[3]
+        dpos = d[4:4 + K]  # [K, n]: the draft steps' positions
+        tpos = d[4 + K:].reshape(-1)  # [n (K + 1)]: position of target token c of sequence b at b (K + 1) + c
+        ud = st.device(at_u, (3 * K + 1) * n).view(torch.float32)
+        nk = n * K
+        u_draft = ud[:nk].view(K, n)
+        u_accept, u_residual, u_bonus = ud[nk:2 * nk].view(n, K), ud[2 * nk:3 * nk].view(n, K), ud[3 * nk:]
+        tokens_host = torch.empty(n, K + 1, dtype=torch.int32, pin_memory=True)
+        counts_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+        with_states = hasattr(self.sampler, "sample_states")
+        extend = getattr(self.model, "extend", None)
+        draft_into = getattr(self.draft_model, "decode_into", None)
+        target_into = getattr(self.model, "decode_into", None)
+        feed = not getattr(self.draft_model, "stateless", False)
+        # The logits' shape from one eager feed of the token before the last (the graph's own
+        # first step, so a model with state sees nothing it would not see anyway), then the
+        # buffers the graph writes the draft and target logits into.
+        st.send()
+        probe = self.draft_model.decode(slots, gtok, gpos)
+        vocab, ldt = int(probe.shape[-1]), probe.dtype
+        del probe
+        dbuf = torch.empty(n, K, vocab, dtype=ldt, device=dev) if draft_into is not None else None
+        tbuf = torch.empty(n, K + 1, vocab, dtype=ldt, device=dev) if extend is None and target_into else None
+        toks = torch.empty(n, K + 1, dtype=torch.int64, device=dev)  # the last token, then the drafts
+        slots_rep = slots.repeat_interleave(K + 1) if extend is None else None  # (fixed per membership)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            st.dev[: st.n].copy_(st.host[: st.n], non_blocking=True)
+            if feed:
+                self.draft_model.decode(slots, gtok, gpos)
+            toks[:, 0].copy_(last)
+            x = last
+            draft_rows, states = [], []
+            for j in range(K):
+                if dbuf is not None:
+                    draft_into(slots, x, dpos[j], dbuf[:, j])
+                    logits = dbuf[:, j]
+                else:
+                    logits = self.draft_model.decode(slots, x, dpos[j])
+                    draft_rows.append(logits)
+                if with_states:
+                    ids, state = self.sampler.sample_states(logits, params, u_draft[j])
+                    states.append(state)
+                else:
+                    ids, _ = self.sampler.sample_batch(logits, params, u_draft[j])
+                toks[:, j + 1].copy_(ids)
+                x = toks[:, j + 1]
+            dl = dbuf if dbuf is not None else torch.stack(draft_rows, dim=1)
+            if extend is not None:
+                target = extend(slots, toks, dpos[0])
+            else:
+                tt = toks.reshape(-1)
+                if tbuf is not None:
+                    target_into(slots_rep, tt, tpos, tbuf.view(n * (K + 1), vocab))
+                    target = tbuf
+                else:
+                    target = self.model.decode(slots_rep, tt, tpos).view(n, K + 1, -1)
+            tokens, counts = self.sampler.verify(
+                target, dl, toks[:, 1:], params, u_accept, u_residual, u_bonus,
+                draft_states=torch.stack(states, dim=1) if with_states else None,
+            )
+            tokens_host.copy_(tokens, non_blocking=True)
+            counts_host.copy_(counts, non_blocking=True)  # (after the tokens: the host polls these)
+        torch.cuda.synchronize(dev)
+        gs.graph = graph
+        gs.keep = [st, tokens_host, counts_host, toks, slots_rep, dbuf, tbuf]
+        gs.tokens_np = tokens_host.numpy()
+        gs.counts_np = counts_host.numpy()
+        return gs

@@ -175,6 +175,8 @@ class SyntheticLM:
         self.pos = torch.randn(64, dim, generator=g).to(dtype).to(self.device)
         self.head = (torch.randn(dim, vocab, generator=g) * (scale / (2 * dim) ** 0.5)).to(dtype).to(self.device)
 
+    stateless = True  # (a decode loop need not feed it tokens whose logits it does not use)
+
     def decode(self, slots: torch.Tensor, tokens: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         h = self.emb[tokens] + self.pos[positions % 64]
         return h @ self.head
