@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 7
+#define VSAMP_ABI_VERSION 8
 
 /* Bytes of one row's sampling state (vsamp_sample_states), an opaque record. */
 #define VSAMP_ROW_STATE_BYTES 40
@@ -258,6 +258,15 @@ int vsamp_logprobs_tiles(const vsamp_args* args, const float* tile_max, const fl
  * Replaces the sampler call after the engine's LM head (models/qwen/model.py:230-233 ->
  * runtime/sampler.py:68-77) when the LM head is vsamp_lm_head. */
 int vsamp_sample_tiles(const vsamp_args* args, const float* tile_max, void* stream);
+
+/* vsamp_sample over bf16 logits from any source, for small batches: a first launch of many
+ * workgroups per row writes each row's tile maxima (the max of every VSAMP_LM_TILE logits) into
+ * `tile_max` (caller-allocated device memory, [batch, ceil(vocab / VSAMP_LM_TILE)] fp32), then
+ * vsamp_sample_tiles runs on them. Same outputs as vsamp_sample, bit for bit. One row of 151936
+ * on one workgroup spends ~10 us in its pass; the maxima take ~3 us over the chip, so greedy,
+ * top-k and min-p rows without penalties finish sooner (the engine's per-token call, B = 1,
+ * sampler.py:68-77 via generate.py:129); other rows pay the extra launch. */
+int vsamp_sample_tile_pass(const vsamp_args* args, float* tile_max, void* stream);
 
 /* Host function (no device work): the draw's uniform of (seeds[i], positions[i]) into out[i],
  * i < n, all host memory. u = (splitmix64(position_seed(seed, position)) >> 40) * 2^-24, where

@@ -1,4 +1,6 @@
-"""The draw over the LM head's logits with its tile maxima (``vsamp_sample_tiles``).
+"""The draw over bf16 logits with their tile maxima: from the LM head's epilogue
+(``vsamp_sample_tiles``) or from a launch of their own (``vsamp_sample_tile_pass``, which the
+per-token call takes for the rows the maxima decide).
 
 ``sample_tiles`` must give exactly what ``sample_batch`` gives on the same logits and arguments:
 the same ids and the same draft probabilities, bit for bit, whether a row is decided from a few
@@ -174,3 +176,58 @@ def test_gpu_sample_tiles_rejects_bad_arguments():
         s.sample_tiles(logits, torch.zeros(2, 7, device=DEV), pp, u)
     with pytest.raises(ValueError, match="bf16"):
         s.sample_tiles(logits.float(), torch.zeros(2, 8, device=DEV), pp, u)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,V,pad,offset", [(1, 151936, 0, 0), (3, 4099, 5, 0), (8, 151936, 0, 3), (16, 20000, 0, 0),
+                                            (2, 100, 0, 1)])
+def test_gpu_tile_pass_equals_sample_batch(B, V, pad, offset):
+    # bf16 logits from any source: the tile maxima come from their own launch (rows unaligned
+    # when offset is odd: the maxima kernel then reads them element by element)
+    g = torch.Generator().manual_seed(B * 7 + V)
+    rng = np.random.default_rng(V + B)
+    x = torch.randn(B, V, generator=g) * 2.0
+    x[:, :5] += 8.0
+    buf = torch.zeros(B * (V + pad) + offset + 8, dtype=torch.bfloat16)
+    view = buf[offset : offset + B * (V + pad)].view(B, V + pad)[:, :V]
+    view.copy_(x.to(torch.bfloat16))
+    logits = buf.to(DEV)[offset : offset + B * (V + pad)].view(B, V + pad)[:, :V]
+    params = mixed_params(rng, B, V, penalties_every=4)
+    hist = [rng.integers(0, V, 50).tolist() for _ in range(B)]
+    hi, ho = pack_history(hist)
+    pp = pack_params(params)
+    u = torch.from_numpy(rng.random(B, dtype=np.float32))
+    draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
+    s = hip()
+    print(f"tile pass B={B} V={V} pad={pad} offset={offset}", flush=True)
+    d = lambda t: t.to(DEV)  # noqa: E731
+    a, ap = s.sample_tile_pass(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
+    b, bp = s.sample_batch(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu())
+    assert torch.equal(ap.cpu().view(torch.int32), bp.cpu().view(torch.int32))
+    w = Workload("tile pass", logits.cpu(), pp, u, hi, ho, draft)
+    ties, bad = compare_ids(a.cpu(), oracle(w), ap.cpu())
+    assert not bad, bad[:10]
+
+
+@pytest.mark.gpu
+def test_gpu_per_token_call_through_the_tile_pass():
+    # the engine's per-token call on bf16 rows with parameters the tile maxima decide (it takes
+    # the tile pass) against the batched call on the same row and uniform
+    from vinfer_amd.sampling import uniform
+
+    s = hip()
+    V = 151936
+    g = torch.Generator().manual_seed(17)
+    row = (torch.randn(V, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    cases = [SamplingParams(temperature=0.7, top_k=20, top_p=0.8), SamplingParams(temperature=0.0),
+             SamplingParams(temperature=1.0, min_p=0.2, top_p=0.95), SamplingParams(temperature=1.3, top_k=256),
+             SamplingParams(temperature=0.9, top_k=300)]
+    print("per-token call through the tile pass", flush=True)
+    for ci, sp in enumerate(cases):
+        for pos in range(6):
+            tok = s.sample(row, sp, 3 + ci, pos)
+            u = torch.tensor([uniform(3 + ci, pos)], dtype=torch.float32, device=DEV)
+            want, _ = s.sample_batch(row.view(1, V), pack_params([sp], DEV), u)
+            assert tok == int(want[0]), (ci, pos)

@@ -405,6 +405,23 @@ int vsamp_sample_tiles(const vsamp_args* a, const float* tile_max, void* stream)
   return run_sample<uint16_t>(a, nullptr, 0, static_cast<hipStream_t>(stream), nullptr, 1, tile_max);
 }
 
+int vsamp_sample_tile_pass(const vsamp_args* a, float* tile_max, void* stream) {
+  g_err.clear();
+  if (int rc = validate(a, true)) return rc;
+  if (a->dtype != VSAMP_BF16) return fail(VSAMP_E_DTYPE, "vsamp_sample_tile_pass takes bf16 logits");
+  if (a->batch == 0) return VSAMP_OK;
+  if (!tile_max) return fail(VSAMP_E_ARG, "tile_max is NULL");
+  if (int rc = check_current_device()) return rc;
+  const int nT = (a->vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(vs::k_tile_max, dim3((nT + vs::kTilesPerBlock - 1) / vs::kTilesPerBlock, a->batch),
+                     dim3(vs::kTileMaxThreads), 0, st, static_cast<const uint16_t*>(a->logits), a->row_stride,
+                     a->vocab, nT, tile_max);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "launch k_tile_max");
+  return run_sample<uint16_t>(a, nullptr, 0, st, nullptr, 1, tile_max);
+}
+
 int vsamp_sample_noalloc(const vsamp_args* a, void* stream) {
   g_err.clear();
   if (int rc = validate(a, true)) return rc;

@@ -1902,8 +1902,16 @@ __device__ __forceinline__ uint32_t low4(uint32_t lo, uint32_t hi) { return __bu
 // 0 exactly when one of the four bytes of w is zero.
 __device__ __forceinline__ uint32_t zero_bytes(uint32_t w) { return (w - 0x01010101u) & ~w & 0x80808080u; }
 
+//
+// Penalised ids need no position bitmap here: the bulk marking above marks every position whose
+// original value is vd, penalised or not, and each thread then corrects the ids of its own
+// penalised entries (`sl`: id << 13 | count, `og`: the original bf16 bits; f.eval holds the
+// non-empty ones' new values at e0, e0 + estep, ...): a penalised id is a member exactly when
+// its new value is vd.
 __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem& f, int ne, float vd, u64 j,
-                                            uint8_t* cells, uint32_t mxk, const uint32_t (&low)[2 * kLowBlocks]) {
+                                            uint8_t* cells, uint32_t mxk, const uint32_t (&low)[2 * kLowBlocks],
+                                            const uint32_t (&sl)[4], const uint32_t (&og)[4], uint32_t e0,
+                                            uint32_t estep) {
   const int tid = threadIdx.x;
   const uint32_t vb = __float_as_uint(vd);
   const bool bf = (vb & 0xFFFFu) == 0u;  // vd is a bf16 value: bulk tokens can hold it
@@ -1917,7 +1925,6 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     const int b = id / kBlk;
     atomicOr(&cw[b >> 2], 1u << (8 * (b & 3) + id % kBlk));
   };
-  auto penalised = [&](int id) -> bool { return row.bm && ((row.bm[id / kBlk] >> (id % kBlk)) & 1u); };
   // The member lanes of an 8-element block: xor with the pattern zeroes the matching 16-bit
   // halves, v_pk_min_u16(x, 1) leaves 0 (match) or 1 per half, and three shifted ors gather the
   // halves of the 4 words into bits 0, 2, 4, 6 (low halves) and 16, 18, 20, 22 (high halves).
@@ -1956,8 +1963,7 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     // as many slots as its lane with the most candidates (a lane without one rereads its first
     // block, unused).
     auto mark = [&](int b, uint4 w) {
-      uint32_t mask = match8(w);
-      if (row.bm) mask &= ~static_cast<uint32_t>(row.bm[b]);
+      const uint32_t mask = match8(w);
       if (mask) cells[b] = static_cast<uint8_t>(mask);  // (block b belongs to this thread alone)
     };
     auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
@@ -1995,13 +2001,29 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     if (cand) {
       for (int i = nfull * kBlk + tid; i < V; i += kThreads) {
         const uint32_t raw = base[i];
-        if ((raw == t16 || raw == t16b) && !penalised(i)) cell_or(i);
+        if (raw == t16 || raw == t16b) cell_or(i);
       }
     }
   }
-  // penalised ids whose new value is vd are members
-  for (int e = tid; e < ne; e += kThreads)
-    if (f.eval[e] == vd) cell_or(f.eid[e]);
+  lds_barrier();  // (every bulk mark is in before the corrections)
+  // this thread's penalised entries (at e0, e0 + estep, ... in the order of sl): members by
+  // their new value, not their original one
+  uint32_t e = e0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (sl[k] == kEmpty) continue;
+    const int id = static_cast<int>(sl[k] >> 13);
+    const uint32_t raw = og[k] & 0xFFFFu;
+    const bool was = bf && (raw == t16 || raw == t16b);  // (the bulk marking set its bit)
+    const bool is = f.eval[e] == vd;
+    e += estep;
+    if (was != is) {
+      const int b = id / kBlk;
+      const uint32_t bit = 1u << (8 * (b & 3) + id % kBlk);
+      if (is) atomicOr(&cw[b >> 2], bit);
+      else atomicAnd(&cw[b >> 2], ~bit);
+    }
+  }
   lds_barrier();
   // the cell holding the j-th member: per-thread member counts of `per` consecutive cells (one
   // popcount per 4 cells), then a scan
@@ -2542,15 +2564,22 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   const uint32_t mkey = uniform_u(f.plan.mkey);
   const float mz = uniform_f(f.plan.mz);
   Kept k;
+  // The histogram is dead from here on: the id searches use its memory. The penalised ids'
+  // position bitmap is built only for a search that passes over the row (find_first, split
+  // rows' slice search, probabilities): the member search corrects penalised ids itself.
+  auto need_bitmap = [&]() {  // (uniform)
+    if (ne > 0 && !row.bm) build_bitmap(row, hist + kBitmapOffset);
+  };
   if (status == kPlanPoint) {
     const float xmax = val_of(mkey);
-    // the histogram is dead: the id searches use its memory
-    if (ne > 0) build_bitmap(row, hist + kBitmapOffset);
     // point rows: the first NaN, the first max (greedy), the first +inf z, or index 0 (all -inf)
-    if (f.plan.nnan) k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
-    else if (!(T > 0.0f)) {
+    if (f.plan.nnan) {
+      need_bitmap();
+      k.point = find_first(row, [&](float x, int) -> u64 { return x != x; }, 0ull, srch);
+    } else if (!(T > 0.0f)) {
       int pt = -1;
       if constexpr (SPLIT) {
+        need_bitmap();
         pt = split_find(a, row, f, ne, xmax, 0ull, srch, hist + kMatchOffset, recs);
       } else if (!a.out_probs && cells_per(row) * kThreads <= 4 * kMatchWords) {  // (uniform)
         // the first id holding the max, by the member search from the kept low bytes (as the
@@ -2560,11 +2589,17 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
         for (int i = tid; i < ncq; i += kThreads) reinterpret_cast<uint4*>(cells)[i] = make_uint4(0, 0, 0, 0);
         if (tid == 0) f.si[6] = -1;
         lds_barrier();
-        pt = select_member(row, f, ne, xmax, 0ull, cells, mxk, low);
+        pt = select_member(row, f, ne, xmax, 0ull, cells, mxk, low, sl, og, e0, estep);
       }
-      k.point = pt >= 0 ? pt : find_first(row, [&](float x, int) -> u64 { return x == xmax; }, 0ull, srch);
+      if (pt < 0) {  // (uniform)
+        need_bitmap();
+        pt = find_first(row, [&](float x, int) -> u64 { return x == xmax; }, 0ull, srch);
+      }
+      k.point = pt;
+    } else {
+      need_bitmap();
+      if (!degenerate(row, p, mkey, 0, mz, srch, k)) k.point = 0;
     }
-    else if (!degenerate(row, p, mkey, 0, mz, srch, k)) k.point = 0;
     finish<STATE>(a, row, p, mz, k, 0, &srch.vslot, r);
     return true;
   }
@@ -2741,20 +2776,21 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   k.S = f.plan.S;
   const float vd = f.plan.vd;
   const u64 j = f.plan.j;
-  // the histogram is dead: the id searches below use its memory. One pass zeroes the position
-  // bitmap of the penalised ids and the member search's cells.
+  // One pass zeroes the member search's cells and, when a pass over the row will need it, the
+  // position bitmap of the penalised ids.
   const bool cells_fit = !SPLIT && !a.out_probs && cells_per(row) * kThreads <= 4 * kMatchWords;
+  const bool bitmap_now = ne > 0 && !cells_fit;  // (uniform)
   {
     uint32_t* bmw = hist + kBitmapOffset;
     // (16-byte stores: both regions start 16-byte aligned, and the bitmap's last quad stays in
     // its region)
-    const int nbq = ne > 0 ? (row.nblk + 15) / 16 : 0;
+    const int nbq = bitmap_now ? (row.nblk + 15) / 16 : 0;
     const int ncq = cells_fit ? cells_per(row) * kThreads / 16 : 0;
     for (int i = tid; i < nbq; i += kThreads) reinterpret_cast<uint4*>(bmw)[i] = make_uint4(0, 0, 0, 0);
     for (int i = tid; i < ncq; i += kThreads) reinterpret_cast<uint4*>(hist + kMatchOffset)[i] = make_uint4(0, 0, 0, 0);
     if (tid == 0) f.si[6] = -1;
     lds_barrier();
-    if (ne > 0) {
+    if (bitmap_now) {
       for (int e = tid; e < ne; e += kThreads) {
         const uint32_t id = static_cast<uint32_t>(f.eid[e]);
         atomicOr(&bmw[id >> 5], 1u << (id & 31u));
@@ -2773,23 +2809,31 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
       int id = -1;
       if (cells_fit) {
         uint8_t* cells = reinterpret_cast<uint8_t*>(hist + kMatchOffset);
-        id = select_member(row, f, ne, k.vc, static_cast<u64>(k.r - 1), cells, mxk, low);
+        id = select_member(row, f, ne, k.vc, static_cast<u64>(k.r - 1), cells, mxk, low, sl, og, e0, estep);
         const int ncq = cells_per(row) * kThreads / 16;
         for (int i = tid; i < ncq; i += kThreads) reinterpret_cast<uint4*>(cells)[i] = make_uint4(0, 0, 0, 0);
         if (tid == 0) f.si[6] = -1;
         lds_barrier();
       }
       const float vc = k.vc;
-      k.idr = id >= 0 ? id : find_first(row, [&](float x, int) -> u64 { return x == vc; }, static_cast<u64>(k.r - 1), srch);
+      if (id < 0) {  // (uniform)
+        need_bitmap();
+        id = find_first(row, [&](float x, int) -> u64 { return x == vc; }, static_cast<u64>(k.r - 1), srch);
+      }
+      k.idr = id;
     }
   }
   int draw = 0;
   if (!a.out_probs) {
     if constexpr (SPLIT) draw = split_find(a, row, f, ne, vd, j, srch, hist + kMatchOffset, recs);
     else
-      draw = cells_fit ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, low)
+      draw = cells_fit ? select_member(row, f, ne, vd, j, reinterpret_cast<uint8_t*>(hist + kMatchOffset), mxk, low,
+                                       sl, og, e0, estep)
                        : -1;
-    if (draw < 0) draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
+    if (draw < 0) {  // (uniform)
+      need_bitmap();
+      draw = find_first(row, [&](float x, int) -> u64 { return x == vd; }, j, srch);
+    }
   }
   finish<STATE>(a, row, p, mz, k, draw, &srch.vslot, r);
   return true;
@@ -2854,6 +2898,42 @@ __device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk,
     above = sh[1];
   }
   return (hi << 8) | sh[0];
+}
+
+// The tile maxima of bf16 rows from any source (what k_lm_head's epilogue writes beside its
+// logits): the max of every kStatTile consecutive logits of a row, as a value (ordered keys: a
+// NaN is the largest; -0.0 and +0.0 are one value). Sixteen lanes take a tile, eight logits a
+// lane, and reduce over their 16-lane row; grid (ceil(nT / 16), B) of 256-thread workgroups, so
+// even one row spreads over the chip.
+constexpr int kTileMaxThreads = 256;
+constexpr int kTilesPerBlock = kTileMaxThreads / 16;
+__global__ __launch_bounds__(kTileMaxThreads) void k_tile_max(const uint16_t* logits, int64_t stride, int V,
+                                                             int nT, float* out) {
+  const int r = blockIdx.y;
+  const int l16 = threadIdx.x & 15;
+  const int t = blockIdx.x * kTilesPerBlock + (threadIdx.x >> 4);  // (the same in a 16-lane row)
+  const uint16_t* row = as_global(logits) + static_cast<int64_t>(r) * stride;
+  const int i0 = t * kStatTile + 8 * l16;  // this lane's first logit
+  uint32_t mk = 0;                         // (below every key)
+  if (t < nT) {
+    if ((reinterpret_cast<uintptr_t>(row + i0) & 15u) == 0 && i0 + 8 <= V) {
+      const uint4 q = ld_global_u4(reinterpret_cast<const uint4*>(row + i0));
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        mk = max(mk, key_of(__uint_as_float(w[i] << 16)));
+        mk = max(mk, key_of(__uint_as_float(w[i] & 0xFFFF0000u)));
+      }
+    } else {
+      for (int i = i0; i < i0 + 8 && i < V; ++i) mk = max(mk, key_of(bf16_to_f32(ld_global(row + i))));
+    }
+  }
+  auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  mk = umax(mk, dpp::mov<dpp::kXor1>(mk));
+  mk = umax(mk, dpp::mov<dpp::kXor2>(mk));
+  mk = umax(mk, dpp::mov<dpp::kHalfMirror>(mk));
+  mk = umax(mk, dpp::mov<dpp::kMirror>(mk));
+  if (t < nT && l16 == 0) as_global(out)[static_cast<int64_t>(r) * nT + t] = val_of(mk);
 }
 
 // Returns true when the row was decided (outputs written) from its tile maxima; false, having

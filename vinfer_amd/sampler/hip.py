@@ -315,6 +315,26 @@ class HipSampler:
         del keep
         return ids, dprob
 
+    def sample_tile_pass(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
+        """``sample_batch`` for small batches of bf16 logits from any source
+        (``vsamp_sample_tile_pass``): the rows' tile maxima are computed by a launch spread over
+        the chip first, then greedy, top-k and min-p rows without penalties are decided from a
+        few tiles. The same ids and draft probabilities as ``sample_batch``."""
+        dev = self._device(logits)
+        if logits.dtype != torch.bfloat16:
+            raise ValueError("sample_tile_pass takes bf16 logits")
+        B, V = logits.shape
+        a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids)
+        a.flags &= ~_lib.VSAMP_SPLIT_ROWS
+        ids = torch.empty(B, dtype=torch.int32, device=dev)
+        dprob = torch.empty(B, dtype=torch.float32, device=dev) if draft_ids is not None else None
+        a.out_ids = ids.data_ptr()
+        a.out_draft_prob = _ptr(dprob)
+        tiles = self._tiles(dev, B * ((V + _lib.LM_TILE - 1) // _lib.LM_TILE))
+        _lib.check(self._lib.vsamp_sample_tile_pass(ctypes.byref(a), tiles, self._stream(dev)))
+        del keep
+        return ids, dprob
+
     def prepare_tiles(self, logits, tile_max, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
         """``prepare_batch`` for ``sample_tiles``: a reusable launch on fixed buffers (the logits
         and tile maxima may be rewritten in place between launches)."""
@@ -433,7 +453,19 @@ class HipSampler:
         stream = torch.cuda.current_stream(dev)
         out = t.out_np
         out[0] = -1
-        _lib.check(self._lib.vsamp_sample(t.ref, ctypes.c_void_p(stream.cuda_stream)))
+        # bf16 greedy and top-k (<= 256) rows without penalties take the tile pass: the row's tile
+        # maxima over the chip, then a few tiles, instead of the whole row on one workgroup
+        # (greedy 29.9 -> 24.7 us per call, top-k 20 34.2 -> 31.0 on MI355X). Rows with min-p alone
+        # do not: their candidates depend on the logits (N(0, 4) rows keep ~900 tokens at min-p
+        # 0.05, more than the tile path's list), and a row handed on pays both launches.
+        top_k = params.top_k
+        if (row.dtype == torch.bfloat16 and n == 0 and not penalized(params)
+                and (not params.temperature > 0 or 0 < top_k <= 256 and top_k < V)):
+            code = self._lib.vsamp_sample_tile_pass(t.ref, self._tiles(dev, (V + _lib.LM_TILE - 1) // _lib.LM_TILE),
+                                                    ctypes.c_void_p(stream.cuda_stream))
+        else:
+            code = self._lib.vsamp_sample(t.ref, ctypes.c_void_p(stream.cuda_stream))
+        _lib.check(code)
         # the kernel writes the id last, after every read of the parameters and the history: the
         # call returns as soon as the id reaches the pinned word (sooner than a stream
         # synchronisation returns), and a synchronisation settles it past any draw's time
@@ -453,6 +485,14 @@ class HipSampler:
         if t is None:
             t = paths[dev] = _TokenPath(dev)
         return t
+
+    def _tiles(self, dev: torch.device, n: int) -> int:
+        """A device buffer of ``n`` fp32 tile maxima, this thread's for ``dev``."""
+        bufs = self._local.__dict__.setdefault("tiles", {})
+        t = bufs.get(dev)
+        if t is None or t.numel() < n:
+            t = bufs[dev] = torch.empty(max(n, 2048), dtype=torch.float32, device=dev)
+        return t.data_ptr()
 
     def _workspace(self, dev: torch.device, need: int) -> int:
         """A 256-byte aligned device workspace of ``need`` bytes, this thread's for ``dev``."""
