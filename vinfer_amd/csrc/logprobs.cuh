@@ -257,7 +257,7 @@ __global__ __launch_bounds__(kThreads) void k_logprobs(LogprobArgs a) {
         nk += tid + i * kThreads < a.nT;
       }
       const uint32_t nnt = static_cast<uint32_t>(min(n, a.V));
-      const uint32_t th = kth_key16(k16, nk, nnt, rdx.hcnt, sh);
+      const uint32_t th = kth_key16(k16, nk, nnt, rdx.hcnt, reinterpret_cast<uint32_t*>(rdx.hmass), sh);
       uint32_t mine = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) mine += i < nk && k16[i] >= th;

@@ -1053,23 +1053,37 @@ static_assert(kMatchOffset + 2 * kCandCap + 2 * kStreamCap <= kChunk, "the stage
 static_assert(kMatchOffset + 2 * kCandCap + 2 * kSortCap <= kChunk, "the sort's staging must fit");
 
 // Sorts c[0, n), n <= kSortCap, in place (rank by counting; tmp holds n entries). Every thread
-// calls; the sorted list is visible on return.
+// calls; the sorted list is visible on return. The order is one 64-bit key per entry, ordered key
+// above the complemented id (larger first: larger value, then smaller id), staged in tmp; each
+// entry's rank is the count of larger keys, and it is written there (every read of c is done
+// before the first barrier).
 __device__ __forceinline__ void sort_cands(Cand* c, int n, Cand* tmp) {
   const int i = threadIdx.x;
+  u64* kk = reinterpret_cast<u64*>(tmp);
+  static_assert(sizeof(Cand) == sizeof(u64), "one staged key per entry");
+  Cand me{0.0f, 0};
+  u64 km = 0;
   if (i < n) {
-    const Cand me = c[i];
-    const uint32_t km = key_of(me.x);
-    uint32_t rank = 0;
-    for (int j = 0; j < n; ++j) {  // (j uniform: one broadcast read per wave)
-      const Cand o = c[j];
-      const uint32_t ko = key_of(o.x);
-      rank += (ko > km || (ko == km && o.id < me.id)) ? 1u : 0u;
-    }
-    tmp[rank] = me;
+    me = c[i];
+    km = (static_cast<u64>(key_of(me.x)) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(me.id));
+    kk[i] = km;
   }
   lds_barrier();
-  if (i < n) c[i] = tmp[i];
+  if (i < n) {
+    uint32_t rank = 0;
+    for (int j = 0; j < n; ++j) rank += kk[j] > km ? 1u : 0u;  // (j uniform: one broadcast read per wave)
+    c[rank] = me;
+  }
   lds_barrier();
+}
+
+// floor(a / b) for a < 2^53 and b > 0 (both exact in fp64): the fp64 quotient is at most one
+// above it (a representable integer quotient is exact, and rounding is monotonic), corrected by
+// one integer product.
+__device__ __forceinline__ u64 udiv53(u64 a, u64 b) {
+  u64 q = static_cast<u64>(static_cast<double>(a) / static_cast<double>(b));
+  if (q * b > a) --q;
+  return q;
 }
 
 // Top-p cutoff and draw over a sorted list c[0, n) that holds every element >= k.x0 (the kept
@@ -1114,22 +1128,27 @@ __device__ __forceinline__ bool sorted_tail(const SampleArgs& a, const Row<Tin>&
 #pragma unroll
     for (int t = 1; t < 4; ++t) E[t] = E[t - 1] + q[t - 1];
     const u64 S0 = dpp::last(incl);
-    // sums over the kept elements of one key group: count above / in, mass above / in
-    auto group = [&](uint32_t gk, uint32_t* f, uint32_t* cnt, u64* above, u64* mass) {
-      uint32_t cf = 0, cg = 0;
-      u64 ma = 0, mg = 0;
+    // entry i's value of a per-slot array (i uniform): slot i mod 4 of lane i / 4
+    auto at64 = [&](const u64 (&v)[4], uint32_t i) {
+      const uint32_t t = i & 3u;
+      return readlane64(t == 0u ? v[0] : t == 1u ? v[1] : t == 2u ? v[2] : v[3], static_cast<int>(i >> 2));
+    };
+    // one key group of the kept prefix (a kept key, gk != 0): its first index (the kept elements
+    // with a larger key, all before it), its size and the mass above it (E at its first index);
+    // its members are contiguous and have one mass, returned in q1
+    auto group = [&](uint32_t gk, uint32_t* f, uint32_t* cnt, u64* above, u64* q1) {
+      uint32_t first = 0xFFFFFFFFu, m = 0;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const bool kept = key[t] != 0u;
-        cf += kept && key[t] > gk ? 1u : 0u;
-        cg += kept && key[t] == gk ? 1u : 0u;
-        ma += kept && key[t] > gk ? q[t] : 0ull;
-        mg += kept && key[t] == gk ? q[t] : 0ull;
+        const u64 b = __ballot(key[t] == gk);
+        m += static_cast<uint32_t>(__popcll(b));
+        const uint32_t i = b ? 4u * static_cast<uint32_t>(__ffsll(static_cast<long long>(b)) - 1) + t : 0xFFFFFFFFu;
+        first = i < first ? i : first;
       }
-      *f = wave_sum<uint32_t>(cf);
-      *cnt = wave_sum<uint32_t>(cg);
-      *above = wave_sum<u64>(ma);
-      *mass = wave_sum<u64>(mg);
+      *f = first;
+      *cnt = m;
+      *above = at64(E, first);
+      *q1 = at64(q, first);
     };
     bool ok = true;
     u64 S = S0;
@@ -1144,11 +1163,11 @@ __device__ __forceinline__ bool sorted_tail(const SampleArgs& a, const Row<Tin>&
       const uint32_t nb = wave_sum<uint32_t>(below);
       ok = nb > 0;
       if (ok) {
-        const int js = static_cast<int>(nb) - 1;  // the last element with E < P
-        ck = key_of(c[js].x);
-        u64 massc;
-        group(ck, &fc, &nc, &mabove, &massc);
-        qc = nc ? massc / nc : 0ull;
+        const uint32_t js = nb - 1u;  // the last element with E < P
+        const uint32_t tj = js & 3u;
+        ck = __builtin_amdgcn_readlane(tj == 0u ? key[0] : tj == 1u ? key[1] : tj == 2u ? key[2] : key[3],
+                                       static_cast<int>(js >> 2));
+        group(ck, &fc, &nc, &mabove, &qc);
         rr = nc;
         if (qc > 0) {
           const double cr = ceil((P - static_cast<double>(mabove)) / static_cast<double>(qc));
@@ -1164,7 +1183,7 @@ __device__ __forceinline__ bool sorted_tail(const SampleArgs& a, const Row<Tin>&
       const u64 td = static_cast<u64>(static_cast<double>(p.u) * static_cast<double>(S));
       const u64 tdc = td < S ? td : S - 1;
       if (has_cut && tdc >= mabove && qc > 0) {
-        di = fc + static_cast<uint32_t>((tdc - mabove) / qc);
+        di = fc + static_cast<uint32_t>(udiv53(tdc - mabove, qc));
       } else {
         // the group holding tdc among the elements >= x0 (x0 raised to the cutoff value when
         // the cutoff group is whole)
@@ -1181,10 +1200,9 @@ __device__ __forceinline__ bool sorted_tail(const SampleArgs& a, const Row<Tin>&
         if (ok) {
           const uint32_t dk = __builtin_amdgcn_readlane(mine, __ffsll(static_cast<long long>(hl)) - 1);
           uint32_t fd, nd;
-          u64 maboved, massd;
-          group(dk, &fd, &nd, &maboved, &massd);
-          const u64 qd = nd ? massd / nd : 0ull;
-          u64 j = qd ? (tdc - maboved) / qd : 0ull;
+          u64 maboved, qd;
+          group(dk, &fd, &nd, &maboved, &qd);
+          u64 j = qd ? udiv53(tdc - maboved, qd) : 0ull;
           if (j >= nd) j = nd ? nd - 1 : 0;
           di = fd + static_cast<uint32_t>(j);
         }
@@ -2861,18 +2879,22 @@ constexpr int kTileRowTiles = 64;   // candidate tiles a row decided from its ti
 
 // The key of the k-th largest (1-based, with multiplicity) of the 16-bit keys keys[0 .. nk) of
 // every thread (nk <= 4; k <= the number of keys): two rounds over the high and the low byte,
-// each a 256-bin LDS histogram that wave 0 walks from the top. `h` is 256 words, `sh` 4 words.
-__device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk, uint32_t k, uint32_t* h, uint32_t* sh) {
+// each a 256-bin LDS histogram (h0, then h1: both zeroed at the start) that wave 0 walks from
+// the top. `h0` and `h1` are 256 words each, `sh` 4 words.
+__device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk, uint32_t k, uint32_t* h0, uint32_t* h1,
+                                              uint32_t* sh) {
   const int tid = threadIdx.x;
   uint32_t hi = 0, above = 0;
+  if (tid < 256) h0[tid] = 0;
+  else if (tid < 512) h1[tid - 256] = 0;
+  lds_barrier();
   for (int round = 0; round < 2; ++round) {
-    if (tid < 256) h[tid] = 0;
-    __syncthreads();
+    uint32_t* h = round == 0 ? h0 : h1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (i < nk && (round == 0 || (keys[i] >> 8) == hi)) atomicAdd(&h[round == 0 ? keys[i] >> 8 : keys[i] & 0xFFu], 1u);
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < kWave) {
       // lane l: bins 255 - 4l .. 252 - 4l, descending
       uint32_t c[4], s4 = 0;
@@ -2893,7 +2915,7 @@ __device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk,
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (round == 0) hi = sh[0];
     above = sh[1];
   }
@@ -3002,7 +3024,7 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t
       k16[i] = kt[i] >> 16;  // (a bf16 value's key is the top half of its fp32 key)
       nk += tid + i * kThreads < nT ? 1 : 0;
     }
-    theta = val16(kth_key16(k16, nk, static_cast<uint32_t>(p.K), g.rdx.hcnt, sh + 2));
+    theta = val16(kth_key16(k16, nk, static_cast<uint32_t>(p.K), g.rdx.hcnt, reinterpret_cast<uint32_t*>(g.rdx.hmass), sh + 2));
   }
   if (tid < kWave) {
     float xlo = -INFINITY, xm = -INFINITY;
