@@ -686,7 +686,8 @@ int vsamp_lm_head(const vsamp_lm_head_args* a, void* stream) {
   l.vec_out = !(reinterpret_cast<uintptr_t>(a->logits) & 15u) && a->logits_stride % 8 == 0;
   static_assert(vs::kLmBN == VSAMP_LM_TILE, "the statistics' tile is the kernel's column tile");
   // (up to 4 rows: matrix-vector products, for the hidden sizes they are built for; batches of
-  // at most 64 rows: 64-row tiles, four times less MFMA work on padding)
+  // at most 64 rows: the weight streamed into registers, 640 vocabulary rows a workgroup; larger
+  // batches: 256 x 128 tiles with both operands staged through LDS)
   const int cpl = a->dim % 512 == 0 ? a->dim / 512 : 0;  // hidden chunks per lane
   if (a->batch <= 4 && (cpl == 1 || cpl == 2 || cpl == 4 || cpl == 8)) {
     const int nb = a->batch == 1 ? 1 : a->batch == 2 ? 2 : 4;
@@ -698,7 +699,8 @@ int vsamp_lm_head(const vsamp_lm_head_args* a, void* stream) {
     VS_GEMV(1, 4); VS_GEMV(2, 4); VS_GEMV(4, 4); VS_GEMV(8, 4);
 #undef VS_GEMV
   } else if (a->batch <= 64)
-    hipLaunchKernelGGL(vs::k_lm_head<64>, dim3(l.nT, 1), dim3(vs::kLmThreads), 0, static_cast<hipStream_t>(stream), l);
+    hipLaunchKernelGGL(vs::k_lm_stream, dim3((a->vocab + vs::kLsRows - 1) / vs::kLsRows), dim3(vs::kLsThreads), 0,
+                       static_cast<hipStream_t>(stream), l);
   else
     hipLaunchKernelGGL(vs::k_lm_head<256>, dim3(l.nT, (a->batch + 255) / 256), dim3(vs::kLmThreads), 0,
                        static_cast<hipStream_t>(stream), l);

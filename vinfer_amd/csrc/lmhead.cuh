@@ -6,7 +6,7 @@
 // reads only the few tiles that can hold its top n, instead of two passes over the row.
 //
 // MFMA tiling (gfx950, v_mfma_f32_32x32x16_bf16): a workgroup of 8 waves computes a BM x 128
-// tile of the output (BM = 256, or 64 for batches of at most 64 rows) over the hidden dimension
+// tile of the output (BM = 256: batches above 64 rows) over the hidden dimension
 // in steps of 64. Both operands are K-contiguous rows, and both are staged through a ring of S
 // LDS stages (BM + 128 rows of 128 bytes each) by direct global-to-LDS loads
 // (global_load_lds_dwordx4: lane L of a load writes the 16 bytes at stage offset 16 L, so one
@@ -39,10 +39,6 @@ template <>
 struct LmTile<256> {
   static constexpr int WM = 4, MT = 2, NT = 2, S = 3;  // waves over M; tiles per wave; stages
 };
-template <>
-struct LmTile<64> {
-  static constexpr int WM = 2, MT = 1, NT = 1, S = 5;
-};
 template <int BM>
 constexpr int lm_stage_bytes() { return (BM + kLmBN) * 128; }
 template <int BM>
@@ -67,6 +63,7 @@ struct LmHeadArgs {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -252,6 +249,189 @@ __global__ __launch_bounds__(kLmThreads, 1) void k_lm_head(LmHeadArgs a) {
       *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(srcp);
     } else {
       for (int i = 0; i < min(8, ncol - c0); ++i) dst[i] = srcp[i];
+    }
+  }
+}
+
+// ---- decode batches (B <= 64): the weight streamed into registers ---------------------------
+// A 64-row version of the tile above (both operands through LDS) took 296-318 us at B = 8-64: each
+// of its 1,187 workgroups brings the whole hidden block (64 x d) in beside its 128 weight rows,
+// ~600 MB of hidden re-reads beside the 1.24 GB weight, through the same intake. Here the weight goes straight from the HBM into the
+// MFMA's A operand (v_mfma_f32_16x16x32_bf16; the output computed transposed: M = vocabulary rows,
+// N = batch rows), and a workgroup covers kLsRows = 640 weight rows, so that V = 151,936 takes 238
+// workgroups -- one round on 256 CUs, with a fifth of the hidden re-reads (241-252 us at
+// B = 8-64, d = 4096). A 256-row workgroup of 32-row waves took 323-337 us: 594 workgroups are
+// 1.16 rounds of two per CU, and the second round runs on a sixth of the chip. Each of its 8 waves owns
+// 80 weight rows (five 16-row tiles) and the whole 64-row batch (four 16-row tiles): 20
+// accumulator tiles, 80 VGPRs, affordable at two waves per SIMD. Lane l holds row l % 16 of a
+// tile at k 32 t + 8 (l / 16) .. + 7 of a 64-deep chunk (step t of two): four lanes read 64
+// contiguous bytes of a row. kLsRing chunks of the weight are in flight per wave (20 KB; 160 KB a
+// CU); the hidden chunk (64 rows x 128 bytes, the swizzled stage layout above, B operand: batch row
+// l % 16 of a tile at the same k) rides a ring of kLsRing + 1 LDS stages filled by direct
+// global-to-LDS loads, one wave-wide load per wave per chunk.
+//
+// Epilogue: the accumulators go to LDS as bf16, batch-major (row b: the workgroup's 640 logits of
+// batch row b); thread t < 320 computes batch row t / 5's statistics over tile t % 5, and the
+// logits are stored 16 bytes at a time.
+constexpr int kLsThreads = 512;  // 8 waves
+constexpr int kLsMT = 5;         // 16-row weight tiles per wave
+constexpr int kLsRows = kLsThreads / kWave * 16 * kLsMT;  // 640: five statistics tiles
+constexpr int kLsTiles = kLsRows / kLmBN;
+constexpr int kLsRing = 2;       // weight chunks in flight per wave (40 VGPRs each)
+constexpr int kLsStages = kLsRing + 1;
+constexpr int kLsHStage = 64 * 128;        // bytes of a hidden stage: 64 rows x 64 k
+constexpr int kLsOStride = kLsRows + 8;    // LDS row stride of the output staging (bf16)
+constexpr int kLsLds = kLsStages * kLsHStage > 64 * kLsOStride * 2 ? kLsStages * kLsHStage : 64 * kLsOStride * 2;
+static_assert(kLsRows % kLmBN == 0, "whole statistics tiles");
+
+__global__ __launch_bounds__(kLsThreads, 1) void k_lm_stream(LmHeadArgs a) {
+  __shared__ __align__(16) uint8_t lds[kLsLds];
+  const int tid = threadIdx.x;
+  const int l = lane_id();
+  const int w = tid / kWave;
+  const int nb = blockIdx.x * kLsRows;  // the workgroup's first weight row
+  const int nk = a.d / kLmBK;
+  // this lane's weight rows 80 w + 16 mt + l % 16 (rows past the vocabulary read the last one,
+  // unused) at k 8 (l / 16) .. + 7 of each 32-deep step
+  const uint4* wsrc[kLsMT];
+#pragma unroll
+  for (int mt = 0; mt < kLsMT; ++mt)
+    wsrc[mt] = reinterpret_cast<const uint4*>(
+        as_global(a.W) + static_cast<int64_t>(min(nb + 16 * kLsMT * w + 16 * mt + (l & 15), a.V - 1)) * a.ldw +
+        8 * (l >> 4));
+  // the hidden stage rows 8 w .. 8 w + 7 this wave fills: lane l the 16 bytes at slot l % 8 of
+  // row 8 w + l / 8, i.e. chunk (l % 8) ^ (l / 8) of that row (rows past the batch read its last)
+  const uint16_t* hsrc = as_global(a.hidden) + static_cast<int64_t>(min(8 * w + (l >> 3), a.B - 1)) * a.ldh +
+                         8 * ((l & 7) ^ (l >> 3));
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  auto issue_h = [&](int kc) { lds_dma16(hsrc + kc * kLmBK, lds0 + static_cast<uint32_t>((kc % kLsStages) * kLsHStage) + 1024u * wu); };
+  // q[2 mt + t]: tile mt, step t
+  auto issue_w = [&](int kc, uint4 (&q)[2 * kLsMT]) {
+#pragma unroll
+    for (int mt = 0; mt < kLsMT; ++mt)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) q[2 * mt + t] = wsrc[mt][kc * (kLmBK / 8) + 4 * t];
+  };
+  uint4 wq[kLsRing][2 * kLsMT];
+  f32x4_t acc[kLsMT][4];
+#pragma unroll
+  for (int mt = 0; mt < kLsMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{};
+  // chunk c's loads: its hidden stage, then its weight (eleven per wave); chunks 0 .. kLsRing - 1
+  // now. Every chunk issues the loads of chunk kc + kLsRing, of the last chunk when that is past
+  // the end (unused; into registers and a stage no later chunk reads): loads on a branch would
+  // make the compiler's waits before each product assume they were the latest, which waits for
+  // every load in flight.
+  constexpr int kPerChunk = 1 + 2 * kLsMT;
+#pragma unroll
+  for (int c = 0; c < kLsRing; ++c) {
+    issue_h(min(c, nk - 1));
+    issue_w(min(c, nk - 1), wq[c]);
+  }
+  // one chunk: wait for its loads (issued after them: the next kLsRing - 1 chunks' loads), the
+  // barrier (every wave's hidden rows are in; every wave is done with chunk kc - 1's stage, which
+  // chunk kc + kLsRing then fills), the products, and the weight of chunk kc + kLsRing into the
+  // registers just used
+  auto chunk = [&](int kc, uint4 (&q)[2 * kLsMT]) {
+    wait_vm<kPerChunk * (kLsRing - 1)>();
+    lds_barrier();
+    const int next = min(kc + kLsRing, nk - 1);
+    issue_h(next);
+    const uint8_t* stage = lds + (kc % kLsStages) * kLsHStage;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int c = 4 * t + (l >> 4);  // the hidden row's 16-byte chunk: k 8 c .. 8 c + 7 of the chunk
+      bf16x8_t bv[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int r = 16 * nt + (l & 15);
+        bv[nt] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + r * 128 + 16 * (c ^ (r & 7))));
+      }
+#pragma unroll
+      for (int mt = 0; mt < kLsMT; ++mt) {
+        const bf16x8_t av = as_bf16x8(q[2 * mt + t]);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv[nt], acc[mt][nt], 0, 0, 0);
+      }
+    }
+    issue_w(next, q);
+  };
+  static_assert(kLsRing == 2, "the chunk loop is unrolled twice");
+  int kc = 0;
+#pragma unroll 1
+  for (; kc + 2 <= nk; kc += 2) {
+    chunk(kc, wq[0]);
+    chunk(kc + 1, wq[1]);
+  }
+  if (kc < nk) chunk(kc, wq[0]);
+  wait_vm<0>();   // (the unused loads past the end, some into LDS stages, are done)
+  lds_barrier();  // (every wave is done with the stages: the output goes over them)
+  // ---- epilogue: lane l, accumulator j of tile (mt, nt): weight row 80 w + 16 mt + 4 (l / 16) + j,
+  // batch row 16 nt + l % 16
+  uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+  for (int mt = 0; mt < kLsMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        ot[(16 * nt + (l & 15)) * kLsOStride + 16 * kLsMT * w + 16 * mt + 4 * (l >> 4) + j] =
+            static_cast<uint16_t>(bf16_rne(acc[mt][nt][j]));
+  lds_barrier();
+  const int ncolw = min(kLsRows, a.V - nb);  // the workgroup's columns inside the vocabulary
+  if (tid < kLsTiles * 64) {
+    const int b = tid / kLsTiles, t = tid % kLsTiles;
+    const int ncol = min(kLmBN, ncolw - kLmBN * t);
+    if (b < a.B && ncol > 0) {
+      uint4 v[kLmBN / 8];
+#pragma unroll
+      for (int c = 0; c < kLmBN / 8; ++c) v[c] = *reinterpret_cast<const uint4*>(ot + b * kLsOStride + kLmBN * t + 8 * c);
+      auto lo = [](uint32_t x) { return __uint_as_float(x << 16); };
+      auto hi = [](uint32_t x) { return __uint_as_float(x & 0xFFFF0000u); };
+      // (the max by ordered keys: a NaN is the largest, as in the log-softmax over the row)
+      uint32_t mkey = 0;
+#pragma unroll
+      for (int c = 0; c < kLmBN / 8; ++c) {
+        const uint32_t q[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (8 * c + 2 * i < ncol) mkey = max(mkey, key_of(lo(q[i])));
+          if (8 * c + 2 * i + 1 < ncol) mkey = max(mkey, key_of(hi(q[i])));
+        }
+      }
+      const float mx = val_of(mkey);
+      float sum = 0.0f;
+      if (mx > -INFINITY && mx < INFINITY) {  // (false for a NaN max)
+#pragma unroll
+        for (int c = 0; c < kLmBN / 8; ++c) {
+          const uint32_t q[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (8 * c + 2 * i < ncol) sum += __expf(lo(q[i]) - mx);
+            if (8 * c + 2 * i + 1 < ncol) sum += __expf(hi(q[i]) - mx);
+          }
+        }
+      }
+      const int64_t at = static_cast<int64_t>(b) * a.nT + nb / kLmBN + t;
+      a.tmax[at] = mx;
+      a.tsum[at] = sum;
+    }
+  }
+  // the logits: kLsRows / 8 chunks of 16 bytes per batch row; rows that are not 16-byte aligned,
+  // and a chunk that crosses the end of the vocabulary, element by element
+  uint16_t* out = as_global(a.logits);
+  for (int q = tid; q < 64 * (kLsRows / 8); q += kLsThreads) {
+    const int b = q / (kLsRows / 8), c0 = 8 * (q % (kLsRows / 8));
+    if (b >= a.B || c0 >= ncolw) continue;
+    uint16_t* dst = out + static_cast<int64_t>(b) * a.ldo + nb + c0;
+    const uint16_t* srcp = ot + b * kLsOStride + c0;
+    if (a.vec_out && c0 + 8 <= ncolw) {
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(srcp);
+    } else {
+      for (int i = 0; i < min(8, ncolw - c0); ++i) dst[i] = srcp[i];
     }
   }
 }
