@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 8
+#define VSAMP_ABI_VERSION 9
 
 /* Bytes of one row's sampling state (vsamp_sample_states), an opaque record. */
 #define VSAMP_ROW_STATE_BYTES 40
@@ -273,6 +273,13 @@ int vsamp_sample_tile_pass(const vsamp_args* args, float* tile_max, void* stream
  * position_seed is the engine's per-token seed, sampler.py:44-47 (BLAKE2b-8 of
  * "<seed>:<position>", little-endian, top bit cleared); `uniforms` of vsamp_args takes these. */
 int vsamp_uniforms(const int64_t* seeds, const int64_t* positions, int32_t n, float* out);
+
+/* vsamp_uniforms on the device: seeds, positions and out are device memory; enqueued on `stream`
+ * (ABI version 9). The same function of (seed, position), bit for bit. For decode loops whose
+ * steps are replayed from a captured HIP graph: the host stages the positions, and the uniforms
+ * are computed by a node of the graph instead of on the host between two replays (the engine
+ * draws its per-token seeds on the host, sampler.py:44-47, one step at a time). */
+int vsamp_uniforms_device(const int64_t* seeds, const int64_t* positions, int32_t n, float* out, void* stream);
 
 /* Description of the last failure on this thread ("" if none). */
 const char* vsamp_last_error(void);

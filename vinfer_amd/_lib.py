@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 ROW_STATE_BYTES = 40
 
 VSAMP_BF16 = 0
@@ -33,6 +33,7 @@ EXPORTS = (
     "vsamp_probs",
     "vsamp_penalized_logits",
     "vsamp_uniforms",
+    "vsamp_uniforms_device",
     "vsamp_logprobs",
     "vsamp_logprobs_tiles",
     "vsamp_sample_tiles",
@@ -194,6 +195,9 @@ def load() -> ctypes.CDLL:
         lib.vsamp_lm_head.restype = ctypes.c_int
         lib.vsamp_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
         lib.vsamp_uniforms.restype = ctypes.c_int
+        lib.vsamp_uniforms_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
+                                              ctypes.c_void_p]
+        lib.vsamp_uniforms_device.restype = ctypes.c_int
         lib.vsamp_last_error.restype = ctypes.c_char_p
         version = lib.vsamp_abi_version()
         if version != ABI_VERSION:

@@ -729,6 +729,18 @@ int vsamp_uniforms(const int64_t* seeds, const int64_t* positions, int32_t n, fl
   return VSAMP_OK;
 }
 
+int vsamp_uniforms_device(const int64_t* seeds, const int64_t* positions, int32_t n, float* out, void* stream) {
+  g_err.clear();
+  if (n < 0) return fail(VSAMP_E_ARG, "n must be >= 0, got %d", n);
+  if (n == 0) return VSAMP_OK;
+  if (!seeds || !positions || !out) return fail(VSAMP_E_ARG, "seeds, positions and out must be set");
+  if (int rc = check_current_device()) return rc;
+  hipLaunchKernelGGL(vs_host::k_uniforms, dim3((n + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     seeds, positions, static_cast<int>(n), out);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_uniforms");
+}
+
 const char* vsamp_last_error(void) { return g_err.c_str(); }
 
 }  // extern "C"

@@ -1,4 +1,6 @@
-// Host code: the draw's uniform of (seed, position), for many rows per call.
+// The draw's uniform of (seed, position), for many rows per call: host code (vsamp_uniforms), and
+// the same functions compiled for the device (vsamp_uniforms_device, for loops whose steps are
+// replayed from a captured graph and cannot run host code between them).
 //
 // position_seed(seed, position) is BLAKE2b with an 8-byte digest of the ASCII text
 // "<seed>:<position>", read little-endian, top bit cleared (src/vinfer/runtime/sampler.py:44-47).
@@ -11,6 +13,8 @@
 #include <cstring>
 
 namespace vs_host {
+
+#define VS_HD __host__ __device__ __forceinline__
 
 constexpr uint64_t kBlakeIV[8] = {0x6A09E667F3BCC908ull, 0xBB67AE8584CAA73Bull, 0x3C6EF372FE94F82Bull,
                                   0xA54FF53A5F1D36F1ull, 0x510E527FADE682D1ull, 0x9B05688C2B3E6C1Full,
@@ -25,9 +29,9 @@ constexpr uint8_t kSigma[10][16] = {
     {6, 15, 14, 9, 11, 3, 0, 8, 12, 2, 13, 7, 1, 4, 10, 5}, {10, 2, 8, 4, 7, 6, 1, 5, 15, 11, 9, 14, 3, 12, 13, 0},
 };
 
-inline uint64_t rotr64(uint64_t x, int n) { return (x >> n) | (x << (64 - n)); }
+VS_HD uint64_t rotr64(uint64_t x, int n) { return (x >> n) | (x << (64 - n)); }
 
-inline void blake_mix(uint64_t* v, int a, int b, int c, int d, uint64_t x, uint64_t y) {
+VS_HD void blake_mix(uint64_t* v, int a, int b, int c, int d, uint64_t x, uint64_t y) {
   v[a] = v[a] + v[b] + x;
   v[d] = rotr64(v[d] ^ v[a], 32);
   v[c] = v[c] + v[d];
@@ -39,19 +43,23 @@ inline void blake_mix(uint64_t* v, int a, int b, int c, int d, uint64_t x, uint6
 }
 
 // The first 8 bytes (little-endian) of the 8-byte BLAKE2b digest of text[0, n), n <= 128.
-inline uint64_t blake2b_8(const char* text, int n) {
+// (The loops are unrolled: the tables are then indexed by constants on the device too.)
+VS_HD uint64_t blake2b_8(const char* text, int n) {
   uint64_t m[16] = {};
   std::memcpy(m, text, static_cast<size_t>(n));  // little-endian words, zero padded
   uint64_t h[8];
+#pragma unroll
   for (int i = 0; i < 8; ++i) h[i] = kBlakeIV[i];
   h[0] ^= 0x01010000ull ^ 8ull;  // depth 1, fanout 1, no key, 8-byte digest
   uint64_t v[16];
+#pragma unroll
   for (int i = 0; i < 8; ++i) {
     v[i] = h[i];
     v[i + 8] = kBlakeIV[i];
   }
   v[12] ^= static_cast<uint64_t>(n);  // bytes compressed (the high counter word stays 0)
   v[14] = ~v[14];                     // the last block
+#pragma unroll
   for (int r = 0; r < 12; ++r) {
     const uint8_t* s = kSigma[r % 10];
     blake_mix(v, 0, 4, 8, 12, m[s[0]], m[s[1]]);
@@ -67,7 +75,7 @@ inline uint64_t blake2b_8(const char* text, int n) {
 }
 
 // Decimal text of x at p; returns the characters written (at most 20).
-inline int put_decimal(char* p, uint64_t x) {
+VS_HD int put_decimal(char* p, uint64_t x) {
   char tmp[20];
   int n = 0;
   do {
@@ -78,7 +86,7 @@ inline int put_decimal(char* p, uint64_t x) {
   return n;
 }
 
-inline uint64_t position_seed(int64_t seed, int64_t position) {
+VS_HD uint64_t position_seed(int64_t seed, int64_t position) {
   char text[48];
   int n = 0;
   uint64_t s = static_cast<uint64_t>(seed);
@@ -97,15 +105,23 @@ inline uint64_t position_seed(int64_t seed, int64_t position) {
   return blake2b_8(text, n) & ((uint64_t(1) << 63) - 1);
 }
 
-inline uint64_t splitmix64(uint64_t x) {
+VS_HD uint64_t splitmix64(uint64_t x) {
   uint64_t z = x + 0x9E3779B97F4A7C15ull;
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
   z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
   return z ^ (z >> 31);
 }
 
-inline float position_uniform(int64_t seed, int64_t position) {
+VS_HD float position_uniform(int64_t seed, int64_t position) {
   return static_cast<float>(splitmix64(position_seed(seed, position)) >> 40) * 0x1p-24f;
+}
+
+#undef VS_HD
+
+// The device form: one thread per (seed, position) pair.
+__global__ __launch_bounds__(256) void k_uniforms(const int64_t* seeds, const int64_t* positions, int n, float* out) {
+  const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (i < n) out[i] = position_uniform(seeds[i], positions[i]);
 }
 
 }  // namespace vs_host

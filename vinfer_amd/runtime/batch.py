@@ -217,15 +217,18 @@ class _StepGraphs:
 class _SpecGraph:
     """A membership's captured speculative iteration: the inputs' copy (slots, last tokens, the
     token before each last one and its position, the draft steps' and the target's positions,
-    every uniform of the iteration), the draft model fed that earlier token (unless it keeps no
-    state), K draft steps and draws, the target's step, the verify, and its tokens and counts
-    copied to pinned memory (the counts last: the host polls them)."""
+    every uniform's position, or every uniform), the uniforms computed from their seeds and
+    positions (with a sampler that computes them on the device), the draft model fed that
+    earlier token (unless it keeps no state), K draft steps and draws, the target's step, the
+    verify, and its tokens and counts copied to pinned memory (the counts last: the host polls
+    them)."""
 
     key: tuple[int, ...]
     graph: object
     keep: list
     ints: np.ndarray  # int64 [4 + K + (K + 1), n]: slots, last, earlier token, its position, positions
-    u: np.ndarray  # float32 [(3K + 1) n]
+    u: np.ndarray | None  # float32 [(3K + 1) n], staged uniforms (host-computed)
+    upos: np.ndarray | None  # int64 [(3K + 1) n], staged positions of the uniforms (device-computed)
     useeds: np.ndarray  # int64 [(3K + 1) n]
     tokens_np: np.ndarray  # int32 [n, K + 1]
     counts_np: np.ndarray  # int32 [n]
@@ -896,14 +899,28 @@ class SpeculativeDecoder(BatchDecoder):
             s.draft_gap = None  # (the graph feeds every sequence the token before its last)
         return self._emit(seqs, tokens, counts, ready=not ahead)
 
-    def _spec_uniforms(self, gs: _SpecGraph, position: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
-        """Every uniform of an iteration at ``position`` (the next token's, per sequence): the
-        draft draws ([K, n]), acceptances and residuals ([n, K] each) and the bonus ([n])."""
+    def _spec_positions(self, position: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
+        """The uniforms' positions of an iteration at ``position`` (the next token's, per
+        sequence), in the order of ``_SpecGraph.useeds``: the draft draws ([K, n]), acceptances and
+        residuals ([n, K] each) and the bonus ([n])."""
         K = self.num_draft
+        n = position.shape[0]
+        out = np.empty((3 * K + 1) * n, np.int64) if out is None else out
         at = position[:, None] + np.arange(K, dtype=np.int64)[None, :]
-        upos = np.concatenate([-(4 * at.T + 1).ravel(), -(4 * at + 2).ravel(), -(4 * at + 3).ravel(),
-                               -(4 * (position + K) + 4)])
-        return position_uniforms(gs.useeds, upos, out=out)
+        nk = n * K
+        np.negative(4 * at.T + 1, out=out[:nk].reshape(K, n))
+        np.negative(4 * at + 2, out=out[nk:2 * nk].reshape(n, K))
+        np.negative(4 * at + 3, out=out[2 * nk:3 * nk].reshape(n, K))
+        np.negative(4 * (position + K) + 4, out=out[3 * nk:])
+        return out
+
+    def _spec_uniforms(self, gs: _SpecGraph, position: np.ndarray) -> None:
+        """Every uniform of an iteration at ``position`` into the graph's staging: their
+        positions when the graph computes them on the device, else the uniforms."""
+        if gs.upos is not None:
+            self._spec_positions(position, out=gs.upos)
+        else:
+            position_uniforms(gs.useeds, self._spec_positions(position), out=gs.u)
 
     def _launch_spec(self, gs: _SpecGraph) -> None:
         gs.counts_np[:] = -1  # (counts are >= 1)
@@ -946,7 +963,7 @@ class SpeculativeDecoder(BatchDecoder):
         ints[4:4 + K] = position[None, :] - 1 + np.arange(K, dtype=np.int64)[:, None]  # draft steps
         # the target's positions, sequence-major: token c of sequence b at b (K + 1) + c
         ints[4 + K:].reshape(-1)[:] = (position[:, None] - 1 + np.arange(K + 1, dtype=np.int64)[None, :]).reshape(-1)
-        self._spec_uniforms(gs, position, out=gs.u)
+        self._spec_uniforms(gs, position)
 
     def _capture_spec(self, key: tuple[int, ...], seqs: list[_Seq]) -> _SpecGraph:
         n = len(seqs)
@@ -955,21 +972,32 @@ class SpeculativeDecoder(BatchDecoder):
         g = self._group(seqs, dev)
         params = g.params
         rows = 4 + K + (K + 1)
-        st = _Staging(dev, 2 * rows * n + (3 * K + 1) * n + 8)
+        nu = (3 * K + 1) * n
+        # (the uniforms are computed in the graph from staged positions when the sampler can:
+        # host-computed uniforms would sit between the counts' arrival and the next replay)
+        dev_u = hasattr(self.sampler, "uniforms_device")
+        st = _Staging(dev, 2 * rows * n + 2 * nu + 8)
         at_i = st.reserve(2 * rows * n, align=2)
-        at_u = st.reserve((3 * K + 1) * n)
+        at_u = st.reserve(2 * nu if dev_u else nu, align=2)
         ints = st.host_view(at_i, 2 * rows * n).view(np.int64).reshape(rows, n)
-        u_host = st.host_view(at_u, (3 * K + 1) * n).view(np.float32)
+        u_host = None if dev_u else st.host_view(at_u, nu).view(np.float32)
+        upos_host = st.host_view(at_u, 2 * nu).view(np.int64) if dev_u else None
         ints[0] = g.slots
-        gs = _SpecGraph(key, None, [], ints, u_host,
-                        np.concatenate([np.tile(g.seeds, K), np.repeat(g.seeds, K), np.repeat(g.seeds, K), g.seeds]),
+        useeds = np.concatenate([np.tile(g.seeds, K), np.repeat(g.seeds, K), np.repeat(g.seeds, K), g.seeds])
+        gs = _SpecGraph(key, None, [], ints, u_host, upos_host, useeds,
                         np.zeros((n, K + 1), np.int32), np.zeros(n, np.int32))
         self._stage_spec(gs, seqs, None, None)
         d = st.device(at_i, 2 * rows * n).view(torch.int64).view(rows, n)
         slots, last, gtok, gpos = d[0], d[1], d[2], d[3]
         dpos = d[4:4 + K]  # [K, n]: the draft steps' positions
         tpos = d[4 + K:].reshape(-1)  # [n (K + 1)]: position of target token c of sequence b at b (K + 1) + c
-        ud = st.device(at_u, (3 * K + 1) * n).view(torch.float32)
+        if dev_u:
+            useeds_d = torch.from_numpy(useeds).to(dev)
+            upos_d = st.device(at_u, 2 * nu).view(torch.int64)
+            ud = torch.empty(nu, dtype=torch.float32, device=dev)
+        else:
+            useeds_d = upos_d = None
+            ud = st.device(at_u, nu).view(torch.float32)
         nk = n * K
         u_draft = ud[:nk].view(K, n)
         u_accept, u_residual, u_bonus = ud[nk:2 * nk].view(n, K), ud[2 * nk:3 * nk].view(n, K), ud[3 * nk:]
@@ -995,6 +1023,8 @@ class SpeculativeDecoder(BatchDecoder):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             st.dev[: st.n].copy_(st.host[: st.n], non_blocking=True)
+            if dev_u:
+                self.sampler.uniforms_device(useeds_d, upos_d, out=ud)
             if feed:
                 self.draft_model.decode(slots, gtok, gpos)
             toks[:, 0].copy_(last)
@@ -1032,7 +1062,7 @@ class SpeculativeDecoder(BatchDecoder):
             counts_host.copy_(counts, non_blocking=True)  # (after the tokens: the host polls these)
         torch.cuda.synchronize(dev)
         gs.graph = graph
-        gs.keep = [st, tokens_host, counts_host, toks, slots_rep, dbuf, tbuf]
+        gs.keep = [st, tokens_host, counts_host, toks, slots_rep, dbuf, tbuf, useeds_d, ud]
         gs.tokens_np = tokens_host.numpy()
         gs.counts_np = counts_host.numpy()
         return gs

@@ -359,6 +359,27 @@ class HipSampler:
         del keep
         return ids, states.view(torch.uint8).view(B, _lib.ROW_STATE_BYTES)
 
+    def uniforms_device(self, seeds: torch.Tensor, positions: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """The draw's uniforms of ``(seeds[i], positions[i])`` computed on the device
+        (``vsamp_uniforms_device``; the same values as ``sampling.uniform``, bit for bit), on the
+        current stream: int64 device tensors in, a float32 device tensor out. A decode loop
+        replaying its steps from a captured graph puts this in the graph and stages only the
+        positions."""
+        for name, t in (("seeds", seeds), ("positions", positions)):
+            if t.dtype != torch.int64 or t.device.type != "cuda" or t.dim() != 1 or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous 1-D int64 tensor on a GPU")
+        n = seeds.shape[0]
+        if positions.shape[0] != n or positions.device != seeds.device:
+            raise ValueError(f"positions must have {n} entries on {seeds.device}")
+        dev = seeds.device
+        if out is None:
+            out = torch.empty(n, dtype=torch.float32, device=dev)
+        elif out.dtype != torch.float32 or out.device != dev or out.dim() != 1 or out.shape[0] < n or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous float32 tensor of at least {n} entries on {dev}")
+        _lib.check(self._lib.vsamp_uniforms_device(seeds.data_ptr(), positions.data_ptr(), n, out.data_ptr(),
+                                                   self._stream(dev)))
+        return out
+
     def verify(self, target_logits, draft_logits, draft_tokens, params, u_accept, u_residual, u_bonus,
                draft_params=None, draft_states=None):
         if target_logits.dim() != 3 or draft_logits.dim() != 3:
