@@ -281,6 +281,24 @@ int vsamp_uniforms(const int64_t* seeds, const int64_t* positions, int32_t n, fl
  * draws its per-token seeds on the host, sampler.py:44-47, one step at a time). */
 int vsamp_uniforms_device(const int64_t* seeds, const int64_t* positions, int32_t n, float* out, void* stream);
 
+/* The inputs of a speculative decode loop's next iteration, advanced on the device (ABI version 9;
+ * no counterpart in the reference, whose loop runs one token at a time on the host,
+ * generate.py:105-146): for loops that replay each iteration from a captured HIP graph and queue
+ * the next replay before the host has read this one's tokens. `inputs` ([4 + 2 num_draft + 1, n]
+ * int64, row-major, device memory): slot; last token; the token before it; that token's
+ * position (position - 2, `position` being the next token's); the draft steps' positions
+ * (position - 1 + j, j < num_draft); the target's positions sequence-major (entry
+ * b (num_draft + 1) + c of the remaining rows: position - 1 + c). With `tokens` ([n, num_draft
+ * + 1] int32) and `counts` ([n] int32: sequence b emitted its first counts[b] tokens) the inputs
+ * move past that iteration (position += counts[b]); without them (both NULL) they stay. Either
+ * way `uniforms` (float32, (3 num_draft + 1) n) receives the iteration's draw uniforms from the
+ * sequences' `seeds` ([n] int64): the draft draws [num_draft, n] at positions -(4 (position + j)
+ * + 1), acceptances and residuals [n, num_draft] at -(4 (position + j) + 2) and -(4 (position +
+ * j) + 3), the bonus [n] at -(4 (position + num_draft) + 4), each as vsamp_uniforms computes it.
+ * num_draft <= 21. */
+int vsamp_spec_advance(int64_t* inputs, int32_t n, int32_t num_draft, const int32_t* tokens, const int32_t* counts,
+                       const int64_t* seeds, float* uniforms, void* stream);
+
 /* Description of the last failure on this thread ("" if none). */
 const char* vsamp_last_error(void);
 

@@ -34,6 +34,7 @@ EXPORTS = (
     "vsamp_penalized_logits",
     "vsamp_uniforms",
     "vsamp_uniforms_device",
+    "vsamp_spec_advance",
     "vsamp_logprobs",
     "vsamp_logprobs_tiles",
     "vsamp_sample_tiles",
@@ -198,6 +199,9 @@ def load() -> ctypes.CDLL:
         lib.vsamp_uniforms_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
                                               ctypes.c_void_p]
         lib.vsamp_uniforms_device.restype = ctypes.c_int
+        lib.vsamp_spec_advance.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.vsamp_spec_advance.restype = ctypes.c_int
         lib.vsamp_last_error.restype = ctypes.c_char_p
         version = lib.vsamp_abi_version()
         if version != ABI_VERSION:

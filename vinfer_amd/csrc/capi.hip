@@ -741,6 +741,23 @@ int vsamp_uniforms_device(const int64_t* seeds, const int64_t* positions, int32_
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_uniforms");
 }
 
+int vsamp_spec_advance(int64_t* inputs, int32_t n, int32_t num_draft, const int32_t* tokens, const int32_t* counts,
+                       const int64_t* seeds, float* uniforms, void* stream) {
+  g_err.clear();
+  if (n < 0) return fail(VSAMP_E_ARG, "n must be >= 0, got %d", n);
+  if (num_draft < 1 || 3 * num_draft + 1 > 64) return fail(VSAMP_E_ARG, "num_draft must be in [1, 21], got %d", num_draft);
+  if (n == 0) return VSAMP_OK;
+  if (!inputs || !seeds || !uniforms) return fail(VSAMP_E_ARG, "inputs, seeds and uniforms must be set");
+  if (!tokens != !counts) return fail(VSAMP_E_ARG, "tokens and counts are given together or not at all");
+  if (int rc = check_current_device()) return rc;
+  int G = 1;
+  while (G < 3 * num_draft + 1) G *= 2;
+  hipLaunchKernelGGL(vs_host::k_spec_advance, dim3((n * G + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     inputs, static_cast<int>(n), static_cast<int>(num_draft), G, tokens, counts, seeds, uniforms);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_spec_advance");
+}
+
 const char* vsamp_last_error(void) { return g_err.c_str(); }
 
 }  // extern "C"

@@ -124,4 +124,52 @@ __global__ __launch_bounds__(256) void k_uniforms(const int64_t* seeds, const in
   if (i < n) out[i] = position_uniform(seeds[i], positions[i]);
 }
 
+// A speculative decode loop's per-sequence inputs ([4 + 2K + 1, n] int64, row-major: slot, last
+// token, the token before it, that token's position (position - 2, with `position` the next
+// token's), the K draft steps' positions (position - 1 + j), the target's K + 1 positions
+// sequence-major (entry b (K + 1) + c of rows 4 + K ..: position - 1 + c)), advanced past one
+// iteration whose verified tokens and counts (c tokens of sequence b emitted: position += c) are
+// given, and the next iteration's 3K + 1 uniforms per sequence: draft draws [K, n] at -(4 (p + j)
+// + 1), acceptances and residuals [n, K] at -(4 (p + j) + 2) and -(4 (p + j) + 3), the bonus [n]
+// at -(4 (p + K) + 4), of the sequence's seed. Without counts the inputs stay and only the
+// uniforms are computed. A group of G lanes (the power of two >= 3K + 1, so a group never
+// straddles a wave) takes a sequence: every lane reads the position first, lane 0 then writes the
+// new inputs (in the same wave: its stores follow the group's loads).
+__global__ __launch_bounds__(256) void k_spec_advance(int64_t* inputs, int n, int K, int G, const int32_t* tokens,
+                                                      const int32_t* counts, const int64_t* seeds, float* uniforms) {
+  const int t = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  const int b = t / G, u = t % G;
+  if (b >= n) return;  // (whole groups)
+  const int64_t pos0 = inputs[3 * static_cast<int64_t>(n) + b] + 2;
+  const int c = counts ? counts[b] : 0;
+  const int64_t pos = pos0 + c;
+  if (u < 3 * K + 1) {
+    int64_t q;
+    int64_t at;
+    if (u < K) {
+      q = -(4 * (pos + u) + 1);
+      at = static_cast<int64_t>(u) * n + b;
+    } else if (u < 2 * K) {
+      q = -(4 * (pos + (u - K)) + 2);
+      at = static_cast<int64_t>(K) * n + static_cast<int64_t>(b) * K + (u - K);
+    } else if (u < 3 * K) {
+      q = -(4 * (pos + (u - 2 * K)) + 3);
+      at = 2 * static_cast<int64_t>(K) * n + static_cast<int64_t>(b) * K + (u - 2 * K);
+    } else {
+      q = -(4 * (pos + K) + 4);
+      at = 3 * static_cast<int64_t>(K) * n + b;
+    }
+    uniforms[at] = position_uniform(seeds[b], q);
+  }
+  if (counts && u == 0) {
+    const int32_t* tk = tokens + static_cast<int64_t>(b) * (K + 1);
+    const int64_t last = inputs[static_cast<int64_t>(n) + b];
+    inputs[static_cast<int64_t>(n) + b] = tk[c - 1];
+    inputs[2 * static_cast<int64_t>(n) + b] = c >= 2 ? static_cast<int64_t>(tk[c - 2]) : last;
+    inputs[3 * static_cast<int64_t>(n) + b] = pos - 2;
+    for (int j = 0; j < K; ++j) inputs[static_cast<int64_t>(4 + j) * n + b] = pos - 1 + j;
+    for (int j = 0; j <= K; ++j) inputs[static_cast<int64_t>(4 + K) * n + static_cast<int64_t>(b) * (K + 1) + j] = pos - 1 + j;
+  }
+}
+
 }  // namespace vs_host

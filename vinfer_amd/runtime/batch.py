@@ -215,23 +215,25 @@ class _StepGraphs:
 
 @dataclass(eq=False)
 class _SpecGraph:
-    """A membership's captured speculative iteration: the inputs' copy (slots, last tokens, the
-    token before each last one and its position, the draft steps' and the target's positions,
-    every uniform's position, or every uniform), the uniforms computed from their seeds and
-    positions (with a sampler that computes them on the device), the draft model fed that
-    earlier token (unless it keeps no state), K draft steps and draws, the target's step, the
-    verify, and its tokens and counts copied to pinned memory (the counts last: the host polls
-    them)."""
+    """A membership's captured speculative iteration, twice (the two captures differ only in the
+    pinned buffers their tokens and counts go to, so that two replays can be in flight): the draft
+    model fed the token before each last one (unless it keeps no state), K draft steps and draws,
+    the target's step, the verify, the next iteration's inputs and uniforms advanced on the
+    device from this one's tokens (``vsamp_spec_advance``), and the tokens and counts copied to
+    pinned memory (the counts last: the host polls them). The inputs live on the device between
+    replays; the host stages them only when a run of replays starts."""
 
     key: tuple[int, ...]
-    graph: object
+    graphs: list
     keep: list
-    ints: np.ndarray  # int64 [4 + K + (K + 1), n]: slots, last, earlier token, its position, positions
-    u: np.ndarray | None  # float32 [(3K + 1) n], staged uniforms (host-computed)
-    upos: np.ndarray | None  # int64 [(3K + 1) n], staged positions of the uniforms (device-computed)
-    useeds: np.ndarray  # int64 [(3K + 1) n]
-    tokens_np: np.ndarray  # int32 [n, K + 1]
-    counts_np: np.ndarray  # int32 [n]
+    st: object  # _Staging: the inputs' host words and their device copy
+    ints: np.ndarray  # int64 [4 + K + (K + 1), n] (host): slots, last, earlier token, its position, positions
+    ints_d: object  # the same words on the device (what the graphs read and advance)
+    seeds_d: object  # int64 [n]
+    ud: object  # float32 [(3K + 1) n]: the iteration's uniforms
+    tokens_np: list  # per capture: int32 [n, K + 1]
+    counts_np: list  # per capture: int32 [n]
+    next: int = 0  # the capture the next replay uses
 
 
 class BatchDecoder:
@@ -713,9 +715,9 @@ class SpeculativeDecoder(BatchDecoder):
         self._spec_graph: _SpecGraph | None = None
         self._spec_key: tuple[int, ...] | None = None  # the last membership and its run
         self._spec_run = 0
-        # (graphs) an iteration launched before the host took the previous one's tokens:
-        # (its graph, its sequences)
-        self._spec_inflight: tuple[_SpecGraph, list[_Seq]] | None = None
+        # (graphs) iterations launched before the host took their tokens, oldest first: (the
+        # graph, its capture, the sequences); at most two
+        self._spec_q: deque[tuple[_SpecGraph, int, list[_Seq]]] = deque()
 
     def submit(self, prompt_ids: list[int], params: SamplingParams) -> int:
         if penalized(params):
@@ -729,7 +731,7 @@ class SpeculativeDecoder(BatchDecoder):
 
     def step(self) -> list[tuple[int, Step]]:
         out: list[tuple[int, Step]] = []
-        if self._spec_inflight is not None:
+        if self._spec_q:
             out += self._take_inflight()
         else:
             spec = [s for s in self._ready if s.rid in self._running]
@@ -758,7 +760,7 @@ class SpeculativeDecoder(BatchDecoder):
         return out
 
     def _speculate(self, seqs: list[_Seq]) -> list[tuple[int, Step]]:
-        if self.graphs:
+        if self.graphs and hasattr(self.sampler, "spec_advance"):
             key = tuple(s.rid for s in seqs)
             if key == self._spec_key:
                 self._spec_run += 1
@@ -855,115 +857,77 @@ class SpeculativeDecoder(BatchDecoder):
     # ---- the iteration as a HIP graph -----------------------------------------------------------
     def _speculate_graph(self, key: tuple[int, ...], seqs: list[_Seq]) -> list[tuple[int, Step]]:
         """The iteration of a membership that held for ``graph_after`` iterations, replayed from a
-        HIP graph: the host stages the inputs, replays and polls the counts; then, while no
-        request waits for a free slot, it launches the next iteration on inputs derived from
-        these tokens before it runs this iteration's per-request logic, which then overlaps the
-        GPU's work. Every sequence's draft model is fed the token before its last one, at its
-        position (a sequence whose previous block was fully accepted needs it; for the others it
-        repeats a step already taken, which a model whose state is indexed by position, as the
-        loop's overwriting of rejected positions already assumes, takes unchanged; a draft model
-        without state is not fed)."""
+        HIP graph. The host stages the inputs from the sequences once; from then on each replay
+        advances them on the device for the next, so while the membership can hold (no request
+        waits for a free slot) the next iteration is queued before the host waits for this one,
+        and the host's per-request logic overlaps the GPU's work. Every sequence's draft model is
+        fed the token before its last one, at its position (a sequence whose previous block was
+        fully accepted needs it; for the others it repeats a step already taken, which a model
+        whose state is indexed by position, as the loop's overwriting of rejected positions
+        already assumes, takes unchanged; a draft model without state is not fed)."""
         gs = self._spec_graph
         if gs is None or gs.key != key:
             self._spec_graph = None  # (the old graph's memory goes back before the new capture)
             gs = self._spec_graph = self._capture_spec(key, seqs)
-        self._stage_spec(gs, seqs, None, None)
-        self._launch_spec(gs)
-        tokens, counts = self._wait_spec(gs)
-        return self._after_spec(gs, seqs, tokens, counts)
+        self._stage_spec(gs, seqs)
+        gs.st.send()
+        self.sampler.spec_advance(gs.ints_d, self.num_draft, gs.seeds_d, gs.ud)  # (this iteration's uniforms)
+        self._launch_spec(gs, seqs)
+        return self._take_inflight()
 
     def _take_inflight(self) -> list[tuple[int, Step]]:
-        """The iteration launched ahead by the previous step: its tokens for the sequences still
-        running (a sequence that ended meanwhile has its block dropped)."""
-        gs, seqs = self._spec_inflight
-        self._spec_inflight = None
-        tokens, counts = self._wait_spec(gs)
+        """The oldest iteration in flight: first the next one is queued when the membership can
+        hold (at most two in flight), then its tokens, for the sequences still running (a
+        sequence that ended meanwhile has its block dropped)."""
+        gs, buf, seqs = self._spec_q[0]
+        if (len(self._spec_q) == 1 and gs is self._spec_graph and not (self._waiting and self._free)
+                and not self._ready and all(s.rid in self._running for s in seqs)):
+            self._launch_spec(gs, seqs)
+        tokens, counts = self._wait_spec(gs, buf)
+        self._spec_q.popleft()
+        ready = not self._spec_q  # (else these sequences are in the iteration still in flight)
         alive = [s.rid in self._running for s in seqs]
-        if all(alive):
-            return self._after_spec(gs, seqs, tokens, counts)
-        keep = [i for i, a in enumerate(alive) if a]
-        live = [seqs[i] for i in keep]
-        for s in live:
-            s.draft_gap = None
-        return self._emit(live, [tokens[i] for i in keep], [counts[i] for i in keep])
-
-    def _after_spec(self, gs: _SpecGraph, seqs: list[_Seq], tokens: list[list[int]],
-                    counts: list[int]) -> list[tuple[int, Step]]:
-        """Launch the next iteration ahead when the membership can hold, then emit."""
-        ahead = not (self._waiting and self._free) and not self._ready
-        if ahead:
-            self._stage_spec(gs, seqs, tokens, counts)
-            self._launch_spec(gs)
-            self._spec_inflight = (gs, seqs)
+        if not all(alive):
+            keep = [i for i, a in enumerate(alive) if a]
+            seqs, tokens, counts = [seqs[i] for i in keep], [tokens[i] for i in keep], [counts[i] for i in keep]
         for s in seqs:
             s.draft_gap = None  # (the graph feeds every sequence the token before its last)
-        return self._emit(seqs, tokens, counts, ready=not ahead)
+        return self._emit(seqs, tokens, counts, ready=ready)
 
-    def _spec_positions(self, position: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
-        """The uniforms' positions of an iteration at ``position`` (the next token's, per
-        sequence), in the order of ``_SpecGraph.useeds``: the draft draws ([K, n]), acceptances and
-        residuals ([n, K] each) and the bonus ([n])."""
-        K = self.num_draft
-        n = position.shape[0]
-        out = np.empty((3 * K + 1) * n, np.int64) if out is None else out
-        at = position[:, None] + np.arange(K, dtype=np.int64)[None, :]
-        nk = n * K
-        np.negative(4 * at.T + 1, out=out[:nk].reshape(K, n))
-        np.negative(4 * at + 2, out=out[nk:2 * nk].reshape(n, K))
-        np.negative(4 * at + 3, out=out[2 * nk:3 * nk].reshape(n, K))
-        np.negative(4 * (position + K) + 4, out=out[3 * nk:])
-        return out
-
-    def _spec_uniforms(self, gs: _SpecGraph, position: np.ndarray) -> None:
-        """Every uniform of an iteration at ``position`` into the graph's staging: their
-        positions when the graph computes them on the device, else the uniforms."""
-        if gs.upos is not None:
-            self._spec_positions(position, out=gs.upos)
-        else:
-            position_uniforms(gs.useeds, self._spec_positions(position), out=gs.u)
-
-    def _launch_spec(self, gs: _SpecGraph) -> None:
-        gs.counts_np[:] = -1  # (counts are >= 1)
-        gs.graph.replay()
+    def _launch_spec(self, gs: _SpecGraph, seqs: list[_Seq]) -> None:
+        buf = gs.next
+        gs.next = 1 - buf
+        gs.counts_np[buf][:] = -1  # (counts are >= 1; this capture's last replay was read)
+        gs.graphs[buf].replay()
+        self._spec_q.append((gs, buf, seqs))
         self.graph_steps += 1
 
-    def _wait_spec(self, gs: _SpecGraph) -> tuple[list[list[int]], list[int]]:
+    def _wait_spec(self, gs: _SpecGraph, buf: int) -> tuple[list[list[int]], list[int]]:
+        counts = gs.counts_np[buf]
         spins = 0
-        while (gs.counts_np < 0).any():
+        while (counts < 0).any():
             spins += 1
             if spins == 1 << 20:  # (long past any iteration: the graph's end settles it)
                 torch.cuda.current_stream(self.model.device).synchronize()
-                if (gs.counts_np < 0).any():
+                if (counts < 0).any():
                     raise RuntimeError("the verified tokens never reached the host")
-        return gs.tokens_np.tolist(), gs.counts_np.tolist()
+        return gs.tokens_np[buf].tolist(), counts.tolist()
 
-    def _stage_spec(self, gs: _SpecGraph, seqs: list[_Seq], tokens, counts) -> None:
-        """An iteration's inputs into the graph's pinned staging words (the graph's first node
-        copies them to the device): from the sequences as they stand, or, with ``tokens`` and
-        ``counts`` of an iteration whose per-request logic has not run yet, as they stand after
-        it."""
+    def _stage_spec(self, gs: _SpecGraph, seqs: list[_Seq]) -> None:
+        """An iteration's inputs, from the sequences as they stand, into the graph's pinned
+        staging words (sent to the device before a run of replays starts)."""
         n = len(seqs)
         K = self.num_draft
         ints = gs.ints
-        if tokens is None:
-            position = np.fromiter((s.position for s in seqs), np.int64, n)
-            ints[1] = np.fromiter((s.generated[-1] for s in seqs), np.int64, n)
-            # the token at position - 2: the second-to-last generated one, or the prompt's last
-            ints[2] = np.fromiter((s.generated[-2] if len(s.generated) >= 2 else s.prompt[-1] for s in seqs),
-                                  np.int64, n)
-        else:
-            c = np.asarray(counts, dtype=np.int64)
-            tk = np.asarray(tokens, dtype=np.int64)
-            rows = np.arange(n)
-            position = np.fromiter((s.position for s in seqs), np.int64, n) + c
-            ints[1] = tk[rows, c - 1]
-            last = np.fromiter((s.generated[-1] for s in seqs), np.int64, n)
-            ints[2] = np.where(c >= 2, tk[rows, np.maximum(c - 2, 0)], last)
+        position = np.fromiter((s.position for s in seqs), np.int64, n)
+        ints[1] = np.fromiter((s.generated[-1] for s in seqs), np.int64, n)
+        # the token at position - 2: the second-to-last generated one, or the prompt's last
+        ints[2] = np.fromiter((s.generated[-2] if len(s.generated) >= 2 else s.prompt[-1] for s in seqs),
+                              np.int64, n)
         ints[3] = position - 2
         ints[4:4 + K] = position[None, :] - 1 + np.arange(K, dtype=np.int64)[:, None]  # draft steps
         # the target's positions, sequence-major: token c of sequence b at b (K + 1) + c
         ints[4 + K:].reshape(-1)[:] = (position[:, None] - 1 + np.arange(K + 1, dtype=np.int64)[None, :]).reshape(-1)
-        self._spec_uniforms(gs, position)
 
     def _capture_spec(self, key: tuple[int, ...], seqs: list[_Seq]) -> _SpecGraph:
         n = len(seqs)
@@ -972,37 +936,21 @@ class SpeculativeDecoder(BatchDecoder):
         g = self._group(seqs, dev)
         params = g.params
         rows = 4 + K + (K + 1)
-        nu = (3 * K + 1) * n
-        # (the uniforms are computed in the graph from staged positions when the sampler can:
-        # host-computed uniforms would sit between the counts' arrival and the next replay)
-        dev_u = hasattr(self.sampler, "uniforms_device")
-        st = _Staging(dev, 2 * rows * n + 2 * nu + 8)
+        st = _Staging(dev, 2 * rows * n + 8)
         at_i = st.reserve(2 * rows * n, align=2)
-        at_u = st.reserve(2 * nu if dev_u else nu, align=2)
         ints = st.host_view(at_i, 2 * rows * n).view(np.int64).reshape(rows, n)
-        u_host = None if dev_u else st.host_view(at_u, nu).view(np.float32)
-        upos_host = st.host_view(at_u, 2 * nu).view(np.int64) if dev_u else None
         ints[0] = g.slots
-        useeds = np.concatenate([np.tile(g.seeds, K), np.repeat(g.seeds, K), np.repeat(g.seeds, K), g.seeds])
-        gs = _SpecGraph(key, None, [], ints, u_host, upos_host, useeds,
-                        np.zeros((n, K + 1), np.int32), np.zeros(n, np.int32))
-        self._stage_spec(gs, seqs, None, None)
-        d = st.device(at_i, 2 * rows * n).view(torch.int64).view(rows, n)
-        slots, last, gtok, gpos = d[0], d[1], d[2], d[3]
-        dpos = d[4:4 + K]  # [K, n]: the draft steps' positions
-        tpos = d[4 + K:].reshape(-1)  # [n (K + 1)]: position of target token c of sequence b at b (K + 1) + c
-        if dev_u:
-            useeds_d = torch.from_numpy(useeds).to(dev)
-            upos_d = st.device(at_u, 2 * nu).view(torch.int64)
-            ud = torch.empty(nu, dtype=torch.float32, device=dev)
-        else:
-            useeds_d = upos_d = None
-            ud = st.device(at_u, nu).view(torch.float32)
+        ints_d = st.device(at_i, 2 * rows * n).view(torch.int64).view(rows, n)
+        seeds_d = torch.from_numpy(g.seeds).to(dev)
+        ud = torch.empty((3 * K + 1) * n, dtype=torch.float32, device=dev)
+        gs = _SpecGraph(key, [], [], st, ints, ints_d, seeds_d, ud, [], [])
+        self._stage_spec(gs, seqs)
+        slots, last, gtok, gpos = ints_d[0], ints_d[1], ints_d[2], ints_d[3]
+        dpos = ints_d[4:4 + K]  # [K, n]: the draft steps' positions
+        tpos = ints_d[4 + K:].reshape(-1)  # [n (K + 1)]: position of target token c of sequence b at b (K + 1) + c
         nk = n * K
         u_draft = ud[:nk].view(K, n)
         u_accept, u_residual, u_bonus = ud[nk:2 * nk].view(n, K), ud[2 * nk:3 * nk].view(n, K), ud[3 * nk:]
-        tokens_host = torch.empty(n, K + 1, dtype=torch.int32, pin_memory=True)
-        counts_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
         with_states = hasattr(self.sampler, "sample_states")
         extend = getattr(self.model, "extend", None)
         draft_into = getattr(self.draft_model, "decode_into", None)
@@ -1012,6 +960,7 @@ class SpeculativeDecoder(BatchDecoder):
         # first step, so a model with state sees nothing it would not see anyway), then the
         # buffers the graph writes the draft and target logits into.
         st.send()
+        self.sampler.spec_advance(ints_d, K, seeds_d, ud)
         probe = self.draft_model.decode(slots, gtok, gpos)
         vocab, ldt = int(probe.shape[-1]), probe.dtype
         del probe
@@ -1020,49 +969,57 @@ class SpeculativeDecoder(BatchDecoder):
         toks = torch.empty(n, K + 1, dtype=torch.int64, device=dev)  # the last token, then the drafts
         slots_rep = slots.repeat_interleave(K + 1) if extend is None else None  # (fixed per membership)
         torch.cuda.synchronize(dev)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            st.dev[: st.n].copy_(st.host[: st.n], non_blocking=True)
-            if dev_u:
-                self.sampler.uniforms_device(useeds_d, upos_d, out=ud)
-            if feed:
-                self.draft_model.decode(slots, gtok, gpos)
-            toks[:, 0].copy_(last)
-            x = last
-            draft_rows, states = [], []
-            for j in range(K):
-                if dbuf is not None:
-                    draft_into(slots, x, dpos[j], dbuf[:, j])
-                    logits = dbuf[:, j]
+        pool = None
+        outs = []
+        for _ in range(2):
+            tokens_host = torch.empty(n, K + 1, dtype=torch.int32, pin_memory=True)
+            counts_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+            graph = torch.cuda.CUDAGraph()
+            # (the two captures share a memory pool: they are replayed one after the other on one
+            # stream, never at once)
+            with torch.cuda.graph(graph, pool=pool):
+                if feed:
+                    self.draft_model.decode(slots, gtok, gpos)
+                toks[:, 0].copy_(last)
+                x = last
+                draft_rows, states = [], []
+                for j in range(K):
+                    if dbuf is not None:
+                        draft_into(slots, x, dpos[j], dbuf[:, j])
+                        logits = dbuf[:, j]
+                    else:
+                        logits = self.draft_model.decode(slots, x, dpos[j])
+                        draft_rows.append(logits)
+                    if with_states:
+                        ids, state = self.sampler.sample_states(logits, params, u_draft[j])
+                        states.append(state)
+                    else:
+                        ids, _ = self.sampler.sample_batch(logits, params, u_draft[j])
+                    toks[:, j + 1].copy_(ids)
+                    x = toks[:, j + 1]
+                dl = dbuf if dbuf is not None else torch.stack(draft_rows, dim=1)
+                if extend is not None:
+                    target = extend(slots, toks, dpos[0])
                 else:
-                    logits = self.draft_model.decode(slots, x, dpos[j])
-                    draft_rows.append(logits)
-                if with_states:
-                    ids, state = self.sampler.sample_states(logits, params, u_draft[j])
-                    states.append(state)
-                else:
-                    ids, _ = self.sampler.sample_batch(logits, params, u_draft[j])
-                toks[:, j + 1].copy_(ids)
-                x = toks[:, j + 1]
-            dl = dbuf if dbuf is not None else torch.stack(draft_rows, dim=1)
-            if extend is not None:
-                target = extend(slots, toks, dpos[0])
-            else:
-                tt = toks.reshape(-1)
-                if tbuf is not None:
-                    target_into(slots_rep, tt, tpos, tbuf.view(n * (K + 1), vocab))
-                    target = tbuf
-                else:
-                    target = self.model.decode(slots_rep, tt, tpos).view(n, K + 1, -1)
-            tokens, counts = self.sampler.verify(
-                target, dl, toks[:, 1:], params, u_accept, u_residual, u_bonus,
-                draft_states=torch.stack(states, dim=1) if with_states else None,
-            )
-            tokens_host.copy_(tokens, non_blocking=True)
-            counts_host.copy_(counts, non_blocking=True)  # (after the tokens: the host polls these)
-        torch.cuda.synchronize(dev)
-        gs.graph = graph
-        gs.keep = [st, tokens_host, counts_host, toks, slots_rep, dbuf, tbuf, useeds_d, ud]
-        gs.tokens_np = tokens_host.numpy()
-        gs.counts_np = counts_host.numpy()
+                    tt = toks.reshape(-1)
+                    if tbuf is not None:
+                        target_into(slots_rep, tt, tpos, tbuf.view(n * (K + 1), vocab))
+                        target = tbuf
+                    else:
+                        target = self.model.decode(slots_rep, tt, tpos).view(n, K + 1, -1)
+                tokens, counts = self.sampler.verify(
+                    target, dl, toks[:, 1:], params, u_accept, u_residual, u_bonus,
+                    draft_states=torch.stack(states, dim=1) if with_states else None,
+                )
+                # the next iteration's inputs and uniforms, then the tokens and counts to the host
+                self.sampler.spec_advance(ints_d, K, seeds_d, ud, tokens, counts)
+                tokens_host.copy_(tokens, non_blocking=True)
+                counts_host.copy_(counts, non_blocking=True)  # (after the tokens: the host polls these)
+            torch.cuda.synchronize(dev)
+            pool = graph.pool()
+            gs.graphs.append(graph)
+            gs.tokens_np.append(tokens_host.numpy())
+            gs.counts_np.append(counts_host.numpy())
+            outs += [tokens_host, counts_host]
+        gs.keep = [toks, slots_rep, dbuf, tbuf, *outs]
         return gs

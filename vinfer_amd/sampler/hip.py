@@ -380,6 +380,34 @@ class HipSampler:
                                                    self._stream(dev)))
         return out
 
+    def spec_advance(self, inputs: torch.Tensor, num_draft: int, seeds: torch.Tensor, uniforms: torch.Tensor,
+                     tokens: torch.Tensor | None = None, counts: torch.Tensor | None = None) -> None:
+        """A speculative loop's next-iteration inputs and uniforms on the device, in place
+        (``vsamp_spec_advance``): ``inputs`` int64 ``[4 + 2 K + 1, n]`` (slot, last token, the
+        token before it, its position, the draft steps' and the target's positions), moved past
+        the iteration whose verified ``tokens`` ``[n, K + 1]`` and ``counts`` ``[n]`` (int32) are
+        given (none: they stay), and ``uniforms`` float32 ``[(3K + 1) n]`` from ``seeds`` int64
+        ``[n]``, on the current stream."""
+        K = int(num_draft)
+        if inputs.dtype != torch.int64 or inputs.dim() != 2 or inputs.shape[0] != 4 + 2 * K + 1 or not inputs.is_contiguous():
+            raise ValueError(f"inputs must be a contiguous int64 [{4 + 2 * K + 1}, n] tensor")
+        n = inputs.shape[1]
+        dev = inputs.device
+        if seeds.dtype != torch.int64 or seeds.shape != (n,) or seeds.device != dev or not seeds.is_contiguous():
+            raise ValueError(f"seeds must be a contiguous int64 [{n}] tensor on {dev}")
+        if uniforms.dtype != torch.float32 or uniforms.numel() < (3 * K + 1) * n or uniforms.device != dev or not uniforms.is_contiguous():
+            raise ValueError(f"uniforms must be a contiguous float32 tensor of {(3 * K + 1) * n} entries on {dev}")
+        if (tokens is None) != (counts is None):
+            raise ValueError("tokens and counts are given together or not at all")
+        if tokens is not None:
+            if tokens.dtype != torch.int32 or tokens.shape != (n, K + 1) or not tokens.is_contiguous() or tokens.device != dev:
+                raise ValueError(f"tokens must be a contiguous int32 [{n}, {K + 1}] tensor on {dev}")
+            if counts.dtype != torch.int32 or counts.shape != (n,) or not counts.is_contiguous() or counts.device != dev:
+                raise ValueError(f"counts must be a contiguous int32 [{n}] tensor on {dev}")
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        _lib.check(self._lib.vsamp_spec_advance(inputs.data_ptr(), n, K, ptr(tokens), ptr(counts), seeds.data_ptr(),
+                                                uniforms.data_ptr(), self._stream(dev)))
+
     def verify(self, target_logits, draft_logits, draft_tokens, params, u_accept, u_residual, u_bonus,
                draft_params=None, draft_states=None):
         if target_logits.dim() != 3 or draft_logits.dim() != 3:
