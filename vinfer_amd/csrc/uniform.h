@@ -4,13 +4,13 @@
 //
 // position_seed(seed, position) is BLAKE2b with an 8-byte digest of the ASCII text
 // "<seed>:<position>", read little-endian, top bit cleared (src/vinfer/runtime/sampler.py:44-47).
-// BLAKE2b here follows RFC 7693 (unkeyed, one 128-byte block: the text is at most 41 bytes).
+// BLAKE2b here follows RFC 7693 (unkeyed, one 128-byte block: the text is at most 41 bytes,
+// built into registers: no byte array, so the device code needs no scratch memory).
 // The uniform is then the top 24 bits of the SplitMix64 output function (Steele, Lea, Flood
 // 2014) of that seed, times 2^-24: a multiple of 2^-24 in [0, 1), exact in fp32.
 #pragma once
 
 #include <cstdint>
-#include <cstring>
 
 namespace vs_host {
 
@@ -42,11 +42,13 @@ VS_HD void blake_mix(uint64_t* v, int a, int b, int c, int d, uint64_t x, uint64
   v[b] = rotr64(v[b] ^ v[c], 63);
 }
 
-// The first 8 bytes (little-endian) of the 8-byte BLAKE2b digest of text[0, n), n <= 128.
-// (The loops are unrolled: the tables are then indexed by constants on the device too.)
-VS_HD uint64_t blake2b_8(const char* text, int n) {
-  uint64_t m[16] = {};
-  std::memcpy(m, text, static_cast<size_t>(n));  // little-endian words, zero padded
+// The first 8 bytes (little-endian) of the 8-byte BLAKE2b digest of a text of n <= 48 bytes held
+// as six little-endian words (zero past the text). The loops are unrolled: the tables are then
+// indexed by constants and the message words are registers, on the device too.
+VS_HD uint64_t blake2b_8(const uint64_t (&t)[6], int n) {
+  uint64_t m[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) m[i] = i < 6 ? t[i] : 0ull;
   uint64_t h[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) h[i] = kBlakeIV[i];
@@ -74,35 +76,63 @@ VS_HD uint64_t blake2b_8(const char* text, int n) {
   return h[0] ^ v[0] ^ v[8];
 }
 
-// Decimal text of x at p; returns the characters written (at most 20).
-VS_HD int put_decimal(char* p, uint64_t x) {
-  char tmp[20];
-  int n = 0;
-  do {
-    tmp[n++] = static_cast<char>('0' + x % 10);
-    x /= 10;
-  } while (x);
-  for (int i = 0; i < n; ++i) p[i] = tmp[n - 1 - i];
-  return n;
+// A text built byte by byte into six little-endian words: the open word `acc` takes the next
+// byte at `k`; a full word goes to word `nw` (selected, so the words stay registers).
+struct TextWords {
+  uint64_t w[6] = {0, 0, 0, 0, 0, 0};
+  uint64_t acc = 0;
+  int k = 0, nw = 0;
+  VS_HD void put(uint32_t c) {
+    acc |= static_cast<uint64_t>(c) << (8 * k);
+    if (++k == 8) {
+#pragma unroll
+      for (int i = 0; i < 6; ++i) w[i] = nw == i ? acc : w[i];
+      acc = 0;
+      k = 0;
+      ++nw;
+    }
+  }
+  VS_HD int finish() {  // the open word in place; returns the length
+#pragma unroll
+    for (int i = 0; i < 6; ++i) w[i] = nw == i ? acc : w[i];
+    return 8 * nw + k;
+  }
+};
+
+constexpr uint64_t kPow10[20] = {1ull, 10ull, 100ull, 1000ull, 10000ull, 100000ull, 1000000ull, 10000000ull,
+                                 100000000ull, 1000000000ull, 10000000000ull, 100000000000ull, 1000000000000ull,
+                                 10000000000000ull, 100000000000000ull, 1000000000000000ull, 10000000000000000ull,
+                                 100000000000000000ull, 1000000000000000000ull, 10000000000000000000ull};
+
+// The decimal text of x (no leading zeros; "0" for 0), most significant digit first.
+VS_HD void put_decimal(TextWords& t, uint64_t x) {
+  bool started = false;
+#pragma unroll
+  for (int i = 19; i >= 0; --i) {
+    const uint64_t d = x / kPow10[i];
+    x -= d * kPow10[i];
+    started = started || d != 0 || i == 0;
+    if (started) t.put('0' + static_cast<uint32_t>(d));
+  }
 }
 
 VS_HD uint64_t position_seed(int64_t seed, int64_t position) {
-  char text[48];
-  int n = 0;
+  TextWords t;
   uint64_t s = static_cast<uint64_t>(seed);
   if (seed < 0) {
-    text[n++] = '-';
+    t.put('-');
     s = 0 - s;  // magnitude, also for INT64_MIN
   }
-  n += put_decimal(text + n, s);
-  text[n++] = ':';
+  put_decimal(t, s);
+  t.put(':');
   uint64_t p = static_cast<uint64_t>(position);
   if (position < 0) {
-    text[n++] = '-';
+    t.put('-');
     p = 0 - p;
   }
-  n += put_decimal(text + n, p);
-  return blake2b_8(text, n) & ((uint64_t(1) << 63) - 1);
+  put_decimal(t, p);
+  const int n = t.finish();  // (at most 41 bytes)
+  return blake2b_8(t.w, n) & ((uint64_t(1) << 63) - 1);
 }
 
 VS_HD uint64_t splitmix64(uint64_t x) {
