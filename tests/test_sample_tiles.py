@@ -180,10 +180,11 @@ def test_gpu_sample_tiles_rejects_bad_arguments():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("B,V,pad,offset", [(1, 151936, 0, 0), (3, 4099, 5, 0), (8, 151936, 0, 3), (16, 20000, 0, 0),
-                                            (2, 100, 0, 1)])
+                                            (2, 100, 0, 1), (16, 151936, 0, 0), (13, 151936, 0, 1)])
 def test_gpu_tile_pass_equals_sample_batch(B, V, pad, offset):
-    # bf16 logits from any source: the tile maxima come from their own launch (rows unaligned
-    # when offset is odd: the maxima kernel then reads them element by element)
+    # bf16 logits from any source: the tile maxima computed by the same launch while B times the
+    # workgroups per row fits one round on the CUs (B <= 13 at V = 151936), else by their own
+    # launch first (rows unaligned when offset is odd: the maxima are read element by element)
     g = torch.Generator().manual_seed(B * 7 + V)
     rng = np.random.default_rng(V + B)
     x = torch.randn(B, V, generator=g) * 2.0
@@ -204,6 +205,8 @@ def test_gpu_tile_pass_equals_sample_batch(B, V, pad, offset):
     a, ap = s.sample_tile_pass(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
     b, bp = s.sample_batch(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
     torch.cuda.synchronize()
+    # (small batches run one launch whose rows' last workgroups reset the arrival words)
+    assert not s._local.tiles[DEV][1].any()
     assert torch.equal(a.cpu(), b.cpu())
     assert torch.equal(ap.cpu().view(torch.int32), bp.cpu().view(torch.int32))
     w = Workload("tile pass", logits.cpu(), pp, u, hi, ho, draft)

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 ROW_STATE_BYTES = 40
 
 VSAMP_BF16 = 0
@@ -190,7 +190,8 @@ def load() -> ctypes.CDLL:
         lib.vsamp_logprobs_tiles.restype = ctypes.c_int
         lib.vsamp_sample_tiles.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p, ctypes.c_void_p]
         lib.vsamp_sample_tiles.restype = ctypes.c_int
-        lib.vsamp_sample_tile_pass.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p, ctypes.c_void_p]
+        lib.vsamp_sample_tile_pass.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p]
         lib.vsamp_sample_tile_pass.restype = ctypes.c_int
         lib.vsamp_lm_head.argtypes = [ctypes.POINTER(VsampLmHeadArgs), ctypes.c_void_p]
         lib.vsamp_lm_head.restype = ctypes.c_int

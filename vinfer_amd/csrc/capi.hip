@@ -262,7 +262,8 @@ int launch_penalties(const vs::PenaltyArgs& p, int B, hipStream_t st) {
 
 template <class Tin>
 int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStream_t st,
-               vs::RowState* state = nullptr, int param_div = 1, const float* tile_max = nullptr) {
+               vs::RowState* state = nullptr, int param_div = 1, const float* tile_max = nullptr,
+               uint32_t* tile_arrive = nullptr, int tile_G = 1) {
   const bool pen = wants_penalties(a);
   if (state && pen) return fail(VSAMP_E_ARG, "row states are written without penalties only");
   if ((a->flags & VSAMP_HIST_APPEND) && (state || probs))
@@ -298,10 +299,13 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
   if (tile_max) {  // (bf16 rows with the LM head's tile maxima: no split rows, no states)
     s.tile_max = tile_max;
     s.nT = (a->vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
+    s.tile_arrive = tile_arrive;  // (set: tile_G workgroups per row compute the maxima first)
+    s.tile_G = tile_G;
+    const dim3 grid(a->batch * (tile_arrive ? tile_G : 1));
     if (pen)
-      hipLaunchKernelGGL((vs::k_sample<Tin, true, false, false, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
+      hipLaunchKernelGGL((vs::k_sample<Tin, true, false, false, true>), grid, dim3(vs::kThreads), 0, st, s);
     else
-      hipLaunchKernelGGL((vs::k_sample<Tin, false, false, false, true>), dim3(a->batch), dim3(vs::kThreads), 0, st, s);
+      hipLaunchKernelGGL((vs::k_sample<Tin, false, false, false, true>), grid, dim3(vs::kThreads), 0, st, s);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_sample (tile maxima)");
   }
@@ -405,15 +409,23 @@ int vsamp_sample_tiles(const vsamp_args* a, const float* tile_max, void* stream)
   return run_sample<uint16_t>(a, nullptr, 0, static_cast<hipStream_t>(stream), nullptr, 1, tile_max);
 }
 
-int vsamp_sample_tile_pass(const vsamp_args* a, float* tile_max, void* stream) {
+int vsamp_sample_tile_pass(const vsamp_args* a, float* tile_max, uint32_t* arrive, void* stream) {
   g_err.clear();
   if (int rc = validate(a, true)) return rc;
   if (a->dtype != VSAMP_BF16) return fail(VSAMP_E_DTYPE, "vsamp_sample_tile_pass takes bf16 logits");
   if (a->batch == 0) return VSAMP_OK;
-  if (!tile_max) return fail(VSAMP_E_ARG, "tile_max is NULL");
+  if (!tile_max || !arrive) return fail(VSAMP_E_ARG, "tile_max and arrive must be set");
+  if ((reinterpret_cast<uintptr_t>(tile_max) | reinterpret_cast<uintptr_t>(arrive)) & 3u)
+    return fail(VSAMP_E_ARG, "tile_max and arrive must be 4-byte aligned");
   if (int rc = check_current_device()) return rc;
   const int nT = (a->vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // One launch while the rows' workgroups fit one round on the CUs: G per row, each the maxima of
+  // at most 64 tiles (one 16-byte load per thread), the last of a row's G finishing it; larger
+  // batches take a launch of the maxima first (256-thread workgroups), then the draw.
+  const int G = (nT + 63) / 64;
+  if (static_cast<int64_t>(a->batch) * G <= vs::kTileFusedWorkgroups)
+    return run_sample<uint16_t>(a, nullptr, 0, st, nullptr, 1, tile_max, arrive, G);
   hipLaunchKernelGGL(vs::k_tile_max, dim3((nT + vs::kTilesPerBlock - 1) / vs::kTilesPerBlock, a->batch),
                      dim3(vs::kTileMaxThreads), 0, st, static_cast<const uint16_t*>(a->logits), a->row_stride,
                      a->vocab, nT, tile_max);

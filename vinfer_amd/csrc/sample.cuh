@@ -73,6 +73,10 @@ struct SampleArgs {
   // (vsamp_sample_tiles) the rows' tile maxima [B, nT], one per kStatTile logits
   const float* tile_max;
   int nT;
+  // (vsamp_sample_tile_pass, one launch) tile_G workgroups per row compute the maxima, and the
+  // last to count itself in at the row's arrival word (zero between launches) finishes the row
+  uint32_t* tile_arrive;
+  int tile_G;
 };
 
 // The row of this workgroup.
@@ -2927,6 +2931,7 @@ __device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk,
 // NaN is the largest; -0.0 and +0.0 are one value). Sixteen lanes take a tile, eight logits a
 // lane, and reduce over their 16-lane row; grid (ceil(nT / 16), B) of 256-thread workgroups, so
 // even one row spreads over the chip.
+constexpr int kTileFusedWorkgroups = 256;  // (one round on the CUs; vsamp_sample_tile_pass)
 constexpr int kTileMaxThreads = 256;
 constexpr int kTilesPerBlock = kTileMaxThreads / 16;
 __global__ __launch_bounds__(kTileMaxThreads) void k_tile_max(const uint16_t* logits, int64_t stride, int V,
@@ -2958,6 +2963,54 @@ __global__ __launch_bounds__(kTileMaxThreads) void k_tile_max(const uint16_t* lo
   if (t < nT && l16 == 0) as_global(out)[static_cast<int64_t>(r) * nT + t] = val_of(mk);
 }
 
+// (the fused tile pass) Workgroup g of row r's G computes the maxima of tiles g * per .. (per =
+// ceil(nT / G), at most 64: one 16-byte load per thread), sixteen lanes a tile as k_tile_max, into
+// a.tile_max with device-coherent stores; waits for them; then thread 0 counts the workgroup in
+// at the row's arrival word. The last of the G resets the word to 0 (nothing else touches it in
+// this launch) and returns true: it finishes the row, the others return false and exit. `flag`
+// is an LDS word.
+__device__ __forceinline__ bool tile_share(const SampleArgs& a, int r, int g, int* flag) {
+  const int G = a.tile_G, nT = a.nT;
+  const int per = (nT + G - 1) / G;
+  const int t = g * per + static_cast<int>(threadIdx.x >> 4);  // (the same in a 16-lane row)
+  const int l16 = threadIdx.x & 15;
+  const uint16_t* row = as_global(static_cast<const uint16_t*>(a.logits)) + static_cast<int64_t>(r) * a.stride;
+  const int V = a.V;
+  uint32_t mk = 0;  // (below every key)
+  const bool mine = t < nT && t < (g + 1) * per;
+  if (mine) {
+    const int i0 = t * kStatTile + 8 * l16;
+    if ((reinterpret_cast<uintptr_t>(row + i0) & 15u) == 0 && i0 + 8 <= V) {
+      const uint4 q = ld_global_u4(reinterpret_cast<const uint4*>(row + i0));
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        mk = max(mk, key_of(__uint_as_float(w[i] << 16)));
+        mk = max(mk, key_of(__uint_as_float(w[i] & 0xFFFF0000u)));
+      }
+    } else {
+      for (int i = i0; i < i0 + 8 && i < V; ++i) mk = max(mk, key_of(bf16_to_f32(ld_global(row + i))));
+    }
+  }
+  auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  mk = umax(mk, dpp::mov<dpp::kXor1>(mk));
+  mk = umax(mk, dpp::mov<dpp::kXor2>(mk));
+  mk = umax(mk, dpp::mov<dpp::kHalfMirror>(mk));
+  mk = umax(mk, dpp::mov<dpp::kMirror>(mk));
+  if (mine && l16 == 0) st_dev<float>(const_cast<float*>(a.tile_max) + static_cast<int64_t>(r) * nT + t, val_of(mk));
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // (every thread's stores have completed)
+  if (threadIdx.x == 0) {
+    uint32_t* word = a.tile_arrive + r;
+    const uint32_t old = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == static_cast<uint32_t>(G - 1);
+    if (last) st_dev<uint32_t>(word, 0u);
+    *flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  return *flag != 0;
+}
+
 // Returns true when the row was decided (outputs written) from its tile maxima; false, having
 // written nothing, when it needs the row passes. Every thread calls; `p.u` is clamped to >= 0.
 template <bool PEN>
@@ -2981,7 +3034,7 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = tid + i * kThreads;
-    mt[i] = t < nT ? ld_global(tm + t) : -INFINITY;
+    mt[i] = t < nT ? ld_dev(tm + t) : -INFINITY;  // (device-coherent: other workgroups of a fused pass wrote them)
     kt[i] = t < nT ? key_of(mt[i]) : 0u;  // (0: below every key)
     mk = kt[i] > mk ? kt[i] : mk;
   }
@@ -3120,6 +3173,7 @@ __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
   a.slices = as_global(a.slices);
   a.arrive = as_global(a.arrive);
   a.tile_max = as_global(a.tile_max);
+  a.tile_arrive = as_global(a.tile_arrive);
   return a;
 }
 
@@ -3136,7 +3190,8 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   __shared__ FastSmem f;
   static_assert(sizeof(GenericSmem) <= sizeof(uint32_t) * kBitmapOffset, "scratch must fit below the bitmap");
   static_assert(kMatchOffset + kMatchWords <= kChunk, "count cells must fit");
-  const int r = SPLIT ? row_index(a) : static_cast<int>(blockIdx.x);
+  const bool fused = TILES && a.tile_arrive != nullptr;  // (uniform)
+  const int r = SPLIT ? row_index(a) : fused ? static_cast<int>(blockIdx.x) / a.tile_G : static_cast<int>(blockIdx.x);
   const int tid = threadIdx.x;
   exp_table_init();  // (published by the first barrier of either path)
   // the row's parameters: thread w < kParamWords loads word w, the others word 0 (every thread
@@ -3156,6 +3211,8 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   row.eval = f.eval;
   GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
   if constexpr (TILES && sizeof(Tin) == 2 && !STATE && !SPLIT) {
+    // (a fused pass: this workgroup's share of the row's tile maxima; the row's last goes on)
+    if (fused && !tile_share(a, r, static_cast<int>(blockIdx.x) % a.tile_G, &f.si[7])) return;  // (uniform)
     if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
     lds_barrier();
     RowParams pt = f.prm;

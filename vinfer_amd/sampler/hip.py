@@ -13,6 +13,7 @@ synchronising, except ``sample`` which returns a Python ``int`` as the engine's 
 from __future__ import annotations
 
 import ctypes
+import struct
 import threading
 from collections.abc import Sequence
 
@@ -146,7 +147,9 @@ class HipSampler:
 
     @staticmethod
     def _stream(dev: torch.device) -> ctypes.c_void_p:
-        return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        # (the raw handle of the device's current stream: what torch.cuda.current_stream(dev)
+        # .cuda_stream returns, without building the Stream object, ~4 us a call)
+        return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(dev.index))
 
     # ---- the interface ----------------------------------------------------------------------
     def prepare_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None,
@@ -330,8 +333,8 @@ class HipSampler:
         dprob = torch.empty(B, dtype=torch.float32, device=dev) if draft_ids is not None else None
         a.out_ids = ids.data_ptr()
         a.out_draft_prob = _ptr(dprob)
-        tiles = self._tiles(dev, B * ((V + _lib.LM_TILE - 1) // _lib.LM_TILE))
-        _lib.check(self._lib.vsamp_sample_tile_pass(ctypes.byref(a), tiles, self._stream(dev)))
+        tiles, arrive = self._tiles(dev, B * ((V + _lib.LM_TILE - 1) // _lib.LM_TILE), B)
+        _lib.check(self._lib.vsamp_sample_tile_pass(ctypes.byref(a), tiles, arrive, self._stream(dev)))
         del keep
         return ids, dprob
 
@@ -462,28 +465,49 @@ class HipSampler:
         position: int,
         history: Sequence[int] | torch.Tensor | None = None,
     ) -> int:
-        require_history(params, history)
+        # (each extension field read once: the per-token call's host time is most of its cost)
+        rep_p = field(params, "repetition_penalty")
+        pres_p = field(params, "presence_penalty")
+        freq_p = field(params, "frequency_penalty")
+        pen = rep_p != 1.0 or pres_p != 0.0 or freq_p != 0.0  # (penalized(params))
+        if pen and history is None:
+            require_history(params, history)
         if logits.dim() != 1 and not (logits.dim() == 2 and logits.shape[0] == 1):
             raise ValueError(f"sample takes one row of logits ([V] or [1, V]), got {tuple(logits.shape)}")
         row = logits.reshape(-1)
         if row.stride(0) != 1:
             raise ValueError("logits must have unit stride")
-        dev = self._device(row.reshape(1, -1))
+        dev = row.device
+        if dev.type != "cuda" or row.dtype not in _DTYPES:
+            self._device(row.reshape(1, -1))  # (raises with the reason)
         V = row.shape[0]
         t = self._token_path(dev)
-        # the row's parameters, its uniform and its history's range: one pinned block, one copy
-        f = t.words.view(np.float32)
-        f[0], f[1], f[2] = params.temperature, params.top_p, field(params, "min_p")
-        f[3] = field(params, "repetition_penalty")
-        f[4] = field(params, "presence_penalty")
-        f[5] = field(params, "frequency_penalty")
-        t.words[6] = params.top_k
-        f[7] = uniform(seed, position)
-        n = len(history) if penalized(params) else 0
+        # the row's parameters and its uniform (one pinned block the kernel reads in place)
+        top_k = params.top_k
+        u = uniform(seed, position)
+        try:
+            _WORDS.pack_into(t.mem, 0, params.temperature, params.top_p, field(params, "min_p"), rep_p, pres_p, freq_p,
+                             top_k, u)
+        except (struct.error, OverflowError):  # (values past fp32 or int32: numpy's conversions)
+            f = t.words.view(np.float32)
+            f[0], f[1], f[2] = params.temperature, params.top_p, field(params, "min_p")
+            f[3], f[4], f[5] = rep_p, pres_p, freq_p
+            t.words[6] = top_k
+            f[7] = u
+        n = len(history) if pen else 0
         a = t.args
-        a.logits, a.dtype, a.vocab, a.row_stride = row.data_ptr(), _DTYPES[row.dtype], V, V
-        a.hist_ids = a.hist_offsets = a.workspace = None
-        a.hist_total = a.workspace_bytes = 0
+        a.logits = row.data_ptr()
+        if t.shape != (V, row.dtype):
+            t.shape = (V, row.dtype)
+            a.dtype, a.vocab, a.row_stride = _DTYPES[row.dtype], V, V
+            # (the tile pass's maxima and arrival word: this path's own, zero until first used)
+            t.tile_bufs = (torch.empty(max((V + _lib.LM_TILE - 1) // _lib.LM_TILE, 2048), dtype=torch.float32, device=dev),
+                           torch.zeros(64, dtype=torch.int32, device=dev))
+            t.tiles = (t.tile_bufs[0].data_ptr(), t.tile_bufs[1].data_ptr())
+        if t.hist:  # (the previous call passed a history)
+            a.hist_ids = a.hist_offsets = a.workspace = None
+            a.hist_total = a.workspace_bytes = 0
+            t.hist = False
         keep = None
         if n > 0:
             if isinstance(history, torch.Tensor) and history.device.type != "cpu":
@@ -499,7 +523,8 @@ class HipSampler:
             need = int(self._lib.vsamp_workspace_bytes(1, V, n))
             a.hist_ids, a.hist_offsets, a.hist_total = hist_ptr, t.base + 32, n
             a.workspace, a.workspace_bytes = self._workspace(dev, need), need
-        stream = torch.cuda.current_stream(dev)
+            t.hist = True
+        stream = self._stream(dev)
         out = t.out_np
         out[0] = -1
         # bf16 greedy and top-k (<= 256) rows without penalties take the tile pass: the row's tile
@@ -507,13 +532,11 @@ class HipSampler:
         # (greedy 29.9 -> 24.7 us per call, top-k 20 34.2 -> 31.0 on MI355X). Rows with min-p alone
         # do not: their candidates depend on the logits (N(0, 4) rows keep ~900 tokens at min-p
         # 0.05, more than the tile path's list), and a row handed on pays both launches.
-        top_k = params.top_k
-        if (row.dtype == torch.bfloat16 and n == 0 and not penalized(params)
+        if (row.dtype == torch.bfloat16 and n == 0 and not pen
                 and (not params.temperature > 0 or 0 < top_k <= 256 and top_k < V)):
-            code = self._lib.vsamp_sample_tile_pass(t.ref, self._tiles(dev, (V + _lib.LM_TILE - 1) // _lib.LM_TILE),
-                                                    ctypes.c_void_p(stream.cuda_stream))
+            code = self._lib.vsamp_sample_tile_pass(t.ref, t.tiles[0], t.tiles[1], stream)
         else:
-            code = self._lib.vsamp_sample(t.ref, ctypes.c_void_p(stream.cuda_stream))
+            code = self._lib.vsamp_sample(t.ref, stream)
         _lib.check(code)
         # the kernel writes the id last, after every read of the parameters and the history: the
         # call returns as soon as the id reaches the pinned word (sooner than a stream
@@ -522,7 +545,7 @@ class HipSampler:
         while out[0] < 0:
             spins += 1
             if spins == 1 << 20:
-                stream.synchronize()
+                torch.cuda.current_stream(dev).synchronize()
                 if out[0] < 0:
                     raise RuntimeError("the drawn id never reached the host")
         del keep
@@ -535,13 +558,15 @@ class HipSampler:
             t = paths[dev] = _TokenPath(dev)
         return t
 
-    def _tiles(self, dev: torch.device, n: int) -> int:
-        """A device buffer of ``n`` fp32 tile maxima, this thread's for ``dev``."""
+    def _tiles(self, dev: torch.device, n: int, rows: int) -> tuple[int, int]:
+        """Device buffers of ``n`` fp32 tile maxima and ``rows`` arrival words (zero, and left
+        zero by every call), this thread's for ``dev``."""
         bufs = self._local.__dict__.setdefault("tiles", {})
         t = bufs.get(dev)
-        if t is None or t.numel() < n:
-            t = bufs[dev] = torch.empty(max(n, 2048), dtype=torch.float32, device=dev)
-        return t.data_ptr()
+        if t is None or t[0].numel() < n or t[1].numel() < rows:
+            t = bufs[dev] = (torch.empty(max(n, 2048), dtype=torch.float32, device=dev),
+                             torch.zeros(max(rows, 64), dtype=torch.int32, device=dev))
+        return t[0].data_ptr(), t[1].data_ptr()
 
     def _workspace(self, dev: torch.device, need: int) -> int:
         """A 256-byte aligned device workspace of ``need`` bytes, this thread's for ``dev``."""
@@ -550,6 +575,11 @@ class HipSampler:
         if w is None or w.numel() < need + 256:
             w = spaces[dev] = torch.empty(need + 256, dtype=torch.uint8, device=dev)
         return (w.data_ptr() + 255) & ~255
+
+
+# the per-token call's parameter words: temperature, top_p, min_p, the three penalties (fp32),
+# top_k (int32), the uniform (fp32)
+_WORDS = struct.Struct("<6fif")
 
 
 class _TokenPath:
@@ -565,7 +595,12 @@ class _TokenPath:
     def __init__(self, dev: torch.device) -> None:
         self.words_t = torch.zeros(16, dtype=torch.int32, pin_memory=True)
         self.words = self.words_t.numpy()
+        self.mem = memoryview(self.words).cast("B")
         self.base = self.words_t.data_ptr()
+        self.shape = None  # (V, dtype) the argument block was last set up for, with its tile buffers
+        self.tile_bufs = None
+        self.tiles = (0, 0)
+        self.hist = False  # the argument block points at a history
         self.hist_host = torch.empty(0, dtype=torch.int32, pin_memory=True)
         self.out = torch.empty(1, dtype=torch.int32, pin_memory=True)
         self.out_np = self.out.numpy()
@@ -591,7 +626,7 @@ class PreparedStep:
     def launch(self, stream: int | None = None) -> None:
         """Enqueue the step on ``stream`` (a hipStream_t as int; default: torch's current)."""
         if stream is None:
-            stream = torch.cuda.current_stream(self.ids.device).cuda_stream
+            stream = torch._C._cuda_getCurrentRawStream(self.ids.device.index)
         if self._tiles is None:
             code = self._lib.vsamp_sample(self._ref, ctypes.c_void_p(stream))
         else:
