@@ -3035,53 +3035,90 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t
   for (int i = 0; i < 4; ++i) {
     const int t = tid + i * kThreads;
     mt[i] = t < nT ? ld_dev(tm + t) : -INFINITY;  // (device-coherent: other workgroups of a fused pass wrote them)
-    kt[i] = t < nT ? key_of(mt[i]) : 0u;  // (0: below every key)
-    mk = kt[i] > mk ? kt[i] : mk;
   }
-  mk = static_cast<uint32_t>(block_max_u64(mk, g.srch.red64));
-  if (mk > key_of(INFINITY)) return false;  // a NaN: the row passes find the first one
-  const float M = val_of(mk);
   Kept k;
   if (greedy) {
-    // the first tile whose max is the row max, then its first element equal to it
-    uint32_t first = 0xFFFFFFFFu;
+    // the row max and the first tile holding it in one reduction (key above the complemented
+    // tile: equal values, -0 and +0 included, have one key), then that tile's first element equal
+    // to it, by wave 0 (two elements a lane)
+    u64 best = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t t = static_cast<uint32_t>(tid + i * kThreads);
-      if (t < static_cast<uint32_t>(nT) && mt[i] == M) first = t < first ? t : first;
+      const int t = tid + i * kThreads;
+      const u64 v = t < nT ? (static_cast<u64>(key_of(mt[i])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(t)) : 0ull;
+      best = v > best ? v : best;
     }
-    first = ~static_cast<uint32_t>(block_max_u64(~first, g.srch.red64));
-    if (first >= static_cast<uint32_t>(nT)) return false;  // (tile maxima not of these logits)
-    uint32_t id = 0xFFFFFFFFu;
-    if (tid < kStatTile) {
-      const int i = static_cast<int>(first) * kStatTile + tid;
-      if (i < V && load_one<uint16_t>(row.p, i) == M) id = static_cast<uint32_t>(i);
+    best = block_max_u64(best, g.srch.red64);
+    mk = static_cast<uint32_t>(best >> 32);
+    if (mk > key_of(INFINITY)) return false;  // a NaN: the row passes find the first one
+    const float M = val_of(mk);
+    const uint32_t first = 0xFFFFFFFFu - static_cast<uint32_t>(best);
+    if (tid < kWave) {
+      uint32_t id = 0xFFFFFFFFu;
+#pragma unroll
+      for (int h = 1; h >= 0; --h) {
+        const int i = static_cast<int>(first) * kStatTile + tid + h * kWave;
+        if (i < V && load_one<uint16_t>(row.p, i) == M) id = static_cast<uint32_t>(i);
+      }
+      id = dpp::reduce(id, [](uint32_t x, uint32_t y) { return x < y ? x : y; });
+      if (tid == 0) sh[0] = id;
     }
-    id = ~static_cast<uint32_t>(block_max_u64(~id, g.srch.red64));
+    lds_barrier();
+    const uint32_t id = sh[0];
     if (id >= static_cast<uint32_t>(V)) return false;  // (tile maxima not of these logits)
     k.point = static_cast<int>(id);
     finish<false>(a, row, p, 0.0f, k, 0, &g.srch.vslot, r);
     return true;
   }
+  // Top-k rows count their tiles' maxima by the top 12 bits of their 16-bit keys (4096 bins in
+  // LDS): the lowest value of the bin holding the K-th largest is at most the K-th largest tile
+  // max, so at most the K-th largest logit. The row max rides the same barrier (one LDS
+  // atomicMax per wave).
+  uint32_t* h12 = reinterpret_cast<uint32_t*>(&g) + kBitmapOffset;
+  uint32_t* smax = &g.rdx.ncand;
+  if (topk) reinterpret_cast<uint4*>(h12)[tid] = make_uint4(0, 0, 0, 0);
+  if (tid == 0) *smax = 0;
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = tid + i * kThreads;
+    kt[i] = t < nT ? key_of(mt[i]) : 0u;  // (0: below every key)
+    mk = kt[i] > mk ? kt[i] : mk;
+    if (topk && t < nT) atomicAdd(&h12[kt[i] >> 20], 1u);
+  }
+  mk = dpp::reduce(mk, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+  if (lane_id() == 0) atomicMax(smax, mk);
+  lds_barrier();
+  mk = *smax;
+  if (mk > key_of(INFINITY)) return false;  // a NaN: the row passes find the first one
+  const float M = val_of(mk);
   const float T = p.T;
   const float mz = M / T;
   if (!(mz > -INFINITY && mz < INFINITY)) return false;  // point rows: the row passes
-  // xlo: no kept token lies below it (wave 0 bisects; the others wait at the barrier)
+  // xlo: no kept token lies below it (wave 0 decides; the others wait at the barrier)
   const uint32_t lo_key = key_of(-INFINITY);
-  float theta = -INFINITY;
-  if (topk) {
-    uint32_t k16[4];
-    int nk = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      k16[i] = kt[i] >> 16;  // (a bf16 value's key is the top half of its fp32 key)
-      nk += tid + i * kThreads < nT ? 1 : 0;
-    }
-    theta = val16(kth_key16(k16, nk, static_cast<uint32_t>(p.K), g.rdx.hcnt, reinterpret_cast<uint32_t*>(g.rdx.hmass), sh + 2));
-  }
   if (tid < kWave) {
     float xlo = -INFINITY, xm = -INFINITY;
     if (topk) {
+      // the bin of the K-th largest: lane l sums bins 4095 - 64 l - 63 .. 4095 - 64 l (lane 0
+      // the top ones), then lane i of the crossing lane's 64 bins takes bin 4095 - 64 L - i
+      const uint32_t K = static_cast<uint32_t>(p.K);
+      const int l = tid;
+      uint32_t sum = 0;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const uint4 v = reinterpret_cast<const uint4*>(h12 + 4032 - 64 * l)[q];
+        sum += v.x + v.y + v.z + v.w;
+      }
+      const uint32_t incl = wave_incl_scan<uint32_t>(sum);
+      const int L = __ffsll(static_cast<long long>(__ballot(incl >= K))) - 1;  // (K <= nT: some lane crosses)
+      const uint32_t above = __builtin_amdgcn_readlane(incl, L) - __builtin_amdgcn_readlane(sum, L);
+      const uint32_t c = h12[4095 - 64 * L - l];
+      const uint32_t incl2 = above + wave_incl_scan<uint32_t>(c);
+      const int i = __ffsll(static_cast<long long>(__ballot(incl2 >= K))) - 1;
+      const uint32_t bin = static_cast<uint32_t>(4095 - 64 * L - i);
+      const uint32_t k16 = (bin << 4) > 0x007Fu ? (bin << 4) : 0x007Fu;  // (not below -inf's key)
+      const float theta = val16(k16);
       const float zt = theta / T;
       xlo = val_of(wave_bisect(lo_key, key_of(theta), key_of(zt * T), [&](float x) { return x / T >= zt; }));
     }
