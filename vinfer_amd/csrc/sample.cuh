@@ -3011,6 +3011,18 @@ __device__ __forceinline__ bool tile_share(const SampleArgs& a, int r, int g, in
   return *flag != 0;
 }
 
+// Whether a fused tile pass computes a row's maxima: greedy rows and top-k rows (0 < K <= kSortCap,
+// K < V) without penalties, whose candidates the maxima bound; rows with top-p or min-p alone keep
+// a share of the row that depends on its values (hundreds to thousands of tokens) and go to the
+// row passes directly.
+template <bool PEN>
+__device__ __forceinline__ bool tile_candidate(const SampleArgs& a, const RowParams& p) {
+  const bool pen_on = PEN && p.h1 > p.h0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
+  if (pen_on || a.out_probs || a.out_state || a.nT > 4 * kThreads) return false;
+  if (!(p.T > 0.0f)) return true;
+  return p.K > 0 && p.K < a.V && p.K <= kSortCap && p.K <= a.nT;
+}
+
 // Returns true when the row was decided (outputs written) from its tile maxima; false, having
 // written nothing, when it needs the row passes. Every thread calls; `p.u` is clamped to >= 0.
 template <bool PEN>
@@ -3248,14 +3260,23 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   row.eval = f.eval;
   GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
   if constexpr (TILES && sizeof(Tin) == 2 && !STATE && !SPLIT) {
-    // (a fused pass: this workgroup's share of the row's tile maxima; the row's last goes on)
-    if (fused && !tile_share(a, r, static_cast<int>(blockIdx.x) % a.tile_G, &f.si[7])) return;  // (uniform)
     if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
     lds_barrier();
     RowParams pt = f.prm;
     pt.u = pt.u >= 0.0f ? pt.u : 0.0f;
-    if (tile_row<PEN>(a, row, pt, g, r)) return;
-    lds_barrier();  // (every thread is done with the tile path's LDS)
+    // (a fused pass) a row the maxima can decide: this workgroup's share of its tile maxima, and
+    // the row's last workgroup goes on; another row: its first workgroup runs the row passes and
+    // the others exit
+    bool try_tiles = true;
+    if (fused) {
+      const int gi = static_cast<int>(blockIdx.x) % a.tile_G;
+      try_tiles = tile_candidate<PEN>(a, pt);  // (uniform)
+      if (try_tiles ? !tile_share(a, r, gi, &f.si[7]) : gi != 0) return;
+    }
+    if (try_tiles) {
+      if (tile_row<PEN>(a, row, pt, g, r)) return;
+      lds_barrier();  // (every thread is done with the tile path's LDS)
+    }
   }
   if constexpr (sizeof(Tin) == 2) {
     if (fast_row<PEN, STATE, SPLIT>(a, row, f.prm, big, f, g.srch, pw, r)) return;

@@ -163,12 +163,16 @@ class HipSampler:
             ws = torch.empty(a.workspace_bytes + 256, dtype=torch.uint8, device=logits.device)
             a.workspace = (ws.data_ptr() + 255) & ~255
             keep = keep + (ws,)
-        B = logits.shape[0]
+        B, V = logits.shape
         ids = torch.empty(B, dtype=torch.int32, device=logits.device)
         dprob = torch.empty(B, dtype=torch.float32, device=logits.device) if draft_ids is not None else None
         a.out_ids = ids.data_ptr()
         a.out_draft_prob = _ptr(dprob)
-        return PreparedStep(self._lib, a, keep, ids, dprob)
+        tile_pass = None
+        if self._one_launch_tiles(a, logits):  # (the step's own maxima and arrival words)
+            tile_pass = (torch.empty(B * _n_tiles(V), dtype=torch.float32, device=logits.device),
+                         torch.zeros(B, dtype=torch.int32, device=logits.device))
+        return PreparedStep(self._lib, a, keep, ids, dprob, tile_pass=tile_pass)
 
     def sample_batch(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None,
                      append_history=False):
@@ -182,9 +186,24 @@ class HipSampler:
         dprob = torch.empty(B, dtype=torch.float32, device=dev) if draft_ids is not None else None
         a.out_ids = ids.data_ptr()
         a.out_draft_prob = _ptr(dprob)
-        _lib.check(self._lib.vsamp_sample(ctypes.byref(a), self._stream(dev)))
+        if self._one_launch_tiles(a, logits):
+            tiles, arrive = self._tiles(dev, B * _n_tiles(logits.shape[1]), B)
+            _lib.check(self._lib.vsamp_sample_tile_pass(ctypes.byref(a), tiles, arrive, self._stream(dev)))
+        else:
+            _lib.check(self._lib.vsamp_sample(ctypes.byref(a), self._stream(dev)))
         del keep
         return ids, dprob
+
+    @staticmethod
+    def _one_launch_tiles(a, logits: torch.Tensor) -> bool:
+        """Whether a batch takes the tile pass as one launch (``vsamp_sample_tile_pass``): bf16
+        rows, few enough that their workgroups fit one round on the CUs, and no split rows. Its
+        greedy and top-k rows without penalties are then decided from a few tiles; the other
+        rows run the row passes on one workgroup each, as ``vsamp_sample`` would (the same
+        outputs either way)."""
+        B, V = logits.shape
+        return (logits.dtype == torch.bfloat16 and not (a.flags & _lib.VSAMP_SPLIT_ROWS)
+                and B * ((_n_tiles(V) + 63) // 64) <= _TILE_FUSED_WORKGROUPS)
 
     def probs(self, logits, params, hist_ids=None, hist_offsets=None):
         a, keep = self._args(logits, params, hist_ids, hist_offsets)
@@ -577,6 +596,14 @@ class HipSampler:
         return (w.data_ptr() + 255) & ~255
 
 
+def _n_tiles(V: int) -> int:
+    return (V + _lib.LM_TILE - 1) // _lib.LM_TILE
+
+
+# batches up to this many workgroups (rows times workgroups per row) take the tile pass in one
+# launch (the library's rule)
+_TILE_FUSED_WORKGROUPS = 256
+
 # the per-token call's parameter words: temperature, top_p, min_p, the three penalties (fp32),
 # top_k (int32), the uniform (fp32)
 _WORDS = struct.Struct("<6fif")
@@ -617,20 +644,25 @@ class _TokenPath:
 class PreparedStep:
     """One batch's sampler launch with its argument block built (see ``prepare_batch``)."""
 
-    def __init__(self, lib, args, keep, ids, dprob, tile_max=None) -> None:
+    def __init__(self, lib, args, keep, ids, dprob, tile_max=None, tile_pass=None) -> None:
         self._lib, self._args, self._keep = lib, args, keep
         self._ref = ctypes.byref(args)
         self.ids, self.draft_prob = ids, dprob
         self._tiles = None if tile_max is None else ctypes.c_void_p(tile_max.data_ptr())
+        # (a small bf16 batch: the tile pass in one launch, on the step's own maxima and arrival words)
+        self._pass = tile_pass
+        self._pass_ptrs = None if tile_pass is None else tuple(ctypes.c_void_p(t.data_ptr()) for t in tile_pass)
 
     def launch(self, stream: int | None = None) -> None:
         """Enqueue the step on ``stream`` (a hipStream_t as int; default: torch's current)."""
         if stream is None:
             stream = torch._C._cuda_getCurrentRawStream(self.ids.device.index)
-        if self._tiles is None:
-            code = self._lib.vsamp_sample(self._ref, ctypes.c_void_p(stream))
-        else:
+        if self._tiles is not None:
             code = self._lib.vsamp_sample_tiles(self._ref, self._tiles, ctypes.c_void_p(stream))
+        elif self._pass_ptrs is not None:
+            code = self._lib.vsamp_sample_tile_pass(self._ref, *self._pass_ptrs, ctypes.c_void_p(stream))
+        else:
+            code = self._lib.vsamp_sample(self._ref, ctypes.c_void_p(stream))
         if code:
             _lib.check(code)
 
