@@ -423,7 +423,7 @@ int vsamp_sample_tile_pass(const vsamp_args* a, float* tile_max, uint32_t* arriv
   // One launch while the rows' workgroups fit one round on the CUs: G per row, each the maxima of
   // at most 64 tiles (one 16-byte load per thread), the last of a row's G finishing it; larger
   // batches take a launch of the maxima first (256-thread workgroups), then the draw.
-  const int G = (nT + 63) / 64;
+  const int G = (nT + vs::kTileSharePasses * vs::kWave - 1) / (vs::kTileSharePasses * vs::kWave);
   if (static_cast<int64_t>(a->batch) * G <= vs::kTileFusedWorkgroups)
     return run_sample<uint16_t>(a, nullptr, 0, st, nullptr, 1, tile_max, arrive, G);
   hipLaunchKernelGGL(vs::k_tile_max, dim3((nT + vs::kTilesPerBlock - 1) / vs::kTilesPerBlock, a->batch),

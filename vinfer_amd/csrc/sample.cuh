@@ -1110,10 +1110,19 @@ __device__ __forceinline__ bool sorted_tail(const SampleArgs& a, const Row<Tin>&
   // bq[2] mass of one member of the cutoff group
   uint32_t* res = g.rdx.hcnt;
   u64* resq = g.rdx.bq;
+  // every entry's mass, one per thread (rdx.hmass holds kSortCap), for wave 0
+  const uint32_t k0 = key_of(k.x0);
+  {
+    const int i = threadIdx.x;
+    if (i < n) {
+      const float x = c[i].x;
+      g.rdx.hmass[i] = key_of(x) >= k0 ? mass_q(ptilde(x, p.T, mz)) : 0ull;
+    }
+  }
+  static_assert(sizeof(g.rdx.hmass) / sizeof(u64) >= kSortCap, "a mass per sorted entry");
+  lds_barrier();
   if (threadIdx.x < kWave) {
     const int l = lane_id();
-    const float T = p.T;
-    const uint32_t k0 = key_of(k.x0);
     uint32_t key[4];
     u64 q[4];
     u64 ls = 0;
@@ -1123,7 +1132,7 @@ __device__ __forceinline__ bool sorted_tail(const SampleArgs& a, const Row<Tin>&
       const float x = i < n ? c[i].x : 0.0f;
       const bool in = i < n && key_of(x) >= k0;
       key[t] = in ? key_of(x) : 0u;  // (0: below every kept key)
-      q[t] = in ? mass_q(ptilde(x, T, mz)) : 0ull;
+      q[t] = in ? g.rdx.hmass[i] : 0ull;
       ls += q[t];
     }
     const u64 incl = wave_incl_scan<u64>(ls);
@@ -2964,40 +2973,56 @@ __global__ __launch_bounds__(kTileMaxThreads) void k_tile_max(const uint16_t* lo
 }
 
 // (the fused tile pass) Workgroup g of row r's G computes the maxima of tiles g * per .. (per =
-// ceil(nT / G), at most 64: one 16-byte load per thread), sixteen lanes a tile as k_tile_max, into
-// a.tile_max with device-coherent stores; waits for them; then thread 0 counts the workgroup in
-// at the row's arrival word. The last of the G resets the word to 0 (nothing else touches it in
-// this launch) and returns true: it finishes the row, the others return false and exit. `flag`
-// is an LDS word.
+// ceil(nT / G), at most kTileSharePasses * 64: sixteen lanes a tile as k_tile_max, up to
+// kTileSharePasses 16-byte loads per thread issued before any is used) into a.tile_max with
+// device-coherent stores; waits for them; then thread 0 counts the workgroup in at the row's
+// arrival word. The last of the G resets the word to 0 (nothing else touches it in this launch)
+// and returns true: it finishes the row, the others return false and exit. `flag` is an LDS word.
+// One pass (at most 64 tiles a workgroup): more workgroups a row measured faster than four passes
+// (a CU reading 16 KB of the row instead of 64 KB; 11.7 against 13.2 us for one 151936-logit row).
+constexpr int kTileSharePasses = 1;
 __device__ __forceinline__ bool tile_share(const SampleArgs& a, int r, int g, int* flag) {
   const int G = a.tile_G, nT = a.nT;
   const int per = (nT + G - 1) / G;
-  const int t = g * per + static_cast<int>(threadIdx.x >> 4);  // (the same in a 16-lane row)
+  const int end = min(nT, (g + 1) * per);
   const int l16 = threadIdx.x & 15;
   const uint16_t* row = as_global(static_cast<const uint16_t*>(a.logits)) + static_cast<int64_t>(r) * a.stride;
   const int V = a.V;
-  uint32_t mk = 0;  // (below every key)
-  const bool mine = t < nT && t < (g + 1) * per;
-  if (mine) {
+  float* out = const_cast<float*>(a.tile_max) + static_cast<int64_t>(r) * nT;
+  // pass q: tile g * per + threadIdx.x / 16 + 64 q (the same in a 16-lane row); whole aligned
+  // 16-byte chunks are loaded first (every lane issues its loads: one that has none reads a
+  // constant aligned block, unused), the rest element by element
+  uint4 v[kTileSharePasses];
+  bool whole[kTileSharePasses];
+#pragma unroll
+  for (int q = 0; q < kTileSharePasses; ++q) {
+    const int t = g * per + static_cast<int>(threadIdx.x >> 4) + kWave * q;
     const int i0 = t * kStatTile + 8 * l16;
-    if ((reinterpret_cast<uintptr_t>(row + i0) & 15u) == 0 && i0 + 8 <= V) {
-      const uint4 q = ld_global_u4(reinterpret_cast<const uint4*>(row + i0));
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    whole[q] = t < end && (reinterpret_cast<uintptr_t>(row + i0) & 15u) == 0 && i0 + 8 <= V;
+    v[q] = ld_global_u4(whole[q] ? reinterpret_cast<const uint4*>(row + i0) : reinterpret_cast<const uint4*>(g_unused_block));
+  }
+  auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+#pragma unroll
+  for (int q = 0; q < kTileSharePasses; ++q) {
+    const int t = g * per + static_cast<int>(threadIdx.x >> 4) + kWave * q;
+    uint32_t mk = 0;  // (below every key)
+    if (whole[q]) {
+      const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         mk = max(mk, key_of(__uint_as_float(w[i] << 16)));
         mk = max(mk, key_of(__uint_as_float(w[i] & 0xFFFF0000u)));
       }
-    } else {
+    } else if (t < end) {
+      const int i0 = t * kStatTile + 8 * l16;
       for (int i = i0; i < i0 + 8 && i < V; ++i) mk = max(mk, key_of(bf16_to_f32(ld_global(row + i))));
     }
+    mk = umax(mk, dpp::mov<dpp::kXor1>(mk));
+    mk = umax(mk, dpp::mov<dpp::kXor2>(mk));
+    mk = umax(mk, dpp::mov<dpp::kHalfMirror>(mk));
+    mk = umax(mk, dpp::mov<dpp::kMirror>(mk));
+    if (t < end && l16 == 0) st_dev<float>(out + t, val_of(mk));
   }
-  auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
-  mk = umax(mk, dpp::mov<dpp::kXor1>(mk));
-  mk = umax(mk, dpp::mov<dpp::kXor2>(mk));
-  mk = umax(mk, dpp::mov<dpp::kHalfMirror>(mk));
-  mk = umax(mk, dpp::mov<dpp::kMirror>(mk));
-  if (mine && l16 == 0) st_dev<float>(const_cast<float*>(a.tile_max) + static_cast<int64_t>(r) * nT + t, val_of(mk));
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();  // (every thread's stores have completed)
   if (threadIdx.x == 0) {
@@ -3088,6 +3113,7 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t
   // atomicMax per wave).
   uint32_t* h12 = reinterpret_cast<uint32_t*>(&g) + kBitmapOffset;
   uint32_t* smax = &g.rdx.ncand;
+  uint32_t* tcount = reinterpret_cast<uint32_t*>(g.rdx.bq);  // (the candidate tiles' count)
   if (topk) reinterpret_cast<uint4*>(h12)[tid] = make_uint4(0, 0, 0, 0);
   if (tid == 0) *smax = 0;
   lds_barrier();
@@ -3142,24 +3168,32 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t
     if (tid == 0) {
       reinterpret_cast<float*>(sh)[0] = xlo > xm ? xlo : xm;
       reinterpret_cast<float*>(sh)[1] = xm;
+      *tcount = 0;
     }
   }
   lds_barrier();
   const float xlo = reinterpret_cast<const float*>(sh)[0];
   const float xm = reinterpret_cast<const float*>(sh)[1];
-  // the tiles that can hold a kept token, listed in LDS
-  uint32_t mine = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) mine += tid + i * kThreads < nT && mt[i] >= xlo ? 1u : 0u;
-  uint32_t ntile;
-  uint32_t at = block_excl_scan<uint32_t>(mine, g.rdx.hcnt, &ntile);
-  if (ntile > static_cast<uint32_t>(kTileRowTiles)) return false;  // (uniform)
+  // the tiles that can hold a kept token, listed in LDS in any order (one counter update per
+  // wave and ballot)
   int* ctile = reinterpret_cast<int*>(g.srch.tw);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (tid + i * kThreads < nT && mt[i] >= xlo) ctile[at++] = tid + i * kThreads;
+  for (int i = 0; i < 4; ++i) {
+    const int t = tid + i * kThreads;
+    const bool in = t < nT && mt[i] >= xlo;
+    const u64 bal = __ballot(in);
+    if (bal) {  // (uniform over the wave)
+      const int leader = __ffsll(static_cast<long long>(bal)) - 1;
+      uint32_t pos = 0;
+      if (lane_id() == leader) pos = atomicAdd(tcount, static_cast<uint32_t>(__popcll(bal)));
+      pos = __builtin_amdgcn_readlane(pos, leader) + static_cast<uint32_t>(__popcll(bal & ((1ull << lane_id()) - 1ull)));
+      if (in && pos < static_cast<uint32_t>(kTileRowTiles)) ctile[pos] = t;
+    }
+  }
   if (tid == 0) sh[2] = 0;
   lds_barrier();
+  const uint32_t ntile = *tcount;
+  if (ntile > static_cast<uint32_t>(kTileRowTiles)) return false;  // (uniform)
   // their elements >= xlo, into the candidate list (every element's load first)
   Cand* c = reinterpret_cast<Cand*>(reinterpret_cast<uint32_t*>(&g) + kMatchOffset);
   constexpr int kPer = kTileRowTiles * kStatTile / kThreads;
