@@ -137,6 +137,12 @@ def test_host_uniforms_equal_the_python_derivation():
         -(1 << 63), (1 << 63) - 1, 3000, dtype=np.int64
     ).tolist()
     positions = [0, 1, 2, 3, 10**12, (1 << 63) - 1, -5, 99] + rng.integers(0, 1 << 40, 3000).tolist()
+    # every decimal length of both numbers, signed: 10^k - 1, 10^k, 10^k + 1 crossed
+    edges = sorted({v for k in range(19) for v in (10**k - 1, 10**k, 10**k + 1)} | {(1 << 63) - 1})
+    edges += [-v for v in edges if v > 0] + [-(1 << 63)]
+    pairs = [(a, b) for a in edges for b in edges[::3]] + [(a, b) for a in edges[1::3] for b in edges]
+    seeds += [a for a, _ in pairs]
+    positions += [b for _, b in pairs]
     got = _lib.position_uniforms(seeds, positions)
     want = np.array([uniform(s, p) for s, p in zip(seeds, positions)], np.float32)
     assert np.array_equal(got, want)

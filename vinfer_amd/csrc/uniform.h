@@ -29,7 +29,28 @@ constexpr uint8_t kSigma[10][16] = {
     {6, 15, 14, 9, 11, 3, 0, 8, 12, 2, 13, 7, 1, 4, 10, 5}, {10, 2, 8, 4, 7, 6, 1, 5, 15, 11, 9, 14, 3, 12, 13, 0},
 };
 
-VS_HD uint64_t rotr64(uint64_t x, int n) { return (x >> n) | (x << (64 - n)); }
+// x rotated right by n (0 < n < 64, a constant once inlined). The device pass writes it as two
+// funnel shifts of the 32-bit halves (v_alignbit_b32; a rotation by 32 swaps them), which the
+// compiler does not form from the 64-bit expression.
+VS_HD uint64_t rotr64(uint64_t x, int n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t lo = static_cast<uint32_t>(x), hi = static_cast<uint32_t>(x >> 32);
+  uint32_t nl, nh;
+  if (n == 32) {
+    nl = hi;
+    nh = lo;
+  } else if (n < 32) {
+    nl = __builtin_amdgcn_alignbit(hi, lo, n);
+    nh = __builtin_amdgcn_alignbit(lo, hi, n);
+  } else {
+    nl = __builtin_amdgcn_alignbit(lo, hi, n - 32);
+    nh = __builtin_amdgcn_alignbit(hi, lo, n - 32);
+  }
+  return (static_cast<uint64_t>(nh) << 32) | nl;
+#else
+  return (x >> n) | (x << (64 - n));
+#endif
+}
 
 VS_HD void blake_mix(uint64_t* v, int a, int b, int c, int d, uint64_t x, uint64_t y) {
   v[a] = v[a] + v[b] + x;
@@ -76,63 +97,118 @@ VS_HD uint64_t blake2b_8(const uint64_t (&t)[6], int n) {
   return h[0] ^ v[0] ^ v[8];
 }
 
-// A text built byte by byte into six little-endian words: the open word `acc` takes the next
-// byte at `k`; a full word goes to word `nw` (selected, so the words stay registers).
-struct TextWords {
-  uint64_t w[6] = {0, 0, 0, 0, 0, 0};
-  uint64_t acc = 0;
-  int k = 0, nw = 0;
-  VS_HD void put(uint32_t c) {
-    acc |= static_cast<uint64_t>(c) << (8 * k);
-    if (++k == 8) {
-#pragma unroll
-      for (int i = 0; i < 6; ++i) w[i] = nw == i ? acc : w[i];
-      acc = 0;
-      k = 0;
-      ++nw;
-    }
-  }
-  VS_HD int finish() {  // the open word in place; returns the length
-#pragma unroll
-    for (int i = 0; i < 6; ++i) w[i] = nw == i ? acc : w[i];
-    return 8 * nw + k;
-  }
-};
-
 constexpr uint64_t kPow10[20] = {1ull, 10ull, 100ull, 1000ull, 10000ull, 100000ull, 1000000ull, 10000000ull,
                                  100000000ull, 1000000000ull, 10000000000ull, 100000000000ull, 1000000000000ull,
                                  10000000000000ull, 100000000000000ull, 1000000000000000ull, 10000000000000000ull,
                                  100000000000000000ull, 1000000000000000000ull, 10000000000000000000ull};
 
-// The decimal text of x (no leading zeros; "0" for 0), most significant digit first.
-VS_HD void put_decimal(TextWords& t, uint64_t x) {
-  bool started = false;
+// ---- the decimal text "<seed>:<position>" as little-endian message words ---------------------
+// Built without per-character placement: each number's digits come from three base-10^8 parts
+// (two 64-bit divisions by a constant, then 32-bit ones), as twenty ASCII digits with leading
+// zeros in five little-endian 32-bit words (byte 0 = the most significant digit); the leading
+// zeros are dropped by one variable shift, and the parts are placed at their byte offsets by
+// variable shifts of the whole message.
+
+// The eight ASCII digits of v < 10^8 (leading zeros kept), most significant first in byte order:
+// lo = bytes 0-3, hi = bytes 4-7.
+VS_HD void ascii8(uint32_t v, uint32_t& lo, uint32_t& hi) {
+  uint32_t d[8];
 #pragma unroll
-  for (int i = 19; i >= 0; --i) {
-    const uint64_t d = x / kPow10[i];
-    x -= d * kPow10[i];
-    started = started || d != 0 || i == 0;
-    if (started) t.put('0' + static_cast<uint32_t>(d));
+  for (int k = 7; k >= 0; --k) {  // k = 7: the units digit
+    const uint32_t q = v / 10u;
+    d[k] = v - 10u * q;
+    v = q;
   }
+  lo = d[0] | (d[1] << 8) | (d[2] << 16) | (d[3] << 24) | 0x30303030u;
+  hi = d[4] | (d[5] << 8) | (d[6] << 16) | (d[7] << 24) | 0x30303030u;
 }
 
+// The decimal text of x (no leading zeros; "0" for 0) in five little-endian words, zero past its
+// end; returns its length (1 .. 20).
+VS_HD int decimal_text(uint64_t x, uint32_t (&t)[5]) {
+  const uint64_t q = x / 100000000u;
+  const uint32_t r0 = static_cast<uint32_t>(x - q * 100000000u);
+  const uint32_t q2 = static_cast<uint32_t>(q / 100000000u);  // < 1845
+  const uint32_t r1 = static_cast<uint32_t>(q - static_cast<uint64_t>(q2) * 100000000u);
+  uint32_t s[6];  // the 20 digits at bytes 4 .. 23 of s (bytes 0 .. 3 unused, zero)
+  uint32_t top_lo, top_hi;
+  ascii8(q2, top_lo, top_hi);  // (its first four digits are zeros)
+  s[0] = 0;
+  s[1] = top_hi;
+  ascii8(r1, s[2], s[3]);
+  ascii8(r0, s[4], s[5]);
+  int n = 1;
+#pragma unroll
+  for (int k = 1; k < 20; ++k) n += x >= kPow10[k] ? 1 : 0;
+  // drop the 20 - n leading zeros: the text starts at byte 24 - n of s
+  const int z = 24 - n;
+  const int wz = z >> 2, bz = 8 * (z & 3);
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    uint32_t a = 0, b = 0;  // words wz + i and wz + i + 1 of s (zero past the end)
+#pragma unroll
+    for (int j = 1; j < 6; ++j) {
+      a = wz + i == j ? s[j] : a;
+      b = wz + i + 1 == j ? s[j] : b;
+    }
+    t[i] = static_cast<uint32_t>(((static_cast<uint64_t>(b) << 32) | a) >> bz);
+  }
+  return n;
+}
+
+// m (twelve little-endian words, the 48-byte message) |= the 20-byte string x placed at byte
+// offset o (0 <= o <= 28).
+VS_HD void place(uint32_t (&m)[12], const uint32_t (&x)[5], int o) {
+  const int bo = 8 * (o & 3);
+  uint32_t y[12];
+  // the byte shift within words
+#pragma unroll
+  for (int j = 0; j < 12; ++j) {
+    const uint32_t hi = j < 5 ? x[j] : 0u, lo = j >= 1 && j - 1 < 5 ? x[j - 1] : 0u;
+    y[j] = static_cast<uint32_t>(((static_cast<uint64_t>(hi) << 32) | lo) >> (32 - bo));
+  }
+  // the word shift, o / 4 = 4 a + 2 b + c words, by halving steps
+  const int wo = o >> 2;
+#pragma unroll
+  for (int step = 4; step >= 1; step >>= 1) {
+    const bool on = (wo & step) != 0;
+#pragma unroll
+    for (int j = 11; j >= 0; --j) y[j] = on ? (j >= step ? y[j - step] : 0u) : y[j];
+  }
+#pragma unroll
+  for (int j = 0; j < 12; ++j) m[j] |= y[j];
+}
+
+// m |= byte ch at offset p (0 <= p < 48).
+VS_HD void place_byte(uint32_t (&m)[12], uint32_t ch, int p) {
+  const uint32_t v = ch << (8 * (p & 3));
+#pragma unroll
+  for (int j = 0; j < 12; ++j) m[j] |= (p >> 2) == j ? v : 0u;
+}
+
+
 VS_HD uint64_t position_seed(int64_t seed, int64_t position) {
-  TextWords t;
-  uint64_t s = static_cast<uint64_t>(seed);
-  if (seed < 0) {
-    t.put('-');
-    s = 0 - s;  // magnitude, also for INT64_MIN
-  }
-  put_decimal(t, s);
-  t.put(':');
-  uint64_t p = static_cast<uint64_t>(position);
-  if (position < 0) {
-    t.put('-');
-    p = 0 - p;
-  }
-  put_decimal(t, p);
-  const int n = t.finish();  // (at most 41 bytes)
-  return blake2b_8(t.w, n) & ((uint64_t(1) << 63) - 1);
+  // magnitudes (also of INT64_MIN) and signs
+  const uint64_t sa = seed < 0 ? 0 - static_cast<uint64_t>(seed) : static_cast<uint64_t>(seed);
+  const uint64_t pa = position < 0 ? 0 - static_cast<uint64_t>(position) : static_cast<uint64_t>(position);
+  const int s1 = seed < 0 ? 1 : 0, s2 = position < 0 ? 1 : 0;
+  uint32_t t1[5], t2[5];
+  const int n1 = decimal_text(sa, t1);
+  const int n2 = decimal_text(pa, t2);
+  uint32_t m[12];
+#pragma unroll
+  for (int j = 0; j < 12; ++j) m[j] = 0;
+  place_byte(m, '-', 0);
+  m[0] = s1 ? m[0] : 0u;  // (a '-' only for a negative seed)
+  place(m, t1, s1);
+  place_byte(m, ':', s1 + n1);
+  place_byte(m, s2 ? '-' : 0u, s1 + n1 + 1);
+  place(m, t2, s1 + n1 + 1 + s2);
+  const int n = s1 + n1 + 1 + s2 + n2;  // (at most 41 bytes)
+  uint64_t w[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) w[i] = (static_cast<uint64_t>(m[2 * i + 1]) << 32) | m[2 * i];
+  return blake2b_8(w, n) & ((uint64_t(1) << 63) - 1);
 }
 
 VS_HD uint64_t splitmix64(uint64_t x) {
