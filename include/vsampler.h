@@ -259,7 +259,7 @@ int vsamp_logprobs_tiles(const vsamp_args* args, const float* tile_max, const fl
  * runtime/sampler.py:68-77) when the LM head is vsamp_lm_head. */
 int vsamp_sample_tiles(const vsamp_args* args, const float* tile_max, void* stream);
 
-/* vsamp_sample over bf16 logits from any source, for small batches: each row's tile maxima (the
+/* vsamp_sample over bf16 or fp32 logits from any source, for small batches: each row's tile maxima (the
  * max of every VSAMP_LM_TILE logits) go into `tile_max` (caller-allocated device memory,
  * [batch, ceil(vocab / VSAMP_LM_TILE)] fp32), computed by many workgroups per row, and
  * vsamp_sample_tiles runs on them. While batch * ceil(ceil(vocab / VSAMP_LM_TILE) / 64) <= 256 it
@@ -267,8 +267,8 @@ int vsamp_sample_tiles(const vsamp_args* args, const float* tile_max, void* stre
  * the row's word of `arrive` (caller-allocated device memory, batch uint32 words that must be
  * zero before the first call; every call leaves them zero; calls sharing `arrive` must not run
  * at once), and the last of them finishes the row; larger batches take a launch for the maxima
- * first. Same outputs as vsamp_sample, bit for bit. One row of 151936 on one workgroup spends ~10
- * us in its pass; the maxima take ~2 us over the chip, so greedy and top-k rows without penalties
+ * first. Same outputs as vsamp_sample, bit for bit. One bf16 row of 151936 on one workgroup spends
+ * ~10 us in its pass (an fp32 row ~20); the maxima take ~2 us over the chip, so greedy and top-k rows without penalties
  * finish sooner (the engine's per-token call, B = 1, sampler.py:68-77 via generate.py:129); other
  * rows pay the extra work. (ABI version 10: `arrive` added.) */
 int vsamp_sample_tile_pass(const vsamp_args* args, float* tile_max, uint32_t* arrive, void* stream);

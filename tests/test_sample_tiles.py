@@ -1,8 +1,9 @@
-"""The draw over bf16 logits with their tile maxima: from the LM head's epilogue
-(``vsamp_sample_tiles``) or from a launch of their own (``vsamp_sample_tile_pass``, which the
-per-token call takes for the rows the maxima decide).
+"""The draw over logits with their tile maxima: bf16 logits from the LM head's epilogue
+(``vsamp_sample_tiles``), or bf16 and fp32 logits whose maxima a launch computes itself
+(``vsamp_sample_tile_pass``, which the per-token call and small batches take).
 
-``sample_tiles`` must give exactly what ``sample_batch`` gives on the same logits and arguments:
+Both must give exactly what the row passes give on the same logits and arguments (``sample_batch``
+with ``tile_pass`` off):
 the same ids and the same draft probabilities, bit for bit, whether a row is decided from a few
 tiles (greedy rows, and top-k or min-p rows, without penalties) or takes the row passes
 (penalties, top-p alone, NaN and infinite rows, too many candidates). Both are then checked
@@ -32,6 +33,15 @@ TILE = _lib.LM_TILE
 
 def hip():
     return SAMPLER.resolve("hip", BackendContext(DEV, torch.bfloat16))
+
+
+def row_passes(s, *args):
+    """``sample_batch`` through the row passes alone (no tile pass)."""
+    s.tile_pass = False
+    try:
+        return s.sample_batch(*args)
+    finally:
+        s.tile_pass = True
 
 
 def tile_max(logits: torch.Tensor) -> torch.Tensor:
@@ -86,10 +96,12 @@ def check(logits, params, seed, hist=None, label=""):
     d = lambda t: None if t is None else t.to(DEV)  # noqa: E731
     print(f"sample_tiles {label} B={B} V={V}", flush=True)
     a, ap = s.sample_tiles(logits, tm, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
-    b, bp = s.sample_batch(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
+    b, bp = row_passes(s, logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
+    c, cp = s.sample_batch(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))  # (a small batch: the tile pass)
     torch.cuda.synchronize()
     assert torch.equal(a.cpu(), b.cpu()), (label, a.cpu(), b.cpu())
     assert torch.equal(ap.cpu().view(torch.int32), bp.cpu().view(torch.int32)), label
+    assert torch.equal(c.cpu(), b.cpu()) and torch.equal(cp.cpu().view(torch.int32), bp.cpu().view(torch.int32)), label
     w = Workload(label, logits.cpu(), pp, u, hi, ho, draft)
     ties, bad = compare_ids(a.cpu(), oracle(w), ap.cpu())
     assert not bad, (label, bad[:10])
@@ -179,19 +191,24 @@ def test_gpu_sample_tiles_rejects_bad_arguments():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,V,pad,offset", [(1, 151936, 0, 0), (3, 4099, 5, 0), (8, 151936, 0, 3), (16, 20000, 0, 0),
-                                            (2, 100, 0, 1), (16, 151936, 0, 0), (13, 151936, 0, 1)])
-def test_gpu_tile_pass_equals_sample_batch(B, V, pad, offset):
-    # bf16 logits from any source: the tile maxima computed by the same launch while B times the
+@pytest.mark.parametrize("B,V,pad,offset,dtype", [
+    (1, 151936, 0, 0, torch.bfloat16), (3, 4099, 5, 0, torch.bfloat16), (8, 151936, 0, 3, torch.bfloat16),
+    (16, 20000, 0, 0, torch.bfloat16), (2, 100, 0, 1, torch.bfloat16), (16, 151936, 0, 0, torch.bfloat16),
+    (13, 151936, 0, 1, torch.bfloat16),
+    (1, 151936, 0, 0, torch.float32), (3, 4099, 5, 0, torch.float32), (8, 151936, 0, 3, torch.float32),
+    (2, 100, 0, 1, torch.float32), (14, 151936, 0, 0, torch.float32), (13, 151936, 0, 2, torch.float32)])
+def test_gpu_tile_pass_equals_sample_batch(B, V, pad, offset, dtype):
+    # logits from any source: the tile maxima computed by the same launch while B times the
     # workgroups per row fits one round on the CUs (B <= 13 at V = 151936), else by their own
-    # launch first (rows unaligned when offset is odd: the maxima are read element by element)
+    # launch first (rows not 16-byte aligned when offset is not a multiple of 16 bytes: the
+    # maxima are read element by element); against the row passes and the oracle
     g = torch.Generator().manual_seed(B * 7 + V)
     rng = np.random.default_rng(V + B)
     x = torch.randn(B, V, generator=g) * 2.0
     x[:, :5] += 8.0
-    buf = torch.zeros(B * (V + pad) + offset + 8, dtype=torch.bfloat16)
+    buf = torch.zeros(B * (V + pad) + offset + 8, dtype=dtype)
     view = buf[offset : offset + B * (V + pad)].view(B, V + pad)[:, :V]
-    view.copy_(x.to(torch.bfloat16))
+    view.copy_(x.to(dtype))
     logits = buf.to(DEV)[offset : offset + B * (V + pad)].view(B, V + pad)[:, :V]
     params = mixed_params(rng, B, V, penalties_every=4)
     hist = [rng.integers(0, V, 50).tolist() for _ in range(B)]
@@ -200,10 +217,10 @@ def test_gpu_tile_pass_equals_sample_batch(B, V, pad, offset):
     u = torch.from_numpy(rng.random(B, dtype=np.float32))
     draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
     s = hip()
-    print(f"tile pass B={B} V={V} pad={pad} offset={offset}", flush=True)
+    print(f"tile pass B={B} V={V} pad={pad} offset={offset} {dtype}", flush=True)
     d = lambda t: t.to(DEV)  # noqa: E731
     a, ap = s.sample_tile_pass(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
-    b, bp = s.sample_batch(logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
+    b, bp = row_passes(s, logits, pp.to(DEV), d(u), d(hi), d(ho), d(draft))
     torch.cuda.synchronize()
     # (small batches run one launch whose rows' last workgroups reset the arrival words)
     assert not s._local.tiles[DEV][1].any()
@@ -228,9 +245,59 @@ def test_gpu_per_token_call_through_the_tile_pass():
              SamplingParams(temperature=1.0, min_p=0.2, top_p=0.95), SamplingParams(temperature=1.3, top_k=256),
              SamplingParams(temperature=0.9, top_k=300)]
     print("per-token call through the tile pass", flush=True)
-    for ci, sp in enumerate(cases):
-        for pos in range(6):
-            tok = s.sample(row, sp, 3 + ci, pos)
-            u = torch.tensor([uniform(3 + ci, pos)], dtype=torch.float32, device=DEV)
-            want, _ = s.sample_batch(row.view(1, V), pack_params([sp], DEV), u)
-            assert tok == int(want[0]), (ci, pos)
+    for r in (row, (torch.randn(V, generator=g) * 2).to(DEV)):  # (bf16, then fp32)
+        for ci, sp in enumerate(cases):
+            for pos in range(6):
+                tok = s.sample(r, sp, 3 + ci, pos)
+                u = torch.tensor([uniform(3 + ci, pos)], dtype=torch.float32, device=DEV)
+                want, _ = row_passes(s, r.view(1, V), pack_params([sp], DEV), u)
+                assert tok == int(want[0]), (r.dtype, ci, pos)
+
+
+@pytest.mark.gpu
+def test_gpu_tile_pass_on_crafted_fp32_rows():
+    # fp32 rows whose values bf16 cannot hold: ties of the max across tiles below bf16's
+    # resolution, signed zeros, -inf, NaN and +inf rows, a top-k boundary inside a tie of 300
+    V = 4099
+    g = torch.Generator().manual_seed(5)
+    base = torch.randn(V, generator=g, dtype=torch.float64).float()
+    rows = []
+    x = base.clone()
+    x[[700, 300, 4098]] = 9.000001
+    x[301] = 9.0  # (just below the max: one fp32 ulp apart)
+    rows.append(x)
+    x = -base.abs() - 1.0
+    x[2000] = 0.0
+    x[129] = -0.0
+    rows.append(x)
+    rows.append(torch.full((V,), -math.inf))
+    x = base.clone()
+    x[1500] = float("nan")
+    rows.append(x)
+    x = base.clone()
+    x[17] = math.inf
+    rows.append(x)
+    x = base * 1e-6  # values packed into a tiny range: many tiles' maxima within a few ulps
+    rows.append(x)
+    x = base.clone()
+    x[:300] = 5.0
+    rows.append(x)
+    logits = torch.stack(rows).to(DEV)
+    B = logits.shape[0]
+    s = hip()
+    rng = np.random.default_rng(2)
+    for T, kw in [(0.0, {}), (1.0, dict(top_k=20)), (0.7, dict(min_p=0.3)), (1.2, dict(top_k=5, min_p=0.05)),
+                  (1.0, dict(top_k=1)), (0.5, dict(top_k=20, top_p=0.5)), (0.9, dict(top_k=256))]:
+        params = [SamplingParams(temperature=T, **kw) for _ in range(B)]
+        pp = pack_params(params)
+        u = torch.from_numpy(rng.random(B, dtype=np.float32))
+        draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
+        print(f"crafted fp32 T={T} {kw}", flush=True)
+        a, ap = s.sample_tile_pass(logits, pp.to(DEV), u.to(DEV), None, None, draft.to(DEV))
+        b, bp = row_passes(s, logits, pp.to(DEV), u.to(DEV), None, None, draft.to(DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(a.cpu(), b.cpu()), (T, kw, a.cpu(), b.cpu())
+        assert torch.equal(ap.cpu().view(torch.int32), bp.cpu().view(torch.int32)), (T, kw)
+        w = Workload("crafted fp32", logits.cpu(), pp, u, None, None, draft)
+        ties, bad = compare_ids(a.cpu(), oracle(w), ap.cpu())
+        assert not bad, (T, kw, bad[:10])

@@ -338,6 +338,23 @@ int run_sample(const vsamp_args* a, float* probs, int64_t probs_stride, hipStrea
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_sample");
 }
 
+template <class Tin>
+int run_tile_pass(const vsamp_args* a, float* tile_max, uint32_t* arrive, hipStream_t st) {
+  const int nT = (a->vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
+  // One launch while the rows' workgroups fit one round on the CUs: G per row, each the maxima of
+  // at most 64 tiles (one or two 16-byte loads per thread), the last of a row's G finishing it;
+  // larger batches take a launch of the maxima first (256-thread workgroups), then the draw.
+  const int G = (nT + vs::kTileSharePasses * vs::kWave - 1) / (vs::kTileSharePasses * vs::kWave);
+  if (static_cast<int64_t>(a->batch) * G <= vs::kTileFusedWorkgroups)
+    return run_sample<Tin>(a, nullptr, 0, st, nullptr, 1, tile_max, arrive, G);
+  hipLaunchKernelGGL(vs::k_tile_max<Tin>, dim3((nT + vs::kTilesPerBlock - 1) / vs::kTilesPerBlock, a->batch),
+                     dim3(vs::kTileMaxThreads), 0, st, static_cast<const Tin*>(a->logits), a->row_stride, a->vocab, nT,
+                     tile_max);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "launch k_tile_max");
+  return run_sample<Tin>(a, nullptr, 0, st, nullptr, 1, tile_max);
+}
+
 struct VerifyLayout {
   size_t tids, dids, ts, ds, jr, done, sums, rej, nrej, total;
 };
@@ -412,26 +429,14 @@ int vsamp_sample_tiles(const vsamp_args* a, const float* tile_max, void* stream)
 int vsamp_sample_tile_pass(const vsamp_args* a, float* tile_max, uint32_t* arrive, void* stream) {
   g_err.clear();
   if (int rc = validate(a, true)) return rc;
-  if (a->dtype != VSAMP_BF16) return fail(VSAMP_E_DTYPE, "vsamp_sample_tile_pass takes bf16 logits");
   if (a->batch == 0) return VSAMP_OK;
   if (!tile_max || !arrive) return fail(VSAMP_E_ARG, "tile_max and arrive must be set");
   if ((reinterpret_cast<uintptr_t>(tile_max) | reinterpret_cast<uintptr_t>(arrive)) & 3u)
     return fail(VSAMP_E_ARG, "tile_max and arrive must be 4-byte aligned");
   if (int rc = check_current_device()) return rc;
-  const int nT = (a->vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // One launch while the rows' workgroups fit one round on the CUs: G per row, each the maxima of
-  // at most 64 tiles (one 16-byte load per thread), the last of a row's G finishing it; larger
-  // batches take a launch of the maxima first (256-thread workgroups), then the draw.
-  const int G = (nT + vs::kTileSharePasses * vs::kWave - 1) / (vs::kTileSharePasses * vs::kWave);
-  if (static_cast<int64_t>(a->batch) * G <= vs::kTileFusedWorkgroups)
-    return run_sample<uint16_t>(a, nullptr, 0, st, nullptr, 1, tile_max, arrive, G);
-  hipLaunchKernelGGL(vs::k_tile_max, dim3((nT + vs::kTilesPerBlock - 1) / vs::kTilesPerBlock, a->batch),
-                     dim3(vs::kTileMaxThreads), 0, st, static_cast<const uint16_t*>(a->logits), a->row_stride,
-                     a->vocab, nT, tile_max);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "launch k_tile_max");
-  return run_sample<uint16_t>(a, nullptr, 0, st, nullptr, 1, tile_max);
+  return a->dtype == VSAMP_BF16 ? run_tile_pass<uint16_t>(a, tile_max, arrive, st)
+                                : run_tile_pass<float>(a, tile_max, arrive, st);
 }
 
 int vsamp_sample_noalloc(const vsamp_args* a, void* stream) {

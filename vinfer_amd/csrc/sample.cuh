@@ -2943,25 +2943,53 @@ __device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk,
 constexpr int kTileFusedWorkgroups = 256;  // (one round on the CUs; vsamp_sample_tile_pass)
 constexpr int kTileMaxThreads = 256;
 constexpr int kTilesPerBlock = kTileMaxThreads / 16;
-__global__ __launch_bounds__(kTileMaxThreads) void k_tile_max(const uint16_t* logits, int64_t stride, int V,
-                                                             int nT, float* out) {
+// A lane's eight logits of a tile (16-byte loads: one of bf16, two of fp32) and their largest key.
+template <class Tin>
+constexpr int kTileLoads = sizeof(Tin) == 2 ? 1 : 2;
+template <class Tin>
+__device__ __forceinline__ uint32_t lane_tile_key(const uint4 (&v)[kTileLoads<Tin>]) {
+  uint32_t mk = 0;  // (below every key)
+#pragma unroll
+  for (int j = 0; j < kTileLoads<Tin>; ++j) {
+    const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (sizeof(Tin) == 2) {
+        mk = max(mk, key_of(__uint_as_float(w[i] << 16)));
+        mk = max(mk, key_of(__uint_as_float(w[i] & 0xFFFF0000u)));
+      } else {
+        mk = max(mk, key_of(__uint_as_float(w[i])));
+      }
+    }
+  }
+  return mk;
+}
+// The same for a lane whose eight logits are not one aligned run inside the row: element by
+// element (fewer past the end).
+template <class Tin>
+__device__ __forceinline__ uint32_t lane_tile_key_each(const Tin* row, int i0, int V) {
+  uint32_t mk = 0;
+  for (int i = i0; i < i0 + 8 && i < V; ++i) mk = max(mk, key_of(load_one<Tin>(row, i)));
+  return mk;
+}
+
+template <class Tin>
+__global__ __launch_bounds__(kTileMaxThreads) void k_tile_max(const Tin* logits, int64_t stride, int V, int nT,
+                                                             float* out) {
   const int r = blockIdx.y;
   const int l16 = threadIdx.x & 15;
   const int t = blockIdx.x * kTilesPerBlock + (threadIdx.x >> 4);  // (the same in a 16-lane row)
-  const uint16_t* row = as_global(logits) + static_cast<int64_t>(r) * stride;
+  const Tin* row = as_global(logits) + static_cast<int64_t>(r) * stride;
   const int i0 = t * kStatTile + 8 * l16;  // this lane's first logit
   uint32_t mk = 0;                         // (below every key)
   if (t < nT) {
     if ((reinterpret_cast<uintptr_t>(row + i0) & 15u) == 0 && i0 + 8 <= V) {
-      const uint4 q = ld_global_u4(reinterpret_cast<const uint4*>(row + i0));
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+      uint4 q[kTileLoads<Tin>];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        mk = max(mk, key_of(__uint_as_float(w[i] << 16)));
-        mk = max(mk, key_of(__uint_as_float(w[i] & 0xFFFF0000u)));
-      }
+      for (int j = 0; j < kTileLoads<Tin>; ++j) q[j] = ld_global_u4(reinterpret_cast<const uint4*>(row + i0) + j);
+      mk = lane_tile_key<Tin>(q);
     } else {
-      for (int i = i0; i < i0 + 8 && i < V; ++i) mk = max(mk, key_of(bf16_to_f32(ld_global(row + i))));
+      mk = lane_tile_key_each<Tin>(row, i0, V);
     }
   }
   auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
@@ -2981,42 +3009,37 @@ __global__ __launch_bounds__(kTileMaxThreads) void k_tile_max(const uint16_t* lo
 // One pass (at most 64 tiles a workgroup): more workgroups a row measured faster than four passes
 // (a CU reading 16 KB of the row instead of 64 KB; 11.7 against 13.2 us for one 151936-logit row).
 constexpr int kTileSharePasses = 1;
+template <class Tin>
 __device__ __forceinline__ bool tile_share(const SampleArgs& a, int r, int g, int* flag) {
   const int G = a.tile_G, nT = a.nT;
   const int per = (nT + G - 1) / G;
   const int end = min(nT, (g + 1) * per);
   const int l16 = threadIdx.x & 15;
-  const uint16_t* row = as_global(static_cast<const uint16_t*>(a.logits)) + static_cast<int64_t>(r) * a.stride;
+  const Tin* row = as_global(static_cast<const Tin*>(a.logits)) + static_cast<int64_t>(r) * a.stride;
   const int V = a.V;
   float* out = const_cast<float*>(a.tile_max) + static_cast<int64_t>(r) * nT;
   // pass q: tile g * per + threadIdx.x / 16 + 64 q (the same in a 16-lane row); whole aligned
   // 16-byte chunks are loaded first (every lane issues its loads: one that has none reads a
   // constant aligned block, unused), the rest element by element
-  uint4 v[kTileSharePasses];
+  uint4 v[kTileSharePasses][kTileLoads<Tin>];
   bool whole[kTileSharePasses];
 #pragma unroll
   for (int q = 0; q < kTileSharePasses; ++q) {
     const int t = g * per + static_cast<int>(threadIdx.x >> 4) + kWave * q;
     const int i0 = t * kStatTile + 8 * l16;
     whole[q] = t < end && (reinterpret_cast<uintptr_t>(row + i0) & 15u) == 0 && i0 + 8 <= V;
-    v[q] = ld_global_u4(whole[q] ? reinterpret_cast<const uint4*>(row + i0) : reinterpret_cast<const uint4*>(g_unused_block));
+#pragma unroll
+    for (int j = 0; j < kTileLoads<Tin>; ++j)
+      v[q][j] = ld_global_u4(whole[q] ? reinterpret_cast<const uint4*>(row + i0) + j
+                                      : reinterpret_cast<const uint4*>(g_unused_block));
   }
   auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
 #pragma unroll
   for (int q = 0; q < kTileSharePasses; ++q) {
     const int t = g * per + static_cast<int>(threadIdx.x >> 4) + kWave * q;
     uint32_t mk = 0;  // (below every key)
-    if (whole[q]) {
-      const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        mk = max(mk, key_of(__uint_as_float(w[i] << 16)));
-        mk = max(mk, key_of(__uint_as_float(w[i] & 0xFFFF0000u)));
-      }
-    } else if (t < end) {
-      const int i0 = t * kStatTile + 8 * l16;
-      for (int i = i0; i < i0 + 8 && i < V; ++i) mk = max(mk, key_of(bf16_to_f32(ld_global(row + i))));
-    }
+    if (whole[q]) mk = lane_tile_key<Tin>(v[q]);
+    else if (t < end) mk = lane_tile_key_each<Tin>(row, t * kStatTile + 8 * l16, V);
     mk = umax(mk, dpp::mov<dpp::kXor1>(mk));
     mk = umax(mk, dpp::mov<dpp::kXor2>(mk));
     mk = umax(mk, dpp::mov<dpp::kHalfMirror>(mk));
@@ -3050,8 +3073,8 @@ __device__ __forceinline__ bool tile_candidate(const SampleArgs& a, const RowPar
 
 // Returns true when the row was decided (outputs written) from its tile maxima; false, having
 // written nothing, when it needs the row passes. Every thread calls; `p.u` is clamped to >= 0.
-template <bool PEN>
-__device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t>& row, const RowParams& p, GenericSmem& g,
+template <bool PEN, class Tin>
+__device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<Tin>& row, const RowParams& p, GenericSmem& g,
                                          int r) {
   const int tid = threadIdx.x;
   const int V = row.V;
@@ -3095,7 +3118,7 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t
 #pragma unroll
       for (int h = 1; h >= 0; --h) {
         const int i = static_cast<int>(first) * kStatTile + tid + h * kWave;
-        if (i < V && load_one<uint16_t>(row.p, i) == M) id = static_cast<uint32_t>(i);
+        if (i < V && load_one<Tin>(row.p, i) == M) id = static_cast<uint32_t>(i);
       }
       id = dpp::reduce(id, [](uint32_t x, uint32_t y) { return x < y ? x : y; });
       if (tid == 0) sh[0] = id;
@@ -3155,8 +3178,15 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t
       const uint32_t incl2 = above + wave_incl_scan<uint32_t>(c);
       const int i = __ffsll(static_cast<long long>(__ballot(incl2 >= K))) - 1;
       const uint32_t bin = static_cast<uint32_t>(4095 - 64 * L - i);
-      const uint32_t k16 = (bin << 4) > 0x007Fu ? (bin << 4) : 0x007Fu;  // (not below -inf's key)
-      const float theta = val16(k16);
+      // the bin's least value (not below -inf): of bf16 values, its least 16-bit key's
+      float theta;
+      if constexpr (sizeof(Tin) == 2) {
+        const uint32_t k16 = (bin << 4) > 0x007Fu ? (bin << 4) : 0x007Fu;
+        theta = val16(k16);
+      } else {
+        const uint32_t k32 = (bin << 20) > key_of(-INFINITY) ? (bin << 20) : key_of(-INFINITY);
+        theta = val_of(k32);
+      }
       const float zt = theta / T;
       xlo = val_of(wave_bisect(lo_key, key_of(theta), key_of(zt * T), [&](float x) { return x / T >= zt; }));
     }
@@ -3203,7 +3233,7 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<uint16_t
   for (int q = 0; q < kPer; ++q) {
     const int e = tid + q * kThreads;
     ids[q] = e < static_cast<int>(ntile) * kStatTile ? ctile[e / kStatTile] * kStatTile + e % kStatTile : V;
-    xs[q] = load_one<uint16_t>(row.p, ids[q] < V ? ids[q] : 0);
+    xs[q] = load_one<Tin>(row.p, ids[q] < V ? ids[q] : 0);
   }
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
@@ -3262,7 +3292,7 @@ __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
 
 // STATE: also write each row's RowState (the speculative verify's launches; never with PEN).
 // SPLIT: a bf16 split-row launch (grid B * G).
-// TILES: bf16 rows with their tile maxima (a.tile_max): the rows tile_row can decide are decided
+// TILES: rows (bf16 or fp32) with their tile maxima (a.tile_max): the rows tile_row can decide are decided
 // from a few tiles, the others take the row passes below.
 template <class Tin, bool PEN, bool STATE = false, bool SPLIT = false, bool TILES = false>
 __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
@@ -3293,7 +3323,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   row.eid = f.eid;   // the fast path keeps the penalised ids and values in LDS
   row.eval = f.eval;
   GenericSmem& g = *reinterpret_cast<GenericSmem*>(big);
-  if constexpr (TILES && sizeof(Tin) == 2 && !STATE && !SPLIT) {
+  if constexpr (TILES && !STATE && !SPLIT) {
     if (tid < kParamWords) reinterpret_cast<uint32_t*>(&f.prm)[tid] = pw;
     lds_barrier();
     RowParams pt = f.prm;
@@ -3305,10 +3335,10 @@ __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
     if (fused) {
       const int gi = static_cast<int>(blockIdx.x) % a.tile_G;
       try_tiles = tile_candidate<PEN>(a, pt);  // (uniform)
-      if (try_tiles ? !tile_share(a, r, gi, &f.si[7]) : gi != 0) return;
+      if (try_tiles ? !tile_share<Tin>(a, r, gi, &f.si[7]) : gi != 0) return;
     }
     if (try_tiles) {
-      if (tile_row<PEN>(a, row, pt, g, r)) return;
+      if (tile_row<PEN, Tin>(a, row, pt, g, r)) return;
       lds_barrier();  // (every thread is done with the tile path's LDS)
     }
   }

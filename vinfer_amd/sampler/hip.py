@@ -59,6 +59,9 @@ class HipSampler:
         # Split small bf16 batches' rows over several workgroups (VSAMP_SPLIT_ROWS): identical
         # results, slower than whole rows on MI355X at every batch measured, so off by default.
         self.split_rows = False
+        # Small batches take the tile pass in one launch (vsamp_sample_tile_pass), whose rows the
+        # tile maxima decide from a few tiles; identical results. False: the row passes only.
+        self.tile_pass = True
 
     # ---- argument checks ---------------------------------------------------------------------
     def _device(self, logits: torch.Tensor) -> torch.device:
@@ -194,15 +197,14 @@ class HipSampler:
         del keep
         return ids, dprob
 
-    @staticmethod
-    def _one_launch_tiles(a, logits: torch.Tensor) -> bool:
-        """Whether a batch takes the tile pass as one launch (``vsamp_sample_tile_pass``): bf16
-        rows, few enough that their workgroups fit one round on the CUs, and no split rows. Its
-        greedy and top-k rows without penalties are then decided from a few tiles; the other
-        rows run the row passes on one workgroup each, as ``vsamp_sample`` would (the same
-        outputs either way)."""
+    def _one_launch_tiles(self, a, logits: torch.Tensor) -> bool:
+        """Whether a batch takes the tile pass as one launch (``vsamp_sample_tile_pass``): rows
+        few enough that their workgroups fit one round on the CUs, no split rows, and
+        ``tile_pass`` on. Its greedy and top-k rows without penalties are then decided from a few
+        tiles; the other rows run the row passes on one workgroup each, as ``vsamp_sample`` would
+        (the same outputs either way)."""
         B, V = logits.shape
-        return (logits.dtype == torch.bfloat16 and not (a.flags & _lib.VSAMP_SPLIT_ROWS)
+        return (self.tile_pass and not (a.flags & _lib.VSAMP_SPLIT_ROWS)
                 and B * ((_n_tiles(V) + 63) // 64) <= _TILE_FUSED_WORKGROUPS)
 
     def probs(self, logits, params, hist_ids=None, hist_offsets=None):
@@ -338,13 +340,11 @@ class HipSampler:
         return ids, dprob
 
     def sample_tile_pass(self, logits, params, uniforms, hist_ids=None, hist_offsets=None, draft_ids=None):
-        """``sample_batch`` for small batches of bf16 logits from any source
+        """``sample_batch`` for small batches of bf16 or fp32 logits from any source
         (``vsamp_sample_tile_pass``): the rows' tile maxima are computed by a launch spread over
         the chip first, then greedy, top-k and min-p rows without penalties are decided from a
         few tiles. The same ids and draft probabilities as ``sample_batch``."""
         dev = self._device(logits)
-        if logits.dtype != torch.bfloat16:
-            raise ValueError("sample_tile_pass takes bf16 logits")
         B, V = logits.shape
         a, keep = self._args(logits, params, hist_ids, hist_offsets, uniforms, draft_ids)
         a.flags &= ~_lib.VSAMP_SPLIT_ROWS
@@ -546,12 +546,13 @@ class HipSampler:
         stream = self._stream(dev)
         out = t.out_np
         out[0] = -1
-        # bf16 greedy and top-k (<= 256) rows without penalties take the tile pass: the row's tile
+        # Greedy and top-k (<= 256) rows without penalties take the tile pass: the row's tile
         # maxima over the chip, then a few tiles, instead of the whole row on one workgroup
-        # (greedy 29.9 -> 24.7 us per call, top-k 20 34.2 -> 31.0 on MI355X). Rows with min-p alone
-        # do not: their candidates depend on the logits (N(0, 4) rows keep ~900 tokens at min-p
-        # 0.05, more than the tile path's list), and a row handed on pays both launches.
-        if (row.dtype == torch.bfloat16 and n == 0 and not pen
+        # (bf16: greedy 29.9 -> 24.7 us per call, top-k 20 34.2 -> 31.0 on MI355X, as first
+        # built). Rows with min-p alone do not: their candidates depend on the logits (N(0, 4) rows
+        # keep ~900 tokens at min-p 0.05, more than the tile path's list), and a row handed on pays
+        # both launches.
+        if (self.tile_pass and n == 0 and not pen
                 and (not params.temperature > 0 or 0 < top_k <= 256 and top_k < V)):
             code = self._lib.vsamp_sample_tile_pass(t.ref, t.tiles[0], t.tiles[1], stream)
         else:
@@ -649,7 +650,7 @@ class PreparedStep:
         self._ref = ctypes.byref(args)
         self.ids, self.draft_prob = ids, dprob
         self._tiles = None if tile_max is None else ctypes.c_void_p(tile_max.data_ptr())
-        # (a small bf16 batch: the tile pass in one launch, on the step's own maxima and arrival words)
+        # (a small batch: the tile pass in one launch, on the step's own maxima and arrival words)
         self._pass = tile_pass
         self._pass_ptrs = None if tile_pass is None else tuple(ctypes.c_void_p(t.data_ptr()) for t in tile_pass)
 
