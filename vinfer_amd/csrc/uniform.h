@@ -198,8 +198,7 @@ VS_HD uint64_t position_seed(int64_t seed, int64_t position) {
   uint32_t m[12];
 #pragma unroll
   for (int j = 0; j < 12; ++j) m[j] = 0;
-  place_byte(m, '-', 0);
-  m[0] = s1 ? m[0] : 0u;  // (a '-' only for a negative seed)
+  place_byte(m, s1 ? '-' : 0u, 0);  // (a zero byte adds nothing)
   place(m, t1, s1);
   place_byte(m, ':', s1 + n1);
   place_byte(m, s2 ? '-' : 0u, s1 + n1 + 1);
