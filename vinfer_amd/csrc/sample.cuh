@@ -2870,9 +2870,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
   return true;
 }
 
-// ---- rows decided from the LM head's tile maxima (vsamp_sample_tiles) ------------------------
+// ---- rows decided from their tile maxima (vsamp_sample_tiles, vsamp_sample_tile_pass) ---------
 // k_lm_head writes, beside the bf16 logits, the max of every kStatTile consecutive logits of a
-// row (as a value: the max of bf16 values, NaN the largest). For some rows those maxima bound
+// row (as a value: NaN the largest); the tile pass computes the same maxima of bf16 or fp32
+// rows from any source. For some rows those maxima bound
 // where every token the draw can keep lies, and the row is decided from a few tiles:
 //   * greedy rows: the first id holding the row max lies in the first tile whose max equals the
 //     row max (as values: -0 equals +0), and only that tile is read;
@@ -2935,7 +2936,7 @@ __device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk,
   return (hi << 8) | sh[0];
 }
 
-// The tile maxima of bf16 rows from any source (what k_lm_head's epilogue writes beside its
+// The tile maxima of bf16 or fp32 rows from any source (what k_lm_head's epilogue writes beside its
 // logits): the max of every kStatTile consecutive logits of a row, as a value (ordered keys: a
 // NaN is the largest; -0.0 and +0.0 are one value). Sixteen lanes take a tile, eight logits a
 // lane, and reduce over their 16-lane row; grid (ceil(nT / 16), B) of 256-thread workgroups, so
