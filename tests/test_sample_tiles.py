@@ -301,3 +301,35 @@ def test_gpu_tile_pass_on_crafted_fp32_rows():
         w = Workload("crafted fp32", logits.cpu(), pp, u, None, None, draft)
         ties, bad = compare_ids(a.cpu(), oracle(w), ap.cpu())
         assert not bad, (T, kw, bad[:10])
+
+
+@pytest.mark.gpu
+def test_gpu_tile_pass_random_shapes_and_parameters():
+    # seeded random batches of either dtype, vocabularies with ragged last tiles, peaked and flat
+    # rows, every kind of parameters: the tile pass against the row passes, and the oracle
+    s = hip()
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        dtype = torch.float32 if case % 2 else torch.bfloat16
+        B = int(rng.integers(1, 14))
+        V = int(rng.choice([int(rng.integers(100, 5000)), int(rng.integers(5000, 60000)), 151936]))
+        scale = float(rng.choice([0.01, 1.0, 3.0]))
+        g = torch.Generator().manual_seed(case)
+        x = torch.randn(B, V, generator=g) * scale
+        peaked = rng.random(B) < 0.3
+        for b in np.nonzero(peaked)[0]:
+            x[b, int(rng.integers(0, V))] += 12.0
+        logits = x.to(dtype).to(DEV)
+        params = mixed_params(rng, B, V)
+        pp = pack_params(params)
+        u = torch.from_numpy(rng.random(B, dtype=np.float32))
+        draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
+        print(f"random tile pass case {case}: B={B} V={V} {dtype} scale={scale}", flush=True)
+        a, ap = s.sample_tile_pass(logits, pp.to(DEV), u.to(DEV), None, None, draft.to(DEV))
+        b, bp = row_passes(s, logits, pp.to(DEV), u.to(DEV), None, None, draft.to(DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(a.cpu(), b.cpu()), (case, a.cpu(), b.cpu())
+        assert torch.equal(ap.cpu().view(torch.int32), bp.cpu().view(torch.int32)), case
+        w = Workload("random tile pass", logits.cpu(), pp, u, None, None, draft)
+        ties, bad = compare_ids(a.cpu(), oracle(w), ap.cpu())
+        assert not bad, (case, bad[:10])
