@@ -457,10 +457,11 @@ def logprobs_bench(args) -> int:
 
 def lm_head_bench(args) -> int:
     """``--lm-head``: the LM head plus log-probabilities (token and top 20) at d=4096, V=151936,
-    B in {256, 64, 1}: unfused (torch's bf16 matmul, i.e. hipBLASLt, then ``vsamp_logprobs``'s two
-    passes over each row) against fused (``vsamp_lm_head``: the hand-written MFMA GEMM whose
-    epilogue writes the tile statistics, then ``vsamp_logprobs_tiles``). One JSON line per batch,
-    HIP events on the launch stream, synthetic bf16 operands."""
+    B in {256, 64, 1}: unfused (the engine's ``F.linear(hidden, W)``, i.e. hipBLASLt, then
+    ``vsamp_logprobs``'s two passes over each row) against fused (the backend's ``lm_head``: up to
+    64 rows ``vsamp_lm_head``, the hand-written GEMM whose epilogue writes the tile statistics;
+    above, ``F.linear`` and ``vsamp_tile_stats``; then ``vsamp_logprobs_tiles``). One JSON line
+    per batch, HIP events on the launch stream, synthetic bf16 operands."""
     import math
 
     import torch
@@ -491,10 +492,11 @@ def lm_head_bench(args) -> int:
             torch.cuda.synchronize()
             return e0.elapsed_time(e1) * 1e3 / n
 
-        logits_t = hidden @ W.T
+        linear = torch.nn.functional.linear
+        logits_t = linear(hidden, W)
         logits_f, tmax, tsum = s.lm_head(hidden, W)
         us = {
-            "torch_matmul": timed(lambda: hidden @ W.T),
+            "torch_matmul": timed(lambda: linear(hidden, W)),
             "logprobs_rows": timed(lambda: s.logprobs(logits_t, tokens, n_top)),
             "lm_head_fused": timed(lambda: s.lm_head(hidden, W)),
             "logprobs_tiles": timed(lambda: s.logprobs_tiles(logits_f, tmax, tsum, tokens, n_top)),
@@ -506,7 +508,9 @@ def lm_head_bench(args) -> int:
         bytes_ = V * d * 2 + B * d * 2 + B * V * 2 + B * nT * 8
         flops = 2.0 * B * d * V
         t = us["lm_head_fused"] * 1e-6
-        print(json.dumps({"lm_head": {"batch": B, "dim": d, "vocab": V, "n_top": n_top}, "us": us,
+        path = ("vsamp_lm_head: k_lm_gemv" if B <= 4 else "vsamp_lm_head: k_lm_stream" if B <= 64
+                else "F.linear + vsamp_tile_stats")
+        print(json.dumps({"lm_head": {"batch": B, "dim": d, "vocab": V, "n_top": n_top, "path": path}, "us": us,
                           "fused_speedup": us["unfused_total"] / us["fused_total"],
                           "k_lm_head": {"tflops": flops / t / 1e12, "mfma_frac_bf16": flops / t / 2.5e15,
                                         "gbs": bytes_ / t / 1e9, "hbm_frac": bytes_ / t / 1e9 / HBM_PEAK_GBS,
@@ -517,11 +521,12 @@ def lm_head_bench(args) -> int:
 
 
 def lm_head_sample_bench(args) -> int:
-    """``--lm-head-sample``: the LM head plus the draw at d=4096, V=151936, B in {1, 64}, for three
+    """``--lm-head-sample``: the LM head plus the draw at d=4096, V=151936, B in {1, 64, 256}, for three
     kinds of rows without penalties: greedy, peaked (one logit far above the rest: the hidden
     state near one weight row; T 1.0, top-p 0.95, min-p 0.05 as the headline's peaked rows) and
-    top-k (T 0.7, top-k 20, top-p 0.8). Unfused: torch's bf16 matmul, then ``sample_batch``;
-    fused: ``vsamp_lm_head``, then ``sample_tiles`` over its tile maxima; each draw a prepared
+    top-k (T 0.7, top-k 20, top-p 0.8). Unfused: the engine's ``F.linear``, then ``sample_batch``;
+    fused: the backend's ``lm_head`` (``vsamp_lm_head`` up to 64 rows, ``F.linear`` and
+    ``vsamp_tile_stats`` above), then ``sample_tiles`` over its tile maxima; each draw a prepared
     launch. Both draws are also run on the fused logits, whose ids must agree. One JSON line per
     (batch, kind), HIP events on the launch stream, synthetic bf16 operands."""
     import math
@@ -557,7 +562,7 @@ def lm_head_sample_bench(args) -> int:
         "peaked": SamplingParams(temperature=1.0, top_p=0.95, min_p=0.05),
         "top_k": SamplingParams(temperature=0.7, top_k=20, top_p=0.8),
     }
-    for B in (1, 64):
+    for B in (1, 64, 256):
         for kind, sp in kinds.items():
             hidden = torch.randn(B, d, generator=g, device=dev) * 0.5
             if kind == "peaked":
@@ -566,7 +571,8 @@ def lm_head_sample_bench(args) -> int:
             hidden = hidden.to(torch.bfloat16)
             params = pack_params([sp] * B, dev)
             u = torch.rand(B, generator=g, device=dev)
-            logits_t = hidden @ W.T
+            linear = torch.nn.functional.linear
+            logits_t = linear(hidden, W)
             logits_f, tmax, _ = s.lm_head(hidden, W)
             a, _ = s.sample_tiles(logits_f, tmax, params, u)
             b, _ = s.sample_batch(logits_f, params, u)
@@ -574,7 +580,7 @@ def lm_head_sample_bench(args) -> int:
             st_rows = s.prepare_batch(logits_t, params, u)
             st_tiles = s.prepare_tiles(logits_f, tmax, params, u)
             us = {
-                "torch_matmul": timed(lambda: hidden @ W.T),
+                "torch_matmul": timed(lambda: linear(hidden, W)),
                 "sample_batch": timed(lambda: st_rows.launch(stream.cuda_stream)),
                 "lm_head_fused": timed(lambda: s.lm_head(hidden, W)),
                 "sample_tiles": timed(lambda: st_tiles.launch(stream.cuda_stream)),

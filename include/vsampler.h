@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VSAMP_ABI_VERSION 10
+#define VSAMP_ABI_VERSION 11
 
 /* Bytes of one row's sampling state (vsamp_sample_states), an opaque record. */
 #define VSAMP_ROW_STATE_BYTES 40
@@ -272,6 +272,17 @@ int vsamp_sample_tiles(const vsamp_args* args, const float* tile_max, void* stre
  * finish sooner (the engine's per-token call, B = 1, sampler.py:68-77 via generate.py:129); other
  * rows pay the extra work. (ABI version 10: `arrive` added.) */
 int vsamp_sample_tile_pass(const vsamp_args* args, float* tile_max, uint32_t* arrive, void* stream);
+
+/* The tile statistics vsamp_lm_head writes beside its logits, for bf16 logits another GEMM wrote
+ * (ABI version 11; no counterpart in the reference: it completes `F.linear(hidden, W)`,
+ * models/qwen/model.py:230-233, run by the library's GEMM, which beats vsamp_lm_head's MFMA
+ * tiles above 64 rows): per row of `logits` (device memory, [batch, vocab] bf16, rows
+ * `row_stride` elements apart) and VSAMP_LM_TILE logits, the max (a NaN is the largest) into
+ * `tile_max` and the fp32 sum of exp(x - max) over the tile (0 when the max is infinite or NaN)
+ * into `tile_sum` ([batch, ceil(vocab / VSAMP_LM_TILE)] fp32 each, device memory). For
+ * vsamp_logprobs_tiles and vsamp_sample_tiles. */
+int vsamp_tile_stats(const void* logits, int64_t row_stride, int32_t batch, int32_t vocab, float* tile_max,
+                     float* tile_sum, void* stream);
 
 /* Host function (no device work): the draw's uniform of (seeds[i], positions[i]) into out[i],
  * i < n, all host memory. u = (splitmix64(position_seed(seed, position)) >> 40) * 2^-24, where

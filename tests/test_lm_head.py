@@ -146,3 +146,43 @@ def test_gpu_lm_head_rejects_bad_shapes():
         s.lm_head(h, w)
     with pytest.raises(ValueError):
         s.lm_head(h.float(), w)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,V,pad", [(3, 1000, 0), (5, 4099, 7), (2, 151936, 0), (70, 20000, 3)])
+def test_gpu_tile_stats_of_logits_from_any_gemm(B, V, pad):
+    # vsamp_tile_stats on bf16 rows it did not write (padded strides, a ragged last tile), with
+    # NaN, +inf and all -inf rows and ties of the max: the max exactly, the sums to 1e-5
+    g = torch.Generator().manual_seed(B + V)
+    x = torch.randn(B, V, generator=g) * 3
+    x[0, V // 2] = 40.0
+    x[0, V // 3] = 40.0  # (a tie of the max in two tiles)
+    if B > 1:
+        x[1] = -math.inf
+    if B > 2:
+        x[2, 7] = float("nan")
+        x[2, V - 1] = math.inf
+    buf = torch.zeros(B, V + pad, dtype=torch.bfloat16)
+    buf[:, :V] = x.to(torch.bfloat16)
+    logits = buf.to(DEV)[:, :V]
+    print(f"tile_stats B={B} V={V} pad={pad}", flush=True)
+    tmax, tsum = hip().tile_stats(logits)
+    torch.cuda.synchronize()
+    m, s = tile_stats(logits)
+    same = (tmax.double() == m) | (torch.isnan(tmax.double()) & torch.isnan(m))
+    assert bool(same.all())
+    fin = torch.isfinite(m)
+    torch.testing.assert_close(tsum.double()[fin], s[fin], rtol=1e-5, atol=0)
+    assert bool((tsum[~fin.cpu()] == 0).all())
+
+
+def test_tile_stats_rejects_bad_arguments_before_any_launch():
+    lib = _lib.load()
+    assert lib.vsamp_tile_stats(None, 10, -1, 10, None, None, None) == 1
+    assert "batch" in lib.vsamp_last_error().decode()
+    assert lib.vsamp_tile_stats(None, 5, 2, 10, None, None, None) == 1
+    assert "row_stride" in lib.vsamp_last_error().decode()
+    assert lib.vsamp_tile_stats(None, 10, 2, 0, None, None, None) == 1
+    assert lib.vsamp_tile_stats(None, 10, 0, 10, None, None, None) == 0
+    assert lib.vsamp_tile_stats(None, 10, 2, 10, None, None, None) == 1
+    assert "must be set" in lib.vsamp_last_error().decode()

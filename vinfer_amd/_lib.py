@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libvsampler.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 ROW_STATE_BYTES = 40
 
 VSAMP_BF16 = 0
@@ -39,6 +39,7 @@ EXPORTS = (
     "vsamp_logprobs_tiles",
     "vsamp_sample_tiles",
     "vsamp_sample_tile_pass",
+    "vsamp_tile_stats",
     "vsamp_lm_head",
     "vsamp_sample_states",
     "vsamp_verify",
@@ -193,6 +194,9 @@ def load() -> ctypes.CDLL:
         lib.vsamp_sample_tile_pass.argtypes = [ctypes.POINTER(VsampArgs), ctypes.c_void_p, ctypes.c_void_p,
                                                ctypes.c_void_p]
         lib.vsamp_sample_tile_pass.restype = ctypes.c_int
+        lib.vsamp_tile_stats.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.vsamp_tile_stats.restype = ctypes.c_int
         lib.vsamp_lm_head.argtypes = [ctypes.POINTER(VsampLmHeadArgs), ctypes.c_void_p]
         lib.vsamp_lm_head.restype = ctypes.c_int
         lib.vsamp_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]

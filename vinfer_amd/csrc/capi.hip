@@ -725,6 +725,26 @@ int vsamp_lm_head(const vsamp_lm_head_args* a, void* stream) {
   return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_lm_head");
 }
 
+int vsamp_tile_stats(const void* logits, int64_t row_stride, int32_t batch, int32_t vocab, float* tile_max,
+                     float* tile_sum, void* stream) {
+  g_err.clear();
+  if (batch < 0) return fail(VSAMP_E_ARG, "batch must be >= 0, got %d", batch);
+  if (vocab < 1 || vocab > kMaxVocab)
+    return fail(VSAMP_E_ARG, "vocab must be in [1, %lld], got %d", static_cast<long long>(kMaxVocab), vocab);
+  if (row_stride < vocab)
+    return fail(VSAMP_E_ARG, "row_stride (%lld) must be >= vocab (%d)", static_cast<long long>(row_stride), vocab);
+  if (batch == 0) return VSAMP_OK;
+  if (!logits || !tile_max || !tile_sum) return fail(VSAMP_E_ARG, "logits, tile_max and tile_sum must be set");
+  if (int rc = check_current_device()) return rc;
+  const int nT = (vocab + VSAMP_LM_TILE - 1) / VSAMP_LM_TILE;
+  constexpr int kTiles = vs::kTsThreads / 16;
+  hipLaunchKernelGGL(vs::k_tile_stats, dim3((nT + kTiles - 1) / kTiles, batch), dim3(vs::kTsThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(logits), row_stride, vocab, nT,
+                     tile_max, tile_sum);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VSAMP_OK : hip_fail(e, "launch k_tile_stats");
+}
+
 int vsamp_sample_states(const vsamp_args* a, void* out_states, void* stream) {
   g_err.clear();
   if (int rc = validate(a, true)) return rc;

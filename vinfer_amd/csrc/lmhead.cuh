@@ -436,6 +436,66 @@ __global__ __launch_bounds__(kLsThreads, 1) void k_lm_stream(LmHeadArgs a) {
   }
 }
 
+// ---- the tile statistics of logits from another GEMM ----------------------------------------
+// What the epilogues above write beside their own logits, for bf16 logits another GEMM wrote
+// (above 64 rows the library's GEMM beats the MFMA tiles above): per row and kLmBN logits, the
+// max (ordered keys: a NaN is the largest) and the fp32 sum of exp(x - max) over the tile (0 when
+// the max is infinite or NaN). Sixteen lanes a tile, eight logits a lane, 16-lane DPP reductions
+// (the sum in another order than an epilogue's, so it may differ in the last bits); grid
+// (ceil(nT / 16), B) of 256-thread workgroups.
+constexpr int kTsThreads = 256;
+__global__ __launch_bounds__(kTsThreads) void k_tile_stats(const uint16_t* logits, int64_t stride, int V, int nT,
+                                                           float* tmax, float* tsum) {
+  const int r = blockIdx.y;
+  const int l16 = threadIdx.x & 15;
+  const int t = blockIdx.x * (kTsThreads / 16) + static_cast<int>(threadIdx.x >> 4);  // (the same in a 16-lane row)
+  const uint16_t* row = as_global(logits) + static_cast<int64_t>(r) * stride;
+  const int i0 = t * kLmBN + 8 * l16;  // this lane's first logit
+  float x[8];
+  int nv = 0;  // this lane's logits inside the row
+  if (t < nT) {
+    if ((reinterpret_cast<uintptr_t>(row + i0) & 15u) == 0 && i0 + 8 <= V) {
+      const uint4 q = ld_global_u4(reinterpret_cast<const uint4*>(row + i0));
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(w[i] << 16);
+        x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+      }
+      nv = 8;
+    } else {
+      nv = max(0, min(8, V - i0));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = i < nv ? bf16_to_f32(ld_global(row + i0 + i)) : 0.0f;
+    }
+  }
+  uint32_t mk = 0;  // (below every key)
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < nv) mk = max(mk, key_of(x[i]));
+  auto umax = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  mk = umax(mk, dpp::mov<dpp::kXor1>(mk));
+  mk = umax(mk, dpp::mov<dpp::kXor2>(mk));
+  mk = umax(mk, dpp::mov<dpp::kHalfMirror>(mk));
+  mk = umax(mk, dpp::mov<dpp::kMirror>(mk));
+  const float mx = val_of(mk);
+  float s = 0.0f;
+  if (mx > -INFINITY && mx < INFINITY) {  // (false for a NaN max)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < nv) s += __expf(x[i] - mx);
+  }
+  auto fadd = [](float a, uint32_t b) { return a + __uint_as_float(b); };
+  s = fadd(s, dpp::mov<dpp::kXor1>(__float_as_uint(s)));
+  s = fadd(s, dpp::mov<dpp::kXor2>(__float_as_uint(s)));
+  s = fadd(s, dpp::mov<dpp::kHalfMirror>(__float_as_uint(s)));
+  s = fadd(s, dpp::mov<dpp::kMirror>(__float_as_uint(s)));
+  if (t < nT && l16 == 0) {
+    as_global(tmax)[static_cast<int64_t>(r) * nT + t] = mx;
+    as_global(tsum)[static_cast<int64_t>(r) * nT + t] = s;
+  }
+}
+
 // ---- a few batch rows: matrix-vector products -------------------------------------------------
 // At B <= 4 the 64-row tile above loads 60 or more rows of padding beside each step's weight (a
 // CU's intake, not the HBM, bounds the kernel), so these batches take a kernel of their own:

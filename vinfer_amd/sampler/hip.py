@@ -269,6 +269,13 @@ class HipSampler:
         if d2 != d or weight.device != hidden.device:
             raise ValueError(f"weight must be [V, {d}] on {hidden.device}, got {tuple(weight.shape)} on {weight.device}")
         dev = hidden.device
+        if B > _LM_OWN_ROWS:
+            # above 64 rows the library's GEMM (F.linear, hipBLASLt) beats the MFMA tiles (at
+            # d = 4096, V = 151936: 286-353 us against 472-525 at B = 65-256 on MI355X); the
+            # statistics then come from one read of its logits
+            logits = torch.nn.functional.linear(hidden, weight)
+            tmax, tsum = self.tile_stats(logits)
+            return logits, tmax, tsum
         nT = (V + _lib.LM_TILE - 1) // _lib.LM_TILE
         logits = torch.empty(B, V, dtype=torch.bfloat16, device=dev)
         tmax = torch.empty(B, nT, dtype=torch.float32, device=dev)
@@ -281,6 +288,21 @@ class HipSampler:
         a.batch, a.dim, a.vocab = B, d, V
         _lib.check(self._lib.vsamp_lm_head(ctypes.byref(a), self._stream(dev)))
         return logits, tmax, tsum
+
+    def tile_stats(self, logits):
+        """The tile statistics ``lm_head`` returns, for bf16 logits ``[B, V]`` from any GEMM
+        (``vsamp_tile_stats``): per row and 128 logits, the max and the sum of exp(x - max).
+        Returns ``(tile_max, tile_sum)``, fp32 ``[B, ceil(V / 128)]`` each."""
+        dev = self._device(logits)
+        if logits.dtype != torch.bfloat16 or logits.dim() != 2 or logits.stride(1) != 1:
+            raise ValueError("tile_stats takes bf16 [B, V] logits with unit stride along V")
+        B, V = logits.shape
+        nT = (V + _lib.LM_TILE - 1) // _lib.LM_TILE
+        tmax = torch.empty(B, nT, dtype=torch.float32, device=dev)
+        tsum = torch.empty(B, nT, dtype=torch.float32, device=dev)
+        _lib.check(self._lib.vsamp_tile_stats(logits.data_ptr(), logits.stride(0) if B > 1 else V, B, V,
+                                              tmax.data_ptr(), tsum.data_ptr(), self._stream(dev)))
+        return tmax, tsum
 
     def logprobs_tiles(self, logits, tile_max, tile_sum, tokens=None, n_top=0):
         """``logprobs`` over the bf16 logits ``lm_head`` wrote, with its tile statistics
@@ -604,6 +626,7 @@ def _n_tiles(V: int) -> int:
 # batches up to this many workgroups (rows times workgroups per row) take the tile pass in one
 # launch (the library's rule)
 _TILE_FUSED_WORKGROUPS = 256
+_LM_OWN_ROWS = 64  # (lm_head: the library GEMM and vsamp_tile_stats above this many rows)
 
 # the per-token call's parameter words: temperature, top_p, min_p, the three penalties (fp32),
 # top_k (int32), the uniform (fp32)
