@@ -3003,7 +3003,8 @@ __global__ __launch_bounds__(kTileMaxThreads) void k_tile_max(const Tin* logits,
 
 // (the fused tile pass) Workgroup g of row r's G computes the maxima of tiles g * per .. (per =
 // ceil(nT / G), at most kTileSharePasses * 64: sixteen lanes a tile as k_tile_max, up to
-// kTileSharePasses 16-byte loads per thread issued before any is used) into a.tile_max with
+// kTileSharePasses runs of eight logits per thread, their 16-byte loads (one a run of bf16, two
+// of fp32) issued before any is used) into a.tile_max with
 // device-coherent stores; waits for them; then thread 0 counts the workgroup in at the row's
 // arrival word. The last of the G resets the word to 0 (nothing else touches it in this launch)
 // and returns true: it finishes the row, the others return false and exit. `flag` is an LDS word.
@@ -3131,8 +3132,8 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<Tin>& ro
     finish<false>(a, row, p, 0.0f, k, 0, &g.srch.vslot, r);
     return true;
   }
-  // Top-k rows count their tiles' maxima by the top 12 bits of their 16-bit keys (4096 bins in
-  // LDS): the lowest value of the bin holding the K-th largest is at most the K-th largest tile
+  // Top-k rows count their tiles' maxima by the top 12 bits of their keys (4096 bins in LDS; of
+  // a bf16 value, the top 12 bits of its 16-bit key): the lowest value of the bin holding the K-th largest is at most the K-th largest tile
   // max, so at most the K-th largest logit. The row max rides the same barrier (one LDS
   // atomicMax per wave).
   uint32_t* h12 = reinterpret_cast<uint32_t*>(&g) + kBitmapOffset;
@@ -3179,7 +3180,8 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<Tin>& ro
       const uint32_t incl2 = above + wave_incl_scan<uint32_t>(c);
       const int i = __ffsll(static_cast<long long>(__ballot(incl2 >= K))) - 1;
       const uint32_t bin = static_cast<uint32_t>(4095 - 64 * L - i);
-      // the bin's least value (not below -inf): of bf16 values, its least 16-bit key's
+      // the least value of the bin (not below -inf): of bf16 rows, the bf16 value of its least
+      // 16-bit key; of fp32 rows, the value of its least 32-bit key
       float theta;
       if constexpr (sizeof(Tin) == 2) {
         const uint32_t k16 = (bin << 4) > 0x007Fu ? (bin << 4) : 0x007Fu;

@@ -260,7 +260,8 @@ class HipSampler:
         ``logits [B, V] = hidden [B, d] @ weight [V, d]^T`` (fp32 accumulation, rounded to bf16, as
         ``F.linear`` returns it; model.py:230-233) and, per row and 128 logits, their max and sum of
         exp(x - max). Returns ``(logits, tile_max, tile_sum)``; the statistics feed
-        ``logprobs_tiles``."""
+        ``logprobs_tiles``. Up to 64 rows the fused kernel runs (d a multiple of 64); above, the
+        library GEMM (``F.linear``, any d) and ``tile_stats`` over its logits."""
         for name, t in (("hidden", hidden), ("weight", weight)):
             if t.dtype != torch.bfloat16 or t.device.type != "cuda" or t.dim() != 2 or t.stride(1) != 1:
                 raise ValueError(f"{name} must be a bf16 2-D tensor on a GPU with unit stride along d")
