@@ -371,15 +371,25 @@ __device__ __forceinline__ uint32_t Row<float>::load(int b, float v[kBlk]) const
   return valid;
 }
 
-// Stripes in flight in for_each_ahead's rolling window (0: groups of kDepth stripes, each group's
+// Stripes in flight in for_each_block_ahead's rolling window (0: groups of kDepth stripes, each group's
 // loads issued together and used before the next group's).
 constexpr int kRollDepth = 2;
 
-// Visit every element of the row once: bulk lanes through `f(x, id)` in the calling thread's
-// blocks, exceptions spread over the workgroup. The groups of kDepth stripes wholly inside an
-// aligned row have their loads (and lane masks) issued together, ahead of the work on them.
-template <class Tin, class F>
-__device__ __forceinline__ void for_each_ahead(const Row<Tin>& row, F f, int j0 = 0) {
+// The IEEE maximum of a block's eight values (NaN when one of them is; -0 below +0), as a chain
+// that compiles to four three-operand maxima (v_maximum3_f32).
+__device__ __forceinline__ float max_of8(const float (&x)[kBlk]) {
+  float r = x[0];
+#pragma unroll
+  for (int i = 1; i < kBlk; ++i) r = __builtin_elementwise_maximum(r, x[i]);
+  return r;
+}
+
+// Every block of the row once, as fb(v, out, b) in the calling thread: v its eight values and
+// `out` the lanes that hold no bulk value (penalised, or past the row's end). The groups of kDepth
+// stripes wholly inside an aligned row have their loads (and lane masks) issued together, ahead
+// of the work on them. Exceptions are the caller's.
+template <class Tin, class FB>
+__device__ __forceinline__ void for_each_block_ahead(const Row<Tin>& row, FB fb, int j0 = 0) {
   constexpr int kDepth = 2;  // (measured on logprobs and fp32 rows: 2 beats 4 and 8)
   const int whole = row.vec ? row.V / kBlk / kThreads : 0;  // (uniform) such stripes
   int j = j0;  // (the stripes below j0, a multiple of kDepth, were visited by the caller)
@@ -408,9 +418,7 @@ __device__ __forceinline__ void for_each_ahead(const Row<Tin>& row, F f, int j0 
           const int bn = (j + D + k < end ? j + D + k : j + k) * kThreads + threadIdx.x;
           q[k].load(row.p, bn);
           masked[k] = row.bm ? row.bm[bn] : 0u;
-#pragma unroll
-          for (int i = 0; i < kBlk; ++i)
-            if (!(m & (1u << i))) f(v[i], b * kBlk + i);
+          fb(v, m, b);
         }
       }
     }
@@ -429,18 +437,25 @@ __device__ __forceinline__ void for_each_ahead(const Row<Tin>& row, F f, int j0 
       const int b = (j + k) * kThreads + threadIdx.x;
       float v[kBlk];
       q[k].values(v);
-#pragma unroll
-      for (int i = 0; i < kBlk; ++i)
-        if (!(masked[k] & (1u << i))) f(v[i], b * kBlk + i);
+      fb(v, masked[k], b);
     }
   }
   for (int b = j * kThreads + threadIdx.x; b < row.nblk; b += kThreads) {
     float v[kBlk];
     const uint32_t valid = row.load(b, v);
+    fb(v, ~valid & 0xFFu, b);
+  }
+}
+
+// Visit every element of the row once: bulk lanes through `f(x, id)` in the calling thread's
+// blocks, exceptions spread over the workgroup.
+template <class Tin, class F>
+__device__ __forceinline__ void for_each_ahead(const Row<Tin>& row, F f, int j0 = 0) {
+  for_each_block_ahead(row, [&](const float (&v)[kBlk], uint32_t out, int b) {
 #pragma unroll
     for (int i = 0; i < kBlk; ++i)
-      if (valid & (1u << i)) f(v[i], b * kBlk + i);
-  }
+      if (!(out & (1u << i))) f(v[i], b * kBlk + i);
+  }, j0);
   for (int e = threadIdx.x; e < row.nexc; e += kThreads) f(row.eval[e], row.eid[e]);
 }
 
@@ -1389,10 +1404,35 @@ __device__ __forceinline__ void generic_row(const SampleArgs& a, Row<Tin> row, c
         for (int i = 0; i < kBlk; ++i)
           if (!(masked[k] & (1u << i))) append(v[k][i], (k * kThreads + static_cast<int>(threadIdx.x)) * kBlk + i);
       }
-      for_each_ahead(row, [&](float x, int id) {
-        visit_max(x, id);
-        append(x, id);
-      }, kStreamDepth);
+      if (!kGreedy && tau_x > -INFINITY) {  // (uniform)
+        // The rest of the row block by block: lanes without a bulk value enter as -inf (below
+        // tau_x: never staged, never the max), the block's max by IEEE maximum (NaN when a value
+        // is: the row's NaN test, after the loop), and the staging tests only where some lane's
+        // block reaches tau_x -- in place of each element's branch, canonicalised fmax and NaN flag
+        float mx = -INFINITY;
+        for_each_block_ahead(row, [&](const float (&v)[kBlk], uint32_t out, int b) {
+          float x[kBlk];
+#pragma unroll
+          for (int i = 0; i < kBlk; ++i) x[i] = out & (1u << i) ? -INFINITY : v[i];
+          const float bx = max_of8(x);
+          mx = __builtin_elementwise_maximum(mx, bx);
+          if (__ballot(!(bx < tau_x))) {  // (uniform over the wave; a NaN block takes it too)
+#pragma unroll
+            for (int i = 0; i < kBlk; ++i) append(x[i], b * kBlk + i);
+          }
+        }, kStreamDepth);
+        for (int e = threadIdx.x; e < row.nexc; e += kThreads) {
+          visit_max(row.eval[e], row.eid[e]);
+          append(row.eval[e], row.eid[e]);
+        }
+        vnan |= mx != mx ? 1u : 0u;
+        vmax = fmaxf(vmax, mx);  // (mx: no NaN unless vnan)
+      } else {
+        for_each_ahead(row, [&](float x, int id) {
+          visit_max(x, id);
+          append(x, id);
+        }, kStreamDepth);
+      }
     } else {
       for_each(row, visit);
     }
