@@ -81,14 +81,15 @@ def mixed_params(rng, B, V, penalties_every=0):
     return out
 
 
-def check(logits, params, seed, hist=None, label=""):
+def check(logits, params, seed, hist=None, label="", draft=None):
     B, V = logits.shape
     rng = np.random.default_rng(seed)
     s = hip()
     tm = tile_max(logits)
     pp = pack_params(params)
     u = torch.from_numpy(rng.random(B, dtype=np.float32))
-    draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
+    if draft is None:
+        draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32))
     if hist is not None:
         hi, ho = pack_history(hist)
     else:
@@ -176,6 +177,37 @@ def test_gpu_sample_tiles_on_crafted_rows():
                   (1.0, dict(top_k=1)), (0.5, dict(top_k=20, top_p=0.5))]:
         params = [SamplingParams(temperature=T, **kw) for _ in range(B)]
         check(logits, params, int(T * 10) + len(kw), label=f"crafted T={T} {kw}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("V", [4099, 8192])
+def test_gpu_partial_cutoff_member_then_draw(V):
+    # Rows of massive ties whose top-p cutoff splits a group of equal values, each with a draft
+    # id inside that group: the row finds the group's r-th member (the draft's probability needs
+    # it) and then the draw's member, two member searches in one workgroup through the same LDS
+    # result word. Unaligned rows (V = 4099) search their elements one by one, aligned ones from
+    # the low bytes kept in registers. Every row against the row passes, the tile pass and the
+    # oracle.
+    g = torch.Generator().manual_seed(11)
+    B = 48
+    rows, drafts = [], []
+    for b in range(B):
+        kind = b % 3
+        if kind == 0:
+            x = torch.full((V,), 0.25)  # one value: the cutoff inside it
+        elif kind == 1:
+            x = torch.randn(V, generator=g)
+            x[: 300 + b] = 5.0  # a tied group above the rest, the cutoff inside it
+        else:
+            x = (torch.randn(V, generator=g) * 0.01).clone()  # a few values, ties at every boundary
+            x[b % 97 : b % 97 + 600] = 0.0390625
+        rows.append(x)
+        drafts.append(b % 150)  # (inside the kept part of the tied group)
+    logits = torch.stack(rows).to(torch.bfloat16).to(DEV)
+    draft = torch.tensor(drafts, dtype=torch.int32)
+    for T, kw in [(0.5, dict(top_k=20, top_p=0.5)), (1.0, dict(top_p=0.3)), (0.8, dict(top_k=400, top_p=0.4))]:
+        params = [SamplingParams(temperature=T, **kw) for _ in range(B)]
+        check(logits, params, 7 + len(kw), label=f"partial V={V} T={T} {kw}", draft=draft)
 
 
 @pytest.mark.gpu

@@ -2145,7 +2145,7 @@ __device__ __forceinline__ int select_member(const Row<uint16_t>& row, FastSmem&
     f.si[6] = (c0 + 4 * wi + bi) * kBlk + __ffs(mask) - 1;
   }
   lds_barrier();
-  return f.si[6];  // (nothing writes f.si[6] again in this launch)
+  return f.si[6];  // (a caller that searches again resets f.si[6] only after another barrier)
 }
 
 // (merge mode) The id of the j-th (0-based, ascending id) token whose penalised value is v, or
@@ -2881,6 +2881,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, Row<uint16_t> row,
       if (cells_fit) {
         uint8_t* cells = reinterpret_cast<uint8_t*>(hist + kMatchOffset);
         id = select_member(row, f, ne, k.vc, static_cast<u64>(k.r - 1), cells, mxk, low, sl, og, e0, estep);
+        lds_barrier();  // (every wave has read f.si[6] before thread 0 resets it for the draw's search)
         const int ncq = cells_per(row) * kThreads / 16;
         for (int i = tid; i < ncq; i += kThreads) reinterpret_cast<uint4*>(cells)[i] = make_uint4(0, 0, 0, 0);
         if (tid == 0) f.si[6] = -1;
