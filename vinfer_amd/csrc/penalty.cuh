@@ -6,8 +6,9 @@
 //
 // Workspace output for row r (ids with c > 0 are the row's "exceptions"), in no particular order:
 //   n_exc[r]                         number of distinct history ids in [0, V)
-//   exc_id/exc_val/exc_cnt[h0 + e]   e-th exception (h0 = hist_offsets[r]; a row has at most L_r
-//                                    of them, so the slots never overlap)
+//   exc_id/exc_val[h0 + e]           e-th exception (h0 = hist_offsets[r]; a row has at most L_r
+//                                    of them, so the slots never overlap); exc_cnt[h0 + e] its
+//                                    count where a counting path gathers from the workspace
 #pragma once
 
 #include "common.cuh"
@@ -20,7 +21,7 @@ struct Workspace {
   uint32_t* n_exc;   // [B]
   int32_t* exc_id;   // [H]
   float* exc_val;    // [H]
-  int32_t* exc_cnt;  // [H]
+  int32_t* exc_cnt;  // [H] (the counting passes' own pairs for their gather; not always written)
 };
 
 struct PenaltyArgs {
@@ -231,10 +232,7 @@ __device__ __forceinline__ bool bitmap_count(const PenaltyArgs& a, uint32_t* lds
       const int id = rid[e];
       const int c = count_of(e);
       if (dc) dc[id] = c;
-      if (on) {
-        a.ws.exc_id[h0 + e] = id;
-        a.ws.exc_cnt[h0 + e] = c;
-      }
+      if (on) a.ws.exc_id[h0 + e] = id;  // (the counts stay in LDS for the gather: no exc_cnt)
     }
     if (on)
       gather_values<Tin>(a, row, h0, total, [&](uint32_t e) { return make_int2(rid[e], count_of(e)); }, rep, pres,
