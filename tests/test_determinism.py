@@ -5,7 +5,8 @@ and barriers; a missing barrier shows first as a launch whose result depends on 
 happen to interleave, which one run against the oracle can miss. Each path below runs REPEAT
 times on fixed inputs -- rows with penalties, drafts and mixed parameters, rows of massive ties
 whose top-p cutoff splits a group of equal values (two member searches in one workgroup), row
-states, split rows, fp32 rows through the generic path -- and every launch must equal the first.
+states, split rows, fp32 rows through the generic path, the speculative verify with its
+residual's hand-off between workgroups -- and every launch must equal the first.
 """
 
 from __future__ import annotations
@@ -103,3 +104,21 @@ def test_gpu_tied_rows_repeat_exactly_on_every_path(V):
         same_every_time(row_passes, label + " row passes")
         same_every_time(lambda: s.sample_tile_pass(logits, pp, u, None, None, draft), label + " tile pass")
         same_every_time(lambda: s.sample_states(logits, pp, u), label + " row states")
+
+
+def test_gpu_verify_repeats_exactly():
+    # the verify's residual hands each rejected row's stripe sums between its workgroups: half the
+    # drafts are the draft rows' argmax (mostly accepted), half random ids (mostly rejected)
+    B, K, V = 96, 2, 151936
+    g = torch.Generator().manual_seed(5)
+    xt = torch.randn(B, K + 1, V, generator=g) * 2.5
+    xq = xt[:, :K] + torch.randn(B, K, V, generator=g) * 0.5
+    drafts = torch.randint(0, V, (B, K), generator=g, dtype=torch.int32)
+    drafts[::2] = xq[::2].argmax(-1).to(torch.int32)
+    pp = pack_params([SamplingParams(temperature=0.8, top_p=0.95) for _ in range(B)], DEV)
+    rng = np.random.default_rng(6)
+    ua, ur = (torch.from_numpy(rng.random((B, K), np.float32)).to(DEV) for _ in range(2))
+    ub = uniforms(B, seed=7)
+    xt, xq, drafts = xt.to(torch.bfloat16).to(DEV), xq.to(torch.bfloat16).to(DEV), drafts.to(DEV)
+    s = hip()
+    same_every_time(lambda: s.verify(xt, xq, drafts, pp, ua, ur, ub), f"verify B={B} K={K} V={V}")
