@@ -36,13 +36,14 @@ PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "
 COPY_PROBE_BYTES = 1 << 30  # bytes read (and written) by one launch of the copy probe
 
 
-def measured_traffic() -> int | None:
-    """HBM bytes per launch of the sampler kernel, from the counter summary's
-    `traffic_bytes_per_launch:` line (None when the summary has none)."""
+def measured_traffic(key: str = "traffic_bytes_per_launch") -> int | None:
+    """HBM bytes per launch of the sampler kernel, from the counter summary's `<key>:` line
+    (traffic: FETCH_SIZE and WRITE_SIZE scaled; fetch_bytes_per_launch: the reads alone; None
+    when the summary has no such line)."""
     try:
         with open(PROFILE) as fh:
             for line in fh:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key + ":"):
                     return int(line.split(":", 1)[1].strip().replace(",", ""))
     except OSError:
         return None
@@ -927,6 +928,7 @@ def main() -> int:
     algo = w.algorithmic_bytes()
     logits_bytes = w.logits.numel() * w.logits.element_size()
     achieved = algo / (us_step * 1e-6) / 1e9  # average launch: the timed region over K
+    fetched = measured_traffic("fetch_bytes_per_launch")
     out = {
         "metric": METRIC,
         "value": B / (us_step * 1e-6),
@@ -968,6 +970,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": measured_traffic(),
+            # HBM reads per launch over one read of the logits (the counters' read bytes, the
+            # histories' included)
+            "logits_passes": None if fetched is None else fetched / logits_bytes,
             "algorithmic_bytes_per_launch": algo,
             "logits_only_frac": logits_bytes / (us_step * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "kernel": "vs::k_sample<bf16, penalties>",
