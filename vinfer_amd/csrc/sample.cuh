@@ -371,8 +371,8 @@ __device__ __forceinline__ uint32_t Row<float>::load(int b, float v[kBlk]) const
   return valid;
 }
 
-// Stripes in flight in for_each_block_ahead's rolling window (0: groups of kDepth stripes, each group's
-// loads issued together and used before the next group's).
+// Stripes in flight in for_each_block_ahead's rolling window (0: groups of kDepth stripes, each
+// group's loads issued together and used before the next group's).
 constexpr int kRollDepth = 2;
 
 // The IEEE maximum of a block's eight values (NaN when one of them is; -0 below +0), as a chain
@@ -3174,9 +3174,9 @@ __device__ __forceinline__ bool tile_row(const SampleArgs& a, const Row<Tin>& ro
     return true;
   }
   // Top-k rows count their tiles' maxima by the top 12 bits of their keys (4096 bins in LDS; of
-  // a bf16 value, the top 12 bits of its 16-bit key): the lowest value of the bin holding the K-th largest is at most the K-th largest tile
-  // max, so at most the K-th largest logit. The row max rides the same barrier (one LDS
-  // atomicMax per wave).
+  // a bf16 value, the top 12 bits of its 16-bit key): the lowest value of the bin holding the
+  // K-th largest is at most the K-th largest tile max, so at most the K-th largest logit. The row
+  // max rides the same barrier (one LDS atomicMax per wave).
   uint32_t* h12 = reinterpret_cast<uint32_t*>(&g) + kBitmapOffset;
   uint32_t* smax = &g.rdx.ncand;
   uint32_t* tcount = reinterpret_cast<uint32_t*>(g.rdx.bq);  // (the candidate tiles' count)
@@ -3336,8 +3336,8 @@ __device__ __forceinline__ SampleArgs globalized(SampleArgs a) {
 
 // STATE: also write each row's RowState (the speculative verify's launches; never with PEN).
 // SPLIT: a bf16 split-row launch (grid B * G).
-// TILES: rows (bf16 or fp32) with their tile maxima (a.tile_max): the rows tile_row can decide are decided
-// from a few tiles, the others take the row passes below.
+// TILES: rows (bf16 or fp32) with their tile maxima (a.tile_max): the rows tile_row can decide
+// are decided from a few tiles, the others take the row passes below.
 template <class Tin, bool PEN, bool STATE = false, bool SPLIT = false, bool TILES = false>
 __global__ __launch_bounds__(kThreads) void k_sample(SampleArgs a_) {
   const SampleArgs a = globalized(a_);
