@@ -265,10 +265,10 @@ def _sub_hist(w: Workload, rows):
 
 def test_large_fp32_full_launch():
     # 1024 x 151936 fp32 rows, histories up to 32768 ids, one launch: a 1024-workgroup grid and
-    # the full-size history workspace; 64 rows checked, and the exact counts of the 8 longest
+    # the full-size history workspace; every row checked, and the exact counts of the 8 longest
     # histories
     w = workloads.make("large_fp32")
-    check_subset(w, 64, seed=11)
+    check_subset(w, w.batch, seed=11)
     lens = (w.hist_offsets[1:] - w.hist_offsets[:-1]).numpy()
     longest = np.argsort(-lens, kind="stable")[:8]
     d = w.to(DEV)
@@ -281,8 +281,9 @@ def test_large_fp32_full_launch():
 
 
 def test_verify_bf16_full_launch():
-    # 192 x 262144 bf16 rows with draft probabilities, one launch; 64 rows checked
-    check_subset(workloads.make("verify_bf16"), 64, seed=12)
+    # 192 x 262144 bf16 rows with draft probabilities, one launch; every row checked
+    w = workloads.make("verify_bf16")
+    check_subset(w, w.batch, seed=12)
 
 
 def test_gpu_torch_division_by_a_scalar():
