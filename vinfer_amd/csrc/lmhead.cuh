@@ -440,9 +440,10 @@ __global__ __launch_bounds__(kLsThreads, 1) void k_lm_stream(LmHeadArgs a) {
 // What the epilogues above write beside their own logits, for bf16 logits another GEMM wrote
 // (above 64 rows the library's GEMM beats the MFMA tiles above): per row and kLmBN logits, the
 // max (ordered keys: a NaN is the largest) and the fp32 sum of exp(x - max) over the tile (0 when
-// the max is infinite or NaN). Sixteen lanes a tile, eight logits a lane, 16-lane DPP reductions
-// (the sum in another order than an epilogue's, so it may differ in the last bits); grid
-// (ceil(nT / 16), B) of 256-thread workgroups.
+// the max is infinite or NaN). Sixteen lanes a tile, eight logits a lane (a lane's max by IEEE
+// maximum, its ordered keys only when a NaN is among them), 16-lane DPP reductions (the sum in
+// another order than an epilogue's, so it may differ in the last bits); grid (ceil(nT / 16), B)
+// of 256-thread workgroups.
 constexpr int kTsThreads = 256;
 __global__ __launch_bounds__(kTsThreads) void k_tile_stats(const uint16_t* logits, int64_t stride, int V, int nT,
                                                            float* tmax, float* tsum) {
@@ -470,9 +471,26 @@ __global__ __launch_bounds__(kTsThreads) void k_tile_stats(const uint16_t* logit
     }
   }
   uint32_t mk = 0;  // (below every key)
+  auto key_max = [&](int n) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < nv) mk = max(mk, key_of(x[i]));
+    for (int i = 0; i < 8; ++i)
+      if (i < n) mk = max(mk, key_of(x[i]));
+  };
+  if (nv == 8) {
+    // the IEEE maximum of the eight (four three-operand maxima; -0 below +0, as in key order): the
+    // value of the largest key unless one of them is a NaN, which makes it a NaN -- then the keys
+    // decide which NaN
+    float bx = x[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) bx = __builtin_elementwise_maximum(bx, x[i]);
+    mk = key_of(bx);
+    if (bx != bx) {
+      mk = 0;
+      key_max(8);
+    }
+  } else {
+    key_max(nv);
+  }
   auto umax = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
   mk = umax(mk, dpp::mov<dpp::kXor1>(mk));
   mk = umax(mk, dpp::mov<dpp::kXor2>(mk));
