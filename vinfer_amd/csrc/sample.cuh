@@ -2985,24 +2985,33 @@ __device__ __forceinline__ uint32_t kth_key16(const uint32_t (&keys)[4], int nk,
 constexpr int kTileFusedWorkgroups = 256;  // (one round on the CUs; vsamp_sample_tile_pass)
 constexpr int kTileMaxThreads = 256;
 constexpr int kTilesPerBlock = kTileMaxThreads / 16;
-// A lane's eight logits of a tile (16-byte loads: one of bf16, two of fp32) and their largest key.
+// A lane's eight logits of a tile (16-byte loads: one of bf16, two of fp32) and their largest key:
+// the key of their IEEE maximum (-0 below +0, as in key order), or, when a NaN among them makes
+// that maximum a NaN, the largest of their keys.
 template <class Tin>
 constexpr int kTileLoads = sizeof(Tin) == 2 ? 1 : 2;
 template <class Tin>
 __device__ __forceinline__ uint32_t lane_tile_key(const uint4 (&v)[kTileLoads<Tin>]) {
-  uint32_t mk = 0;  // (below every key)
+  float x[kBlk];
 #pragma unroll
   for (int j = 0; j < kTileLoads<Tin>; ++j) {
     const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (sizeof(Tin) == 2) {
-        mk = max(mk, key_of(__uint_as_float(w[i] << 16)));
-        mk = max(mk, key_of(__uint_as_float(w[i] & 0xFFFF0000u)));
+        x[2 * i] = __uint_as_float(w[i] << 16);
+        x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
       } else {
-        mk = max(mk, key_of(__uint_as_float(w[i])));
+        x[4 * j + i] = __uint_as_float(w[i]);
       }
     }
+  }
+  const float bx = max_of8(x);
+  uint32_t mk = key_of(bx);
+  if (bx != bx) {
+    mk = 0;  // (below every key)
+#pragma unroll
+    for (int i = 0; i < kBlk; ++i) mk = max(mk, key_of(x[i]));
   }
   return mk;
 }
