@@ -3,7 +3,8 @@ bf16 and fp32, padded row strides, plain, peaked and tied rows, every parameter 
 T = 1.5, top-k past the sorted lists' 256, top-p, min-p, all three penalties) and histories up to
 4096 ids, each launch run twice: every non-tie row's id and draft probability, and the two
 launches bit for bit equal. Log-probabilities, raw and from tile statistics, over rows with ties,
-NaNs and infinities. The speculative verify over random draft counts, vocabularies and scales."""
+NaNs and infinities. The speculative verify over random draft counts, vocabularies and scales.
+The per-token call with its vocabulary, dtype, parameters and history form changing per call."""
 
 from __future__ import annotations
 
@@ -169,3 +170,43 @@ def test_gpu_random_sweep_of_the_verify():
             assert tokens[b, : len(w.tokens)].tolist() == w.tokens, (seed, b)
             assert (tokens[b, len(w.tokens) :] == -1).all(), (seed, b)
     assert residual > 0
+
+
+def test_gpu_random_sweep_of_the_per_token_call():
+    # the engine's per-token call sample(logits[V], params, seed, position, history) through one
+    # sampler whose vocabulary, logits dtype, parameters and history form change from call to call
+    # (its pinned buffers and argument block are cached per shape), rows at odd offsets of a
+    # larger buffer; every non-tie token against the oracle
+    from oracle.sampler_oracle import classify_ties
+    from oracle.sampler_oracle import sample_batch as oracle_batch
+    from vinfer_amd.sampling import uniform
+
+    s = SAMPLER.resolve("hip", BackendContext(DEV, torch.bfloat16))
+    rng = np.random.default_rng(40_000)
+    g = torch.Generator().manual_seed(40_000)
+    for call in range(80):
+        V = int(rng.choice([97, 1000, 4099, 151936]))
+        dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+        off = int(rng.integers(0, 9))
+        big = (torch.randn(V + 16, generator=g) * float(rng.choice([0.1, 2.0, 4.0]))).to(dtype)
+        x = big[off : off + V]
+        sp = SamplingParams(
+            temperature=float(rng.choice([0.0, 0.7, 1.0])),
+            top_k=int(rng.choice([0, 0, 20, 300])),
+            top_p=float(rng.choice([1.0, 0.8, 0.95])),
+            min_p=float(rng.choice([0.0, 0.0, 0.05])),
+            repetition_penalty=float(rng.choice([1.0, 1.0, 1.2])),
+            frequency_penalty=float(rng.choice([0.0, 0.3])),
+        )
+        hist = rng.integers(0, V, int(rng.integers(0, 3000))).tolist()
+        form = call % 3
+        h = [hist, torch.tensor(hist, dtype=torch.int32, device=DEV), torch.tensor(hist, dtype=torch.int64)][form]
+        seed, pos = int(rng.integers(0, 1 << 40)), int(rng.integers(0, 1 << 20))
+        print(f"per-token sweep call {call} V={V} {dtype} offset={off} history={len(hist)} form={form}", flush=True)
+        tok = s.sample(big.to(DEV)[off : off + V], sp, seed, pos, history=h if sp.penalized else None)
+        hi = np.asarray(hist if sp.penalized else [], dtype=np.int32)
+        res = oracle_batch(x.float().numpy()[None], [sp.temperature], [sp.top_k], [sp.top_p], [sp.min_p],
+                           [sp.repetition_penalty], [sp.presence_penalty], [sp.frequency_penalty],
+                           hi, np.array([0, len(hi)], np.int32), [uniform(seed, pos)])[0]
+        if not classify_ties(res):
+            assert tok == res.token, (call, tok, res.token)
