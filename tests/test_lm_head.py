@@ -83,6 +83,40 @@ def test_gpu_lm_head_matches_torch_fp32(B, d, V):
     torch.testing.assert_close(tsum.double(), s, rtol=1e-5, atol=0)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,d,V", [(65, 128, 5000), (100, 192, 9000), (300, 256, 5000), (600, 64, 2100),
+                                   (256, 4096, 151936)])
+def test_gpu_c_abi_lm_head_above_64_rows(B, d, V):
+    # above 64 rows the backend's lm_head takes the library GEMM, while vsamp_lm_head itself (a C
+    # caller's route) runs the 256 x 128 MFMA tiles: called here through the C ABI directly
+    import ctypes
+
+    print(f"vsamp_lm_head B={B} d={d} V={V}", flush=True)
+    hidden, weight = operands(B + d + V, B, d, V)
+    nT = (V + TILE - 1) // TILE
+    logits = torch.empty(B, V, dtype=torch.bfloat16, device=DEV)
+    tmax = torch.empty(B, nT, dtype=torch.float32, device=DEV)
+    tsum = torch.empty(B, nT, dtype=torch.float32, device=DEV)
+    a = _lib.VsampLmHeadArgs()
+    a.hidden, a.hidden_stride = hidden.data_ptr(), d
+    a.weight, a.weight_stride = weight.data_ptr(), d
+    a.logits, a.logits_stride = logits.data_ptr(), V
+    a.tile_max, a.tile_sum = tmax.data_ptr(), tsum.data_ptr()
+    a.batch, a.dim, a.vocab = B, d, V
+    stream = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+    _lib.check(_lib.load().vsamp_lm_head(ctypes.byref(a), stream))
+    torch.cuda.synchronize()
+    ref = hidden.float() @ weight.float().T
+    mag = hidden.float().abs() @ weight.float().abs().T
+    err = (logits.float() - ref).abs()
+    tol = bf16_ulp(ref) + mag * 2.0**-16
+    assert bool((err <= tol).all()), float((err / tol).max())
+    assert float((logits == ref.to(torch.bfloat16)).float().mean()) >= 0.99
+    m, s = tile_stats(logits)
+    assert torch.equal(tmax.double(), m)
+    torch.testing.assert_close(tsum.double(), s, rtol=1e-5, atol=0)
+
+
 def check_logprobs_tiles(logits, tmax, tsum, tokens, n_top, oracle_rows=()):
     s = hip()
     t1, i1, l1 = s.logprobs_tiles(logits, tmax, tsum, tokens, n_top)
