@@ -365,3 +365,39 @@ def test_gpu_tile_pass_random_shapes_and_parameters():
         w = Workload("random tile pass", logits.cpu(), pp, u, None, None, draft)
         ties, bad = compare_ids(a.cpu(), oracle(w), ap.cpu())
         assert not bad, (case, bad[:10])
+
+
+@pytest.mark.gpu
+def test_gpu_prepared_launches_equal_the_calls():
+    # prepare_tiles (sample_tiles on fixed buffers) and prepare_batch on a small batch (the
+    # one-launch tile pass on its own maxima and arrival words), each launched three times with
+    # the logits (and the maxima) rewritten in place between launches: the same ids and draft
+    # probabilities as the one-off calls on those logits
+    s = hip()
+    B, V = 8, 151936
+    g = torch.Generator().manual_seed(21)
+    rng = np.random.default_rng(21)
+    logits = torch.empty(B, V, dtype=torch.bfloat16, device=DEV)
+    tm = torch.empty(B, (V + TILE - 1) // TILE, dtype=torch.float32, device=DEV)
+    pp = pack_params(mixed_params(rng, B, V), DEV)
+    u = torch.from_numpy(rng.random(B, dtype=np.float32)).to(DEV)
+    draft = torch.from_numpy(rng.integers(0, V, B).astype(np.int32)).to(DEV)
+    st_tiles = s.prepare_tiles(logits, tm, pp, u, None, None, draft)
+    st_batch = s.prepare_batch(logits, pp, u, None, None, draft)
+    for rep in range(3):
+        x = torch.randn(B, V, generator=g) * float(rng.choice([0.5, 2.0, 4.0]))
+        x[rep % B, 1234] = 30.0  # (a peaked row)
+        logits.copy_(x.to(torch.bfloat16).to(DEV))
+        tm.copy_(tile_max(logits))
+        print(f"prepared launches rep {rep}", flush=True)
+        st_tiles.launch()
+        st_batch.launch()
+        torch.cuda.synchronize()
+        a, ap = st_tiles.ids.clone(), st_tiles.draft_prob.clone()
+        b, bp = st_batch.ids.clone(), st_batch.draft_prob.clone()
+        want, wantp = row_passes(s, logits, pp, u, None, None, draft)
+        c, cp = s.sample_tiles(logits, tm, pp, u, None, None, draft)
+        torch.cuda.synchronize()
+        for ids, dp in ((a, ap), (b, bp), (c, cp)):
+            assert torch.equal(ids, want), rep
+            assert torch.equal(dp.view(torch.int32), wantp.view(torch.int32)), rep
